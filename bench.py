@@ -1,0 +1,186 @@
+"""Benchmark of the batch-1 Whisper-large-v3-turbo hot path on one MI355X.
+
+Workload (one "step"): a full ``CustomModel.transcribe`` of a seeded 30 s synthetic clip — HIP log-mel,
+32-layer MFMA encoder + cross K/V in a hipGraph, 4-token prompt, then 224 greedy tokens with the 8-step
+decoder hipGraph (fixed length, no EOS stop), with seeded random-init weights of the
+whisper-large-v3-turbo architecture. The reference's timing boundary is kept: the clock starts at an
+in-memory waveform and stops at the token-id list (reference custom/model.py:179-225).
+
+Reported metric: decode-step us (median GPU time per decoder step, HIP events around every 8-step graph
+replay inside the timed transcribes), its achieved HBM GB/s from the algorithmic bytes of a step, the
+30 s-clip E2E ms and TTFT. ``roofline`` covers the LM-head kernel (final LN + tied-embedding GEMV +
+argmax + finalize), timed standalone with HIP events over rotating copies of the 133 MB embedding so it
+streams from HBM as inside the step. ``cpu_baseline`` times the CPU oracle's decoder step on this host.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+METRIC = 'decode-step µs + achieved HBM GB/s; 30 s-clip E2E ms & TTFT, batch 1'
+HBM_PEAK_GBPS = 8000.0
+
+
+def decode_step_bytes(dims, length):
+    """Algorithmic HBM bytes of one decoder step attending over `length` cached positions: every decoder
+    weight, bias and LayerNorm vector once, the tied 51866 x 1280 LM head once, the cross K/V of all
+    layers, the self K/V rows 0..length-1 of all layers, the two embedding rows and the suppress mask."""
+    d, f, L = dims.d_model, dims.ffn, dims.dec_layers
+    per_layer = 2 * (3 * d * d + 3 * d * d + 2 * d * f) + 2 * (3 * d + d + d + d + f + d) + 2 * 6 * d
+    weights = L * per_layer + 2 * 2 * d  # + final LN
+    lm_head = 2 * dims.vocab * d
+    cross = L * 2 * dims.heads * dims.enc_len * dims.head_dim * 2
+    self_kv = L * 2 * dims.heads * length * dims.head_dim * 2
+    return weights + lm_head + cross + self_kv + 2 * 2 * d + dims.vocab
+
+
+def lm_head_bytes(dims):
+    """Algorithmic bytes of one fused LM-head launch: the embedding, the suppress mask, h, x, gamma, beta."""
+    return 2 * dims.vocab * dims.d_model + dims.vocab + 4 * 2 * dims.d_model
+
+
+def time_lm_head(model, reps, copies=3):
+    """Average us per launch of the fused LM-head kernel, HIP events on the launch stream, rotating over
+    `copies` embedding copies (>= 256 MB MALL) so each launch reads its weights from HBM."""
+    import torch
+
+    ext, d = model.ext, model.dims
+    tables = [model.lm_head] + [model.lm_head.clone() for _ in range(copies - 1)]
+    tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
+    state = torch.zeros(2, dtype=torch.long, device='cuda')
+    cur = torch.zeros(1, dtype=torch.long, device='cuda')
+    best = torch.zeros(1, dtype=torch.long, device='cuda')
+    ctr = torch.zeros(1, dtype=torch.int32, device='cuda')
+    g, b, eps = model.final_ln
+    h, x = model.h[0], model.pending
+
+    def launch(i):
+        ext.lm_head_argmax_fused(h, x, g, b, eps, tables[i % copies], model.suppress, best, tokens, state, cur,
+                                 d.max_pos, ctr)
+
+    for i in range(2 * copies):
+        launch(i)
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(reps):
+        launch(i)
+    end.record(stream)
+    end.synchronize()
+    del tables
+    return start.elapsed_time(end) * 1e3 / reps
+
+
+def cpu_baseline(model, seconds):
+    """The CPU oracle's decoder step (numpy fp32 with the reference's fp16 rounding points) on this host,
+    on the GPU model's cross K/V, for a bounded number of steps."""
+    import numpy as np
+
+    from flash_whisper_amd import weights
+    from oracle.decoder import DecoderOracle
+
+    d = model.dims
+    names = [n for n, _, _ in weights.param_specs(d) if n.startswith('model.decoder.')]
+    params = weights.host_params(d, model.seed, names)
+    oracle = DecoderOracle(params, d, model.cross_kv.float().cpu().numpy())
+    del params
+    tok, pos, times = model.prompt[0], 0, []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end and len(times) < 64:
+        t0 = time.perf_counter()
+        logits = oracle.step(tok, pos)
+        times.append(time.perf_counter() - t0)
+        tok, pos = int(np.argmax(logits)), pos + 1
+    threads = int(os.environ.get('OPENBLAS_NUM_THREADS') or os.environ.get('OMP_NUM_THREADS') or os.cpu_count())
+    return dict(value=round(statistics.median(times) * 1e6, 1), unit='us/decode-step', cores=threads,
+                kind='port',
+                sample=f'{len(times)} decoder steps (positions 0..{len(times) - 1}) of the numpy oracle, fp32 math '
+                       f'with fp16 rounding points, median; host {platform.processor() or platform.machine()}, '
+                       f'nproc {os.cpu_count()}')
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=10, help='timed transcribes')
+    ap.add_argument('--warmup', type=int, default=2)
+    ap.add_argument('--tokens', type=int, default=224)
+    ap.add_argument('--kernel-reps', type=int, default=60)
+    ap.add_argument('--cpu-seconds', type=float, default=12.0)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py measures one GPU only (--gpus {args.gpus} requested): this build runs the batch-1 path on '
+              f'a single MI355X; independent clips would shard one per GPU with no exchange.', file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from flash_whisper_amd.audio import synthetic_clip
+    from flash_whisper_amd.config import CHUNK
+    from flash_whisper_amd.model import CustomModel
+
+    model = CustomModel(seed=0)
+    if not model.selftest['ok']:
+        print(f'selftest failed: {[c for c in model.selftest["checks"] if not c["ok"]]}', file=sys.stderr)
+        sys.exit(1)
+    clip = synthetic_clip(0)
+    for _ in range(args.warmup):
+        model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)
+
+    model.record_events = True
+    rows, step_us = [], []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)
+        rows.append(res)
+        chunk_ms = [a.elapsed_time(b) for a, b in model.chunk_events]
+        step_us.append(sum(chunk_ms) * 1e3 / (len(chunk_ms) * CHUNK))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    model.record_events = False
+
+    lm_us = time_lm_head(model, args.kernel_reps)
+    lm_bytes = lm_head_bytes(model.dims)
+    lm_gbps = lm_bytes / (lm_us * 1e-6) / 1e9
+
+    # mean cached length over the decode: positions 4 .. 4 + tokens - 1 attend over pos + 1 keys
+    lengths = np.arange(len(model.prompt) + 1, len(model.prompt) + args.tokens + 1)
+    step_bytes = float(np.mean([decode_step_bytes(model.dims, int(L)) for L in lengths]))
+    med_step = statistics.median(step_us)
+    step_gbps = step_bytes / (med_step * 1e-6) / 1e9
+    med = lambda k: statistics.median(r[k] for r in rows) * 1e3
+
+    out = {
+        'metric': METRIC, 'value': round(med_step, 2), 'unit': 'us/decode-step', 'n_gpus': 1,
+        'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(elapsed * 1e3 / args.steps, 3),
+        'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'fp16',
+        'data': 'synthetic: seeded 30 s clip (3 tones + noise), seeded random-init N(0, 0.02) fp16 weights',
+        'config': {'workload': f'whisper-large-v3-turbo batch 1: 30 s clip -> log-mel -> 32-layer encoder -> '
+                               f'{args.tokens} greedy tokens (8-step decoder hipGraph)',
+                   'clip_s': 30, 'tokens': args.tokens, 'batch': 1},
+        'decode_step_us': round(med_step, 2), 'decode_step_bytes': int(step_bytes),
+        'decode_step_hbm_gbps': round(step_gbps, 1), 'decode_step_roofline_frac': round(step_gbps / HBM_PEAK_GBPS, 4),
+        'e2e_ms': round(med('e2e_s'), 3), 'ttft_ms': round(med('ttft_s'), 3), 'mel_ms': round(med('mel_s'), 3),
+        'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
+        'n_tokens': rows[-1]['n_tokens'],
+        'roofline': {'kernel': 'lm_head_kernel<LN, FIN> (final LN + LM head GEMV + argmax + finalize)',
+                     'bound': 'hbm', 'achieved': round(lm_gbps, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+                     'frac': round(lm_gbps / HBM_PEAK_GBPS, 4), 'traffic': None, 'us_per_launch': round(lm_us, 2),
+                     'bytes_per_launch': lm_bytes},
+    }
+    if not args.no_cpu_baseline:
+        out['cpu_baseline'] = cpu_baseline(model, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,70 @@
+"""ctypes binding of the C ABI in include/flash_whisper.h (libflash_whisper.so, built in-tree).
+
+Loading never compiles: if the library is missing this raises, so no code path can silently run
+without the HIP kernels. Build it with ``python -m flash_whisper_amd.build``.
+"""
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_int64, c_uint64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / 'libflash_whisper.so'
+
+FW_OK, FW_EINVAL, FW_EHIP = 0, -1, -2
+ACT_NONE, ACT_GELU = 0, 1
+EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_BIAS_RESID_CLAMP, EPI_BIAS_GELU_POS, EPI_SCALE_Q = range(6)
+
+P = c_void_p
+# name -> (restype, argtypes); mirrors include/flash_whisper.h one to one.
+SIGNATURES = {
+    'fw_last_error': (ctypes.c_char_p, []),
+    'fw_version': (c_int, []),
+    'fw_lm_head_argmax': (c_int, [P, P, P, c_int, c_int, P, P]),
+    'fw_argmax_finalize': (c_int, [P, P, P, P, c_int, P]),
+    'fw_decode_attention': (c_int, [P, P, P, P, P, P, P, c_int, c_int, P, P, P, c_int64, c_float, P]),
+    'fw_add_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
+    'fw_embed': (c_int, [P, P, P, P, c_int, c_int, P, c_int, P]),
+    'fw_gemv': (c_int, [P, P, P, P, c_int, c_int, c_int, P]),
+    'fw_ln_gemv': (c_int, [P, P, P, P, P, c_float, P, P, P, P, c_int, c_int, P, P, P, c_int, c_int, c_int, P]),
+    'fw_decode_attention_fused': (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, P, c_int64, c_float,
+                                          P]),
+    'fw_lm_head_argmax_fused': (c_int, [P, P, P, P, c_float, P, P, c_int, c_int, P, P, P, P, c_int, P, P]),
+    'fw_log_mel': (c_int, [P, c_int, P, P, P, P, c_int64, P]),
+    'fw_log_mel_ws_floats': (c_int64, [c_int]),
+    'fw_gemm': (c_int, [P, c_int, P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
+    'fw_conv1d': (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, P, c_int, P]),
+    'fw_layernorm_rows': (c_int, [P, P, P, P, c_int, c_int, c_float, P]),
+    'fw_encoder_attention': (c_int, [P, P, c_int, c_int, P]),
+    'fw_cross_kv': (c_int, [P, c_int, P, P, P, c_int, c_int, P]),
+    'fw_synth_normal_f16': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float, P]),
+    'fw_synth_normal_f16_host': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class FwError(RuntimeError):
+    """A non-zero status from the C ABI (validation or HIP launch failure)."""
+
+
+def lib():
+    """The loaded library with typed entry points. Raises if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(f'{LIB_PATH} is missing; build it with `python -m flash_whisper_amd.build`')
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype, fn.argtypes = restype, argtypes
+            _lib = handle
+    return _lib
+
+
+def check(status, what):
+    if status != FW_OK:
+        msg = lib().fw_last_error().decode(errors='replace')
+        raise FwError(f'{what}: {msg} (status {status})')

@@ -1,0 +1,98 @@
+"""Builds the HIP kernels into the in-tree C-ABI library ``flash_whisper_amd/libflash_whisper.so``.
+
+``python -m flash_whisper_amd.build`` compiles every ``csrc/*.hip`` for gfx950 with hipcc (in
+parallel, one object per source) and links them. The library exports the entry points declared in
+``include/flash_whisper.h``. This replaces the reference's JIT extension build (custom/ext.py:13-18),
+which ran nvcc through torch.utils.cpp_extension; here the build is ahead-of-time and in-tree so the
+built library travels with the source tree.
+"""
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / 'csrc'
+BUILD_DIR = Path(os.environ.get('FW_BUILD_DIR', PKG / '_build'))
+LIB = PKG / 'libflash_whisper.so'
+ARCH = os.environ.get('FW_OFFLOAD_ARCH', 'gfx950')
+HIPCC = os.environ.get('HIPCC', shutil.which('hipcc') or '/opt/rocm/bin/hipcc')
+
+COMMON_FLAGS = [
+    f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-Wall', '-Wno-unused-function',
+    # packed fp32 (v_pk_*_f32) codegen stays off on this target
+    '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    '-Xarch_host', '-mfma',
+]
+# The synthetic-weight generator must round identically on host and device: no FMA contraction.
+PER_FILE_FLAGS = {'synth.hip': ['-ffp-contract=off']}
+
+
+def sources():
+    return sorted(CSRC.glob('*.hip'))
+
+
+def _compile(src, verbose):
+    obj = BUILD_DIR / (src.stem + '.o')
+    cmd = [HIPCC, *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), '-c', str(src), '-o', str(obj)]
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 target feature and says so; that is harmless.
+    noise = ('packed-fp32-ops', 'not a recognized feature', 'ignoring feature')
+    msg = '\n'.join(line for line in (proc.stdout + proc.stderr).splitlines()
+                    if not any(n in line for n in noise))
+    if proc.returncode != 0:
+        raise RuntimeError(f'hipcc failed for {src.name}:\n{msg}')
+    if verbose and msg.strip():
+        print(msg, flush=True)
+    return obj
+
+
+def build(verbose=False, jobs=None):
+    """Compiles all sources and links the shared library. Always rebuilds. Returns the library path."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
+    tmp = LIB.with_suffix('.so.tmp')
+    cmd = [HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', '-o', str(tmp), *map(str, objs), '-lpthread']
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f'link failed:\n{proc.stdout}{proc.stderr}')
+    os.replace(tmp, LIB)  # atomic: a process that already mapped the old file keeps it
+    return LIB
+
+
+def resource_usage():
+    """Per-kernel VGPR/SGPR/LDS/spill report from the compiler, for every source."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    lines = []
+    for src in sources():
+        cmd = [HIPCC, *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), '--cuda-device-only',
+               '-Rpass-analysis=kernel-resource-usage', '-c', str(src), '-o', os.devnull]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        lines += [line for line in proc.stderr.splitlines() if 'remark' in line]
+    return lines
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument('-v', '--verbose', action='store_true')
+    parser.add_argument('--resource-usage', action='store_true', help='print per-kernel register/LDS usage')
+    args = parser.parse_args()
+    lib = build(verbose=args.verbose)
+    print(f'built: {lib}')
+    if args.resource_usage:
+        print('\n'.join(resource_usage()))
+
+
+if __name__ == '__main__':
+    sys.exit(main())

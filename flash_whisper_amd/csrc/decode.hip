@@ -1,0 +1,671 @@
+// Batch-1 Whisper decoder kernels for gfx950 (wave64). Every launch goes on the caller's stream and
+// allocates nothing, so a whole decoder step can be captured into one hipGraph.
+//
+// Rounding points follow sp4s-s/flash_whisper custom/kernels/whisper_kernels.cu and the fp16
+// F.linear chain of custom/model.py:107-123: fp16 residual after every add, fp16 LayerNorm output,
+// fp16 GEMV outputs (bias added in fp32 before the single rounding), fp32 softmax with the scale
+// applied after the dot, fp16 attention output, fp16-rounded logits before the argmax.
+#include "fw_common.h"
+
+namespace fw {
+namespace {
+
+// ------------------------------------------------------------------------------------------
+// Residual + LayerNorm prologue shared by add_layernorm, the fused LN+GEMV and the LM head.
+// Produces y = fp16(LN(r) * gamma + beta) for the 1280-wide hidden vector in `y_out` (LDS or
+// global), where r = fp16(a + b) (b may be null) and a, b are either (h, x) or the embedding rows
+// (embed[cur], pos_embed[pos]). Block 0 stores r to r_out when r_out is non-null.
+// ------------------------------------------------------------------------------------------
+template <int NT>
+__device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b, _Float16* r_out,
+                                            const _Float16* gamma, const _Float16* beta, float eps,
+                                            _Float16* y_out, float* red) {
+  constexpr int kPairs = kHidden / 2;
+  constexpr int kPer = (kPairs + NT - 1) / NT;
+  const h2v* a2 = reinterpret_cast<const h2v*>(a);
+  const h2v* b2 = reinterpret_cast<const h2v*>(b);
+  h2v* r2 = reinterpret_cast<h2v*>(r_out);
+  const int tid = threadIdx.x;
+  float2 r[kPer];
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int idx = tid + i * NT;
+    r[i] = make_float2(0.f, 0.f);
+    if (idx < kPairs) {
+      const h2v av = a2[idx];
+      float rx = h2f(av.x), ry = h2f(av.y);
+      if (b2) {
+        const h2v bv = b2[idx];
+        rx = round_h(rx + h2f(bv.x));
+        ry = round_h(ry + h2f(bv.y));
+      }
+      r[i] = make_float2(rx, ry);
+      sum += rx + ry;
+      if (r2 && blockIdx.x == 0) {
+        h2v o;
+        o.x = f2h(rx);
+        o.y = f2h(ry);
+        r2[idx] = o;
+      }
+    }
+  }
+  const float mean = block_sum<NT>(sum, red) * (1.0f / kHidden);
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int idx = tid + i * NT;
+    if (idx < kPairs) {
+      const float dx = r[i].x - mean, dy = r[i].y - mean;
+      sq += dx * dx + dy * dy;
+    }
+  }
+  const float var = block_sum<NT>(sq, red) * (1.0f / kHidden);
+  const float inv = rsqrtf(var + eps);
+  const h2v* g2 = reinterpret_cast<const h2v*>(gamma);
+  const h2v* be2 = reinterpret_cast<const h2v*>(beta);
+  h2v* y2 = reinterpret_cast<h2v*>(y_out);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int idx = tid + i * NT;
+    if (idx < kPairs) {
+      const h2v g = g2[idx], be = be2[idx];
+      h2v o;
+      o.x = f2h((r[i].x - mean) * inv * h2f(g.x) + h2f(be.x));
+      o.y = f2h((r[i].y - mean) * inv * h2f(g.y) + h2f(be.y));
+      y2[idx] = o;
+    }
+  }
+}
+
+__device__ __forceinline__ void embed_rows(const int64_t* cur, const int64_t* state, const _Float16* embed,
+                                           const _Float16* pos_embed, int vocab, int max_pos, const _Float16** a,
+                                           const _Float16** b) {
+  int64_t tok = cur[0], pos = state[0];
+  tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  *a = embed + tok * kHidden;
+  *b = pos_embed + pos * kHidden;
+}
+
+// ------------------------------------------------------------------------------------------
+// add_layernorm (reference semantics: h updated in place, y written to global memory).
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) add_layernorm_kernel(_Float16* h, const _Float16* x, const _Float16* gamma,
+                                                            const _Float16* beta, _Float16* y, float eps) {
+  __shared__ float red[4];
+  // Single block: each thread reads its own elements before writing them back, so in-place is safe.
+  ln_prologue<256>(h, x, x ? h : nullptr, gamma, beta, eps, y, red);
+}
+
+__global__ void __launch_bounds__(256) embed_kernel(const int64_t* cur, const int64_t* state, const _Float16* embed,
+                                                    const _Float16* pos_embed, int vocab, int max_pos, _Float16* h) {
+  const _Float16 *a, *b;
+  embed_rows(cur, state, embed, pos_embed, vocab, max_pos, &a, &b);
+  for (int i = threadIdx.x; i < kHidden; i += blockDim.x) h[i] = f2h(h2f(a[i]) + h2f(b[i]));
+}
+
+// ------------------------------------------------------------------------------------------
+// GEMV: out[n] = act(fp16(W[n,:] . x + bias[n])). Each row is split over kLPR lanes that stream
+// 16-byte chunks; a wave covers 64 / kLPR rows at once and U row groups are loaded before any
+// arithmetic so every lane keeps U * kC 16-byte loads in flight. Blocks own contiguous row ranges.
+// With LN, the 1280-wide input is the LayerNorm of the residual, computed per block into LDS.
+// ------------------------------------------------------------------------------------------
+template <int K>
+struct RowSplit {
+  static constexpr int kChunksRow = K / 8;
+  static constexpr int kLPR = (K == kHidden) ? 32 : 64;
+  static constexpr int kC = kChunksRow / kLPR;
+  static constexpr int kRPW = kWave / kLPR;
+  static_assert(kChunksRow % kLPR == 0, "row must split evenly over the lanes");
+};
+
+struct LnArgs {
+  const _Float16* h;
+  const _Float16* x;
+  _Float16* h_out;
+  const _Float16* gamma;
+  const _Float16* beta;
+  float eps;
+  const int64_t* cur;
+  const int64_t* state;
+  const _Float16* embed;
+  const _Float16* pos_embed;
+  int vocab;
+  int max_pos;
+};
+
+template <int K, int NW, int U, bool LN, int ACT>
+__global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restrict__ xin, LnArgs ln,
+                                                       const _Float16* __restrict__ w,
+                                                       const _Float16* __restrict__ bias, _Float16* __restrict__ out,
+                                                       int n) {
+  using RS = RowSplit<K>;
+  constexpr int kRowsPerBlock = NW * RS::kRPW * U;
+  __shared__ __align__(16) _Float16 y_lds[LN ? kHidden : 8];
+  __shared__ float red[NW];
+  const uint4* xv;
+  if constexpr (LN) {
+    const _Float16 *a = ln.h, *b = ln.x;
+    if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b);
+    ln_prologue<NW * 64>(a, b, ln.h_out, ln.gamma, ln.beta, ln.eps, y_lds, red);
+    __syncthreads();
+    xv = reinterpret_cast<const uint4*>(y_lds);
+  } else {
+    xv = reinterpret_cast<const uint4*>(xin);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % RS::kLPR, rsel = lane / RS::kLPR;
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int c = 0; c < RS::kC; ++c) xr[c] = xv[sub + RS::kLPR * c];
+
+  const int row0 = blockIdx.x * kRowsPerBlock + wave * RS::kRPW * U + rsel;
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+  uint4 wr[U][RS::kC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int row = row0 + u * RS::kRPW;
+#pragma unroll
+    for (int c = 0; c < RS::kC; ++c) {
+      wr[u][c] = make_uint4(0, 0, 0, 0);
+      if (row < n) wr[u][c] = ld_stream(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + RS::kLPR * c);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int row = row0 + u * RS::kRPW;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[u][c], xr[c], acc);
+    acc = group_sum<RS::kLPR>(acc);
+    if (sub == 0 && row < n) {
+      float v = acc + (bias ? h2f(bias[row]) : 0.f);
+      if constexpr (ACT == FW_ACT_GELU) v = gelu_erf(round_h(v));
+      out[row] = f2h(v);
+    }
+  }
+}
+
+template <int K, int NW, int U, bool LN, int ACT>
+void launch_gemv(const _Float16* x, const LnArgs& ln, const _Float16* w, const _Float16* b, _Float16* out, int n,
+                 hipStream_t s) {
+  constexpr int kRows = NW * RowSplit<K>::kRPW * U;
+  const int grid = (n + kRows - 1) / kRows;
+  hipLaunchKernelGGL((gemv_kernel<K, NW, U, LN, ACT>), dim3(grid), dim3(NW * 64), 0, s, x, ln, w, b, out, n);
+}
+
+template <bool LN, int ACT>
+void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const _Float16* w, const _Float16* b, _Float16* out,
+                        int n, hipStream_t s) {
+  if (n >= 3840)
+    launch_gemv<kHidden, 4, 2, LN, ACT>(x, ln, w, b, out, n, s);
+  else
+    launch_gemv<kHidden, 2, 1, LN, ACT>(x, ln, w, b, out, n, s);
+}
+
+// ------------------------------------------------------------------------------------------
+// LM head + argmax (reference lm_head_argmax_kernel, whisper_kernels.cu:28-86): rows of the tied
+// embedding are streamed once; each row's fp32 dot is rounded to fp16, packed with its index and
+// max-reduced to one 64-bit atomicMax per block. The logits vector is never written. With LN the
+// final LayerNorm is recomputed per block; with FIN the last block to finish also runs the
+// finalize step (reference argmax_finalize_kernel, :88-100).
+// ------------------------------------------------------------------------------------------
+constexpr int kLmNW = 4, kLmU = 2;
+constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // 16 rows per block iteration
+
+struct FinArgs {
+  int64_t* tokens;
+  int64_t* state;
+  int64_t* cur;
+  int max_pos;
+  uint32_t* counter;
+};
+
+__device__ __forceinline__ void finalize_token(unsigned long long* best, const FinArgs& f) {
+  const unsigned long long b = __hip_atomic_exchange(best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
+  const int64_t n = f.state[1];
+  if (n < f.max_pos) f.tokens[n] = tok;
+  f.state[1] = n < f.max_pos ? n + 1 : n;
+  f.state[0] = f.state[0] + 1 < f.max_pos ? f.state[0] + 1 : f.max_pos - 1;
+  *f.cur = tok;
+}
+
+template <bool LN, bool FIN>
+__global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __restrict__ yin, LnArgs ln,
+                                                             const _Float16* __restrict__ w,
+                                                             const uint8_t* __restrict__ suppress, int vocab,
+                                                             int rows_per_block, unsigned long long* best,
+                                                             FinArgs fin) {
+  using RS = RowSplit<kHidden>;
+  __shared__ __align__(16) _Float16 y_lds[kHidden];
+  __shared__ float red[kLmNW];
+  __shared__ unsigned long long block_best[kLmNW * 2];
+  __shared__ int s_last;
+  if constexpr (LN) {
+    ln_prologue<kLmNW * 64>(ln.h, ln.x, nullptr, ln.gamma, ln.beta, ln.eps, y_lds, red);
+  } else {
+    for (int i = threadIdx.x; i < kHidden / 8; i += blockDim.x)
+      reinterpret_cast<uint4*>(y_lds)[i] = reinterpret_cast<const uint4*>(yin)[i];
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 31, rsel = lane >> 5;
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(y_lds)[sub + 32 * c];
+
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+  const int r_begin = blockIdx.x * rows_per_block;
+  const int r_end = min(vocab, r_begin + rows_per_block);
+  unsigned long long mine = 0;
+  for (int base = r_begin; base < r_end; base += kLmRowsIter) {
+    const int row0 = base + wave * 2 * kLmU + rsel;
+    uint4 wr[kLmU][RS::kC];
+#pragma unroll
+    for (int u = 0; u < kLmU; ++u) {
+      const int row = row0 + 2 * u;
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) {
+        wr[u][c] = make_uint4(0, 0, 0, 0);
+        if (row < r_end) wr[u][c] = ld_stream(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + 32 * c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kLmU; ++u) {
+      const int row = row0 + 2 * u;
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[u][c], xr[c], acc);
+      acc = group_sum<32>(acc);
+      if (sub == 0 && row < r_end && !suppress[row]) {
+        const unsigned long long s = pack_score(round_h(acc), row);
+        mine = s > mine ? s : mine;
+      }
+    }
+  }
+  if (sub == 0) block_best[wave * 2 + rsel] = mine;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long m = 0;
+#pragma unroll
+    for (int i = 0; i < kLmNW * 2; ++i) m = block_best[i] > m ? block_best[i] : m;
+    if (m) atomicMax(best, m);
+    if constexpr (FIN) {
+      __threadfence();
+      const uint32_t prev = atomicAdd(fin.counter, 1u);
+      __threadfence();
+      s_last = (prev == gridDim.x - 1);
+    }
+  }
+  if constexpr (FIN) {
+    __syncthreads();
+    if (s_last && threadIdx.x == 0) {
+      __threadfence();
+      finalize_token(best, fin);
+      __hip_atomic_store(fin.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+int lm_head_grid(int vocab, int* rows_per_block) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 256;
+  const int max_blocks = cus * 4;
+  const int iters = (vocab + max_blocks * kLmRowsIter - 1) / (max_blocks * kLmRowsIter);
+  *rows_per_block = iters * kLmRowsIter;
+  return (vocab + *rows_per_block - 1) / *rows_per_block;
+}
+
+__global__ void argmax_finalize_kernel(unsigned long long* best, FinArgs fin) { finalize_token(best, fin); }
+
+// ------------------------------------------------------------------------------------------
+// Split-K single-query attention (flash-decoding; reference decode_attention_split_kernel,
+// whisper_kernels.cu:102-189). Block (split, head) covers split_keys keys. A key row is 64 fp16 =
+// 8 lanes x 16 bytes, so one wave scores 8 keys per pass and a 256-thread block 32 keys. Scores,
+// max and exp-sum stay in fp32; the block writes its (m, l, acc[64]) partial. Self mode reads
+// len = state[0] + 1 from device memory and the block owning row pos writes k_new/v_new into the
+// cache while using the new row directly. FUSED: the last block of each head (per-head arrival
+// counter) merges the partials and writes the fp16 output, so no separate combine launch is needed.
+// ------------------------------------------------------------------------------------------
+struct AttnArgs {
+  const _Float16* q;
+  _Float16* k;
+  _Float16* v;
+  const _Float16* k_new;
+  const _Float16* v_new;
+  const int64_t* len_state;
+  int max_len;
+  int split_keys;
+  float scale;
+  float* part_m;
+  float* part_l;
+  float* part_acc;
+  uint32_t* counters;
+  _Float16* out;
+};
+
+__device__ __forceinline__ void combine_head(const AttnArgs& a, int head, int nsplit, int active, int d) {
+  const float* pm = a.part_m + head * nsplit;
+  const float* pl = a.part_l + head * nsplit;
+  const float* pa = a.part_acc + static_cast<size_t>(head) * nsplit * kHeadDim;
+  float m = -INFINITY;
+  for (int s = 0; s < active; ++s) m = fmaxf(m, pm[s]);
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < active; ++s) {
+    if (pl[s] > 0.f) {
+      const float wgt = __expf(pm[s] - m);
+      num = fmaf(pa[s * kHeadDim + d], wgt, num);
+      den = fmaf(pl[s], wgt, den);
+    }
+  }
+  a.out[head * kHeadDim + d] = f2h(num / den);
+}
+
+template <bool FUSED>
+__global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
+  __shared__ float scores[256];
+  __shared__ float red[4];
+  __shared__ float pacc[4][kHeadDim];
+  __shared__ int s_last;
+  const int split = blockIdx.x, head = blockIdx.y, nsplit = gridDim.x;
+  const int slot = head * nsplit + split;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int pos = -1;
+  if (a.len_state) {
+    const int64_t p = a.len_state[0];
+    pos = static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
+  }
+  const int len = a.len_state ? pos + 1 : a.max_len;
+  const int begin = split * a.split_keys;
+  const int n = min(a.split_keys, len - begin);
+  if (n <= 0) {
+    if (!FUSED && tid == 0) {
+      a.part_m[slot] = -INFINITY;
+      a.part_l[slot] = 0.f;
+    }
+    return;
+  }
+  const size_t hoff = static_cast<size_t>(head) * a.max_len * kHeadDim;
+  _Float16* kh = a.k + hoff;
+  _Float16* vh = a.v + hoff;
+  const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + head * kHeadDim) : nullptr;
+  const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + head * kHeadDim) : nullptr;
+  if (kn && pos >= begin && pos < begin + n && tid < 8) {
+    reinterpret_cast<uint4*>(kh + static_cast<size_t>(pos) * kHeadDim)[tid] = kn[tid];
+    reinterpret_cast<uint4*>(vh + static_cast<size_t>(pos) * kHeadDim)[tid] = vn[tid];
+  }
+  const int ks = lane >> 3, c = lane & 7;
+  const uint4 qc = reinterpret_cast<const uint4*>(a.q + head * kHeadDim)[c];
+
+  for (int i0 = 0; i0 < n; i0 += 32) {
+    const int i = i0 + wave * 8 + ks;
+    float s = 0.f;
+    if (i < n) {
+      const int j = begin + i;
+      const uint4* kp = (kn && j == pos) ? kn : reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim);
+      s = dot8(kp[c], qc, 0.f);
+    }
+    s = group_sum<8>(s);
+    if (c == 0 && i < n) scores[i] = s * a.scale;
+  }
+  __syncthreads();
+
+  const float sv = tid < n ? scores[tid] : -INFINITY;
+  float m = group_max<64>(sv);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float e = 0.f;
+  if (tid < n) {
+    e = __expf(sv - m);
+    scores[tid] = e;
+  }
+  const float l = block_sum<256>(e, red);
+
+  float acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+  for (int i0 = 0; i0 < n; i0 += 32) {
+    const int i = i0 + wave * 8 + ks;
+    if (i < n) {
+      const int j = begin + i;
+      const uint4* vp = (vn && j == pos) ? vn : reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim);
+      const uint4 vv = vp[c];
+      const float p = scores[i];
+      const h2v* v2 = reinterpret_cast<const h2v*>(&vv);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[2 * t] = fmaf(p, h2f(v2[t].x), acc[2 * t]);
+        acc[2 * t + 1] = fmaf(p, h2f(v2[t].y), acc[2 * t + 1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    acc[t] += __shfl_xor(acc[t], 8, kWave);
+    acc[t] += __shfl_xor(acc[t], 16, kWave);
+    acc[t] += __shfl_xor(acc[t], 32, kWave);
+  }
+  if (ks == 0) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) pacc[wave][c * 8 + t] = acc[t];
+  }
+  __syncthreads();
+  if (tid < kHeadDim)
+    a.part_acc[static_cast<size_t>(slot) * kHeadDim + tid] = pacc[0][tid] + pacc[1][tid] + pacc[2][tid] + pacc[3][tid];
+  if (tid == 0) {
+    a.part_m[slot] = m;
+    a.part_l[slot] = l;
+  }
+  if constexpr (FUSED) {
+    const int active = (len + a.split_keys - 1) / a.split_keys;
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = atomicAdd(a.counters + head, 1u);
+      __threadfence();
+      s_last = (prev == static_cast<uint32_t>(active - 1));
+    }
+    __syncthreads();
+    if (s_last) {
+      __threadfence();
+      if (tid < kHeadDim) combine_head(a, head, nsplit, active, tid);
+      if (tid == 0) __hip_atomic_store(a.counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Reference decode_attention_combine_kernel (whisper_kernels.cu:191-213): one block per head.
+__global__ void __launch_bounds__(64) attn_combine_kernel(AttnArgs a, int nsplit) {
+  combine_head(a, blockIdx.x, nsplit, nsplit, threadIdx.x);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace fw
+
+using namespace fw;
+
+#define FW_REQUIRE(cond, ...)                         \
+  do {                                                \
+    if (!(cond)) return fw_fail(FW_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+extern "C" int fw_lm_head_argmax(const void* y, const void* w, const uint8_t* suppress, int vocab, int hidden,
+                                 uint64_t* best, hipStream_t stream) {
+  FW_REQUIRE(y && w && suppress && best, "lm_head_argmax: null pointer");
+  FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
+  FW_REQUIRE(vocab > 0, "vocab must be positive");
+  FW_REQUIRE(aligned16(y) && aligned16(w), "lm_head_argmax: y and w must be 16-byte aligned");
+  int rpb = 0;
+  const int grid = lm_head_grid(vocab, &rpb);
+  FinArgs fin{};
+  hipLaunchKernelGGL((lm_head_kernel<false, false>), dim3(grid), dim3(kLmNW * 64), 0, stream,
+                     static_cast<const _Float16*>(y), LnArgs{}, static_cast<const _Float16*>(w), suppress, vocab, rpb,
+                     reinterpret_cast<unsigned long long*>(best), fin);
+  return fw_check_launch("lm_head_argmax");
+}
+
+extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void* gamma, const void* beta, float eps,
+                                       const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
+                                       int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, uint32_t* counter,
+                                       hipStream_t stream) {
+  FW_REQUIRE(h && gamma && beta && w && suppress && best && tokens && state && cur && counter,
+             "lm_head_argmax_fused: null pointer");
+  FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
+  FW_REQUIRE(vocab > 0 && max_pos > 0, "vocab and max_pos must be positive");
+  FW_REQUIRE(aligned16(w), "lm_head_argmax_fused: w must be 16-byte aligned");
+  int rpb = 0;
+  const int grid = lm_head_grid(vocab, &rpb);
+  LnArgs ln{static_cast<const _Float16*>(h), static_cast<const _Float16*>(x), nullptr,
+            static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta), eps, nullptr, nullptr,
+            nullptr, nullptr, 0, 0};
+  FinArgs fin{tokens, state, cur, max_pos, counter};
+  hipLaunchKernelGGL((lm_head_kernel<true, true>), dim3(grid), dim3(kLmNW * 64), 0, stream, nullptr, ln,
+                     static_cast<const _Float16*>(w), suppress, vocab, rpb, reinterpret_cast<unsigned long long*>(best),
+                     fin);
+  return fw_check_launch("lm_head_argmax_fused");
+}
+
+extern "C" int fw_argmax_finalize(uint64_t* best, int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,
+                                  hipStream_t stream) {
+  FW_REQUIRE(best && tokens && state && cur, "argmax_finalize: null pointer");
+  FW_REQUIRE(max_pos > 0, "max_pos must be positive");
+  FinArgs fin{tokens, state, cur, max_pos, nullptr};
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<unsigned long long*>(best),
+                     fin);
+  return fw_check_launch("argmax_finalize");
+}
+
+static int attention_common(const void* q, void* k, void* v, void* out, const int64_t* len_state, const void* k_new,
+                            const void* v_new, int heads, int max_len, int split_keys, float* part_m, float* part_l,
+                            float* part_acc, int64_t ws_slots, AttnArgs* a, int* nsplit) {
+  FW_REQUIRE(q && k && v && out && part_m && part_l && part_acc, "decode_attention: null pointer");
+  FW_REQUIRE(heads > 0 && max_len > 0, "decode_attention: heads and max_len must be positive");
+  FW_REQUIRE((k_new != nullptr) == (v_new != nullptr) && (k_new != nullptr) == (len_state != nullptr),
+             "len_state, k_new and v_new must be given together");
+  FW_REQUIRE(split_keys >= 32 && split_keys <= 256 && split_keys % 32 == 0,
+             "split_keys must be a multiple of 32 in [32, 256]");
+  FW_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && (!k_new || (aligned16(k_new) && aligned16(v_new))),
+             "decode_attention: q, k, v, k_new, v_new must be 16-byte aligned");
+  *nsplit = (max_len + split_keys - 1) / split_keys;
+  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * *nsplit, "workspace too small for %d splits", *nsplit);
+  *a = AttnArgs{static_cast<const _Float16*>(q), static_cast<_Float16*>(k), static_cast<_Float16*>(v),
+                static_cast<const _Float16*>(k_new), static_cast<const _Float16*>(v_new), len_state, max_len,
+                split_keys, 0.f, part_m, part_l, part_acc, nullptr, static_cast<_Float16*>(out)};
+  return FW_OK;
+}
+
+extern "C" int fw_decode_attention(const void* q, void* k, void* v, void* out, const int64_t* len_state,
+                                   const void* k_new, const void* v_new, int heads, int max_len, float* part_m,
+                                   float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream) {
+  AttnArgs a;
+  int nsplit = 0;
+  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, kSplitKeys, part_m, part_l,
+                            part_acc, ws_slots, &a, &nsplit);
+  if (rc != FW_OK) return rc;
+  a.scale = scale;
+  hipLaunchKernelGGL(attn_split_kernel<false>, dim3(nsplit, heads), dim3(256), 0, stream, a);
+  rc = fw_check_launch("decode_attention split");
+  if (rc != FW_OK) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(heads), dim3(kHeadDim), 0, stream, a, nsplit);
+  return fw_check_launch("decode_attention combine");
+}
+
+extern "C" int fw_decode_attention_fused(const void* q, void* k, void* v, void* out, const int64_t* len_state,
+                                         const void* k_new, const void* v_new, int heads, int max_len, int split_keys,
+                                         float* part_m, float* part_l, float* part_acc, uint32_t* counters,
+                                         int64_t ws_slots, float scale, hipStream_t stream) {
+  AttnArgs a;
+  int nsplit = 0;
+  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, split_keys, part_m, part_l,
+                            part_acc, ws_slots, &a, &nsplit);
+  if (rc != FW_OK) return rc;
+  FW_REQUIRE(counters, "decode_attention_fused: null counters");
+  a.scale = scale;
+  a.counters = counters;
+  hipLaunchKernelGGL(attn_split_kernel<true>, dim3(nsplit, heads), dim3(256), 0, stream, a);
+  return fw_check_launch("decode_attention_fused");
+}
+
+extern "C" int fw_add_layernorm(void* h, const void* x, const void* gamma, const void* beta, void* y, int n, float eps,
+                                hipStream_t stream) {
+  FW_REQUIRE(h && gamma && beta && y, "add_layernorm: null pointer");
+  FW_REQUIRE(n == kHidden, "hidden size must be %d", kHidden);
+  FW_REQUIRE(aligned16(h) && aligned16(gamma) && aligned16(beta) && aligned16(y) && (!x || aligned16(x)),
+             "add_layernorm: tensors must be 16-byte aligned");
+  hipLaunchKernelGGL(add_layernorm_kernel, dim3(1), dim3(256), 0, stream, static_cast<_Float16*>(h),
+                     static_cast<const _Float16*>(x), static_cast<const _Float16*>(gamma),
+                     static_cast<const _Float16*>(beta), static_cast<_Float16*>(y), eps);
+  return fw_check_launch("add_layernorm");
+}
+
+extern "C" int fw_embed(const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                        int max_pos, void* h, int hidden, hipStream_t stream) {
+  FW_REQUIRE(cur && state && embed && pos_embed && h, "embed: null pointer");
+  FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
+  FW_REQUIRE(vocab > 0 && max_pos > 0, "vocab and max_pos must be positive");
+  hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, stream, cur, state, static_cast<const _Float16*>(embed),
+                     static_cast<const _Float16*>(pos_embed), vocab, max_pos, static_cast<_Float16*>(h));
+  return fw_check_launch("embed");
+}
+
+extern "C" int fw_gemv(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
+                       hipStream_t stream) {
+  FW_REQUIRE(x && w && out, "gemv: null pointer");
+  FW_REQUIRE(n_out > 0, "gemv: n_out must be positive");
+  FW_REQUIRE(k_in == kHidden || k_in == 4 * kHidden, "gemv: k_in must be 1280 or 5120");
+  FW_REQUIRE(act == FW_ACT_NONE || act == FW_ACT_GELU, "gemv: unknown activation %d", act);
+  FW_REQUIRE(aligned16(x) && aligned16(w), "gemv: x and w must be 16-byte aligned");
+  const auto* xp = static_cast<const _Float16*>(x);
+  const auto* wp = static_cast<const _Float16*>(w);
+  const auto* bp = static_cast<const _Float16*>(bias);
+  auto* op = static_cast<_Float16*>(out);
+  const LnArgs ln{};
+  if (k_in == kHidden) {
+    if (act == FW_ACT_GELU)
+      dispatch_gemv_1280<false, FW_ACT_GELU>(xp, ln, wp, bp, op, n_out, stream);
+    else
+      dispatch_gemv_1280<false, FW_ACT_NONE>(xp, ln, wp, bp, op, n_out, stream);
+  } else {
+    if (act == FW_ACT_GELU)
+      launch_gemv<4 * kHidden, 4, 1, false, FW_ACT_GELU>(xp, ln, wp, bp, op, n_out, stream);
+    else
+      launch_gemv<4 * kHidden, 4, 1, false, FW_ACT_NONE>(xp, ln, wp, bp, op, n_out, stream);
+  }
+  return fw_check_launch("gemv");
+}
+
+extern "C" int fw_ln_gemv(const void* h, const void* x, void* h_out, const void* gamma, const void* beta, float eps,
+                          const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed,
+                          int vocab, int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in,
+                          int act, hipStream_t stream) {
+  FW_REQUIRE(gamma && beta && w && out, "ln_gemv: null pointer");
+  FW_REQUIRE(k_in == kHidden, "ln_gemv: k_in must be %d", kHidden);
+  FW_REQUIRE(n_out > 0, "ln_gemv: n_out must be positive");
+  FW_REQUIRE(act == FW_ACT_NONE || act == FW_ACT_GELU, "ln_gemv: unknown activation %d", act);
+  FW_REQUIRE(aligned16(w), "ln_gemv: w must be 16-byte aligned");
+  if (cur) {
+    FW_REQUIRE(state && embed && pos_embed && vocab > 0 && max_pos > 0, "ln_gemv: embedding mode needs state, tables");
+  } else {
+    FW_REQUIRE(h != nullptr, "ln_gemv: null h");
+    FW_REQUIRE(h_out != h, "ln_gemv: h_out must not alias h");
+  }
+  LnArgs ln{static_cast<const _Float16*>(h), static_cast<const _Float16*>(x), static_cast<_Float16*>(h_out),
+            static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta), eps, cur, state,
+            static_cast<const _Float16*>(embed), static_cast<const _Float16*>(pos_embed), vocab, max_pos};
+  const auto* wp = static_cast<const _Float16*>(w);
+  const auto* bp = static_cast<const _Float16*>(bias);
+  auto* op = static_cast<_Float16*>(out);
+  if (act == FW_ACT_GELU)
+    dispatch_gemv_1280<true, FW_ACT_GELU>(nullptr, ln, wp, bp, op, n_out, stream);
+  else
+    dispatch_gemv_1280<true, FW_ACT_NONE>(nullptr, ln, wp, bp, op, n_out, stream);
+  return fw_check_launch("ln_gemv");
+}

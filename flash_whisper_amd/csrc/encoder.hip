@@ -1,0 +1,469 @@
+// Whisper encoder kernels for gfx950: an MFMA GEMM with fused epilogues (also used as an
+// implicit-GEMM conv1d and for the decoder cross K/V projection), a row LayerNorm and a
+// flash-style encoder self-attention. Semantics follow HF WhisperEncoder.forward in fp16
+// (transformers models/whisper/modeling_whisper.py:592-648, layer :379-414, attention :284-358):
+// every op output is rounded to fp16, accumulation is fp32.
+#include "fw_common.h"
+
+namespace fw {
+namespace {
+
+// ------------------------------------------------------------------------------------------
+// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 32, 4 waves in a 2 x 2
+// arrangement, each wave (BM/2) x 64 built from v_mfma_f32_32x32x16_f16 tiles. A and W tiles are
+// staged through double-buffered LDS (rows padded by 8 halves); the next K slice is fetched into
+// registers while the current one feeds the MFMAs.
+// MFMA 32x32x16 f16 operand layout (lane l, g = l / 32):
+//   A: lane holds A[l % 32][8g .. 8g + 7]      B: lane holds B[8g .. 8g + 7][l % 32]
+//   C: acc[r] = C[8 (r / 4) + 4 g + (r % 4)][l % 32], r = 0 .. 15
+// ------------------------------------------------------------------------------------------
+constexpr int kBN = 128, kBK = 32, kLdsStride = kBK + 8;
+constexpr int kEpiCrossKV = 100;  // internal epilogue: scatter into [layers, 2, heads, t, 64]
+
+struct GemmArgs {
+  const _Float16* a;
+  int lda;
+  const _Float16* w;
+  int ldw;
+  const _Float16* bias;
+  _Float16* out;
+  int ldo;
+  const _Float16* res;
+  int ldr;
+  int m, n, k;
+  int q_cols;
+  // implicit conv1d (k = 3, pad 1): a is x[t_in, c_in]; row m, column kk = tap * c_in + c reads
+  // x[m * stride + tap - 1, c], zero outside [0, t_in).
+  int conv_stride;  // 0: plain GEMM
+  int t_in, c_in;
+  // cross K/V scatter
+  int heads, t_len;
+};
+
+__device__ __forceinline__ float epilogue_value(int epi, float acc, float b, const GemmArgs& g, int row, int col) {
+  float v = round_h(acc + b);
+  switch (epi) {
+    case FW_EPI_BIAS_GELU:
+      v = gelu_erf(v);
+      break;
+    case FW_EPI_BIAS_RESID:
+      v = h2f(g.res[static_cast<size_t>(row) * g.ldr + col]) + v;
+      break;
+    case FW_EPI_BIAS_RESID_CLAMP: {
+      v = round_h(h2f(g.res[static_cast<size_t>(row) * g.ldr + col]) + v);
+      const float c = 65504.0f - 1000.0f;
+      v = fminf(fmaxf(v, -c), c);
+      break;
+    }
+    case FW_EPI_BIAS_GELU_POS:
+      v = round_h(gelu_erf(v)) + h2f(g.res[static_cast<size_t>(row) * g.ldr + col]);
+      break;
+    case FW_EPI_SCALE_Q:
+      if (col < g.q_cols) v = v * 0.125f;
+      break;
+    default:
+      break;
+  }
+  return v;
+}
+
+template <int BM, int EPI>
+__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
+  constexpr int kWM = BM / 2;          // wave tile rows
+  constexpr int kTM = kWM / 32;        // MFMA tiles per wave along M
+  constexpr int kTN = 2;               // MFMA tiles per wave along N (64 columns)
+  constexpr int kAChunks = BM * kBK / 8 / 256;  // 16-byte A chunks per thread per stage
+  constexpr int kBChunks = kBN * kBK / 8 / 256;
+  __shared__ __align__(16) _Float16 As[2][BM][kLdsStride];
+  __shared__ __align__(16) _Float16 Bs[2][kBN][kLdsStride];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * kWM, wn = (wave & 1) * 64;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
+  const int lr = lane & 31, lg = lane >> 5;
+
+  f16v acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  uint4 ra[kAChunks], rb[kBChunks];
+  auto load_global = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, kc = (c & 3) * 8;
+      const int gm = m0 + row;
+      ra[i] = make_uint4(0, 0, 0, 0);
+      if (gm < g.m) {
+        if (g.conv_stride) {
+          const int kk = k0 + kc;
+          const int tap = kk / g.c_in, ch = kk - tap * g.c_in;
+          const int src = gm * g.conv_stride + tap - 1;
+          if (src >= 0 && src < g.t_in)
+            ra[i] = *reinterpret_cast<const uint4*>(g.a + static_cast<size_t>(src) * g.c_in + ch);
+        } else {
+          ra[i] = *reinterpret_cast<const uint4*>(g.a + static_cast<size_t>(gm) * g.lda + k0 + kc);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kBChunks; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, kc = (c & 3) * 8;
+      rb[i] = *reinterpret_cast<const uint4*>(g.w + static_cast<size_t>(n0 + row) * g.ldw + k0 + kc);
+    }
+  };
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<uint4*>(&As[buf][c >> 2][(c & 3) * 8]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kBChunks; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<uint4*>(&Bs[buf][c >> 2][(c & 3) * 8]) = rb[i];
+    }
+  };
+
+  const int kt_n = g.k / kBK;
+  load_global(0);
+  store_lds(0);
+  __syncthreads();
+  for (int kt = 0; kt < kt_n; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < kt_n) load_global((kt + 1) * kBK);
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      h8v av[kTM], bv[kTN];
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+        av[i] = *reinterpret_cast<const h8v*>(&As[buf][wm + 32 * i + lr][16 * s + 8 * lg]);
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+        bv[j] = *reinterpret_cast<const h8v*>(&Bs[buf][wn + 32 * j + lr][16 * s + 8 * lg]);
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < kt_n) store_lds(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int col = n0 + wn + 32 * j + lr;
+    const float b = g.bias ? h2f(g.bias[col]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (row < g.m) {
+          if constexpr (EPI == kEpiCrossKV) {
+            // col = ((layer * 2 + kv) * heads + head) * 64 + d
+            const int d = col & 63, lhk = col >> 6;
+            const size_t o = (static_cast<size_t>(lhk) * g.t_len + row) * 64 + d;
+            g.out[o] = f2h(acc[i][j][r] + b);
+          } else {
+            g.out[static_cast<size_t>(row) * g.ldo + col] = f2h(epilogue_value(EPI, acc[i][j][r], b, g, row, col));
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM>
+int launch_gemm_bm(const GemmArgs& g, int epi, hipStream_t s) {
+  const dim3 grid(g.n / kBN, (g.m + BM - 1) / BM);
+  switch (epi) {
+#define FW_GEMM_CASE(E) \
+  case E:               \
+    hipLaunchKernelGGL((gemm_kernel<BM, E>), grid, dim3(256), 0, s, g); break;
+    FW_GEMM_CASE(FW_EPI_BIAS)
+    FW_GEMM_CASE(FW_EPI_BIAS_GELU)
+    FW_GEMM_CASE(FW_EPI_BIAS_RESID)
+    FW_GEMM_CASE(FW_EPI_BIAS_RESID_CLAMP)
+    FW_GEMM_CASE(FW_EPI_BIAS_GELU_POS)
+    FW_GEMM_CASE(FW_EPI_SCALE_Q)
+    FW_GEMM_CASE(kEpiCrossKV)
+#undef FW_GEMM_CASE
+    default:
+      return fw_fail(FW_EINVAL, "gemm: unknown epilogue %d", epi);
+  }
+  return fw_check_launch("gemm");
+}
+
+// Fewer than ~2 blocks per CU at BM = 128 leaves the chip idle: use 64-row tiles then.
+int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
+  const int tiles128 = (g.n / kBN) * ((g.m + 127) / 128);
+  if (tiles128 < 400) return launch_gemm_bm<64>(g, epi, s);
+  return launch_gemm_bm<128>(g, epi, s);
+}
+
+// ------------------------------------------------------------------------------------------
+// Row LayerNorm over 1280 columns: 32 lanes per row (5 x 16-byte chunks each), 8 rows per block.
+// ------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __restrict__ x,
+                                                             const _Float16* __restrict__ gamma,
+                                                             const _Float16* __restrict__ beta,
+                                                             _Float16* __restrict__ y, int rows, float eps) {
+  constexpr int kC = kHidden / 8 / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 31;
+  const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
+  const bool valid = row < rows;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(valid ? row : 0) * kHidden);
+  float v[kC * 8];
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    const uint4 u = xr[sub + 32 * c];
+    const _Float16* hp = reinterpret_cast<const _Float16*>(&u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[c * 8 + e] = h2f(hp[e]);
+      sum += v[c * 8 + e];
+    }
+  }
+  const float mean = group_sum<32>(sum) * (1.0f / kHidden);
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < kC * 8; ++i) {
+    const float d = v[i] - mean;
+    sq += d * d;
+  }
+  const float inv = rsqrtf(group_sum<32>(sq) * (1.0f / kHidden) + eps);
+  if (!valid) return;
+  const uint4* g4 = reinterpret_cast<const uint4*>(gamma);
+  const uint4* b4 = reinterpret_cast<const uint4*>(beta);
+  uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * kHidden);
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    const uint4 gu = g4[sub + 32 * c], bu = b4[sub + 32 * c];
+    const _Float16* gp = reinterpret_cast<const _Float16*>(&gu);
+    const _Float16* bp = reinterpret_cast<const _Float16*>(&bu);
+    uint4 o;
+    _Float16* op = reinterpret_cast<_Float16*>(&o);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) op[e] = f2h((v[c * 8 + e] - mean) * inv * h2f(gp[e]) + h2f(bp[e]));
+    yr[sub + 32 * c] = o;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Encoder self-attention, flash style. Block = (head, 64 queries), 2 waves of 32 queries each.
+// Per 64-key tile a wave computes S^T = K Q^T (keys x queries) with MFMA so that every lane holds
+// scores of a single query column: the online-softmax max/sum need one cross-lane step (lane ^ 32).
+// P^T is fed straight from the S^T accumulator layout as the B operand of O^T = V^T P^T; the
+// A operand V^T comes from an LDS copy of the V tile stored transposed, read with the same key
+// permutation, so no register shuffles are needed between the two products.
+// ------------------------------------------------------------------------------------------
+constexpr int kAttnQ = 64, kAttnKV = 64, kVtStride = kAttnKV + 8;
+
+__global__ void __launch_bounds__(128) encoder_attention_kernel(const _Float16* __restrict__ qkv,
+                                                                _Float16* __restrict__ out, int seq, int heads) {
+  __shared__ __align__(16) _Float16 vt[kHeadDim][kVtStride];  // V tile transposed: [d][key]
+  const int head = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lg = lane >> 5;
+  const int ld = 3 * heads * kHeadDim;
+  const int q_row = blockIdx.x * kAttnQ + wave * 32 + lr;  // this lane's query column
+  const _Float16* qbase = qkv + head * kHeadDim;
+  const _Float16* kbase = qkv + (heads + head) * kHeadDim;
+  const _Float16* vbase = qkv + (2 * heads + head) * kHeadDim;
+
+  // Q^T as B operand: lane holds Q[q_row][16 s + 8 lg .. + 7] for s = 0..3.
+  h8v qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (q_row < seq) {
+      qf[s] = *reinterpret_cast<const h8v*>(qbase + static_cast<size_t>(q_row) * ld + 16 * s + 8 * lg);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = static_cast<_Float16>(0.f);
+    }
+  }
+  f16v o[2];  // O^T blocks: d in [0, 32) and [32, 64)
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  constexpr float kLog2e = 1.4426950408889634f;
+
+  for (int kv0 = 0; kv0 < seq; kv0 += kAttnKV) {
+    __syncthreads();  // previous tile's vt reads are done
+    // Stage V tile transposed: 64 keys x 64 d; thread loads 16-byte chunks of V rows.
+    for (int c = tid; c < kAttnKV * 8; c += 128) {
+      const int key = c >> 3, d0 = (c & 7) * 8;
+      uint4 u = make_uint4(0, 0, 0, 0);
+      if (kv0 + key < seq) u = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(kv0 + key) * ld + d0);
+      const _Float16* hp = reinterpret_cast<const _Float16*>(&u);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[d0 + e][key] = hp[e];
+    }
+    // S^T = K Q^T for two 32-key blocks.
+    f16v s[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+      const int key = kv0 + 32 * b + lr;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        h8v kf;
+        if (key < seq) {
+          kf = *reinterpret_cast<const h8v*>(kbase + static_cast<size_t>(key) * ld + 16 * st + 8 * lg);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) kf[e] = static_cast<_Float16>(0.f);
+        }
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[b], 0, 0, 0);
+      }
+    }
+    // Mask keys beyond seq; running max over this lane's 32 scores and the partner lane.
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (key >= seq) s[b][r] = -INFINITY;
+        tmax = fmaxf(tmax, s[b][r]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    const float m_new = fmaxf(m_run, tmax);
+    const float corr = exp2f((m_run - m_new) * kLog2e);
+    float psum = 0.f;
+    h8v pf[2][2];  // P^T as B operand, [32-key block][k-step of 16 keys]
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = exp2f((s[b][r] - m_new) * kLog2e);
+        const _Float16 ph = f2h(p);
+        psum += h2f(ph);
+        pf[b][r >> 3][r & 7] = ph;
+      }
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * corr + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+    __syncthreads();  // vt staged
+    // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]. For k-step (b, h) the lane half lg holds keys
+    // 32 b + 16 h + {4 lg .. 4 lg + 3} and 32 b + 16 h + 8 + {4 lg .. 4 lg + 3} (accumulator order).
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int hs = 0; hs < 2; ++hs) {
+        const int kb = 32 * b + 16 * hs + 4 * lg;
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const int d = 32 * db + lr;
+          h8v vf;
+          const uint2 lo = *reinterpret_cast<const uint2*>(&vt[d][kb]);
+          const uint2 hi = *reinterpret_cast<const uint2*>(&vt[d][kb + 8]);
+          const _Float16* lp = reinterpret_cast<const _Float16*>(&lo);
+          const _Float16* hp = reinterpret_cast<const _Float16*>(&hi);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vf[e] = lp[e];
+            vf[4 + e] = hp[e];
+          }
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[b][hs], o[db], 0, 0, 0);
+        }
+      }
+  }
+  if (q_row >= seq) return;
+  const float inv = 1.0f / l_run;
+  _Float16* orow = out + static_cast<size_t>(q_row) * heads * kHeadDim + head * kHeadDim;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) orow[32 * db + 8 * (r >> 2) + 4 * lg + (r & 3)] = f2h(o[db][r] * inv);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace fw
+
+using namespace fw;
+
+extern "C" int fw_gemm(const void* a, int lda, const void* w, int ldw, const void* bias, void* out, int ldo,
+                       const void* res, int ldr, int m, int n, int k, int epilogue, int q_cols, hipStream_t stream) {
+  if (!a || !w || !out) return fw_fail(FW_EINVAL, "gemm: null pointer");
+  if (m <= 0 || n <= 0 || k <= 0 || n % kBN || k % kBK)
+    return fw_fail(FW_EINVAL, "gemm: need m > 0, n %% %d == 0, k %% %d == 0 (m=%d n=%d k=%d)", kBN, kBK, m, n, k);
+  if (lda < k || ldw < k || ldo < n || lda % 8 || ldw % 8 || ldo % 8 || !aligned16(a) || !aligned16(w))
+    return fw_fail(FW_EINVAL, "gemm: leading dimensions must cover the matrix and be multiples of 8");
+  const bool needs_res = epilogue == FW_EPI_BIAS_RESID || epilogue == FW_EPI_BIAS_RESID_CLAMP ||
+                         epilogue == FW_EPI_BIAS_GELU_POS;
+  if (needs_res && (!res || ldr < n)) return fw_fail(FW_EINVAL, "gemm: epilogue %d needs res with ldr >= n", epilogue);
+  if (epilogue < FW_EPI_BIAS || epilogue > FW_EPI_SCALE_Q) return fw_fail(FW_EINVAL, "gemm: unknown epilogue %d", epilogue);
+  GemmArgs g{static_cast<const _Float16*>(a), lda, static_cast<const _Float16*>(w), ldw,
+             static_cast<const _Float16*>(bias), static_cast<_Float16*>(out), ldo,
+             static_cast<const _Float16*>(res), ldr, m, n, k, q_cols, 0, 0, 0, 0, 0};
+  return launch_gemm(g, epilogue, stream);
+}
+
+extern "C" int fw_conv1d(const void* x, int t_in, int c_in, int stride, const void* wp, const void* bias, void* out,
+                         int c_out, const void* res, int epilogue, hipStream_t stream) {
+  if (!x || !wp || !out) return fw_fail(FW_EINVAL, "conv1d: null pointer");
+  if (t_in <= 0 || c_in <= 0 || c_in % 64 || c_out % kBN || (stride != 1 && stride != 2))
+    return fw_fail(FW_EINVAL, "conv1d: need c_in %% 64 == 0, c_out %% %d == 0, stride 1 or 2", kBN);
+  if (epilogue != FW_EPI_BIAS_GELU && epilogue != FW_EPI_BIAS_GELU_POS && epilogue != FW_EPI_BIAS)
+    return fw_fail(FW_EINVAL, "conv1d: unsupported epilogue %d", epilogue);
+  if (epilogue == FW_EPI_BIAS_GELU_POS && !res) return fw_fail(FW_EINVAL, "conv1d: positions required");
+  if (!aligned16(x) || !aligned16(wp)) return fw_fail(FW_EINVAL, "conv1d: x and wp must be 16-byte aligned");
+  const int t_out = (t_in - 1) / stride + 1;
+  GemmArgs g{static_cast<const _Float16*>(x), c_in, static_cast<const _Float16*>(wp), 3 * c_in,
+             static_cast<const _Float16*>(bias), static_cast<_Float16*>(out), c_out,
+             static_cast<const _Float16*>(res), c_out, t_out, c_out, 3 * c_in, 0, stride, t_in, c_in, 0, 0};
+  return launch_gemm(g, epilogue, stream);
+}
+
+extern "C" int fw_layernorm_rows(const void* x, const void* gamma, const void* beta, void* y, int rows, int n,
+                                 float eps, hipStream_t stream) {
+  if (!x || !gamma || !beta || !y) return fw_fail(FW_EINVAL, "layernorm_rows: null pointer");
+  if (n != kHidden || rows <= 0) return fw_fail(FW_EINVAL, "layernorm_rows: n must be %d", kHidden);
+  if (!aligned16(x) || !aligned16(y) || !aligned16(gamma) || !aligned16(beta))
+    return fw_fail(FW_EINVAL, "layernorm_rows: tensors must be 16-byte aligned");
+  hipLaunchKernelGGL(layernorm_rows_kernel, dim3((rows + 7) / 8), dim3(256), 0, stream,
+                     static_cast<const _Float16*>(x), static_cast<const _Float16*>(gamma),
+                     static_cast<const _Float16*>(beta), static_cast<_Float16*>(y), rows, eps);
+  return fw_check_launch("layernorm_rows");
+}
+
+extern "C" int fw_encoder_attention(const void* qkv, void* out, int seq, int heads, hipStream_t stream) {
+  if (!qkv || !out) return fw_fail(FW_EINVAL, "encoder_attention: null pointer");
+  if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_attention: seq and heads must be positive");
+  if (!aligned16(qkv)) return fw_fail(FW_EINVAL, "encoder_attention: qkv must be 16-byte aligned");
+  hipLaunchKernelGGL(encoder_attention_kernel, dim3((seq + kAttnQ - 1) / kAttnQ, heads), dim3(128), 0, stream,
+                     static_cast<const _Float16*>(qkv), static_cast<_Float16*>(out), seq, heads);
+  return fw_check_launch("encoder_attention");
+}
+
+extern "C" int fw_cross_kv(const void* enc, int t, const void* w, const void* bias, void* cross_kv, int layers,
+                           int heads, hipStream_t stream) {
+  if (!enc || !w || !cross_kv) return fw_fail(FW_EINVAL, "cross_kv: null pointer");
+  if (t <= 0 || layers <= 0 || heads * kHeadDim != kHidden)
+    return fw_fail(FW_EINVAL, "cross_kv: need t > 0, layers > 0, heads * 64 == %d", kHidden);
+  if (!aligned16(enc) || !aligned16(w)) return fw_fail(FW_EINVAL, "cross_kv: enc and w must be 16-byte aligned");
+  const int n = layers * 2 * kHidden;
+  GemmArgs g{static_cast<const _Float16*>(enc), kHidden, static_cast<const _Float16*>(w), kHidden,
+             static_cast<const _Float16*>(bias), static_cast<_Float16*>(cross_kv), 0, nullptr, 0, t, n, kHidden, 0,
+             0, 0, 0, heads, t};
+  return launch_gemm(g, kEpiCrossKV, stream);
+}

@@ -1,0 +1,286 @@
+"""Loads the HIP kernels and exposes them as torch-tensor ops: the drop-in for custom/ext.py.
+
+``load_ext()`` keeps the reference's name and call shape (custom/ext.py:13-18): no required
+arguments, returns an object whose ops take caller-allocated torch tensors, launch on the current
+stream, allocate nothing and raise ``RuntimeError`` when an argument is invalid — the contract of the
+reference's ``TORCH_CHECK``s (custom/kernels/whisper_kernels.cu:269-356). The reference JIT-compiles
+a pybind module with nvcc; here the kernels live in an ahead-of-time built C-ABI library
+(include/flash_whisper.h) and this module is a thin ctypes layer over it. Nothing here falls back to
+PyTorch math: without the library, ``load_ext()`` raises.
+
+``python -m custom.ext`` (or ``python -m flash_whisper_amd.ext``) builds the library and prints the
+compiler's per-kernel register, LDS and spill report, like the reference's ``main`` (custom/ext.py:21-50).
+"""
+
+import argparse
+import sys
+
+import torch
+
+from . import _lib
+from ._lib import ACT_GELU, ACT_NONE, EPI_BIAS  # noqa: F401  (re-exported constants)
+from .config import SPLIT_KEYS
+
+HIDDEN, HEAD_DIM = 1280, 64
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _require(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def check_half(t, name):
+    """Reference check_half (whisper_kernels.cu:272-274)."""
+    _require(isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() and t.dtype == torch.float16,
+             f'{name} must be contiguous CUDA fp16')
+
+
+def _check(t, name, dtype, what):
+    _require(isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() and t.dtype == dtype,
+             f'{name} must be contiguous CUDA {what}')
+
+
+class WhisperExt:
+    """The op set of the reference extension plus the fused/encoder/front-end ops of this build."""
+
+    def __init__(self):
+        self.lib = _lib.lib()
+
+    def _call(self, name, *args):
+        _lib.check(getattr(self.lib, name)(*args), name)
+
+    # ---- reference ops -------------------------------------------------------------------
+    def lm_head_argmax(self, h, w, suppress, best):
+        """whisper_kernels.cu:278-289."""
+        check_half(h, 'h')
+        check_half(w, 'w')
+        _require(h.numel() == HIDDEN and w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
+        _require(suppress.dtype == torch.bool and suppress.is_cuda and suppress.is_contiguous()
+                 and suppress.numel() == w.size(0), 'suppress must be bool [vocab]')
+        _require(best.dtype == torch.int64 and best.is_cuda and best.numel() == 1, 'best must be int64 [1]')
+        self._call('fw_lm_head_argmax', h.data_ptr(), w.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN,
+                   best.data_ptr(), _stream())
+
+    def argmax_finalize(self, best, tokens, state, cur, max_pos):
+        """whisper_kernels.cu:291-298."""
+        for t, n in ((tokens, 'tokens'), (state, 'state'), (cur, 'cur')):
+            _require(t.dtype == torch.int64, 'tokens, state and cur must be int64')
+            _require(t.is_cuda and t.is_contiguous(), f'{n} must be a contiguous CUDA tensor')
+        _require(best.dtype == torch.int64 and best.is_cuda and best.numel() == 1, 'best must be int64 [1]')
+        self._call('fw_argmax_finalize', best.data_ptr(), tokens.data_ptr(), state.data_ptr(), cur.data_ptr(),
+                   int(max_pos), _stream())
+
+    def _attn_checks(self, q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc, split_keys):
+        for t, n in ((q, 'q'), (k, 'k'), (v, 'v'), (out, 'out')):
+            check_half(t, n)
+        _require(k.dim() == 3 and k.size(2) == HEAD_DIM and k.shape == v.shape, 'k, v must be [heads, max_len, 64]')
+        heads, max_len = k.size(0), k.size(1)
+        splits = -(-max_len // split_keys)
+        _require(q.numel() == heads * HEAD_DIM and out.numel() == heads * HEAD_DIM, 'q, out must be [heads * 64]')
+        _require((k_new is None) == (v_new is None) == (len_state is None),
+                 'len_state, k_new and v_new must be given together')
+        if k_new is not None:
+            check_half(k_new, 'k_new')
+            check_half(v_new, 'v_new')
+            _require(k_new.numel() == heads * HEAD_DIM and v_new.numel() == heads * HEAD_DIM,
+                     'k_new, v_new must be [heads, 64]')
+            _require(len_state.dtype == torch.int64 and len_state.is_cuda, 'len_state must be CUDA int64')
+        for t in (part_m, part_l, part_acc):
+            _require(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32,
+                     'workspace must be contiguous CUDA fp32')
+        slots = min(part_m.numel(), part_l.numel(), part_acc.numel() // HEAD_DIM)
+        _require(slots >= heads * splits, f'workspace too small for {splits} splits')
+        return heads, max_len, slots
+
+    def decode_attention(self, q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc, scale):
+        """whisper_kernels.cu:300-339: split kernel (64 keys per split) + combine kernel."""
+        heads, max_len, slots = self._attn_checks(q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc,
+                                                  SPLIT_KEYS)
+        self._call('fw_decode_attention', q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _ptr(len_state),
+                   _ptr(k_new), _ptr(v_new), heads, max_len, part_m.data_ptr(), part_l.data_ptr(),
+                   part_acc.data_ptr(), slots, float(scale), _stream())
+
+    def add_layernorm(self, h, x, gamma, beta, y, eps):
+        """whisper_kernels.cu:341-356."""
+        for t, n in ((h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (y, 'y')):
+            check_half(t, n)
+        _require(h.numel() == HIDDEN, f'hidden size must be {HIDDEN}')
+        if x is not None:
+            check_half(x, 'x')
+        self._call('fw_add_layernorm', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(),
+                   HIDDEN, float(eps), _stream())
+
+    # ---- fused decoder ops ---------------------------------------------------------------
+    def embed(self, cur, state, embed, pos_embed, h):
+        check_half(embed, 'embed')
+        check_half(pos_embed, 'pos_embed')
+        check_half(h, 'h')
+        self._call('fw_embed', cur.data_ptr(), state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(),
+                   embed.size(0), pos_embed.size(0), h.data_ptr(), HIDDEN, _stream())
+
+    def gemv(self, x, w, bias, out, act=ACT_NONE):
+        check_half(x, 'x')
+        check_half(w, 'w')
+        check_half(out, 'out')
+        _require(w.dim() == 2 and x.numel() == w.size(1) and out.numel() == w.size(0), 'gemv shape mismatch')
+        if bias is not None:
+            check_half(bias, 'bias')
+            _require(bias.numel() == w.size(0), 'bias must be [n_out]')
+        self._call('fw_gemv', x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), w.size(1), act,
+                   _stream())
+
+    def ln_gemv(self, h, x, h_out, gamma, beta, eps, w, bias, out, act=ACT_NONE, embed=None):
+        """r = fp16(h + x) -> h_out; y = LN(r); out = act(w y + b). embed = (cur, state, table, pos_table)."""
+        for t, n in ((gamma, 'gamma'), (beta, 'beta'), (w, 'w'), (out, 'out')):
+            check_half(t, n)
+        _require(w.dim() == 2 and w.size(1) == HIDDEN and out.numel() == w.size(0), 'ln_gemv shape mismatch')
+        cur = state = table = pos_table = None
+        if embed is not None:
+            cur, state, table, pos_table = embed
+            check_half(table, 'embed')
+            check_half(pos_table, 'pos_embed')
+        else:
+            check_half(h, 'h')
+        for t, n in ((x, 'x'), (h_out, 'h_out'), (bias, 'bias')):
+            if t is not None:
+                check_half(t, n)
+        self._call('fw_ln_gemv', _ptr(h), _ptr(x), _ptr(h_out), gamma.data_ptr(), beta.data_ptr(), float(eps),
+                   _ptr(cur), _ptr(state), _ptr(table), _ptr(pos_table),
+                   0 if table is None else table.size(0), 0 if pos_table is None else pos_table.size(0),
+                   w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), HIDDEN, act, _stream())
+
+    def decode_attention_fused(self, q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc, counters,
+                               scale, split_keys=SPLIT_KEYS):
+        heads, max_len, slots = self._attn_checks(q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc,
+                                                  split_keys)
+        _require(counters.dtype == torch.int32 and counters.is_cuda and counters.numel() >= heads,
+                 'counters must be CUDA int32 [heads]')
+        self._call('fw_decode_attention_fused', q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                   _ptr(len_state), _ptr(k_new), _ptr(v_new), heads, max_len, int(split_keys), part_m.data_ptr(),
+                   part_l.data_ptr(), part_acc.data_ptr(), counters.data_ptr(), slots, float(scale), _stream())
+
+    def lm_head_argmax_fused(self, h, x, gamma, beta, eps, w, suppress, best, tokens, state, cur, max_pos, counter):
+        for t, n in ((h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (w, 'w')):
+            check_half(t, n)
+        if x is not None:
+            check_half(x, 'x')
+        _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
+        _require(suppress.dtype == torch.bool and suppress.numel() == w.size(0), 'suppress must be bool [vocab]')
+        _require(counter.dtype == torch.int32 and counter.is_cuda, 'counter must be CUDA int32 [1]')
+        self._call('fw_lm_head_argmax_fused', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), float(eps),
+                   w.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN, best.data_ptr(), tokens.data_ptr(),
+                   state.data_ptr(), cur.data_ptr(), int(max_pos), counter.data_ptr(), _stream())
+
+    # ---- log-mel front end -------------------------------------------------------------
+    def log_mel_workspace(self, n_samples, device='cuda'):
+        return torch.empty(int(self.lib.fw_log_mel_ws_floats(int(n_samples))), dtype=torch.float32, device=device)
+
+    def log_mel(self, wave, filters, out, out16, ws):
+        _check(wave, 'wave', torch.float32, 'fp32')
+        _check(filters, 'filters', torch.float32, 'fp32')
+        _check(out, 'out', torch.float32, 'fp32')
+        _check(ws, 'ws', torch.float32, 'fp32')
+        n_frames = wave.numel() // 160
+        _require(filters.shape == (201, 128), 'filters must be [201, 128]')
+        _require(out.numel() == 128 * n_frames, f'out must be [128, {n_frames}]')
+        if out16 is not None:
+            check_half(out16, 'out16')
+            _require(out16.numel() == 128 * n_frames, f'out16 must be [{n_frames}, 128]')
+        self._call('fw_log_mel', wave.data_ptr(), wave.numel(), filters.data_ptr(), out.data_ptr(), _ptr(out16),
+                   ws.data_ptr(), ws.numel(), _stream())
+
+    # ---- encoder ---------------------------------------------------------------------------
+    def gemm(self, a, w, bias, out, epilogue=EPI_BIAS, res=None, q_cols=0):
+        """out[m, n] = epilogue(a[m, :k] . w[n, :k]); a, out, res may be row-strided 2-D views."""
+        for t, n in ((a, 'a'), (w, 'w'), (out, 'out')):
+            _require(t.is_cuda and t.dtype == torch.float16 and t.dim() == 2 and t.stride(1) == 1,
+                     f'{n} must be a 2-D CUDA fp16 tensor with unit column stride')
+        m, k = a.shape
+        n = w.size(0)
+        _require(w.size(1) == k and out.shape == (m, n), 'gemm shape mismatch')
+        if bias is not None:
+            check_half(bias, 'bias')
+        ldr = 0
+        if res is not None:
+            _require(res.is_cuda and res.dtype == torch.float16 and res.shape == (m, n) and res.stride(1) == 1,
+                     'res must be [m, n] CUDA fp16')
+            ldr = res.stride(0)
+        self._call('fw_gemm', a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), _ptr(bias), out.data_ptr(),
+                   out.stride(0), _ptr(res), ldr, m, n, k, epilogue, q_cols, _stream())
+
+    def conv1d(self, x, stride, wp, bias, out, epilogue, res=None):
+        check_half(x, 'x')
+        check_half(wp, 'wp')
+        check_half(out, 'out')
+        t_in, c_in = x.shape
+        c_out = wp.size(0)
+        _require(wp.shape == (c_out, 3 * c_in), 'wp must be [c_out, 3 * c_in]')
+        _require(out.shape == ((t_in - 1) // stride + 1, c_out), 'out shape mismatch')
+        if res is not None:
+            check_half(res, 'res')
+            _require(res.shape == out.shape, 'res must match out')
+        self._call('fw_conv1d', x.data_ptr(), t_in, c_in, stride, wp.data_ptr(), _ptr(bias), out.data_ptr(), c_out,
+                   _ptr(res), epilogue, _stream())
+
+    def layernorm_rows(self, x, gamma, beta, y, eps):
+        for t, n in ((x, 'x'), (gamma, 'gamma'), (beta, 'beta'), (y, 'y')):
+            check_half(t, n)
+        _require(x.dim() == 2 and x.size(1) == HIDDEN and y.shape == x.shape, 'layernorm_rows shape mismatch')
+        self._call('fw_layernorm_rows', x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(), x.size(0),
+                   HIDDEN, float(eps), _stream())
+
+    def encoder_attention(self, qkv, out, heads):
+        check_half(qkv, 'qkv')
+        check_half(out, 'out')
+        seq = qkv.size(0)
+        _require(qkv.shape == (seq, 3 * heads * HEAD_DIM) and out.shape == (seq, heads * HEAD_DIM),
+                 'encoder_attention shape mismatch')
+        self._call('fw_encoder_attention', qkv.data_ptr(), out.data_ptr(), seq, heads, _stream())
+
+    def cross_kv(self, enc, w, bias, cross_kv):
+        check_half(enc, 'enc')
+        check_half(w, 'w')
+        check_half(cross_kv, 'cross_kv')
+        layers, _, heads, t, _ = cross_kv.shape
+        _require(enc.shape == (t, HIDDEN) and w.shape == (layers * 2 * HIDDEN, HIDDEN), 'cross_kv shape mismatch')
+        if bias is not None:
+            check_half(bias, 'bias')
+        self._call('fw_cross_kv', enc.data_ptr(), t, w.data_ptr(), _ptr(bias), cross_kv.data_ptr(), layers, heads,
+                   _stream())
+
+
+_ext = None
+
+
+def load_ext(verbose=False):
+    """Returns the extension object (custom/ext.py:13). Raises if the library has not been built."""
+    global _ext
+    if _ext is None:
+        if verbose:
+            print(f'loading {_lib.LIB_PATH}', file=sys.stderr)
+        _ext = WhisperExt()
+    return _ext
+
+
+def main():
+    from . import build as build_mod
+
+    parser = argparse.ArgumentParser(description='Build the HIP library and print per-kernel resource usage.')
+    parser.parse_args()
+    lib = build_mod.build()
+    for line in build_mod.resource_usage():
+        if any(k in line for k in ('Function Name', 'VGPRs', 'Spill', 'LDS Size', 'Occupancy')):
+            print(line.split('remark: ')[-1].replace(' [-Rpass-analysis=kernel-resource-usage]', ''))
+    print(f'built: [{lib}]')
+
+
+if __name__ == '__main__':
+    main()

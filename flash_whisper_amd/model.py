@@ -1,0 +1,393 @@
+"""Batch-1 fp16 Whisper on MI355X: HIP log-mel, MFMA encoder in a hipGraph, hipGraph-captured decoder.
+
+The drop-in for custom/model.py (``CustomModel``, custom/model.py:26-225): same constructor shape,
+``transcribe(audio)`` contract and timing dict, ``selftest`` dict, 1-step and 8-step decoder graphs
+with the position kept on the device. Every kernel is this package's HIP code (csrc/); torch only
+allocates device memory, provides the stream and drives hipGraph capture/replay.
+
+Offline there is no checkpoint or tokenizer, so the constructor builds the Whisper-large-v3-turbo
+architecture with seeded random-init weights (flash_whisper_amd.weights) and fixed prompt/suppress ids
+(flash_whisper_amd.config); ``text`` is then empty.
+"""
+
+import time
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+from . import weights as W
+from ._lib import (ACT_GELU, EPI_BIAS_GELU, EPI_BIAS_GELU_POS, EPI_BIAS_RESID, EPI_BIAS_RESID_CLAMP,
+                   EPI_SCALE_Q)
+from .audio import mel_filters
+from .config import CHUNK, N_SAMPLES, SAMPLE_RATE, SPLIT_KEYS, TURBO, DecodeSetup
+from .ext import load_ext
+from .selftest import run_selftest, workspace
+
+SYNTHETIC = 'synthetic'
+
+
+class CustomModel:
+    @torch.inference_mode()
+    def __init__(self, model_id=SYNTHETIC, cache_dir=None, *, seed=0, dims=TURBO, setup=None, selftest=True,
+                 capture=True, cross_split_keys=SPLIT_KEYS):
+        if not torch.cuda.is_available():
+            raise RuntimeError('CustomModel requires a HIP device')
+        if model_id not in (None, SYNTHETIC):
+            raise NotImplementedError(f'no offline checkpoint loader for {model_id!r}; use model_id="synthetic"')
+        self.ext = load_ext()
+        self.dims, self.seed = dims, seed
+        self.setup = setup or DecodeSetup()
+        d, dev, half = dims, 'cuda', torch.float16
+        self.heads, self.head_dim = d.heads, d.head_dim
+        self.scale = d.head_dim ** -0.5
+        self.max_pos, self.enc_len = d.max_pos, d.enc_len
+        self.prompt = list(self.setup.prompt)
+        self.max_new = self.max_pos - len(self.prompt)
+        self.eos = set(self.setup.eos)
+        self.cross_split_keys = cross_split_keys
+        self.record_events = False   # time every chunk replay with HIP events (bench.py)
+        self.chunk_events = []
+
+        self._specs = W.spec_map(dims)
+        self._init_encoder()
+        self._init_decoder()
+
+        self.mel_filters = torch.from_numpy(mel_filters()).to(dev)
+        self.wave = torch.zeros(N_SAMPLES, device=dev)
+        self.wave_host = torch.zeros(N_SAMPLES, pin_memory=True)
+        self.mel32 = torch.zeros(d.n_mels, d.mel_frames, device=dev)
+        self.mel16 = torch.zeros(d.mel_frames, d.n_mels, dtype=half, device=dev)  # time-major encoder input
+        self.mel_ws = self.ext.log_mel_workspace(N_SAMPLES)
+
+        self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
+        self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
+        self.graph_one = self.graph_chunk = self.graph_enc = None
+        if capture:
+            self.graph_one, self.graph_chunk = self._capture()
+            self.graph_enc = self._capture_encoder()
+        torch.cuda.synchronize()
+
+    # ---- weights -----------------------------------------------------------------------------
+    def _param(self, name, out=None):
+        """Parameter `name` (HF naming) generated on the device, optionally into the view `out`."""
+        shape, kind = self._specs[name]
+        t = out if out is not None else torch.empty(shape, dtype=torch.float16, device='cuda')
+        assert tuple(t.shape) == tuple(shape) and t.is_contiguous()
+        return W.device_fill(t, name, kind, self.seed)
+
+    def _ln(self, prefix):
+        return (self._param(f'{prefix}.weight'), self._param(f'{prefix}.bias'), self.dims.ln_eps)
+
+    def _packed_attn(self, prefix, scaled_bias_zero_k=True):
+        """[q; k; v] weight rows and [b_q; 0; b_v] bias (custom/model.py:87-88)."""
+        d = self.dims.d_model
+        w = torch.empty(3 * d, d, dtype=torch.float16, device='cuda')
+        b = torch.zeros(3 * d, dtype=torch.float16, device='cuda')
+        self._param(f'{prefix}.q_proj.weight', w[:d])
+        self._param(f'{prefix}.k_proj.weight', w[d:2 * d])
+        self._param(f'{prefix}.v_proj.weight', w[2 * d:])
+        self._param(f'{prefix}.q_proj.bias', b[:d])
+        self._param(f'{prefix}.v_proj.bias', b[2 * d:])
+        return w, b
+
+    def _conv_packed(self, name):
+        """HF conv weight [out, in, 3] -> [out, 3 * in] with column tap * in + c (implicit-GEMM order)."""
+        w = self._param(name)
+        return w.permute(0, 2, 1).contiguous().view(w.size(0), -1)
+
+    def _init_encoder(self):
+        d, e = self.dims, 'model.encoder'
+        self.conv1_wp, self.conv1_b = self._conv_packed(f'{e}.conv1.weight'), self._param(f'{e}.conv1.bias')
+        self.conv2_wp, self.conv2_b = self._conv_packed(f'{e}.conv2.weight'), self._param(f'{e}.conv2.bias')
+        self.enc_pos = self._param(f'{e}.embed_positions.weight')
+        self.enc_layers = []
+        for i in range(d.enc_layers):
+            p = f'{e}.layers.{i}'
+            qkv_w, qkv_b = self._packed_attn(f'{p}.self_attn')
+            self.enc_layers.append(SimpleNamespace(
+                ln1=self._ln(f'{p}.self_attn_layer_norm'), qkv_w=qkv_w, qkv_b=qkv_b,
+                out_w=self._param(f'{p}.self_attn.out_proj.weight'), out_b=self._param(f'{p}.self_attn.out_proj.bias'),
+                ln2=self._ln(f'{p}.final_layer_norm'),
+                fc1_w=self._param(f'{p}.fc1.weight'), fc1_b=self._param(f'{p}.fc1.bias'),
+                fc2_w=self._param(f'{p}.fc2.weight'), fc2_b=self._param(f'{p}.fc2.bias')))
+        self.enc_ln = self._ln(f'{e}.layer_norm')
+        t, dm, half = d.enc_len, d.d_model, torch.float16
+        self.x1 = torch.empty(d.mel_frames, dm, dtype=half, device='cuda')
+        self.ex = torch.empty(t, dm, dtype=half, device='cuda')        # residual stream
+        self.ey = torch.empty(t, dm, dtype=half, device='cuda')        # LayerNorm output
+        self.eqkv = torch.empty(t, 3 * dm, dtype=half, device='cuda')
+        self.eattn = torch.empty(t, dm, dtype=half, device='cuda')
+        self.effn = torch.empty(t, d.ffn, dtype=half, device='cuda')
+        self.enc_out = torch.empty(t, dm, dtype=half, device='cuda')
+
+    def _init_decoder(self):
+        d, p, half = self.dims, 'model.decoder', torch.float16
+        self.embed = self._param(f'{p}.embed_tokens.weight')      # tied with the LM head (custom/model.py:49-50)
+        self.pos_embed = self._param(f'{p}.embed_positions.weight')
+        self.lm_head = self.embed
+        self.layers = []
+        dm = d.d_model
+        self.cross_w = torch.empty(d.dec_layers * 2 * dm, dm, dtype=half, device='cuda')
+        self.cross_b = torch.zeros(d.dec_layers * 2 * dm, dtype=half, device='cuda')
+        for i in range(d.dec_layers):
+            q = f'{p}.layers.{i}'
+            qkv_w, qkv_b = self._packed_attn(f'{q}.self_attn')
+            ca = f'{q}.encoder_attn'
+            # custom/model.py:53-55: rows [k_i; v_i] per layer, bias [0; b_v]
+            self._param(f'{ca}.k_proj.weight', self.cross_w[(2 * i) * dm:(2 * i + 1) * dm])
+            self._param(f'{ca}.v_proj.weight', self.cross_w[(2 * i + 1) * dm:(2 * i + 2) * dm])
+            self._param(f'{ca}.v_proj.bias', self.cross_b[(2 * i + 1) * dm:(2 * i + 2) * dm])
+            self.layers.append(SimpleNamespace(
+                ln1=self._ln(f'{q}.self_attn_layer_norm'), ln2=self._ln(f'{q}.encoder_attn_layer_norm'),
+                ln3=self._ln(f'{q}.final_layer_norm'), qkv_w=qkv_w, qkv_b=qkv_b,
+                out=(self._param(f'{q}.self_attn.out_proj.weight'), self._param(f'{q}.self_attn.out_proj.bias')),
+                cross_q=(self._param(f'{ca}.q_proj.weight'), self._param(f'{ca}.q_proj.bias')),
+                cross_out=(self._param(f'{ca}.out_proj.weight'), self._param(f'{ca}.out_proj.bias')),
+                fc1=(self._param(f'{q}.fc1.weight'), self._param(f'{q}.fc1.bias')),
+                fc2=(self._param(f'{q}.fc2.weight'), self._param(f'{q}.fc2.bias'))))
+        self.final_ln = self._ln(f'{p}.layer_norm')
+
+        self.base_mask = torch.zeros(d.vocab, dtype=torch.bool, device='cuda')
+        self.base_mask[list(self.setup.suppress)] = True
+        self.first_mask = self.base_mask.clone()
+        self.first_mask[list(self.setup.begin_suppress)] = True
+        self.suppress = self.base_mask.clone()
+
+        self.self_kv = torch.zeros(d.dec_layers, 2, d.heads, d.max_pos, d.head_dim, dtype=half, device='cuda')
+        self.cross_kv = torch.zeros(d.dec_layers, 2, d.heads, d.enc_len, d.head_dim, dtype=half, device='cuda')
+        self.h = torch.zeros(2, dm, dtype=half, device='cuda')   # ping-pong residual stream
+        self.y = torch.zeros(1, dm, dtype=half, device='cuda')
+        self.qkv = torch.zeros(3 * dm, dtype=half, device='cuda')
+        self.q = torch.zeros(dm, dtype=half, device='cuda')
+        self.attn = torch.zeros(dm, dtype=half, device='cuda')
+        self.xo = torch.zeros(dm, dtype=half, device='cuda')
+        self.ffn = torch.zeros(d.ffn, dtype=half, device='cuda')
+        self.pending = torch.zeros(dm, dtype=half, device='cuda')
+        self.cur = torch.zeros(1, dtype=torch.long, device='cuda')
+        self.state = torch.zeros(2, dtype=torch.long, device='cuda')  # [position, generated count]
+        self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
+        self.best = torch.zeros(1, dtype=torch.long, device='cuda')
+        splits = -(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, self.cross_split_keys))
+        self.workspace = workspace(d.heads, splits)
+        self.attn_counters = torch.zeros(d.heads, dtype=torch.int32, device='cuda')
+        self.lm_counter = torch.zeros(1, dtype=torch.int32, device='cuda')
+
+    # ---- front end ---------------------------------------------------------------------------
+    def _log_mel(self, wave):
+        """HIP log-mel into self.mel32 [128, 3000] fp32 and self.mel16 [3000, 128] fp16 (custom/model.py:93-98)."""
+        self.ext.log_mel(wave, self.mel_filters, self.mel32, self.mel16, self.mel_ws)
+        return self.mel32
+
+    def _mel_diff(self):
+        """Max |HIP log-mel - torch.stft log-mel| on 10 s of seeded noise (custom/model.py:100-105)."""
+        audio = np.random.default_rng(0).standard_normal(10 * SAMPLE_RATE).astype(np.float32) * 0.1
+        wave = torch.zeros(N_SAMPLES, device='cuda')
+        wave[:audio.size] = torch.from_numpy(audio).cuda()
+        window = torch.hann_window(400, device='cuda')
+        stft = torch.stft(wave, 400, 160, window=window, return_complex=True)
+        ref = torch.clamp(self.mel_filters.T @ (stft[..., :-1].abs() ** 2), min=1e-10).log10()
+        ref = (torch.maximum(ref, ref.max() - 8.0) + 4.0) / 4.0
+        mel16 = torch.empty_like(self.mel16)
+        mel32 = torch.empty_like(self.mel32)
+        self.ext.log_mel(wave, self.mel_filters, mel32, mel16, self.mel_ws)
+        return float((mel32 - ref).abs().max())
+
+    # ---- encoder -----------------------------------------------------------------------------
+    def _encode(self):
+        """Conv stem + 32 layers + final LN, then the cross K/V of every decoder layer written straight
+        into self.cross_kv (custom/model.py:143-147; transformers modeling_whisper.py:592-648)."""
+        ext, nh = self.ext, self.heads
+        ext.conv1d(self.mel16, 1, self.conv1_wp, self.conv1_b, self.x1, EPI_BIAS_GELU)
+        ext.conv1d(self.x1, 2, self.conv2_wp, self.conv2_b, self.ex, EPI_BIAS_GELU_POS, res=self.enc_pos)
+        for lay in self.enc_layers:
+            ext.layernorm_rows(self.ex, lay.ln1[0], lay.ln1[1], self.ey, lay.ln1[2])
+            ext.gemm(self.ey, lay.qkv_w, lay.qkv_b, self.eqkv, EPI_SCALE_Q, q_cols=self.dims.d_model)
+            ext.encoder_attention(self.eqkv, self.eattn, nh)
+            ext.gemm(self.eattn, lay.out_w, lay.out_b, self.ex, EPI_BIAS_RESID, res=self.ex)
+            ext.layernorm_rows(self.ex, lay.ln2[0], lay.ln2[1], self.ey, lay.ln2[2])
+            ext.gemm(self.ey, lay.fc1_w, lay.fc1_b, self.effn, EPI_BIAS_GELU)
+            ext.gemm(self.effn, lay.fc2_w, lay.fc2_b, self.ex, EPI_BIAS_RESID_CLAMP, res=self.ex)
+        ext.layernorm_rows(self.ex, self.enc_ln[0], self.enc_ln[1], self.enc_out, self.enc_ln[2])
+        ext.cross_kv(self.enc_out, self.cross_w, self.cross_b, self.cross_kv)
+        return self.enc_out
+
+    def _capture_encoder(self):
+        """Encoder graph with a graph-vs-eager check and eager fallback (custom/model.py:149-171)."""
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self._encode()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._encode()
+            self.mel16.normal_()
+            eager = self._encode().clone()
+            eager_kv = self.cross_kv.clone()
+            graph.replay()
+            diff = max(float((self.enc_out.float() - eager.float()).abs().max()),
+                       float((self.cross_kv.float() - eager_kv.float()).abs().max()))
+            self.selftest['encoder_graph_max_abs_diff'] = diff
+            self.selftest['encoder_graph'] = True
+            return graph
+        except Exception as exc:  # eager fallback, as the reference
+            self.selftest['encoder_graph'] = False
+            self.selftest['encoder_graph_error'] = f'{type(exc).__name__}: {exc}'
+            return None
+        finally:
+            torch.cuda.synchronize()
+
+    # ---- decoder -----------------------------------------------------------------------------
+    def _step(self):
+        """One decoder token, entirely on the device (custom/model.py:107-123) in 33 launches:
+        per layer [LN1+QKV] [self-attn+combine, KV write] [out] [LN2+cross-q] [cross-attn+combine]
+        [cross-out] [LN3+fc1+GELU] [fc2], then [final LN + LM head + argmax + finalize]."""
+        ext, d, dm = self.ext, self.dims, self.dims.d_model
+        ws, ctr = self.workspace, self.attn_counters
+        q, k_new, v_new = self.qkv[:dm], self.qkv[dm:2 * dm], self.qkv[2 * dm:]
+        a, b = 0, 1
+        for i, lay in enumerate(self.layers):
+            g, be, eps = lay.ln1
+            if i == 0:
+                ext.ln_gemv(None, None, self.h[a], g, be, eps, lay.qkv_w, lay.qkv_b, self.qkv,
+                            embed=(self.cur, self.state, self.embed, self.pos_embed))
+            else:
+                ext.ln_gemv(self.h[b], self.pending, self.h[a], g, be, eps, lay.qkv_w, lay.qkv_b, self.qkv)
+            ext.decode_attention_fused(q, self.self_kv[i, 0], self.self_kv[i, 1], self.attn, self.state, k_new, v_new,
+                                       *ws, ctr, self.scale, SPLIT_KEYS)
+            ext.gemv(self.attn, *lay.out, self.xo)
+            g, be, eps = lay.ln2
+            ext.ln_gemv(self.h[a], self.xo, self.h[b], g, be, eps, *lay.cross_q, self.q)
+            ext.decode_attention_fused(self.q, self.cross_kv[i, 0], self.cross_kv[i, 1], self.attn, None, None, None,
+                                       *ws, ctr, self.scale, self.cross_split_keys)
+            ext.gemv(self.attn, *lay.cross_out, self.xo)
+            g, be, eps = lay.ln3
+            ext.ln_gemv(self.h[b], self.xo, self.h[a], g, be, eps, *lay.fc1, self.ffn, act=ACT_GELU)
+            ext.gemv(self.ffn, *lay.fc2, self.pending)
+            a, b = b, a
+        g, be, eps = self.final_ln
+        ext.lm_head_argmax_fused(self.h[b], self.pending, g, be, eps, self.lm_head, self.suppress, self.best,
+                                 self.tokens, self.state, self.cur, self.max_pos, self.lm_counter)
+
+    def _step_reference(self):
+        """The same step at the reference's op granularity (embed, add_layernorm, GEMV, split+combine
+        attention, lm_head_argmax, argmax_finalize); used to check the fused step."""
+        ext, dm = self.ext, self.dims.d_model
+        ws = self.workspace
+        h, y = self.h[0], self.y[0]
+        ext.embed(self.cur, self.state, self.embed, self.pos_embed, h)
+        pending = None
+        for i, lay in enumerate(self.layers):
+            ext.add_layernorm(h, pending, lay.ln1[0], lay.ln1[1], y, lay.ln1[2])
+            ext.gemv(y, lay.qkv_w, lay.qkv_b, self.qkv)
+            ext.decode_attention(self.qkv[:dm], self.self_kv[i, 0], self.self_kv[i, 1], self.attn, self.state,
+                                 self.qkv[dm:2 * dm], self.qkv[2 * dm:], *ws, self.scale)
+            ext.gemv(self.attn, *lay.out, self.xo)
+            ext.add_layernorm(h, self.xo, lay.ln2[0], lay.ln2[1], y, lay.ln2[2])
+            ext.gemv(y, *lay.cross_q, self.q)
+            ext.decode_attention(self.q, self.cross_kv[i, 0], self.cross_kv[i, 1], self.attn, None, None, None, *ws,
+                                 self.scale)
+            ext.gemv(self.attn, *lay.cross_out, self.xo)
+            ext.add_layernorm(h, self.xo, lay.ln3[0], lay.ln3[1], y, lay.ln3[2])
+            ext.gemv(y, *lay.fc1, self.ffn, act=ACT_GELU)
+            ext.gemv(self.ffn, *lay.fc2, self.pending)
+            pending = self.pending
+        ext.add_layernorm(h, pending, self.final_ln[0], self.final_ln[1], y, self.final_ln[2])
+        ext.lm_head_argmax(y, self.lm_head, self.suppress, self.best)
+        ext.argmax_finalize(self.best, self.tokens, self.state, self.cur, self.max_pos)
+
+    def _capture(self):
+        """Warm-up, then 1-step and CHUNK-step decoder graphs (custom/model.py:125-141)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                self._step()
+        torch.cuda.current_stream().wait_stream(side)
+        graphs = []
+        for steps in (1, CHUNK):
+            self.state.zero_()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(steps):
+                    self._step()
+            graphs.append(graph)
+        torch.cuda.synchronize()
+        self.self_kv.zero_()
+        self.state.zero_()
+        return graphs
+
+    def _replay(self, graph, steps):
+        if graph is not None:
+            graph.replay()
+        else:
+            for _ in range(steps):
+                self._step()
+
+    # ---- per-clip ------------------------------------------------------------------------------
+    @torch.inference_mode()
+    def transcribe(self, audio, max_new_tokens=None, stop_at_eos=True):
+        """custom/model.py:173-225. ``max_new_tokens``/``stop_at_eos`` select the fixed-length mode used
+        for the synthetic benchmark (224 tokens, no EOS stop); the defaults are the reference's."""
+        if not isinstance(audio, np.ndarray) or audio.dtype != np.float32 or audio.ndim != 1:
+            raise ValueError('audio must be a one-dimensional float32 NumPy array')
+        if not 0 < audio.size <= N_SAMPLES or not np.isfinite(audio).all():
+            raise ValueError('audio must contain finite samples and be between 0 and 30 seconds')
+        max_new = self.max_new if max_new_tokens is None else min(int(max_new_tokens), self.max_new)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+
+        host = self.wave_host.numpy()
+        host[:audio.size] = audio
+        host[audio.size:] = 0.0
+        self.wave.copy_(self.wave_host, non_blocking=True)
+        self._log_mel(self.wave)
+        torch.cuda.synchronize()
+        mel_s = time.perf_counter() - start
+
+        if self.graph_enc is not None:
+            self.graph_enc.replay()
+        else:
+            self._encode()
+        torch.cuda.synchronize()
+        encoder_s = time.perf_counter() - start - mel_s
+
+        decode_start = time.perf_counter()
+        self.state.zero_()
+        last = len(self.prompt) - 1
+        for i, token in enumerate(self.prompt):
+            self.cur.fill_(token)
+            if i == last:
+                self.suppress.copy_(self.first_mask)
+            self._replay(self.graph_one, 1)
+            if i == last:
+                self.suppress.copy_(self.base_mask)
+            else:
+                self.state[1].zero_()  # predictions made inside the prompt are discarded
+        token_ids = [int(self.tokens[0])]
+        ttft = time.perf_counter() - start
+        self.chunk_events = []
+        while (not stop_at_eos or token_ids[-1] not in self.eos) and len(token_ids) < max_new:
+            if self.record_events:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                ev[0].record()
+                self._replay(self.graph_chunk, CHUNK)
+                ev[1].record()
+                self.chunk_events.append(ev)
+            else:
+                self._replay(self.graph_chunk, CHUNK)
+            for token in self.tokens[len(token_ids):len(token_ids) + CHUNK].tolist():
+                token_ids.append(token)
+                if (stop_at_eos and token in self.eos) or len(token_ids) >= max_new:
+                    break
+        ttlt = time.perf_counter() - start
+        decode_s = time.perf_counter() - decode_start
+        detok_start = time.perf_counter()
+        text = ''  # no tokenizer offline
+        return {
+            'text': text, 'token_ids': token_ids, 'ttft_s': ttft, 'ttlt_s': ttlt,
+            'e2e_s': time.perf_counter() - start, 'mel_s': mel_s, 'encoder_s': encoder_s,
+            'decode_s': decode_s, 'detok_s': time.perf_counter() - detok_start, 'n_tokens': len(token_ids),
+        }

@@ -1,0 +1,153 @@
+"""In-process kernel checks against PyTorch fp32 math on the GPU (the drop-in for custom/selftest.py).
+
+``run_selftest(ext)`` runs the same checks and tolerances as the reference (custom/selftest.py:32-88):
+add_layernorm vs F.layer_norm (<= 2e-2), self attention at lengths {1, 63, 64, 65, 200, 448} with the
+KV write exact (tolerance 0), cross attention over 1500 keys (<= 1e-2), and the LM head argmax whose
+chosen fp32 logit must be within 1e-3 of the maximum with the finalize bookkeeping intact. It adds the
+same checks for the fused ops this build's decoder step uses. ``python -m custom.selftest --out DIR``
+writes selftest.json like the reference's ``main`` (:91-101).
+"""
+
+import argparse
+import json
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+
+from .config import SPLIT_KEYS
+
+HIDDEN, HEADS, HEAD_DIM, VOCAB = 1280, 20, 64, 51866
+
+
+def workspace(heads, splits, device='cuda'):
+    """fp32 partials (max, exp-sum, value sum) for the split-K attention kernels."""
+    return (torch.empty(heads * splits, device=device), torch.empty(heads * splits, device=device),
+            torch.empty(heads * splits * HEAD_DIM, device=device))
+
+
+def _check(name, err, tol):
+    return {'name': name, 'max_err': float(err), 'ok': bool(err <= tol)}
+
+
+def _attention_ref(q, k, v, length, scale):
+    # fp32 math path; bmm operands made contiguous first
+    qf = q.float().unsqueeze(1)                                 # [h, 1, d]
+    kt = k[:, :length].float().transpose(1, 2).contiguous()     # [h, d, l]
+    s = torch.bmm(qf, kt) * scale                               # [h, 1, l]
+    return torch.bmm(s.softmax(-1), v[:, :length].float().contiguous()).squeeze(1)
+
+
+@torch.inference_mode()
+def run_selftest(ext):
+    torch.manual_seed(0)
+    dev, half = 'cuda', torch.float16
+    checks = []
+
+    h = torch.randn(1, HIDDEN, device=dev, dtype=half)
+    x = torch.randn_like(h)
+    gamma, beta = torch.randn(HIDDEN, device=dev, dtype=half), torch.randn(HIDDEN, device=dev, dtype=half)
+    residual = h + x
+    ref = F.layer_norm(residual.float(), (HIDDEN,), gamma.float(), beta.float(), 1e-5)
+    y = torch.empty_like(h)
+    h0 = h.clone()
+    ext.add_layernorm(h, x, gamma, beta, y, 1e-5)
+    checks.append(_check('add_layernorm', max((y.float() - ref).abs().max(), (h - residual).abs().max()), 2e-2))
+
+    # fused residual + LN + GEMV must reproduce add_layernorm followed by the GEMV exactly
+    w = torch.randn(3840, HIDDEN, device=dev, dtype=half) * 0.02
+    b = torch.randn(3840, device=dev, dtype=half) * 0.02
+    out_fused, out_ref, h_out = (torch.empty(3840, device=dev, dtype=half), torch.empty(3840, device=dev, dtype=half),
+                                 torch.empty_like(h0))
+    ext.ln_gemv(h0, x, h_out, gamma, beta, 1e-5, w, b, out_fused)
+    ext.gemv(y, w, b, out_ref)
+    checks.append(_check('ln_gemv_vs_unfused', max((out_fused - out_ref).abs().max(), (h_out - h).abs().max()), 0))
+
+    scale = HEAD_DIM ** -0.5
+    ws = workspace(HEADS, 24)
+    counters = torch.zeros(HEADS, device=dev, dtype=torch.int32)
+    for length in (1, 63, 64, 65, 200, 448):
+        max_len, pos = 448, length - 1
+        q = torch.randn(HEADS * HEAD_DIM, device=dev, dtype=half)
+        k = torch.randn(HEADS, max_len, HEAD_DIM, device=dev, dtype=half)
+        v = torch.randn_like(k)
+        k_new = torch.randn(HEADS, 1, HEAD_DIM, device=dev, dtype=half)
+        v_new = torch.randn_like(k_new)
+        k_ref, v_ref = k.clone(), v.clone()
+        k_ref[:, pos], v_ref[:, pos] = k_new[:, 0], v_new[:, 0]
+        k2, v2 = k.clone(), v.clone()
+        out = torch.empty_like(q)
+        state = torch.tensor([pos, 0], device=dev, dtype=torch.long)
+        ext.decode_attention(q, k, v, out, state, k_new, v_new, *ws, scale)
+        ref = _attention_ref(q.view(HEADS, HEAD_DIM), k_ref, v_ref, length, scale).flatten()
+        checks.append(_check(f'decode_attention_self_{length}', (out.float() - ref).abs().max(), 1e-2))
+        written = max((k[:, pos] - k_new[:, 0]).abs().max(), (v[:, pos] - v_new[:, 0]).abs().max())
+        untouched = max((k - k_ref).abs().max(), (v - v_ref).abs().max())
+        checks.append(_check(f'kv_write_{length}', max(written, untouched), 0))
+        out_f = torch.empty_like(q)
+        ext.decode_attention_fused(q, k2, v2, out_f, state, k_new, v_new, *ws, counters, scale)
+        checks.append(_check(f'decode_attention_fused_self_{length}',
+                             max((out_f - out).abs().max(), (k2 - k).abs().max(), (v2 - v).abs().max()), 0))
+
+    q = torch.randn(HEADS * HEAD_DIM, device=dev, dtype=half)
+    k = torch.randn(HEADS, 1500, HEAD_DIM, device=dev, dtype=half)
+    v = torch.randn_like(k)
+    out = torch.empty_like(q)
+    ext.decode_attention(q, k, v, out, None, None, None, *ws, scale)
+    ref = _attention_ref(q.view(HEADS, HEAD_DIM), k, v, 1500, scale).flatten()
+    checks.append(_check('decode_attention_cross', (out.float() - ref).abs().max(), 1e-2))
+    out_f = torch.empty_like(q)
+    ext.decode_attention_fused(q, k, v, out_f, None, None, None, *ws, counters, scale)
+    checks.append(_check('decode_attention_fused_cross', (out_f - out).abs().max(), 0))
+
+    hidden = torch.randn(1, HIDDEN, device=dev, dtype=half)
+    weight = torch.randn(VOCAB, HIDDEN, device=dev, dtype=half) * 0.02
+    suppress = torch.rand(VOCAB, device=dev) < 0.01
+    logits = (weight.float() @ hidden.float()[0]).masked_fill(suppress, float('-inf'))
+    best, tokens = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
+    state, cur = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
+    ext.lm_head_argmax(hidden, weight, suppress, best)
+    ext.argmax_finalize(best, tokens, state, cur, 448)
+    token = int(tokens[0])
+    # A different index is acceptable only when it ties the reference max at fp16 precision.
+    gap = float(logits.max() - logits[token]) if 0 <= token < VOCAB else float('inf')
+    bookkeeping = int(cur) == token and state.tolist() == [4, 1] and int(best) == 0
+    checks.append(_check('lm_head_argmax', gap if bookkeeping else float('inf'), 1e-3))
+
+    # fused final LN + LM head + finalize vs add_layernorm -> lm_head_argmax -> argmax_finalize
+    hres, xres = torch.randn(1, HIDDEN, device=dev, dtype=half), torch.randn(1, HIDDEN, device=dev, dtype=half)
+    g1, b0 = torch.ones(HIDDEN, device=dev, dtype=half), torch.zeros(HIDDEN, device=dev, dtype=half)
+    h1, y1 = hres.clone(), torch.empty_like(hres)
+    ext.add_layernorm(h1, xres, g1, b0, y1, 1e-5)
+    best1, tok1 = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
+    st1, cur1 = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
+    ext.lm_head_argmax(y1, weight, suppress, best1)
+    ext.argmax_finalize(best1, tok1, st1, cur1, 448)
+    best2, tok2 = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
+    st2, cur2 = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
+    counter = torch.zeros(1, device=dev, dtype=torch.int32)
+    ext.lm_head_argmax_fused(hres, xres, g1, b0, 1e-5, weight, suppress, best2, tok2, st2, cur2, 448, counter)
+    same = (torch.equal(tok1, tok2) and torch.equal(st1, st2) and torch.equal(cur1, cur2) and int(best2) == 0
+            and int(counter) == 0)
+    checks.append(_check('lm_head_argmax_fused_vs_unfused', 0 if same else 1, 0))
+
+    return {'ok': all(c['ok'] for c in checks), 'checks': checks}
+
+
+def main():
+    from .ext import load_ext
+
+    parser = argparse.ArgumentParser()
+    parser.add_argument('--out', type=Path, required=True)
+    args = parser.parse_args()
+    args.out.mkdir(parents=True, exist_ok=True)
+    result = run_selftest(load_ext())
+    (args.out / 'selftest.json').write_text(json.dumps(result, indent=2) + '\n')
+    print(json.dumps(result))
+
+
+if __name__ == '__main__':
+    main()
+
+
+__all__ = ['SPLIT_KEYS', 'workspace', 'run_selftest', 'main']

@@ -1,0 +1,167 @@
+/*
+ * flash_whisper_amd C ABI: batch-1 Whisper-large-v3-turbo hot path on MI355X (gfx950).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t, enqueues its
+ * kernels on that stream without synchronising or allocating, and returns a status:
+ *   FW_OK (0)       success (launch enqueued),
+ *   FW_EINVAL (-1)  argument validation failed before any launch,
+ *   FW_EHIP (-2)    the HIP runtime reported an error for a launch.
+ * fw_last_error() returns the calling thread's last error message.
+ *
+ * fp16 tensors are IEEE binary16 ("half"), passed as void*. All tensors are dense and
+ * row-major (C-contiguous). Reference citations are to sp4s-s/flash_whisper.
+ */
+#ifndef FLASH_WHISPER_H_
+#define FLASH_WHISPER_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FW_OK 0
+#define FW_EINVAL (-1)
+#define FW_EHIP (-2)
+
+/* GEMV epilogue activations. */
+#define FW_ACT_NONE 0
+#define FW_ACT_GELU 1
+
+/* Encoder GEMM epilogues (applied to fp32 acc, rounding points as in HF fp16 Whisper). */
+#define FW_EPI_BIAS 0          /* out = fp16(acc + b)                                   */
+#define FW_EPI_BIAS_GELU 1     /* out = fp16(gelu(fp16(acc + b)))                       */
+#define FW_EPI_BIAS_RESID 2    /* out = fp16(res + fp16(acc + b))   (out may alias res) */
+#define FW_EPI_BIAS_RESID_CLAMP 3 /* as RESID, then clamp to +-(65504 - 1000)           */
+#define FW_EPI_BIAS_GELU_POS 4 /* out = fp16(fp16(gelu(fp16(acc + b))) + res)           */
+#define FW_EPI_SCALE_Q 5       /* columns < q_cols: fp16(fp16(acc + b) * 0.125); k/v as BIAS */
+
+const char* fw_last_error(void);
+int fw_version(void);
+
+/* ---- reference ops (custom/kernels/whisper_kernels.cu) ---------------------------------- */
+
+/* Replaces lm_head_argmax (whisper_kernels.cu:278-289, kernel :28-86).
+ * best <- max(best, pack(fp16(y . w[v]), v)) over v with !suppress[v]; ties -> lower index.
+ * y fp16[hidden], w fp16[vocab, hidden], suppress u8/bool[vocab], best u64[1]. hidden == 1280. */
+int fw_lm_head_argmax(const void* y, const void* w, const uint8_t* suppress, int vocab, int hidden,
+                      uint64_t* best, hipStream_t stream);
+
+/* Replaces argmax_finalize (whisper_kernels.cu:291-298, kernel :88-100).
+ * tok <- unpack(best); best <- 0; if state[1] < max_pos: tokens[state[1]] <- tok;
+ * state[1] <- min(state[1] + 1, max_pos); state[0] <- min(state[0] + 1, max_pos - 1); cur <- tok. */
+int fw_argmax_finalize(uint64_t* best, int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,
+                       hipStream_t stream);
+
+/* Replaces decode_attention (whisper_kernels.cu:300-339, kernels :102-213): split-K single-query
+ * attention, 64 keys per split, then a combine launch. q fp16[heads*64]; k, v fp16[heads, max_len, 64];
+ * out fp16[heads*64]. Self mode: len_state, k_new, v_new all non-NULL, len = len_state[0] + 1, and the
+ * row len_state[0] of k/v is overwritten with k_new/v_new (fp16[heads*64]). Cross mode: all three
+ * NULL, len = max_len. part_m/part_l fp32[ws_slots], part_acc fp32[ws_slots*64],
+ * ws_slots >= heads * ceil(max_len / 64). */
+int fw_decode_attention(const void* q, void* k, void* v, void* out, const int64_t* len_state,
+                        const void* k_new, const void* v_new, int heads, int max_len, float* part_m,
+                        float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream);
+
+/* Replaces add_layernorm (whisper_kernels.cu:341-356, kernel :215-267).
+ * If x != NULL: h <- fp16(h + x). Then y <- fp16(LN(h) * gamma + beta), two-pass fp32 statistics.
+ * h, x, gamma, beta, y fp16[n]; n == 1280. */
+int fw_add_layernorm(void* h, const void* x, const void* gamma, const void* beta, void* y, int n,
+                     float eps, hipStream_t stream);
+
+/* ---- fused decoder ops (no reference counterpart; they fuse the reference's step,
+ *      custom/model.py:107-123, into fewer launches) ------------------------------------- */
+
+/* Token + position embedding (custom/model.py:110): h <- fp16(embed[cur[0]] + pos_embed[state[0]]).
+ * Indices are clamped into [0, vocab) and [0, max_pos). */
+int fw_embed(const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+             int max_pos, void* h, int hidden, hipStream_t stream);
+
+/* out[n] <- act(fp16(w[n, :] . x + bias[n])) for n < n_out; w fp16[n_out, k_in], k_in in {1280, 5120}.
+ * Replaces F.linear (+F.gelu) at custom/model.py:114,116,117,119,120. bias may be NULL. */
+int fw_gemv(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
+            hipStream_t stream);
+
+/* Fused residual + LayerNorm + GEMV (custom/model.py:113-120 chains add_layernorm into F.linear).
+ * r <- fp16(h + x) (x may be NULL: r <- h); if h_out != NULL, h_out <- r (h_out must not alias h);
+ * y <- fp16(LN(r) * gamma + beta); out <- act(fp16(w . y + bias)). k_in == 1280.
+ * Embedding mode: if cur != NULL, r <- fp16(embed[cur[0]] + pos_embed[state[0]]) instead (h, x ignored). */
+int fw_ln_gemv(const void* h, const void* x, void* h_out, const void* gamma, const void* beta, float eps,
+               const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+               int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
+               hipStream_t stream);
+
+/* Split-K attention as fw_decode_attention with the combine fused into the last block of each head
+ * (a per-head arrival counter). split_keys is a multiple of 32 in [32, 256]. counters u32[heads]
+ * must be zero before the first call; every call leaves them zero. */
+int fw_decode_attention_fused(const void* q, void* k, void* v, void* out, const int64_t* len_state,
+                              const void* k_new, const void* v_new, int heads, int max_len, int split_keys,
+                              float* part_m, float* part_l, float* part_acc, uint32_t* counters,
+                              int64_t ws_slots, float scale, hipStream_t stream);
+
+/* Final residual + LayerNorm + LM head + argmax + finalize in one launch
+ * (custom/model.py:121-123): r = fp16(h + x); y = LN(r); best/tokens/state/cur updated exactly as
+ * fw_lm_head_argmax followed by fw_argmax_finalize. counter u32[1] must be zero before the first call
+ * and is left zero; best must be zero on entry and is left zero. */
+int fw_lm_head_argmax_fused(const void* h, const void* x, const void* gamma, const void* beta, float eps,
+                            const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
+                            int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, uint32_t* counter,
+                            hipStream_t stream);
+
+/* ---- log-mel front end (custom/model.py:93-98) ------------------------------------------- */
+
+/* wave fp32[n_samples] (n_samples = 480000; already zero padded) -> out fp32[128, n_frames]
+ * with n_frames = n_samples / 160: periodic Hann(400), reflect-padded centred STFT (hop 160),
+ * power, filters fp32[201, 128] (Slaney), log10(max(., 1e-10)), max(x, max - 8), (x + 4) / 4.
+ * out16 (may be NULL) receives fp16 of the same values, time-major [n_frames, 128].
+ * ws fp32[>= fw_log_mel_ws_floats(n_samples)]. */
+int fw_log_mel(const float* wave, int n_samples, const float* filters, float* out, void* out16, float* ws,
+               int64_t ws_floats, hipStream_t stream);
+int64_t fw_log_mel_ws_floats(int n_samples);
+
+/* ---- encoder (HF WhisperEncoder.forward semantics in fp16; MFMA) ------------------------ */
+
+/* out[m, n] <- epilogue(sum_k a[m, k] * w[n, k]) with fp32 accumulation on MFMA.
+ * a fp16[m, lda], w fp16[n, ldw], out fp16[m, ldo], bias fp16[n], res fp16[m, ldr] (epilogues that read it).
+ * k % 64 == 0, n % 64 == 0. q_cols is used by FW_EPI_SCALE_Q only. */
+int fw_gemm(const void* a, int lda, const void* w, int ldw, const void* bias, void* out, int ldo,
+            const void* res, int ldr, int m, int n, int k, int epilogue, int q_cols, hipStream_t stream);
+
+/* Conv1d(k=3, padding=1, stride) as an implicit GEMM over a time-major input:
+ * x fp16[t_in, c_in]; wp fp16[c_out, 3 * c_in] packed as wp[o, tap * c_in + c] = weight[o, c, tap];
+ * out fp16[t_out, c_out] with t_out = (t_in - 1) / stride + 1. Epilogue FW_EPI_BIAS_GELU or
+ * FW_EPI_BIAS_GELU_POS (res = positions fp16[t_out, c_out]). c_in % 64 == 0. */
+int fw_conv1d(const void* x, int t_in, int c_in, int stride, const void* wp, const void* bias, void* out,
+              int c_out, const void* res, int epilogue, hipStream_t stream);
+
+/* Row LayerNorm: y[r] <- fp16(LN(x[r]) * gamma + beta) for r < rows, n == 1280 (F.layer_norm on fp16). */
+int fw_layernorm_rows(const void* x, const void* gamma, const void* beta, void* y, int rows, int n, float eps,
+                      hipStream_t stream);
+
+/* Encoder self-attention (non-causal, scale 1: q is pre-scaled): qkv fp16[seq, 3 * heads * 64] as
+ * [q | k | v] per row; out fp16[seq, heads * 64]. */
+int fw_encoder_attention(const void* qkv, void* out, int seq, int heads, hipStream_t stream);
+
+/* Cross K/V for all decoder layers (custom/model.py:145-146) written straight into the cache layout:
+ * enc fp16[t, 1280]; w fp16[layers * 2 * 1280, 1280] rows [k_0; v_0; k_1; v_1; ...];
+ * bias fp16[layers * 2 * 1280]; cross_kv fp16[layers, 2, heads, t, 64]. */
+int fw_cross_kv(const void* enc, int t, const void* w, const void* bias, void* cross_kv, int layers, int heads,
+                hipStream_t stream);
+
+/* ---- seeded synthetic weights (the random-init N(mean, std) fp16 generator) -------------- */
+
+/* dst[i] <- fp16(mean + std * z(seed, tensor_id, offset + i)); z is a counter-based standard normal
+ * (splitmix64 hash + Box-Muller in explicitly rounded fp32), identical on host and device. */
+int fw_synth_normal_f16(void* dst, int64_t n, int64_t offset, uint64_t seed, uint64_t tensor_id, float mean,
+                        float std, hipStream_t stream);
+int fw_synth_normal_f16_host(uint16_t* dst, int64_t n, int64_t offset, uint64_t seed, uint64_t tensor_id,
+                             float mean, float std);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_WHISPER_H_ */

@@ -1,0 +1,102 @@
+"""The C-ABI library: every symbol declared in include/flash_whisper.h is exported, argument
+validation fails before any launch with FW_EINVAL and a message, and the torch-level validators raise
+RuntimeError like the reference's TORCH_CHECKs. No GPU work is started. CPU only."""
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT
+
+
+def declared_symbols():
+    text = (ROOT / 'include' / 'flash_whisper.h').read_text()
+    return sorted(set(re.findall(r'^\s*(?:const\s+)?\w+\*?\s+\**(fw_\w+)\s*\(', text, re.M)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ('fw_lm_head_argmax', 'fw_argmax_finalize', 'fw_decode_attention', 'fw_add_layernorm',
+              'fw_log_mel', 'fw_gemm', 'fw_conv1d', 'fw_encoder_attention', 'fw_cross_kv'):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol(built_lib):
+    from flash_whisper_amd import _lib
+
+    for s in declared_symbols():
+        assert hasattr(built_lib, s), s
+        assert s in _lib.SIGNATURES, f'{s} has no ctypes signature'
+
+
+def test_validation_errors_return_einval(built_lib):
+    from flash_whisper_amd import _lib
+
+    lib = built_lib
+    assert lib.fw_gemv(None, None, None, None, 1280, 1280, 0, None) == _lib.FW_EINVAL
+    assert b'null' in lib.fw_last_error()
+    dummy = ctypes.c_void_p(16)
+    assert lib.fw_lm_head_argmax(dummy, dummy, dummy, 51866, 1000, dummy, None) == _lib.FW_EINVAL
+    assert b'hidden size must be 1280' in lib.fw_last_error()
+    # len_state / k_new / v_new must come together (whisper_kernels.cu:313-314)
+    rc = lib.fw_decode_attention(dummy, dummy, dummy, dummy, dummy, None, None, 20, 448, dummy, dummy, dummy,
+                                 1000, 0.125, None)
+    assert rc == _lib.FW_EINVAL and b'given together' in lib.fw_last_error()
+    rc = lib.fw_decode_attention(dummy, dummy, dummy, dummy, None, None, None, 20, 448, dummy, dummy, dummy,
+                                 20 * 7 - 1, 0.125, None)
+    assert rc == _lib.FW_EINVAL and b'workspace too small' in lib.fw_last_error()
+    rc = lib.fw_gemm(dummy, 1280, dummy, 1280, None, dummy, 1280, None, 0, 1500, 1000, 1280, 0, 0, None)
+    assert rc == _lib.FW_EINVAL
+    rc = lib.fw_gemm(dummy, 1280, dummy, 1280, None, dummy, 1280, None, 0, 1500, 1280, 1280, 2, 0, None)
+    assert rc == _lib.FW_EINVAL and b'needs res' in lib.fw_last_error()
+    assert lib.fw_log_mel(dummy, 100, dummy, dummy, None, dummy, 100, None) == _lib.FW_EINVAL
+
+
+def test_status_becomes_runtime_error(built_lib):
+    from flash_whisper_amd import _lib
+
+    with pytest.raises(RuntimeError, match='hidden size'):
+        _lib.check(built_lib.fw_lm_head_argmax(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                               10, 7, ctypes.c_void_p(16), None), 'lm_head_argmax')
+
+
+def test_torch_validators_raise_before_launch(built_lib):
+    from flash_whisper_amd.ext import load_ext
+
+    ext = load_ext()
+    h = torch.zeros(1280, dtype=torch.float16)  # CPU tensor: rejected like the reference's is_cuda check
+    with pytest.raises(RuntimeError, match='contiguous CUDA fp16'):
+        ext.add_layernorm(h, None, h, h, h, 1e-5)
+    with pytest.raises(RuntimeError, match='contiguous CUDA fp16'):
+        ext.lm_head_argmax(h, torch.zeros(4, 1280, dtype=torch.float16), torch.zeros(4, dtype=torch.bool),
+                           torch.zeros(1, dtype=torch.long))
+    with pytest.raises(RuntimeError, match='int64'):
+        ext.argmax_finalize(torch.zeros(1, dtype=torch.long), torch.zeros(4, dtype=torch.int32),
+                            torch.zeros(2, dtype=torch.long), torch.zeros(1, dtype=torch.long), 448)
+
+
+def test_host_synth_is_standard_normal(built_lib):
+    from scipy import stats
+
+    from flash_whisper_amd import weights
+
+    z = weights.host_normal('test.tensor', (400000,), seed=3, std=1.0).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    assert stats.kstest(z, 'norm').pvalue > 1e-3
+    w = weights.host_normal('test.tensor', (400000,), seed=3).astype(np.float64)
+    assert abs(w.std() - 0.02) < 2e-4
+    # different names / seeds give independent streams; same name + seed is reproducible
+    assert not np.array_equal(weights.host_normal('a', (64,)), weights.host_normal('b', (64,)))
+    assert not np.array_equal(weights.host_normal('a', (64,), seed=0), weights.host_normal('a', (64,), seed=1))
+    np.testing.assert_array_equal(weights.host_normal('a', (64,)), weights.host_normal('a', (64,)))
+
+
+def test_product_filterbank_matches_transformers():
+    from conftest import GOLDEN
+    from flash_whisper_amd.audio import mel_filters
+
+    z = np.load(GOLDEN / 'hf_logmel.npz')
+    np.testing.assert_allclose(mel_filters(), z['mel_filters'].astype(np.float32), rtol=1e-6, atol=1e-9)

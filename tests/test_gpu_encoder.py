@@ -1,0 +1,179 @@
+"""GPU parity of the encoder kernels (MFMA GEMM + epilogues, implicit-GEMM conv stem, row LayerNorm,
+flash encoder attention, cross K/V scatter) against the CPU oracle. Tolerance as in
+test_gpu_decode.close_rel: 2e-3 relative in fp16, elementwise with an rms floor."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import encoder as oenc
+from oracle.common import f16, gelu
+from oracle.decoder import layer_norm
+from test_gpu_decode import close_rel, h16, np32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope='module')
+def ext(hip_device):
+    from flash_whisper_amd.ext import load_ext
+
+    return load_ext()
+
+
+def _gemm_ref(a, w, b, epi, res=None, q_cols=0):
+    acc = a.astype(np.float32) @ w.astype(np.float32).T
+    v = f16(acc + (0 if b is None else b.astype(np.float32)))
+    if epi == 1:
+        v = f16(gelu(v))
+    elif epi == 2:
+        v = f16(res.astype(np.float32) + v)
+    elif epi == 3:
+        v = np.clip(f16(res.astype(np.float32) + v), -64504, 64504)
+    elif epi == 4:
+        v = f16(f16(gelu(v)) + res.astype(np.float32))
+    elif epi == 5:
+        v = v.copy()
+        v[:, :q_cols] = f16(v[:, :q_cols] * 0.125)
+    return v
+
+
+@pytest.mark.parametrize('m,n,k,epi', [(1500, 3840, 1280, 5), (1500, 1280, 1280, 2), (1500, 5120, 1280, 1),
+                                       (1500, 1280, 5120, 3), (1500, 1280, 1280, 0), (77, 128, 64, 0),
+                                       (1500, 1280, 1280, 4)])
+def test_gemm_epilogues(ext, hip_device, m, n, k, epi):
+    dev = hip_device
+    rng = np.random.default_rng(m + n + k + epi)
+    a = np.float16(rng.standard_normal((m, k)))
+    w = np.float16(0.02 * rng.standard_normal((n, k)))
+    b = np.float16(0.02 * rng.standard_normal(n))
+    res = np.float16(rng.standard_normal((m, n))) if epi in (2, 3, 4) else None
+    out = torch.empty(m, n, dtype=torch.float16, device=dev)
+    tres = h16(res, dev) if res is not None else None
+    if epi in (2, 3):
+        out = tres  # residual updated in place, as the encoder does
+    ext.gemm(h16(a, dev), h16(w, dev), h16(b, dev), out, epi, res=tres, q_cols=n // 3 if epi == 5 else 0)
+    close_rel(np32(out), _gemm_ref(a, w, b, epi, res, n // 3 if epi == 5 else 0))
+
+
+def test_gemm_row_strided_views(ext, hip_device):
+    """a, out given as column slices of wider matrices (leading dimension > k / n)."""
+    dev = hip_device
+    rng = np.random.default_rng(7)
+    big_a = np.float16(rng.standard_normal((300, 3 * 256)))
+    w = np.float16(0.02 * rng.standard_normal((128, 256)))
+    ta = h16(big_a, dev)
+    out_big = torch.zeros(300, 384, dtype=torch.float16, device=dev)
+    ext.gemm(ta[:, 256:512], h16(w, dev), None, out_big[:, 128:256], 0)
+    close_rel(np32(out_big[:, 128:256]), _gemm_ref(big_a[:, 256:512], w, None, 0))
+    assert float(out_big[:, :128].abs().max()) == 0 and float(out_big[:, 256:].abs().max()) == 0
+
+
+@pytest.mark.parametrize('stride,c_in,t_in', [(1, 128, 3000), (2, 1280, 3000), (2, 128, 61)])
+def test_conv1d(ext, hip_device, stride, c_in, t_in):
+    dev = hip_device
+    rng = np.random.default_rng(stride + c_in)
+    x = np.float16(rng.standard_normal((t_in, c_in)))     # time-major
+    w = np.float16(0.02 * rng.standard_normal((1280, c_in, 3)))
+    b = np.float16(0.02 * rng.standard_normal(1280))
+    wp = np.ascontiguousarray(w.transpose(0, 2, 1).reshape(1280, 3 * c_in))
+    t_out = (t_in - 1) // stride + 1
+    pos = np.float16(rng.standard_normal((t_out, 1280)))
+    out = torch.empty(t_out, 1280, dtype=torch.float16, device=dev)
+    epi = 4 if stride == 2 else 1
+    ext.conv1d(h16(x, dev), stride, h16(wp, dev), h16(b, dev), out, epi, res=h16(pos, dev) if epi == 4 else None)
+    ref = f16(gelu(f16(oenc.conv1d(x.T.astype(np.float32), w, b, stride)))).T
+    if epi == 4:
+        ref = f16(ref + pos.astype(np.float32))
+    close_rel(np32(out), ref)
+
+
+def test_layernorm_rows(ext, hip_device):
+    dev = hip_device
+    rng = np.random.default_rng(8)
+    x = np.float16(3 * rng.standard_normal((1501, 1280)) + 0.5)
+    g, b = np.float16(1 + 0.1 * rng.standard_normal(1280)), np.float16(0.1 * rng.standard_normal(1280))
+    y = torch.empty(1501, 1280, dtype=torch.float16, device=dev)
+    ext.layernorm_rows(h16(x, dev), h16(g, dev), h16(b, dev), y, 1e-5)
+    close_rel(np32(y), f16(layer_norm(x, g, b, 1e-5)))
+
+
+def _attn_ref(qkv, heads):
+    seq = qkv.shape[0]
+    d = heads * 64
+    q = qkv[:, :d].astype(np.float64).reshape(seq, heads, 64).transpose(1, 0, 2)
+    k = qkv[:, d:2 * d].astype(np.float64).reshape(seq, heads, 64).transpose(1, 0, 2)
+    v = qkv[:, 2 * d:].astype(np.float64).reshape(seq, heads, 64).transpose(1, 0, 2)
+    s = q @ k.transpose(0, 2, 1)
+    s -= s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return f16((p @ v).transpose(1, 0, 2).reshape(seq, d))
+
+
+@pytest.mark.parametrize('seq,heads,qscale', [(1500, 20, 0.125), (100, 2, 0.125), (1500, 20, 0.6), (33, 1, 0.3)])
+def test_encoder_attention(ext, hip_device, seq, heads, qscale):
+    dev = hip_device
+    rng = np.random.default_rng(seq + heads)
+    qkv = rng.standard_normal((seq, 3 * heads * 64))
+    qkv[:, :heads * 64] *= qscale  # q arrives pre-scaled; a larger scale sharpens the softmax
+    qkv = np.float16(qkv)
+    out = torch.empty(seq, heads * 64, dtype=torch.float16, device=dev)
+    ext.encoder_attention(h16(qkv, dev), out, heads)
+    close_rel(np32(out), _attn_ref(qkv, heads))
+
+
+def test_cross_kv_layout(ext, hip_device):
+    from flash_whisper_amd.config import TURBO
+
+    dev = hip_device
+    rng = np.random.default_rng(9)
+    enc = np.float16(rng.standard_normal((1500, 1280)))
+    params = {}
+    for i in range(4):
+        a = f'model.decoder.layers.{i}.encoder_attn'
+        params[f'{a}.k_proj.weight'] = np.float16(0.02 * rng.standard_normal((1280, 1280)))
+        params[f'{a}.v_proj.weight'] = np.float16(0.02 * rng.standard_normal((1280, 1280)))
+        params[f'{a}.v_proj.bias'] = np.float16(0.02 * rng.standard_normal(1280))
+    w = np.concatenate([np.concatenate([params[f'model.decoder.layers.{i}.encoder_attn.k_proj.weight'],
+                                        params[f'model.decoder.layers.{i}.encoder_attn.v_proj.weight']])
+                        for i in range(4)])
+    b = np.concatenate([np.concatenate([np.zeros(1280, np.float16),
+                                        params[f'model.decoder.layers.{i}.encoder_attn.v_proj.bias']])
+                        for i in range(4)])
+    ckv = torch.empty(4, 2, 20, 1500, 64, dtype=torch.float16, device=dev)
+    ext.cross_kv(h16(enc, dev), h16(w, dev), h16(b, dev), ckv)
+    close_rel(np32(ckv), oenc.cross_kv(params, enc.astype(np.float32), TURBO))
+
+
+def test_encoder_layer_and_stem_vs_oracle(ext, hip_device):
+    """Stem and encoder layer 0 of the seeded turbo weights, GPU vs oracle from the same input."""
+    from flash_whisper_amd.config import TURBO
+    from flash_whisper_amd.model import CustomModel
+
+    model = CustomModel(selftest=False, capture=False, dims=TURBO)
+    from flash_whisper_amd import weights
+
+    names = [n for n, _, _ in weights.param_specs(TURBO)
+             if n.startswith('model.encoder.layers.0.') or not n.startswith('model.encoder.layers.')]
+    names = [n for n in names if n.startswith('model.encoder.')]
+    params = weights.host_params(TURBO, 0, names)
+    rng = np.random.default_rng(11)
+    mel = np.float16(rng.standard_normal((128, 3000)) * 0.5)
+    model.mel16.copy_(torch.from_numpy(np.ascontiguousarray(mel.T)))
+    ext.conv1d(model.mel16, 1, model.conv1_wp, model.conv1_b, model.x1, 1)
+    ext.conv1d(model.x1, 2, model.conv2_wp, model.conv2_b, model.ex, 4, res=model.enc_pos)
+    stem = oenc.embed_stem(params, mel.astype(np.float32))
+    close_rel(np32(model.ex), stem)
+    # layer 0 from the oracle's stem output, so both sides start from the same fp16 input
+    model.ex.copy_(torch.from_numpy(stem.astype(np.float16)))
+    lay = model.enc_layers[0]
+    ext.layernorm_rows(model.ex, lay.ln1[0], lay.ln1[1], model.ey, lay.ln1[2])
+    ext.gemm(model.ey, lay.qkv_w, lay.qkv_b, model.eqkv, 5, q_cols=1280)
+    ext.encoder_attention(model.eqkv, model.eattn, 20)
+    ext.gemm(model.eattn, lay.out_w, lay.out_b, model.ex, 2, res=model.ex)
+    ext.layernorm_rows(model.ex, lay.ln2[0], lay.ln2[1], model.ey, lay.ln2[2])
+    ext.gemm(model.ey, lay.fc1_w, lay.fc1_b, model.effn, 1)
+    ext.gemm(model.effn, lay.fc2_w, lay.fc2_b, model.ex, 3, res=model.ex)
+    ref = oenc.encoder_layer(stem, oenc.layer_params(params, 0), 20, 1e-5)
+    close_rel(np32(model.ex), ref)

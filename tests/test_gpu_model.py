@@ -1,0 +1,137 @@
+"""End-to-end GPU parity of CustomModel on the seeded synthetic workload (config 5) against the oracle:
+log-mel within 1e-4 absolute, greedy ids bit-exact against the committed oracle fixture
+(tests/golden/e2e_turbo_seed0.json), decoder steps bit-exact against the oracle run on the same
+cross K/V (teacher-forced), hipGraph replays identical to eager steps, and the fused step identical to
+the reference-granularity step."""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from test_gpu_decode import close_rel, np32
+
+pytestmark = pytest.mark.gpu
+FIXTURE = GOLDEN / 'e2e_turbo_seed0.json'
+
+
+@pytest.fixture(scope='module')
+def model(hip_device):
+    from flash_whisper_amd.model import CustomModel
+
+    return CustomModel(seed=0)
+
+
+@pytest.fixture(scope='module')
+def clip():
+    from flash_whisper_amd.audio import synthetic_clip
+
+    return synthetic_clip(0)
+
+
+def test_selftest_and_encoder_graph(model):
+    assert model.selftest['ok'], [c for c in model.selftest['checks'] if not c['ok']]
+    assert model.selftest['mel_max_abs_diff'] < 1e-4
+    assert model.selftest['encoder_graph'] and model.selftest['encoder_graph_max_abs_diff'] == 0.0
+
+
+def test_log_mel_vs_oracle(model, clip):
+    from oracle.logmel import log_mel
+
+    for audio in (clip, clip[:5 * 16000], np.zeros(16000, np.float32)):
+        wave = np.zeros(480000, np.float32)
+        wave[:audio.size] = audio
+        model._log_mel(torch.from_numpy(wave).cuda())
+        ref = log_mel(wave)
+        assert np.abs(np32(model.mel32) - ref).max() <= 1e-4
+        assert np.array_equal(np32(model.mel16), np32(model.mel32).T.astype(np.float16).astype(np.float32))
+
+
+def test_transcribe_ids_match_oracle_fixture(model, clip):
+    from flash_whisper_amd.audio import sha256
+
+    fx = json.loads(FIXTURE.read_text())
+    assert sha256(clip) == fx['clip_sha256']
+    res = model.transcribe(clip, max_new_tokens=fx['n_tokens'], stop_at_eos=False)
+    ids = res['token_ids']
+    first_diff = next((i for i, (a, b) in enumerate(zip(ids, fx['ids'])) if a != b), None)
+    assert first_diff is None and len(ids) == len(fx['ids']), (
+        f'first mismatch at {first_diff}: gpu {ids[first_diff:first_diff + 4] if first_diff is not None else ids[-4:]}'
+        f' oracle {fx["ids"][first_diff:first_diff + 4] if first_diff is not None else fx["ids"][-4:]}'
+        f' margin {fx["margins"][first_diff] if first_diff is not None else None}')
+
+
+def test_encoder_rows_vs_oracle_fixture(model, clip):
+    z = np.load(FIXTURE.with_suffix('.npz'))
+    model.transcribe(clip, max_new_tokens=1, stop_at_eos=False)
+    rows = z['rows']
+    mel_err = np.abs(np32(model.mel16)[rows].T - z['mel_cols'].astype(np.float32)).max()
+    assert mel_err <= 1e-3  # fp16 mel: one ulp at |x| < 2
+    enc = np32(model.enc_out)[rows]
+    ref = z['enc_rows'].astype(np.float32)
+    rel = np.abs(enc - ref).max() / np.abs(ref).max()
+    print(f'encoder output after 32 layers: max abs err {np.abs(enc - ref).max():.3e}, rel-to-max {rel:.3e}')
+    assert rel < 1e-2
+
+
+def test_decoder_teacher_forced_vs_oracle(model, clip):
+    """The oracle decoder on the GPU's own cross K/V: every step's argmax must match bit-exactly."""
+    from flash_whisper_amd import weights
+    from oracle.decoder import DecoderOracle, greedy
+
+    res = model.transcribe(clip, max_new_tokens=24, stop_at_eos=False)
+    names = [n for n, _, _ in weights.param_specs(model.dims) if n.startswith('model.decoder.')]
+    params = weights.host_params(model.dims, model.seed, names)
+    oracle = DecoderOracle(params, model.dims, np32(model.cross_kv))
+    s = model.setup
+    out = greedy(oracle, s.prompt, 24, s.suppress, s.begin_suppress, teacher=res['token_ids'])
+    assert out['ids'] == res['token_ids'], (out['ids'], res['token_ids'], out['margins'])
+
+
+def test_graph_replay_matches_eager(model, clip):
+    res_graph = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
+    g1, gc = model.graph_one, model.graph_chunk
+    try:
+        model.graph_one = model.graph_chunk = None
+        res_eager = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
+    finally:
+        model.graph_one, model.graph_chunk = g1, gc
+    assert res_graph['token_ids'] == res_eager['token_ids']
+    res_graph2 = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
+    assert res_graph2['token_ids'] == res_graph['token_ids']
+
+
+def test_fused_step_matches_reference_granularity_step(model, clip):
+    model.transcribe(clip, max_new_tokens=1, stop_at_eos=False)  # fills cross K/V
+    ids = {}
+    for name, fn in (('fused', model._step), ('reference', model._step_reference)):
+        model.state.zero_()
+        model.cur.fill_(model.prompt[0])
+        model.self_kv.zero_()
+        for _ in range(12):
+            fn()
+        ids[name] = model.tokens[:12].tolist()
+    torch.cuda.synchronize()
+    assert ids['fused'] == ids['reference']
+
+
+def test_transcribe_validation(model):
+    with pytest.raises(ValueError):
+        model.transcribe(np.zeros(10, np.float64))
+    with pytest.raises(ValueError):
+        model.transcribe(np.zeros(480001, np.float32))
+    with pytest.raises(ValueError):
+        model.transcribe(np.array([np.nan], np.float32))
+    with pytest.raises(ValueError):
+        model.transcribe(np.zeros((2, 5), np.float32))
+
+
+def test_short_clip_and_timing_dict(model, clip):
+    res = model.transcribe(clip[:5 * 16000], max_new_tokens=16, stop_at_eos=False)
+    assert res['n_tokens'] == 16 and len(res['token_ids']) == 16
+    for key in ('text', 'token_ids', 'ttft_s', 'ttlt_s', 'e2e_s', 'mel_s', 'encoder_s', 'decode_s', 'detok_s',
+                'n_tokens'):
+        assert key in res
+    assert 0 < res['ttft_s'] <= res['ttlt_s'] <= res['e2e_s']
