@@ -27,9 +27,10 @@ SIGNATURES = {
     'fw_embed': (c_int, [P, P, P, P, c_int, c_int, P, c_int, P]),
     'fw_gemv': (c_int, [P, P, P, P, c_int, c_int, c_int, P]),
     'fw_ln_gemv': (c_int, [P, P, P, P, P, c_float, P, P, P, P, c_int, c_int, P, P, P, c_int, c_int, c_int, P]),
-    'fw_decode_attention_fused': (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, P, c_int64, c_float,
-                                          P]),
-    'fw_lm_head_argmax_fused': (c_int, [P, P, P, P, c_float, P, P, c_int, c_int, P, P, P, P, c_int, P, P]),
+    'fw_decode_attention_fused': (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_float, P]),
+    'fw_attention_split': (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, c_int64, c_float, P]),
+    'fw_attn_out_gemv': (c_int, [P, P, P, c_int64, P, c_int, c_int, c_int, P, P, P, c_int, P]),
+    'fw_lm_head_argmax_fused': (c_int, [P, P, P, P, c_float, P, P, c_int, c_int, P, P, P, P, c_int, P]),
     'fw_log_mel': (c_int, [P, c_int, P, P, P, P, c_int64, P]),
     'fw_log_mel_ws_floats': (c_int64, [c_int]),
     'fw_gemm': (c_int, [P, c_int, P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),

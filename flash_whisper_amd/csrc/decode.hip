@@ -135,31 +135,99 @@ struct LnArgs {
   int max_pos;
 };
 
-template <int K, int NW, int U, bool LN, int ACT>
-__global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restrict__ xin, LnArgs ln,
+// Split-K attention partials consumed by the GEMV that follows the attention (the out projection):
+// the combine of the reference's decode_attention_combine_kernel (whisper_kernels.cu:191-213) runs
+// as that GEMV's prologue, so the attention output never makes a round trip through a separate
+// launch. `len_state` (self attention) limits the combine to the splits that held keys.
+struct CombineArgs {
+  const float* part_m;
+  const float* part_l;
+  const float* part_acc;
+  const int64_t* len_state;
+  int max_len;
+  int split_keys;
+  int nsplit;
+  int heads;
+};
+
+constexpr int kMaxCombineSplits = 8;   // splits per head the combine prologue merges
+constexpr int kMaxCombineHeads = 32;
+
+__device__ __forceinline__ int active_splits(const int64_t* len_state, int max_len, int split_keys, int nsplit) {
+  if (!len_state) return nsplit;
+  int64_t p = len_state[0];
+  p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
+  return static_cast<int>((p + split_keys) / split_keys);  // ceil((p + 1) / split_keys)
+}
+
+// x[h * 64 + d] = fp16(sum_s acc[h, s, d] e^(m_s - M) / sum_s l_s e^(m_s - M)), splits with l = 0 skipped
+// (the arithmetic of the combine launch). Every partial a thread needs is requested before any is used.
+template <int NT>
+__device__ __forceinline__ void combine_prologue(const CombineArgs& c, _Float16* x, float* wgt, float* den_lds) {
+  constexpr int S = kMaxCombineSplits;
+  const int active = active_splits(c.len_state, c.max_len, c.split_keys, c.nsplit);
+  for (int h = threadIdx.x; h < c.heads; h += NT) {
+    float pm[S], pl[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      pm[s] = s < active ? c.part_m[h * c.nsplit + s] : -INFINITY;
+      pl[s] = s < active ? c.part_l[h * c.nsplit + s] : 0.f;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < S; ++s) m = fmaxf(m, pm[s]);
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float w = pl[s] > 0.f ? __expf(pm[s] - m) : 0.f;
+      wgt[h * S + s] = w;
+      den = fmaf(pl[s], w, den);
+    }
+    den_lds[h] = den;
+  }
+  constexpr int kPer = (kHidden + NT - 1) / NT;
+  float pa[kPer][S];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = threadIdx.x + i * NT;
+    const int h = j / kHeadDim, d = j % kHeadDim;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      pa[i][s] = (j < c.heads * kHeadDim && s < active)
+                     ? c.part_acc[(static_cast<size_t>(h) * c.nsplit + s) * kHeadDim + d] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int j = threadIdx.x + i * NT;
+    if (j < c.heads * kHeadDim) {
+      const int h = j / kHeadDim;
+      float num = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        if (wgt[h * S + s] != 0.f) num = fmaf(pa[i][s], wgt[h * S + s], num);
+      x[j] = f2h(num / den_lds[h]);
+    }
+  }
+}
+
+constexpr int kModePlain = 0, kModeLn = 1, kModeCombine = 2;
+
+template <int K, int NW, int U, int MODE, int ACT>
+__global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restrict__ xin, LnArgs ln, CombineArgs cb,
                                                        const _Float16* __restrict__ w,
                                                        const _Float16* __restrict__ bias, _Float16* __restrict__ out,
                                                        int n) {
   using RS = RowSplit<K>;
   constexpr int kRowsPerBlock = NW * RS::kRPW * U;
-  __shared__ __align__(16) _Float16 y_lds[LN ? kHidden : 8];
+  __shared__ __align__(16) _Float16 y_lds[MODE != kModePlain ? K : 8];
   __shared__ float red[NW];
-  const uint4* xv;
-  if constexpr (LN) {
-    const _Float16 *a = ln.h, *b = ln.x;
-    if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b);
-    ln_prologue<NW * 64>(a, b, ln.h_out, ln.gamma, ln.beta, ln.eps, y_lds, red);
-    __syncthreads();
-    xv = reinterpret_cast<const uint4*>(y_lds);
-  } else {
-    xv = reinterpret_cast<const uint4*>(xin);
-  }
+  __shared__ float wgt[MODE == kModeCombine ? kMaxCombineHeads * kMaxCombineSplits : 1];
+  __shared__ float inv_den[MODE == kModeCombine ? kMaxCombineHeads : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % RS::kLPR, rsel = lane / RS::kLPR;
-  uint4 xr[RS::kC];
-#pragma unroll
-  for (int c = 0; c < RS::kC; ++c) xr[c] = xv[sub + RS::kLPR * c];
-
+  // The weight rows do not depend on the input vector: request them first, so the prologue
+  // (LayerNorm or attention combine) runs while they are in flight.
   const int row0 = blockIdx.x * kRowsPerBlock + wave * RS::kRPW * U + rsel;
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
   uint4 wr[U][RS::kC];
@@ -172,6 +240,24 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
       if (row < n) wr[u][c] = ld_stream(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + RS::kLPR * c);
     }
   }
+  const uint4* xv;
+  if constexpr (MODE == kModeLn) {
+    const _Float16 *a = ln.h, *b = ln.x;
+    if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b);
+    ln_prologue<NW * 64>(a, b, ln.h_out, ln.gamma, ln.beta, ln.eps, y_lds, red);
+    __syncthreads();
+    xv = reinterpret_cast<const uint4*>(y_lds);
+  } else if constexpr (MODE == kModeCombine) {
+    combine_prologue<NW * 64>(cb, y_lds, wgt, inv_den);
+    __syncthreads();
+    xv = reinterpret_cast<const uint4*>(y_lds);
+  } else {
+    xv = reinterpret_cast<const uint4*>(xin);
+  }
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int c = 0; c < RS::kC; ++c) xr[c] = xv[sub + RS::kLPR * c];
+
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int row = row0 + u * RS::kRPW;
@@ -187,29 +273,32 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   }
 }
 
-template <int K, int NW, int U, bool LN, int ACT>
-void launch_gemv(const _Float16* x, const LnArgs& ln, const _Float16* w, const _Float16* b, _Float16* out, int n,
-                 hipStream_t s) {
+template <int K, int NW, int U, int MODE, int ACT>
+void launch_gemv(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w, const _Float16* b,
+                 _Float16* out, int n, hipStream_t s) {
   constexpr int kRows = NW * RowSplit<K>::kRPW * U;
   const int grid = (n + kRows - 1) / kRows;
-  hipLaunchKernelGGL((gemv_kernel<K, NW, U, LN, ACT>), dim3(grid), dim3(NW * 64), 0, s, x, ln, w, b, out, n);
+  hipLaunchKernelGGL((gemv_kernel<K, NW, U, MODE, ACT>), dim3(grid), dim3(NW * 64), 0, s, x, ln, cb, w, b, out, n);
 }
 
-template <bool LN, int ACT>
-void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const _Float16* w, const _Float16* b, _Float16* out,
-                        int n, hipStream_t s) {
+template <int MODE, int ACT>
+void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w,
+                        const _Float16* b, _Float16* out, int n, hipStream_t s) {
   if (n >= 3840)
-    launch_gemv<kHidden, 4, 2, LN, ACT>(x, ln, w, b, out, n, s);
+    launch_gemv<kHidden, 4, 2, MODE, ACT>(x, ln, cb, w, b, out, n, s);
   else
-    launch_gemv<kHidden, 2, 1, LN, ACT>(x, ln, w, b, out, n, s);
+    launch_gemv<kHidden, 2, 1, MODE, ACT>(x, ln, cb, w, b, out, n, s);
 }
 
 // ------------------------------------------------------------------------------------------
 // LM head + argmax (reference lm_head_argmax_kernel, whisper_kernels.cu:28-86): rows of the tied
 // embedding are streamed once; each row's fp32 dot is rounded to fp16, packed with its index and
-// max-reduced to one 64-bit atomicMax per block. The logits vector is never written. With LN the
-// final LayerNorm is recomputed per block; with FIN the last block to finish also runs the
-// finalize step (reference argmax_finalize_kernel, :88-100).
+// max-reduced to one 64-bit atomicMax per block. The logits vector is never written. Each block owns
+// a contiguous row range; its first 16 rows are requested before the (optional) final-LayerNorm
+// prologue and every iteration prefetches the next 16 rows, so two row groups are in flight per wave.
+// The finalize step (reference argmax_finalize_kernel, :88-100) is a separate 1-thread launch: a
+// last-block-done finalize needs a device-scope release per block, which on this part writes back
+// the L2 and costs far more than one extra launch.
 // ------------------------------------------------------------------------------------------
 constexpr int kLmNW = 4, kLmU = 2;
 constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // 16 rows per block iteration
@@ -219,11 +308,11 @@ struct FinArgs {
   int64_t* state;
   int64_t* cur;
   int max_pos;
-  uint32_t* counter;
 };
 
 __device__ __forceinline__ void finalize_token(unsigned long long* best, const FinArgs& f) {
-  const unsigned long long b = __hip_atomic_exchange(best, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = *best;
+  *best = 0ull;
   const int64_t tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
   const int64_t n = f.state[1];
   if (n < f.max_pos) f.tokens[n] = tok;
@@ -232,37 +321,23 @@ __device__ __forceinline__ void finalize_token(unsigned long long* best, const F
   *f.cur = tok;
 }
 
-template <bool LN, bool FIN>
+template <bool LN>
 __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __restrict__ yin, LnArgs ln,
                                                              const _Float16* __restrict__ w,
                                                              const uint8_t* __restrict__ suppress, int vocab,
-                                                             int rows_per_block, unsigned long long* best,
-                                                             FinArgs fin) {
+                                                             int rows_per_block, unsigned long long* best) {
   using RS = RowSplit<kHidden>;
   __shared__ __align__(16) _Float16 y_lds[kHidden];
   __shared__ float red[kLmNW];
   __shared__ unsigned long long block_best[kLmNW * 2];
-  __shared__ int s_last;
-  if constexpr (LN) {
-    ln_prologue<kLmNW * 64>(ln.h, ln.x, nullptr, ln.gamma, ln.beta, ln.eps, y_lds, red);
-  } else {
-    for (int i = threadIdx.x; i < kHidden / 8; i += blockDim.x)
-      reinterpret_cast<uint4*>(y_lds)[i] = reinterpret_cast<const uint4*>(yin)[i];
-  }
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane & 31, rsel = lane >> 5;
-  uint4 xr[RS::kC];
-#pragma unroll
-  for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(y_lds)[sub + 32 * c];
-
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
   const int r_begin = blockIdx.x * rows_per_block;
   const int r_end = min(vocab, r_begin + rows_per_block);
-  unsigned long long mine = 0;
-  for (int base = r_begin; base < r_end; base += kLmRowsIter) {
+
+  auto load = [&](int base, uint4 (&wr)[kLmU][RS::kC]) {
     const int row0 = base + wave * 2 * kLmU + rsel;
-    uint4 wr[kLmU][RS::kC];
 #pragma unroll
     for (int u = 0; u < kLmU; ++u) {
       const int row = row0 + 2 * u;
@@ -272,17 +347,44 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
         if (row < r_end) wr[u][c] = ld_stream(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + 32 * c);
       }
     }
+  };
+  uint4 cur[kLmU][RS::kC];
+  load(r_begin, cur);
+
+  if constexpr (LN) {
+    ln_prologue<kLmNW * 64>(ln.h, ln.x, nullptr, ln.gamma, ln.beta, ln.eps, y_lds, red);
+  } else {
+    for (int i = threadIdx.x; i < kHidden / 8; i += blockDim.x)
+      reinterpret_cast<uint4*>(y_lds)[i] = reinterpret_cast<const uint4*>(yin)[i];
+  }
+  __syncthreads();
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(y_lds)[sub + 32 * c];
+
+  unsigned long long mine = 0;
+  for (int base = r_begin; base < r_end; base += kLmRowsIter) {
+    uint4 next[kLmU][RS::kC];
+    const bool more = base + kLmRowsIter < r_end;
+    if (more) load(base + kLmRowsIter, next);
+    const int row0 = base + wave * 2 * kLmU + rsel;
 #pragma unroll
     for (int u = 0; u < kLmU; ++u) {
       const int row = row0 + 2 * u;
       float acc = 0.f;
 #pragma unroll
-      for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[u][c], xr[c], acc);
+      for (int c = 0; c < RS::kC; ++c) acc = dot8(cur[u][c], xr[c], acc);
       acc = group_sum<32>(acc);
       if (sub == 0 && row < r_end && !suppress[row]) {
-        const unsigned long long s = pack_score(round_h(acc), row);
-        mine = s > mine ? s : mine;
+        const unsigned long long sc = pack_score(round_h(acc), row);
+        mine = sc > mine ? sc : mine;
       }
+    }
+    if (more) {
+#pragma unroll
+      for (int u = 0; u < kLmU; ++u)
+#pragma unroll
+        for (int c = 0; c < RS::kC; ++c) cur[u][c] = next[u][c];
     }
   }
   if (sub == 0) block_best[wave * 2 + rsel] = mine;
@@ -292,20 +394,6 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
 #pragma unroll
     for (int i = 0; i < kLmNW * 2; ++i) m = block_best[i] > m ? block_best[i] : m;
     if (m) atomicMax(best, m);
-    if constexpr (FIN) {
-      __threadfence();
-      const uint32_t prev = atomicAdd(fin.counter, 1u);
-      __threadfence();
-      s_last = (prev == gridDim.x - 1);
-    }
-  }
-  if constexpr (FIN) {
-    __syncthreads();
-    if (s_last && threadIdx.x == 0) {
-      __threadfence();
-      finalize_token(best, fin);
-      __hip_atomic_store(fin.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
   }
 }
 
@@ -326,10 +414,10 @@ __global__ void argmax_finalize_kernel(unsigned long long* best, FinArgs fin) { 
 // Split-K single-query attention (flash-decoding; reference decode_attention_split_kernel,
 // whisper_kernels.cu:102-189). Block (split, head) covers split_keys keys. A key row is 64 fp16 =
 // 8 lanes x 16 bytes, so one wave scores 8 keys per pass and a 256-thread block 32 keys. Scores,
-// max and exp-sum stay in fp32; the block writes its (m, l, acc[64]) partial. Self mode reads
+// max and exp-sum stay in fp32; the block writes its (m, l, acc[64]) partial and a second launch
+// merges them (reference decode_attention_combine_kernel, :191-213). Self mode reads
 // len = state[0] + 1 from device memory and the block owning row pos writes k_new/v_new into the
-// cache while using the new row directly. FUSED: the last block of each head (per-head arrival
-// counter) merges the partials and writes the fp16 output, so no separate combine launch is needed.
+// cache while using the new row directly.
 // ------------------------------------------------------------------------------------------
 struct AttnArgs {
   const _Float16* q;
@@ -344,46 +432,28 @@ struct AttnArgs {
   float* part_m;
   float* part_l;
   float* part_acc;
-  uint32_t* counters;
   _Float16* out;
 };
 
-__device__ __forceinline__ void combine_head(const AttnArgs& a, int head, int nsplit, int active, int d) {
-  const float* pm = a.part_m + head * nsplit;
-  const float* pl = a.part_l + head * nsplit;
-  const float* pa = a.part_acc + static_cast<size_t>(head) * nsplit * kHeadDim;
-  float m = -INFINITY;
-  for (int s = 0; s < active; ++s) m = fmaxf(m, pm[s]);
-  float num = 0.f, den = 0.f;
-  for (int s = 0; s < active; ++s) {
-    if (pl[s] > 0.f) {
-      const float wgt = __expf(pm[s] - m);
-      num = fmaf(pa[s * kHeadDim + d], wgt, num);
-      den = fmaf(pl[s], wgt, den);
-    }
-  }
-  a.out[head * kHeadDim + d] = f2h(num / den);
+__device__ __forceinline__ int attn_pos(const AttnArgs& a) {
+  if (!a.len_state) return -1;
+  const int64_t p = a.len_state[0];
+  return static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
 }
 
-template <bool FUSED>
+template <int MAXP>
 __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
-  __shared__ float scores[256];
-  __shared__ float red[4];
-  __shared__ float pacc[4][kHeadDim];
-  __shared__ int s_last;
+  __shared__ float wm[4], wl[4];
+  __shared__ float wacc[4][kHeadDim];
   const int split = blockIdx.x, head = blockIdx.y, nsplit = gridDim.x;
   const int slot = head * nsplit + split;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int pos = -1;
-  if (a.len_state) {
-    const int64_t p = a.len_state[0];
-    pos = static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
-  }
+  const int pos = attn_pos(a);
   const int len = a.len_state ? pos + 1 : a.max_len;
   const int begin = split * a.split_keys;
   const int n = min(a.split_keys, len - begin);
   if (n <= 0) {
-    if (!FUSED && tid == 0) {
+    if (tid == 0) {
       a.part_m[slot] = -INFINITY;
       a.part_l[slot] = 0.f;
     }
@@ -394,56 +464,208 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   _Float16* vh = a.v + hoff;
   const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + head * kHeadDim) : nullptr;
   const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + head * kHeadDim) : nullptr;
-  if (kn && pos >= begin && pos < begin + n && tid < 8) {
-    reinterpret_cast<uint4*>(kh + static_cast<size_t>(pos) * kHeadDim)[tid] = kn[tid];
-    reinterpret_cast<uint4*>(vh + static_cast<size_t>(pos) * kHeadDim)[tid] = vn[tid];
+  if (kn && pos >= begin && pos < begin + n && tid < 16) {
+    if (tid < 8)
+      reinterpret_cast<uint4*>(kh + static_cast<size_t>(pos) * kHeadDim)[tid] = kn[tid];
+    else
+      reinterpret_cast<uint4*>(vh + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = vn[tid - 8];
+  }
+  const int ks = lane >> 3, c = lane & 7;
+  const uint4 qc = reinterpret_cast<const uint4*>(a.q + head * kHeadDim)[c];
+  // keys dealt to the 4 waves in equal multiples of 8; all K and V chunks requested up front
+  const int per_wave = ((n + 31) / 32) * 8;
+  const int w0 = begin + wave * per_wave;
+  const int w1 = min(w0 + per_wave, begin + n);
+  uint4 kr[MAXP], vr[MAXP];
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    const int j = w0 + p * 8 + ks;
+    kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
+    if (j < w1) {
+      const bool fresh = kn && j == pos;
+      kr[p] = fresh ? kn[c] : reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim)[c];
+      vr[p] = fresh ? vn[c] : reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
+    }
+  }
+  float sc[MAXP];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    sc[p] = group_sum<8>(dot8(kr[p], qc, 0.f)) * a.scale;
+    if (w0 + p * 8 + ks >= w1) sc[p] = -INFINITY;
+    mx = fmaxf(mx, sc[p]);
+  }
+  mx = group_max<64>(mx);
+  float acc[8], psum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const float pj = __expf(sc[p] - mx);
+      psum += pj;
+      const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
+        acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
+      }
+    }
+  }
+  psum += __shfl_xor(psum, 8, kWave);
+  psum += __shfl_xor(psum, 16, kWave);
+  psum += __shfl_xor(psum, 32, kWave);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    acc[t] += __shfl_xor(acc[t], 8, kWave);
+    acc[t] += __shfl_xor(acc[t], 16, kWave);
+    acc[t] += __shfl_xor(acc[t], 32, kWave);
+  }
+  if (lane == 0) {
+    wm[wave] = mx;
+    wl[wave] = psum;
+  }
+  if (ks == 0) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) wacc[wave][c * 8 + t] = acc[t];
+  }
+  __syncthreads();
+  if (tid < kHeadDim) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) m = fmaxf(m, wm[w]);
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (wl[w] > 0.f) {
+        const float wgt = __expf(wm[w] - m);
+        l = fmaf(wl[w], wgt, l);
+        o = fmaf(wacc[w][tid], wgt, o);
+      }
+    }
+    a.part_acc[static_cast<size_t>(slot) * kHeadDim + tid] = o;
+    if (tid == 0) {
+      a.part_m[slot] = m;
+      a.part_l[slot] = l;
+    }
+  }
+}
+
+int launch_attn_split(const AttnArgs& a, int nsplit, int heads, hipStream_t s) {
+  const dim3 grid(nsplit, heads);
+  if (a.split_keys <= 64)
+    hipLaunchKernelGGL(attn_split_kernel<2>, grid, dim3(256), 0, s, a);
+  else if (a.split_keys <= 128)
+    hipLaunchKernelGGL(attn_split_kernel<4>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(attn_split_kernel<8>, grid, dim3(256), 0, s, a);
+  return fw_check_launch("attention split");
+}
+
+// Merges the split results of one head; splits with l == 0 are empty and skipped.
+__global__ void __launch_bounds__(64) attn_combine_kernel(AttnArgs a, int nsplit) {
+  const int head = blockIdx.x, d = threadIdx.x;
+  const float* pm = a.part_m + head * nsplit;
+  const float* pl = a.part_l + head * nsplit;
+  const float* pa = a.part_acc + static_cast<size_t>(head) * nsplit * kHeadDim;
+  float m = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) m = fmaxf(m, pm[s]);
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    if (pl[s] > 0.f) {
+      const float wgt = __expf(pm[s] - m);
+      num = fmaf(pa[s * kHeadDim + d], wgt, num);
+      den = fmaf(pl[s], wgt, den);
+    }
+  }
+  a.out[head * kHeadDim + d] = f2h(num / den);
+}
+
+// ------------------------------------------------------------------------------------------
+// Single-launch decode attention: one 1024-thread block (16 waves) per head covers every key, so
+// the split partials never leave the CU (no workspace, no cross-block synchronisation). Keys are
+// dealt to the 16 waves in equal multiples of 8; each wave issues all of its K and V loads at once
+// (up to 12 passes x 8 keys = 96 keys, 24 x 16 B per lane in flight), then scores (fp32, scale after
+// the dot), takes its local max/exp-sum/P.V, and the 16 wave partials are merged through LDS
+// exactly like the split-K combine. Longer sequences run in rounds of 1536 keys with an online
+// merge per wave. Self mode: the block writes k_new/v_new into row pos and uses them for key pos.
+// ------------------------------------------------------------------------------------------
+constexpr int kHeadWaves = 16, kHeadMaxPass = 12;
+constexpr int kHeadRoundKeys = kHeadWaves * kHeadMaxPass * 8;
+
+__global__ void __launch_bounds__(kHeadWaves * 64) attn_head_kernel(AttnArgs a) {
+  __shared__ float wm[kHeadWaves], wl[kHeadWaves];
+  __shared__ float wacc[kHeadWaves][kHeadDim];
+  const int head = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = attn_pos(a);
+  const int len = a.len_state ? pos + 1 : a.max_len;
+  const size_t hoff = static_cast<size_t>(head) * a.max_len * kHeadDim;
+  _Float16* kh = a.k + hoff;
+  _Float16* vh = a.v + hoff;
+  const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + head * kHeadDim) : nullptr;
+  const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + head * kHeadDim) : nullptr;
+  if (kn && tid < 16) {
+    if (tid < 8)
+      reinterpret_cast<uint4*>(kh + static_cast<size_t>(pos) * kHeadDim)[tid] = kn[tid];
+    else
+      reinterpret_cast<uint4*>(vh + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = vn[tid - 8];
   }
   const int ks = lane >> 3, c = lane & 7;
   const uint4 qc = reinterpret_cast<const uint4*>(a.q + head * kHeadDim)[c];
 
-  for (int i0 = 0; i0 < n; i0 += 32) {
-    const int i = i0 + wave * 8 + ks;
-    float s = 0.f;
-    if (i < n) {
-      const int j = begin + i;
-      const uint4* kp = (kn && j == pos) ? kn : reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim);
-      s = dot8(kp[c], qc, 0.f);
-    }
-    s = group_sum<8>(s);
-    if (c == 0 && i < n) scores[i] = s * a.scale;
-  }
-  __syncthreads();
-
-  const float sv = tid < n ? scores[tid] : -INFINITY;
-  float m = group_max<64>(sv);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  float e = 0.f;
-  if (tid < n) {
-    e = __expf(sv - m);
-    scores[tid] = e;
-  }
-  const float l = block_sum<256>(e, red);
-
-  float acc[8];
+  float m_run = -INFINITY, l_run = 0.f, acc[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = 0.f;
-  for (int i0 = 0; i0 < n; i0 += 32) {
-    const int i = i0 + wave * 8 + ks;
-    if (i < n) {
-      const int j = begin + i;
-      const uint4* vp = (vn && j == pos) ? vn : reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim);
-      const uint4 vv = vp[c];
-      const float p = scores[i];
-      const h2v* v2 = reinterpret_cast<const h2v*>(&vv);
+  for (int base = 0; base < len; base += kHeadRoundKeys) {
+    const int n_round = min(kHeadRoundKeys, len - base);
+    const int per_wave = ((n_round + kHeadWaves * 8 - 1) / (kHeadWaves * 8)) * 8;  // multiple of 8
+    const int w0 = base + wave * per_wave;
+    const int w1 = min(w0 + per_wave, base + n_round);
+    uint4 kr[kHeadMaxPass], vr[kHeadMaxPass];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[2 * t] = fmaf(p, h2f(v2[t].x), acc[2 * t]);
-        acc[2 * t + 1] = fmaf(p, h2f(v2[t].y), acc[2 * t + 1]);
+    for (int p = 0; p < kHeadMaxPass; ++p) {
+      const int j = w0 + p * 8 + ks;
+      kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
+      if (j < w1) {
+        const bool fresh = kn && j == pos;
+        kr[p] = fresh ? kn[c] : reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim)[c];
+        vr[p] = fresh ? vn[c] : reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
       }
     }
+    float s[kHeadMaxPass];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < kHeadMaxPass; ++p) {
+      const int j = w0 + p * 8 + ks;
+      s[p] = group_sum<8>(dot8(kr[p], qc, 0.f)) * a.scale;
+      if (j >= w1) s[p] = -INFINITY;
+      mx = fmaxf(mx, s[p]);
+    }
+    mx = group_max<64>(mx);
+    if (mx == -INFINITY) continue;  // this wave has no keys in this round (wave-uniform)
+    const float m_new = fmaxf(m_run, mx);
+    const float corr = __expf(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] *= corr;
+#pragma unroll
+    for (int p = 0; p < kHeadMaxPass; ++p) {
+      const float pj = __expf(s[p] - m_new);  // 0 for masked keys
+      psum += pj;
+      const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
+        acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
+      }
+    }
+    // psum is replicated over the 8 lanes of a key group: sum one lane per group
+    psum += __shfl_xor(psum, 8, kWave);
+    psum += __shfl_xor(psum, 16, kWave);
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * corr + psum;
+    m_run = m_new;
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
@@ -451,38 +673,30 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
     acc[t] += __shfl_xor(acc[t], 16, kWave);
     acc[t] += __shfl_xor(acc[t], 32, kWave);
   }
+  if (lane == 0) {
+    wm[wave] = m_run;
+    wl[wave] = l_run;
+  }
   if (ks == 0) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) pacc[wave][c * 8 + t] = acc[t];
+    for (int t = 0; t < 8; ++t) wacc[wave][c * 8 + t] = acc[t];
   }
   __syncthreads();
-  if (tid < kHeadDim)
-    a.part_acc[static_cast<size_t>(slot) * kHeadDim + tid] = pacc[0][tid] + pacc[1][tid] + pacc[2][tid] + pacc[3][tid];
-  if (tid == 0) {
-    a.part_m[slot] = m;
-    a.part_l[slot] = l;
-  }
-  if constexpr (FUSED) {
-    const int active = (len + a.split_keys - 1) / a.split_keys;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prev = atomicAdd(a.counters + head, 1u);
-      __threadfence();
-      s_last = (prev == static_cast<uint32_t>(active - 1));
+  if (tid < kHeadDim) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kHeadWaves; ++w) m = fmaxf(m, wm[w]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < kHeadWaves; ++w) {
+      if (wl[w] > 0.f) {
+        const float wgt = __expf(wm[w] - m);
+        num = fmaf(wacc[w][tid], wgt, num);
+        den = fmaf(wl[w], wgt, den);
+      }
     }
-    __syncthreads();
-    if (s_last) {
-      __threadfence();
-      if (tid < kHeadDim) combine_head(a, head, nsplit, active, tid);
-      if (tid == 0) __hip_atomic_store(a.counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    a.out[head * kHeadDim + tid] = f2h(num / den);
   }
-}
-
-// Reference decode_attention_combine_kernel (whisper_kernels.cu:191-213): one block per head.
-__global__ void __launch_bounds__(64) attn_combine_kernel(AttnArgs a, int nsplit) {
-  combine_head(a, blockIdx.x, nsplit, nsplit, threadIdx.x);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -505,18 +719,17 @@ extern "C" int fw_lm_head_argmax(const void* y, const void* w, const uint8_t* su
   FW_REQUIRE(aligned16(y) && aligned16(w), "lm_head_argmax: y and w must be 16-byte aligned");
   int rpb = 0;
   const int grid = lm_head_grid(vocab, &rpb);
-  FinArgs fin{};
-  hipLaunchKernelGGL((lm_head_kernel<false, false>), dim3(grid), dim3(kLmNW * 64), 0, stream,
-                     static_cast<const _Float16*>(y), LnArgs{}, static_cast<const _Float16*>(w), suppress, vocab, rpb,
-                     reinterpret_cast<unsigned long long*>(best), fin);
+  hipLaunchKernelGGL(lm_head_kernel<false>, dim3(grid), dim3(kLmNW * 64), 0, stream, static_cast<const _Float16*>(y),
+                     LnArgs{}, static_cast<const _Float16*>(w), suppress, vocab, rpb,
+                     reinterpret_cast<unsigned long long*>(best));
   return fw_check_launch("lm_head_argmax");
 }
 
 extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void* gamma, const void* beta, float eps,
                                        const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
-                                       int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, uint32_t* counter,
+                                       int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,
                                        hipStream_t stream) {
-  FW_REQUIRE(h && gamma && beta && w && suppress && best && tokens && state && cur && counter,
+  FW_REQUIRE(h && gamma && beta && w && suppress && best && tokens && state && cur,
              "lm_head_argmax_fused: null pointer");
   FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
   FW_REQUIRE(vocab > 0 && max_pos > 0, "vocab and max_pos must be positive");
@@ -526,71 +739,69 @@ extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void*
   LnArgs ln{static_cast<const _Float16*>(h), static_cast<const _Float16*>(x), nullptr,
             static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta), eps, nullptr, nullptr,
             nullptr, nullptr, 0, 0};
-  FinArgs fin{tokens, state, cur, max_pos, counter};
-  hipLaunchKernelGGL((lm_head_kernel<true, true>), dim3(grid), dim3(kLmNW * 64), 0, stream, nullptr, ln,
-                     static_cast<const _Float16*>(w), suppress, vocab, rpb, reinterpret_cast<unsigned long long*>(best),
+  hipLaunchKernelGGL(lm_head_kernel<true>, dim3(grid), dim3(kLmNW * 64), 0, stream, nullptr, ln,
+                     static_cast<const _Float16*>(w), suppress, vocab, rpb, reinterpret_cast<unsigned long long*>(best));
+  int rc = fw_check_launch("lm_head_argmax_fused");
+  if (rc != FW_OK) return rc;
+  FinArgs fin{tokens, state, cur, max_pos};
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<unsigned long long*>(best),
                      fin);
-  return fw_check_launch("lm_head_argmax_fused");
+  return fw_check_launch("lm_head_argmax_fused finalize");
 }
 
 extern "C" int fw_argmax_finalize(uint64_t* best, int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,
                                   hipStream_t stream) {
   FW_REQUIRE(best && tokens && state && cur, "argmax_finalize: null pointer");
   FW_REQUIRE(max_pos > 0, "max_pos must be positive");
-  FinArgs fin{tokens, state, cur, max_pos, nullptr};
+  FinArgs fin{tokens, state, cur, max_pos};
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<unsigned long long*>(best),
                      fin);
   return fw_check_launch("argmax_finalize");
 }
 
 static int attention_common(const void* q, void* k, void* v, void* out, const int64_t* len_state, const void* k_new,
-                            const void* v_new, int heads, int max_len, int split_keys, float* part_m, float* part_l,
-                            float* part_acc, int64_t ws_slots, AttnArgs* a, int* nsplit) {
-  FW_REQUIRE(q && k && v && out && part_m && part_l && part_acc, "decode_attention: null pointer");
+                            const void* v_new, int heads, int max_len, AttnArgs* a) {
+  FW_REQUIRE(q && k && v, "decode_attention: null pointer");
   FW_REQUIRE(heads > 0 && max_len > 0, "decode_attention: heads and max_len must be positive");
   FW_REQUIRE((k_new != nullptr) == (v_new != nullptr) && (k_new != nullptr) == (len_state != nullptr),
              "len_state, k_new and v_new must be given together");
-  FW_REQUIRE(split_keys >= 32 && split_keys <= 256 && split_keys % 32 == 0,
-             "split_keys must be a multiple of 32 in [32, 256]");
   FW_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && (!k_new || (aligned16(k_new) && aligned16(v_new))),
              "decode_attention: q, k, v, k_new, v_new must be 16-byte aligned");
-  *nsplit = (max_len + split_keys - 1) / split_keys;
-  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * *nsplit, "workspace too small for %d splits", *nsplit);
   *a = AttnArgs{static_cast<const _Float16*>(q), static_cast<_Float16*>(k), static_cast<_Float16*>(v),
                 static_cast<const _Float16*>(k_new), static_cast<const _Float16*>(v_new), len_state, max_len,
-                split_keys, 0.f, part_m, part_l, part_acc, nullptr, static_cast<_Float16*>(out)};
+                kSplitKeys, 0.f, nullptr, nullptr, nullptr, static_cast<_Float16*>(out)};
   return FW_OK;
 }
 
 extern "C" int fw_decode_attention(const void* q, void* k, void* v, void* out, const int64_t* len_state,
                                    const void* k_new, const void* v_new, int heads, int max_len, float* part_m,
                                    float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream) {
+  FW_REQUIRE(out, "decode_attention: null out");
   AttnArgs a;
-  int nsplit = 0;
-  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, kSplitKeys, part_m, part_l,
-                            part_acc, ws_slots, &a, &nsplit);
+  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, &a);
   if (rc != FW_OK) return rc;
+  FW_REQUIRE(part_m && part_l && part_acc, "decode_attention: null workspace");
+  const int nsplit = (max_len + kSplitKeys - 1) / kSplitKeys;
+  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * nsplit, "workspace too small for %d splits", nsplit);
   a.scale = scale;
-  hipLaunchKernelGGL(attn_split_kernel<false>, dim3(nsplit, heads), dim3(256), 0, stream, a);
-  rc = fw_check_launch("decode_attention split");
+  a.part_m = part_m;
+  a.part_l = part_l;
+  a.part_acc = part_acc;
+  rc = launch_attn_split(a, nsplit, heads, stream);
   if (rc != FW_OK) return rc;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(heads), dim3(kHeadDim), 0, stream, a, nsplit);
   return fw_check_launch("decode_attention combine");
 }
 
 extern "C" int fw_decode_attention_fused(const void* q, void* k, void* v, void* out, const int64_t* len_state,
-                                         const void* k_new, const void* v_new, int heads, int max_len, int split_keys,
-                                         float* part_m, float* part_l, float* part_acc, uint32_t* counters,
-                                         int64_t ws_slots, float scale, hipStream_t stream) {
+                                         const void* k_new, const void* v_new, int heads, int max_len, float scale,
+                                         hipStream_t stream) {
+  FW_REQUIRE(out, "decode_attention_fused: null out");
   AttnArgs a;
-  int nsplit = 0;
-  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, split_keys, part_m, part_l,
-                            part_acc, ws_slots, &a, &nsplit);
+  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, &a);
   if (rc != FW_OK) return rc;
-  FW_REQUIRE(counters, "decode_attention_fused: null counters");
   a.scale = scale;
-  a.counters = counters;
-  hipLaunchKernelGGL(attn_split_kernel<true>, dim3(nsplit, heads), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(attn_head_kernel, dim3(heads), dim3(kHeadWaves * 64), 0, stream, a);
   return fw_check_launch("decode_attention_fused");
 }
 
@@ -628,16 +839,17 @@ extern "C" int fw_gemv(const void* x, const void* w, const void* bias, void* out
   const auto* bp = static_cast<const _Float16*>(bias);
   auto* op = static_cast<_Float16*>(out);
   const LnArgs ln{};
+  const CombineArgs cb{};
   if (k_in == kHidden) {
     if (act == FW_ACT_GELU)
-      dispatch_gemv_1280<false, FW_ACT_GELU>(xp, ln, wp, bp, op, n_out, stream);
+      dispatch_gemv_1280<kModePlain, FW_ACT_GELU>(xp, ln, cb, wp, bp, op, n_out, stream);
     else
-      dispatch_gemv_1280<false, FW_ACT_NONE>(xp, ln, wp, bp, op, n_out, stream);
+      dispatch_gemv_1280<kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
   } else {
     if (act == FW_ACT_GELU)
-      launch_gemv<4 * kHidden, 4, 1, false, FW_ACT_GELU>(xp, ln, wp, bp, op, n_out, stream);
+      launch_gemv<4 * kHidden, 4, 1, kModePlain, FW_ACT_GELU>(xp, ln, cb, wp, bp, op, n_out, stream);
     else
-      launch_gemv<4 * kHidden, 4, 1, false, FW_ACT_NONE>(xp, ln, wp, bp, op, n_out, stream);
+      launch_gemv<4 * kHidden, 4, 1, kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
   }
   return fw_check_launch("gemv");
 }
@@ -663,9 +875,48 @@ extern "C" int fw_ln_gemv(const void* h, const void* x, void* h_out, const void*
   const auto* wp = static_cast<const _Float16*>(w);
   const auto* bp = static_cast<const _Float16*>(bias);
   auto* op = static_cast<_Float16*>(out);
+  const CombineArgs cb{};
   if (act == FW_ACT_GELU)
-    dispatch_gemv_1280<true, FW_ACT_GELU>(nullptr, ln, wp, bp, op, n_out, stream);
+    dispatch_gemv_1280<kModeLn, FW_ACT_GELU>(nullptr, ln, cb, wp, bp, op, n_out, stream);
   else
-    dispatch_gemv_1280<true, FW_ACT_NONE>(nullptr, ln, wp, bp, op, n_out, stream);
+    dispatch_gemv_1280<kModeLn, FW_ACT_NONE>(nullptr, ln, cb, wp, bp, op, n_out, stream);
   return fw_check_launch("ln_gemv");
+}
+
+extern "C" int fw_attention_split(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
+                                  const void* v_new, int heads, int max_len, int split_keys, float* part_m,
+                                  float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream) {
+  AttnArgs a;
+  int rc = attention_common(q, k, v, nullptr, len_state, k_new, v_new, heads, max_len, &a);
+  if (rc != FW_OK) return rc;
+  FW_REQUIRE(part_m && part_l && part_acc, "attention_split: null workspace");
+  FW_REQUIRE(split_keys >= 8 && split_keys <= 256 && split_keys % 8 == 0,
+             "split_keys must be a multiple of 8 in [8, 256]");
+  const int nsplit = (max_len + split_keys - 1) / split_keys;
+  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * nsplit, "workspace too small for %d splits", nsplit);
+  a.out = nullptr;
+  a.split_keys = split_keys;
+  a.scale = scale;
+  a.part_m = part_m;
+  a.part_l = part_l;
+  a.part_acc = part_acc;
+  return launch_attn_split(a, nsplit, heads, stream);
+}
+
+extern "C" int fw_attn_out_gemv(const float* part_m, const float* part_l, const float* part_acc, int64_t ws_slots,
+                                const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
+                                const void* bias, void* out, int n_out, hipStream_t stream) {
+  FW_REQUIRE(part_m && part_l && part_acc && w && out, "attn_out_gemv: null pointer");
+  FW_REQUIRE(heads * kHeadDim == kHidden, "attn_out_gemv: heads * 64 must be %d", kHidden);
+  FW_REQUIRE(max_len > 0 && split_keys >= 8 && n_out > 0, "attn_out_gemv: bad sizes");
+  FW_REQUIRE(aligned16(w), "attn_out_gemv: w must be 16-byte aligned");
+  const int nsplit = (max_len + split_keys - 1) / split_keys;
+  FW_REQUIRE(nsplit <= kMaxCombineSplits && heads <= kMaxCombineHeads,
+             "attn_out_gemv: at most %d splits (got %d) and %d heads", kMaxCombineSplits, nsplit, kMaxCombineHeads);
+  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * nsplit, "attn_out_gemv: workspace too small");
+  const CombineArgs cb{part_m, part_l, part_acc, len_state, max_len, split_keys, nsplit, heads};
+  launch_gemv<kHidden, 4, 1, kModeCombine, FW_ACT_NONE>(nullptr, LnArgs{}, cb, static_cast<const _Float16*>(w),
+                                                         static_cast<const _Float16*>(bias), static_cast<_Float16*>(out),
+                                                         n_out, stream);
+  return fw_check_launch("attn_out_gemv");
 }

@@ -9,15 +9,20 @@ namespace fw {
 namespace {
 
 // ------------------------------------------------------------------------------------------
-// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 32, 4 waves in a 2 x 2
-// arrangement, each wave (BM/2) x 64 built from v_mfma_f32_32x32x16_f16 tiles. A and W tiles are
-// staged through double-buffered LDS (rows padded by 8 halves); the next K slice is fetched into
-// registers while the current one feeds the MFMAs.
+// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 64, 4 waves in a 2 x 2
+// arrangement, each wave (BM/2) x 64 built from v_mfma_f32_32x32x16_f16 tiles.
+//  - LDS: one [rows][64] fp16 tile per operand and stage, 8 x 16-byte chunks per row, chunk c of
+//    row r stored in slot c ^ (r & 7), so the 8 rows a quarter-wave reads for one MFMA operand hit
+//    8 different bank groups (conflict-free ds_read_b128).
+//  - Pipeline: two LDS buffers and two register staging sets. Stage kt + 2 is requested from global
+//    memory while stage kt feeds the MFMAs, so each load has two stages of MFMA work to arrive in.
+//  - Tile order: hardware deals blocks round-robin over the 8 XCDs; the block id is remapped so each
+//    XCD works on a contiguous run of row-major tiles that share A row panels in its L2.
 // MFMA 32x32x16 f16 operand layout (lane l, g = l / 32):
 //   A: lane holds A[l % 32][8g .. 8g + 7]      B: lane holds B[8g .. 8g + 7][l % 32]
 //   C: acc[r] = C[8 (r / 4) + 4 g + (r % 4)][l % 32], r = 0 .. 15
 // ------------------------------------------------------------------------------------------
-constexpr int kBN = 128, kBK = 32, kLdsStride = kBK + 8;
+constexpr int kBN = 128, kBK = 64;
 constexpr int kEpiCrossKV = 100;  // internal epilogue: scatter into [layers, 2, heads, t, 64]
 
 struct GemmArgs {
@@ -67,19 +72,208 @@ __device__ __forceinline__ float epilogue_value(int epi, float acc, float b, con
   return v;
 }
 
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+// Workgroup barrier for LDS hand-off only: waits for this wave's LDS traffic, not for its global
+// loads (__syncthreads would also drain the prefetches that are meant to stay in flight).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int BM>
+struct GemmStage {
+  static constexpr int kA = BM * 8 / 256;   // 16-byte A chunks per thread per stage
+  static constexpr int kB = kBN * 8 / 256;  // 16-byte B chunks per thread per stage
+  u32x4 a[kA];
+  u32x4 b[kB];
+};
+
+template <int BM, bool CONV>
+__device__ __forceinline__ void gemm_load(const GemmArgs& g, int m0, int n0, int k0, int tid, GemmStage<BM>& st) {
+#pragma unroll
+  for (int i = 0; i < GemmStage<BM>::kA; ++i) {
+    const int c = tid + 256 * i;
+    const int row = c >> 3, kc = (c & 7) * 8;
+    const int gm = m0 + row;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (gm < g.m) {
+      if constexpr (CONV) {
+        const int kk = k0 + kc;
+        const int tap = kk / g.c_in, ch = kk - tap * g.c_in;
+        const int src = gm * g.conv_stride + tap - 1;
+        if (src >= 0 && src < g.t_in) v = *reinterpret_cast<const u32x4*>(g.a + static_cast<size_t>(src) * g.c_in + ch);
+      } else {
+        v = *reinterpret_cast<const u32x4*>(g.a + static_cast<size_t>(gm) * g.lda + k0 + kc);
+      }
+    }
+    st.a[i] = v;
+  }
+#pragma unroll
+  for (int i = 0; i < GemmStage<BM>::kB; ++i) {
+    const int c = tid + 256 * i;
+    const int row = c >> 3, kc = (c & 7) * 8;
+    st.b[i] = *reinterpret_cast<const u32x4*>(g.w + static_cast<size_t>(n0 + row) * g.ldw + k0 + kc);
+  }
+}
+
+template <int BM>
+__device__ __forceinline__ void gemm_store(u32x4* As, u32x4* Bs, int tid, const GemmStage<BM>& st) {
+#pragma unroll
+  for (int i = 0; i < GemmStage<BM>::kA; ++i) {
+    const int c = tid + 256 * i;
+    As[swz(c >> 3, c & 7)] = st.a[i];
+  }
+#pragma unroll
+  for (int i = 0; i < GemmStage<BM>::kB; ++i) {
+    const int c = tid + 256 * i;
+    Bs[swz(c >> 3, c & 7)] = st.b[i];
+  }
+}
+
+template <int kTM, int kTN>
+__device__ __forceinline__ void gemm_mma(const u32x4* As, const u32x4* Bs, int wm, int wn, int lr, int lg,
+                                         f16v (&acc)[kTM][kTN]) {
+#pragma unroll
+  for (int s = 0; s < kBK / 16; ++s) {
+    h8v av[kTM], bv[kTN];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) av[i] = __builtin_bit_cast(h8v, As[swz(wm + 32 * i + lr, 2 * s + lg)]);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) bv[j] = __builtin_bit_cast(h8v, Bs[swz(wn + 32 * j + lr, 2 * s + lg)]);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// ---- direct-to-LDS pipeline (plain GEMMs) ------------------------------------------------------
+// global_load_lds_dwordx4 writes one 16-byte chunk per lane straight into LDS at M0 + 16 * lane, so
+// a wave instruction fills 1 KB = 8 rows of a 64-wide k slice. The XOR swizzle is applied on the
+// source side: lane l fills LDS row r0 + l / 8, slot l % 8, so it fetches chunk (l % 8) ^ (row & 7).
+// The copies are issued from inline assembly: the compiler then does not guard every LDS read with
+// a wait for all outstanding copies, and the pipeline depth is set by the explicit vmcnt waits.
+constexpr int kDmaStages = 4;  // LDS ring depth: kDmaStages - 1 stages in flight
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int BM>
+__device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
+                                          uint32_t lds_stage) {
+  constexpr int kAInstr = BM / 8 / 4;    // wave instructions per A tile (8 rows each), per wave
+  constexpr int kBInstr = kBN / 8 / 4;
+  const int rsub = lane >> 3, slot = lane & 7;
+#pragma unroll
+  for (int i = 0; i < kAInstr; ++i) {
+    const int blk = wave * kAInstr + i;  // 8-row block of the tile
+    const int row = blk * 8 + rsub;
+    const int gm = min(m0 + row, g.m - 1);  // rows past m are computed and never stored
+    const int chunk = slot ^ (row & 7);
+    dma16(g.a + static_cast<size_t>(gm) * g.lda + k0 + chunk * 8,
+          __builtin_amdgcn_readfirstlane(lds_stage + blk * 1024));
+  }
+#pragma unroll
+  for (int i = 0; i < kBInstr; ++i) {
+    const int blk = wave * kBInstr + i;
+    const int row = blk * 8 + rsub;
+    const int chunk = slot ^ (row & 7);
+    dma16(g.w + static_cast<size_t>(n0 + row) * g.ldw + k0 + chunk * 8,
+          __builtin_amdgcn_readfirstlane(lds_stage + BM * 128 + blk * 1024));
+  }
+}
+
 template <int BM, int EPI>
+__global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
+  constexpr int kWM = BM / 2, kTM = kWM / 32, kTN = 2;
+  constexpr int kStageBytes = (BM + kBN) * 128;
+  constexpr int kPerStage = (BM / 8 / 4) + (kBN / 8 / 4);  // copies per thread per stage
+  __shared__ __align__(1024) u32x4 lds[kDmaStages * kStageBytes / 16];
+
+  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM, ntiles = ntn * ntm;
+  const int bid = blockIdx.x, full = (ntiles / 8) * 8;
+  const int tile = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+  const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * kBN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * kWM, wn = (wave & 1) * 64;
+  const int lr = lane & 31, lg = lane >> 5;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+
+  f16v acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int kt_n = g.k / kBK;
+#pragma unroll
+  for (int s = 0; s < kDmaStages - 1; ++s)
+    if (s < kt_n) dma_stage<BM>(g, m0, n0, s * kBK, wave, lane, lds0 + s * kStageBytes);
+  for (int kt = 0; kt < kt_n; ++kt) {
+    // this thread's copies of stage kt have landed once at most the later in-flight stages remain
+    const int ahead = min(kDmaStages - 2, kt_n - 1 - kt);
+    if (ahead >= 2) wait_vmcnt<2 * kPerStage>();
+    else if (ahead == 1) wait_vmcnt<kPerStage>();
+    else wait_vmcnt<0>();
+    barrier_only();  // stage kt visible to every wave; every wave is done with stage kt - 1
+    const int nxt = kt + kDmaStages - 1;
+    if (nxt < kt_n) dma_stage<BM>(g, m0, n0, nxt * kBK, wave, lane, lds0 + (nxt % kDmaStages) * kStageBytes);
+    const u32x4* As = lds + (kt % kDmaStages) * (kStageBytes / 16);
+    gemm_mma<kTM, kTN>(As, As + BM * 8, wm, wn, lr, lg, acc);
+  }
+
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int col = n0 + wn + 32 * j + lr;
+    const float b = g.bias ? h2f(g.bias[col]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
+        if (row < g.m) {
+          if constexpr (EPI == kEpiCrossKV) {
+            const int d = col & 63, lhk = col >> 6;
+            const size_t o = (static_cast<size_t>(lhk) * g.t_len + row) * 64 + d;
+            g.out[o] = f2h(acc[i][j][r] + b);
+          } else {
+            g.out[static_cast<size_t>(row) * g.ldo + col] = f2h(epilogue_value(EPI, acc[i][j][r], b, g, row, col));
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int EPI, bool CONV>
 __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
-  constexpr int kWM = BM / 2;          // wave tile rows
-  constexpr int kTM = kWM / 32;        // MFMA tiles per wave along M
-  constexpr int kTN = 2;               // MFMA tiles per wave along N (64 columns)
-  constexpr int kAChunks = BM * kBK / 8 / 256;  // 16-byte A chunks per thread per stage
-  constexpr int kBChunks = kBN * kBK / 8 / 256;
-  __shared__ __align__(16) _Float16 As[2][BM][kLdsStride];
-  __shared__ __align__(16) _Float16 Bs[2][kBN][kLdsStride];
+  constexpr int kWM = BM / 2;                // wave tile rows
+  constexpr int kTM = kWM / 32;              // MFMA tiles per wave along M
+  constexpr int kTN = 2;                     // MFMA tiles per wave along N (64 columns)
+  __shared__ __align__(16) u32x4 As0[BM * 8], As1[BM * 8];
+  __shared__ __align__(16) u32x4 Bs0[kBN * 8], Bs1[kBN * 8];
+
+  // XCD-aware tile order (bijective: the tail beyond a multiple of 8 keeps its id)
+  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM, ntiles = ntn * ntm;
+  const int bid = blockIdx.x, full = (ntiles / 8) * 8;
+  const int tile = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+  const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * kBN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave >> 1) * kWM, wn = (wave & 1) * 64;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
   const int lr = lane & 31, lg = lane >> 5;
 
   f16v acc[kTM][kTN];
@@ -90,70 +284,24 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  uint4 ra[kAChunks], rb[kBChunks];
-  auto load_global = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < kAChunks; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 2, kc = (c & 3) * 8;
-      const int gm = m0 + row;
-      ra[i] = make_uint4(0, 0, 0, 0);
-      if (gm < g.m) {
-        if (g.conv_stride) {
-          const int kk = k0 + kc;
-          const int tap = kk / g.c_in, ch = kk - tap * g.c_in;
-          const int src = gm * g.conv_stride + tap - 1;
-          if (src >= 0 && src < g.t_in)
-            ra[i] = *reinterpret_cast<const uint4*>(g.a + static_cast<size_t>(src) * g.c_in + ch);
-        } else {
-          ra[i] = *reinterpret_cast<const uint4*>(g.a + static_cast<size_t>(gm) * g.lda + k0 + kc);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kBChunks; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 2, kc = (c & 3) * 8;
-      rb[i] = *reinterpret_cast<const uint4*>(g.w + static_cast<size_t>(n0 + row) * g.ldw + k0 + kc);
-    }
-  };
-  auto store_lds = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < kAChunks; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(&As[buf][c >> 2][(c & 3) * 8]) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < kBChunks; ++i) {
-      const int c = tid + 256 * i;
-      *reinterpret_cast<uint4*>(&Bs[buf][c >> 2][(c & 3) * 8]) = rb[i];
-    }
-  };
-
+  GemmStage<BM> st0, st1;
   const int kt_n = g.k / kBK;
-  load_global(0);
-  store_lds(0);
+  gemm_load<BM, CONV>(g, m0, n0, 0, tid, st0);
+  gemm_store<BM>(As0, Bs0, tid, st0);
+  if (kt_n > 1) gemm_load<BM, CONV>(g, m0, n0, kBK, tid, st1);
   __syncthreads();
-  for (int kt = 0; kt < kt_n; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < kt_n) load_global((kt + 1) * kBK);
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      h8v av[kTM], bv[kTN];
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-        av[i] = *reinterpret_cast<const h8v*>(&As[buf][wm + 32 * i + lr][16 * s + 8 * lg]);
-#pragma unroll
-      for (int j = 0; j < kTN; ++j)
-        bv[j] = *reinterpret_cast<const h8v*>(&Bs[buf][wn + 32 * j + lr][16 * s + 8 * lg]);
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < kt_n) store_lds(buf ^ 1);
-    __syncthreads();
+  for (int kt = 0; kt < kt_n; kt += 2) {
+    // stage kt in LDS buffer 0; stage kt + 1 arriving in st1
+    if (kt + 2 < kt_n) gemm_load<BM, CONV>(g, m0, n0, (kt + 2) * kBK, tid, st0);
+    gemm_mma<kTM, kTN>(As0, Bs0, wm, wn, lr, lg, acc);
+    if (kt + 1 < kt_n) gemm_store<BM>(As1, Bs1, tid, st1);
+    lds_barrier();
+    if (kt + 1 >= kt_n) break;
+    // stage kt + 1 in LDS buffer 1; stage kt + 2 arriving in st0
+    if (kt + 3 < kt_n) gemm_load<BM, CONV>(g, m0, n0, (kt + 3) * kBK, tid, st1);
+    gemm_mma<kTM, kTN>(As1, Bs1, wm, wn, lr, lg, acc);
+    if (kt + 2 < kt_n) gemm_store<BM>(As0, Bs0, tid, st0);
+    lds_barrier();
   }
 
 #pragma unroll
@@ -182,11 +330,26 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
 
 template <int BM>
 int launch_gemm_bm(const GemmArgs& g, int epi, hipStream_t s) {
-  const dim3 grid(g.n / kBN, (g.m + BM - 1) / BM);
+  const int tiles = (g.n / kBN) * ((g.m + BM - 1) / BM);
+  const dim3 grid(tiles);
+  if (g.conv_stride) {
+    switch (epi) {
+      case FW_EPI_BIAS: hipLaunchKernelGGL((gemm_kernel<BM, FW_EPI_BIAS, true>), grid, dim3(256), 0, s, g); break;
+      case FW_EPI_BIAS_GELU:
+        hipLaunchKernelGGL((gemm_kernel<BM, FW_EPI_BIAS_GELU, true>), grid, dim3(256), 0, s, g);
+        break;
+      case FW_EPI_BIAS_GELU_POS:
+        hipLaunchKernelGGL((gemm_kernel<BM, FW_EPI_BIAS_GELU_POS, true>), grid, dim3(256), 0, s, g);
+        break;
+      default:
+        return fw_fail(FW_EINVAL, "conv1d: unsupported epilogue %d", epi);
+    }
+    return fw_check_launch("conv1d");
+  }
   switch (epi) {
 #define FW_GEMM_CASE(E) \
   case E:               \
-    hipLaunchKernelGGL((gemm_kernel<BM, E>), grid, dim3(256), 0, s, g); break;
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, E>), grid, dim3(256), 0, s, g); break;
     FW_GEMM_CASE(FW_EPI_BIAS)
     FW_GEMM_CASE(FW_EPI_BIAS_GELU)
     FW_GEMM_CASE(FW_EPI_BIAS_RESID)
@@ -201,10 +364,10 @@ int launch_gemm_bm(const GemmArgs& g, int epi, hipStream_t s) {
   return fw_check_launch("gemm");
 }
 
-// Fewer than ~2 blocks per CU at BM = 128 leaves the chip idle: use 64-row tiles then.
+// Fewer 128-row tiles than CUs leaves the chip idle: use 64-row tiles then.
 int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
   const int tiles128 = (g.n / kBN) * ((g.m + 127) / 128);
-  if (tiles128 < 400) return launch_gemm_bm<64>(g, epi, s);
+  if (tiles128 < 256) return launch_gemm_bm<64>(g, epi, s);
   return launch_gemm_bm<128>(g, epi, s);
 }
 

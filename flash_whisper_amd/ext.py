@@ -157,27 +157,64 @@ class WhisperExt:
                    0 if table is None else table.size(0), 0 if pos_table is None else pos_table.size(0),
                    w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), HIDDEN, act, _stream())
 
-    def decode_attention_fused(self, q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc, counters,
-                               scale, split_keys=SPLIT_KEYS):
-        heads, max_len, slots = self._attn_checks(q, k, v, out, len_state, k_new, v_new, part_m, part_l, part_acc,
-                                                  split_keys)
-        _require(counters.dtype == torch.int32 and counters.is_cuda and counters.numel() >= heads,
-                 'counters must be CUDA int32 [heads]')
+    def decode_attention_fused(self, q, k, v, out, len_state, k_new, v_new, scale):
+        """decode_attention in a single launch (one block per head, no workspace)."""
+        for t, n in ((q, 'q'), (k, 'k'), (v, 'v'), (out, 'out')):
+            check_half(t, n)
+        _require(k.dim() == 3 and k.size(2) == HEAD_DIM and k.shape == v.shape, 'k, v must be [heads, max_len, 64]')
+        heads, max_len = k.size(0), k.size(1)
+        _require(q.numel() == heads * HEAD_DIM and out.numel() == heads * HEAD_DIM, 'q, out must be [heads * 64]')
+        _require((k_new is None) == (v_new is None) == (len_state is None),
+                 'len_state, k_new and v_new must be given together')
+        if k_new is not None:
+            check_half(k_new, 'k_new')
+            check_half(v_new, 'v_new')
+            _require(k_new.numel() == heads * HEAD_DIM and v_new.numel() == heads * HEAD_DIM,
+                     'k_new, v_new must be [heads, 64]')
+            _require(len_state.dtype == torch.int64 and len_state.is_cuda, 'len_state must be CUDA int64')
         self._call('fw_decode_attention_fused', q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                   _ptr(len_state), _ptr(k_new), _ptr(v_new), heads, max_len, int(split_keys), part_m.data_ptr(),
-                   part_l.data_ptr(), part_acc.data_ptr(), counters.data_ptr(), slots, float(scale), _stream())
+                   _ptr(len_state), _ptr(k_new), _ptr(v_new), heads, max_len, float(scale), _stream())
 
-    def lm_head_argmax_fused(self, h, x, gamma, beta, eps, w, suppress, best, tokens, state, cur, max_pos, counter):
+    def attention_split(self, q, k, v, len_state, k_new, v_new, part_m, part_l, part_acc, scale, split_keys=SPLIT_KEYS):
+        """Split half of decode_attention: (m, l, acc) partials per (head, split) into the workspace."""
+        heads, max_len, slots = self._attn_checks(q, k, v, q, len_state, k_new, v_new, part_m, part_l, part_acc,
+                                                  split_keys)
+        self._call('fw_attention_split', q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(len_state), _ptr(k_new),
+                   _ptr(v_new), heads, max_len, int(split_keys), part_m.data_ptr(), part_l.data_ptr(),
+                   part_acc.data_ptr(), slots, float(scale), _stream())
+
+    def attn_out_gemv(self, part_m, part_l, part_acc, len_state, heads, max_len, w, bias, out, split_keys=SPLIT_KEYS):
+        """Combine of attention_split partials + output projection: out = fp16(w . combine + bias)."""
+        for t in (part_m, part_l, part_acc):
+            _require(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32,
+                     'workspace must be contiguous CUDA fp32')
+        check_half(w, 'w')
+        check_half(out, 'out')
+        _require(w.dim() == 2 and w.size(1) == heads * HEAD_DIM == HIDDEN and out.numel() == w.size(0),
+                 'attn_out_gemv shape mismatch')
+        if bias is not None:
+            check_half(bias, 'bias')
+        if len_state is not None:
+            _require(len_state.dtype == torch.int64 and len_state.is_cuda, 'len_state must be CUDA int64')
+        slots = min(part_m.numel(), part_l.numel(), part_acc.numel() // HEAD_DIM)
+        self._call('fw_attn_out_gemv', part_m.data_ptr(), part_l.data_ptr(), part_acc.data_ptr(), slots,
+                   _ptr(len_state), heads, int(max_len), int(split_keys), w.data_ptr(), _ptr(bias), out.data_ptr(),
+                   w.size(0), _stream())
+
+    def lm_head_argmax_fused(self, h, x, gamma, beta, eps, w, suppress, best, tokens, state, cur, max_pos):
+        """Final residual + LN + lm_head_argmax + argmax_finalize."""
         for t, n in ((h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (w, 'w')):
             check_half(t, n)
         if x is not None:
             check_half(x, 'x')
         _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
-        _require(suppress.dtype == torch.bool and suppress.numel() == w.size(0), 'suppress must be bool [vocab]')
-        _require(counter.dtype == torch.int32 and counter.is_cuda, 'counter must be CUDA int32 [1]')
+        _require(suppress.dtype == torch.bool and suppress.is_cuda and suppress.numel() == w.size(0),
+                 'suppress must be bool [vocab]')
+        for t in (best, tokens, state, cur):
+            _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), 'tokens, state and cur must be int64')
         self._call('fw_lm_head_argmax_fused', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), float(eps),
                    w.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN, best.data_ptr(), tokens.data_ptr(),
-                   state.data_ptr(), cur.data_ptr(), int(max_pos), counter.data_ptr(), _stream())
+                   state.data_ptr(), cur.data_ptr(), int(max_pos), _stream())
 
     # ---- log-mel front end -------------------------------------------------------------
     def log_mel_workspace(self, n_samples, device='cuda'):

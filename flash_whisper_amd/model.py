@@ -25,12 +25,13 @@ from .ext import load_ext
 from .selftest import run_selftest, workspace
 
 SYNTHETIC = 'synthetic'
+SELF_SPLIT, CROSS_SPLIT = 64, 256  # keys per split block of the decoder's self / cross attention (<= 8 splits)
 
 
 class CustomModel:
     @torch.inference_mode()
     def __init__(self, model_id=SYNTHETIC, cache_dir=None, *, seed=0, dims=TURBO, setup=None, selftest=True,
-                 capture=True, cross_split_keys=SPLIT_KEYS):
+                 capture=True):
         if not torch.cuda.is_available():
             raise RuntimeError('CustomModel requires a HIP device')
         if model_id not in (None, SYNTHETIC):
@@ -45,7 +46,6 @@ class CustomModel:
         self.prompt = list(self.setup.prompt)
         self.max_new = self.max_pos - len(self.prompt)
         self.eos = set(self.setup.eos)
-        self.cross_split_keys = cross_split_keys
         self.record_events = False   # time every chunk replay with HIP events (bench.py)
         self.chunk_events = []
 
@@ -168,10 +168,8 @@ class CustomModel:
         self.state = torch.zeros(2, dtype=torch.long, device='cuda')  # [position, generated count]
         self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
         self.best = torch.zeros(1, dtype=torch.long, device='cuda')
-        splits = -(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, self.cross_split_keys))
-        self.workspace = workspace(d.heads, splits)
-        self.attn_counters = torch.zeros(d.heads, dtype=torch.int32, device='cuda')
-        self.lm_counter = torch.zeros(1, dtype=torch.int32, device='cuda')
+        # split-K attention partials (both the fused step and the reference-granularity step)
+        self.workspace = workspace(d.heads, -(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, SELF_SPLIT, CROSS_SPLIT)))
 
     # ---- front end ---------------------------------------------------------------------------
     def _log_mel(self, wave):
@@ -241,11 +239,12 @@ class CustomModel:
 
     # ---- decoder -----------------------------------------------------------------------------
     def _step(self):
-        """One decoder token, entirely on the device (custom/model.py:107-123) in 33 launches:
-        per layer [LN1+QKV] [self-attn+combine, KV write] [out] [LN2+cross-q] [cross-attn+combine]
-        [cross-out] [LN3+fc1+GELU] [fc2], then [final LN + LM head + argmax + finalize]."""
+        """One decoder token, entirely on the device (custom/model.py:107-123) in 34 launches:
+        per layer [LN1+QKV] [self-attn split-K + KV write] [combine + out] [LN2+cross-q]
+        [cross-attn split-K] [combine + cross-out] [LN3+fc1+GELU] [fc2], then
+        [final LN + LM head + argmax] [finalize]."""
         ext, d, dm = self.ext, self.dims, self.dims.d_model
-        ws, ctr = self.workspace, self.attn_counters
+        ws = self.workspace
         q, k_new, v_new = self.qkv[:dm], self.qkv[dm:2 * dm], self.qkv[2 * dm:]
         a, b = 0, 1
         for i, lay in enumerate(self.layers):
@@ -255,21 +254,21 @@ class CustomModel:
                             embed=(self.cur, self.state, self.embed, self.pos_embed))
             else:
                 ext.ln_gemv(self.h[b], self.pending, self.h[a], g, be, eps, lay.qkv_w, lay.qkv_b, self.qkv)
-            ext.decode_attention_fused(q, self.self_kv[i, 0], self.self_kv[i, 1], self.attn, self.state, k_new, v_new,
-                                       *ws, ctr, self.scale, SPLIT_KEYS)
-            ext.gemv(self.attn, *lay.out, self.xo)
+            ext.attention_split(q, self.self_kv[i, 0], self.self_kv[i, 1], self.state, k_new, v_new, *ws, self.scale,
+                                SELF_SPLIT)
+            ext.attn_out_gemv(*ws, self.state, d.heads, d.max_pos, *lay.out, self.xo, SELF_SPLIT)
             g, be, eps = lay.ln2
             ext.ln_gemv(self.h[a], self.xo, self.h[b], g, be, eps, *lay.cross_q, self.q)
-            ext.decode_attention_fused(self.q, self.cross_kv[i, 0], self.cross_kv[i, 1], self.attn, None, None, None,
-                                       *ws, ctr, self.scale, self.cross_split_keys)
-            ext.gemv(self.attn, *lay.cross_out, self.xo)
+            ext.attention_split(self.q, self.cross_kv[i, 0], self.cross_kv[i, 1], None, None, None, *ws, self.scale,
+                                CROSS_SPLIT)
+            ext.attn_out_gemv(*ws, None, d.heads, d.enc_len, *lay.cross_out, self.xo, CROSS_SPLIT)
             g, be, eps = lay.ln3
             ext.ln_gemv(self.h[b], self.xo, self.h[a], g, be, eps, *lay.fc1, self.ffn, act=ACT_GELU)
             ext.gemv(self.ffn, *lay.fc2, self.pending)
             a, b = b, a
         g, be, eps = self.final_ln
         ext.lm_head_argmax_fused(self.h[b], self.pending, g, be, eps, self.lm_head, self.suppress, self.best,
-                                 self.tokens, self.state, self.cur, self.max_pos, self.lm_counter)
+                                 self.tokens, self.state, self.cur, self.max_pos)
 
     def _step_reference(self):
         """The same step at the reference's op granularity (embed, add_layernorm, GEMV, split+combine

@@ -65,7 +65,6 @@ def run_selftest(ext):
 
     scale = HEAD_DIM ** -0.5
     ws = workspace(HEADS, 24)
-    counters = torch.zeros(HEADS, device=dev, dtype=torch.int32)
     for length in (1, 63, 64, 65, 200, 448):
         max_len, pos = 448, length - 1
         q = torch.randn(HEADS * HEAD_DIM, device=dev, dtype=half)
@@ -85,9 +84,9 @@ def run_selftest(ext):
         untouched = max((k - k_ref).abs().max(), (v - v_ref).abs().max())
         checks.append(_check(f'kv_write_{length}', max(written, untouched), 0))
         out_f = torch.empty_like(q)
-        ext.decode_attention_fused(q, k2, v2, out_f, state, k_new, v_new, *ws, counters, scale)
-        checks.append(_check(f'decode_attention_fused_self_{length}',
-                             max((out_f - out).abs().max(), (k2 - k).abs().max(), (v2 - v).abs().max()), 0))
+        ext.decode_attention_fused(q, k2, v2, out_f, state, k_new, v_new, scale)
+        checks.append(_check(f'decode_attention_fused_self_{length}', (out_f.float() - ref).abs().max(), 1e-2))
+        checks.append(_check(f'kv_write_fused_{length}', max((k2 - k).abs().max(), (v2 - v).abs().max()), 0))
 
     q = torch.randn(HEADS * HEAD_DIM, device=dev, dtype=half)
     k = torch.randn(HEADS, 1500, HEAD_DIM, device=dev, dtype=half)
@@ -97,8 +96,8 @@ def run_selftest(ext):
     ref = _attention_ref(q.view(HEADS, HEAD_DIM), k, v, 1500, scale).flatten()
     checks.append(_check('decode_attention_cross', (out.float() - ref).abs().max(), 1e-2))
     out_f = torch.empty_like(q)
-    ext.decode_attention_fused(q, k, v, out_f, None, None, None, *ws, counters, scale)
-    checks.append(_check('decode_attention_fused_cross', (out_f - out).abs().max(), 0))
+    ext.decode_attention_fused(q, k, v, out_f, None, None, None, scale)
+    checks.append(_check('decode_attention_fused_cross', (out_f.float() - ref).abs().max(), 1e-2))
 
     hidden = torch.randn(1, HIDDEN, device=dev, dtype=half)
     weight = torch.randn(VOCAB, HIDDEN, device=dev, dtype=half) * 0.02
@@ -125,10 +124,8 @@ def run_selftest(ext):
     ext.argmax_finalize(best1, tok1, st1, cur1, 448)
     best2, tok2 = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
     st2, cur2 = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
-    counter = torch.zeros(1, device=dev, dtype=torch.int32)
-    ext.lm_head_argmax_fused(hres, xres, g1, b0, 1e-5, weight, suppress, best2, tok2, st2, cur2, 448, counter)
-    same = (torch.equal(tok1, tok2) and torch.equal(st1, st2) and torch.equal(cur1, cur2) and int(best2) == 0
-            and int(counter) == 0)
+    ext.lm_head_argmax_fused(hres, xres, g1, b0, 1e-5, weight, suppress, best2, tok2, st2, cur2, 448)
+    same = torch.equal(tok1, tok2) and torch.equal(st1, st2) and torch.equal(cur1, cur2) and int(best2) == 0
     checks.append(_check('lm_head_argmax_fused_vs_unfused', 0 if same else 1, 0))
 
     return {'ok': all(c['ok'] for c in checks), 'checks': checks}

@@ -94,22 +94,33 @@ int fw_ln_gemv(const void* h, const void* x, void* h_out, const void* gamma, con
                int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
                hipStream_t stream);
 
-/* Split-K attention as fw_decode_attention with the combine fused into the last block of each head
- * (a per-head arrival counter). split_keys is a multiple of 32 in [32, 256]. counters u32[heads]
- * must be zero before the first call; every call leaves them zero. */
+/* Decode attention in one launch (same contract as fw_decode_attention, no workspace): one
+ * 1024-thread block per head covers all keys and merges its 16 wave partials on chip. */
 int fw_decode_attention_fused(const void* q, void* k, void* v, void* out, const int64_t* len_state,
-                              const void* k_new, const void* v_new, int heads, int max_len, int split_keys,
-                              float* part_m, float* part_l, float* part_acc, uint32_t* counters,
-                              int64_t ws_slots, float scale, hipStream_t stream);
+                              const void* k_new, const void* v_new, int heads, int max_len, float scale,
+                              hipStream_t stream);
 
-/* Final residual + LayerNorm + LM head + argmax + finalize in one launch
- * (custom/model.py:121-123): r = fp16(h + x); y = LN(r); best/tokens/state/cur updated exactly as
- * fw_lm_head_argmax followed by fw_argmax_finalize. counter u32[1] must be zero before the first call
- * and is left zero; best must be zero on entry and is left zero. */
+/* The split half of fw_decode_attention alone: per (head, split) flash-decoding partials
+ * (m, l, acc[64]) of split_keys keys each (multiple of 8, <= 256) into part_m/part_l/part_acc;
+ * self mode writes the k_new/v_new cache row as fw_decode_attention does. */
+int fw_attention_split(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
+                       const void* v_new, int heads, int max_len, int split_keys, float* part_m, float* part_l,
+                       float* part_acc, int64_t ws_slots, float scale, hipStream_t stream);
+
+/* Attention combine + output projection in one launch: x = combine(partials of fw_attention_split
+ * with the same heads/max_len/split_keys; len_state limits self attention to the filled splits),
+ * rounded to fp16 exactly as the fw_decode_attention output, then out <- fp16(w . x + bias).
+ * heads * 64 == 1280, heads <= 32, ceil(max_len / split_keys) <= 8. */
+int fw_attn_out_gemv(const float* part_m, const float* part_l, const float* part_acc, int64_t ws_slots,
+                     const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
+                     const void* bias, void* out, int n_out, hipStream_t stream);
+
+/* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
+ * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by
+ * fw_argmax_finalize. best must be zero on entry and is left zero. */
 int fw_lm_head_argmax_fused(const void* h, const void* x, const void* gamma, const void* beta, float eps,
                             const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
-                            int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, uint32_t* counter,
-                            hipStream_t stream);
+                            int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, hipStream_t stream);
 
 /* ---- log-mel front end (custom/model.py:93-98) ------------------------------------------- */
 

@@ -15,10 +15,14 @@ pytestmark = pytest.mark.gpu
 RTOL = 2e-3
 
 
-def close_rel(gpu, ref, rtol=RTOL):
+def close_rel(gpu, ref, rtol=RTOL, scale=None):
+    """|gpu - ref| <= rtol * scale + rtol * rms(ref), scale = |ref| unless given. When the result is a
+    sum of rounded terms (a residual add), pass scale = |a| + |b|: a one-ulp difference in a large
+    intermediate that cancels must be measured against the intermediate, not the small result."""
     gpu = np.asarray(gpu, np.float64)
     ref = np.asarray(ref, np.float64)
-    tol = rtol * np.abs(ref) + rtol * np.sqrt(np.mean(ref ** 2))
+    scale = np.abs(ref) if scale is None else np.asarray(scale, np.float64)
+    tol = rtol * scale + rtol * np.sqrt(np.mean(ref ** 2))
     err = np.abs(gpu - ref)
     assert (err <= tol).all(), f'max err {err.max():.3e}, worst ratio {(err / tol).max():.2f}'
 
@@ -133,9 +137,7 @@ def test_self_attention(ext, hip_device, length, fused):
     state = torch.tensor([pos, 0], device=dev)
     ws = workspace(heads, 7)
     if fused:
-        ctr = torch.zeros(heads, dtype=torch.int32, device=dev)
-        ext.decode_attention_fused(h16(q, dev), tk, tv, out, state, h16(k_new, dev), h16(v_new, dev), *ws, ctr, 0.125)
-        assert int(ctr.abs().sum()) == 0
+        ext.decode_attention_fused(h16(q, dev), tk, tv, out, state, h16(k_new, dev), h16(v_new, dev), 0.125)
     else:
         ext.decode_attention(h16(q, dev), tk, tv, out, state, h16(k_new, dev), h16(v_new, dev), *ws, 0.125)
     k_ref, v_ref = k.copy(), v.copy()
@@ -145,24 +147,24 @@ def test_self_attention(ext, hip_device, length, fused):
     assert np.array_equal(tk.cpu().numpy(), k_ref) and np.array_equal(tv.cpu().numpy(), v_ref)
 
 
-@pytest.mark.parametrize('split_keys', [64, 128, 256])
-def test_cross_attention(ext, hip_device, split_keys):
+@pytest.mark.parametrize('max_len,fused', [(1500, True), (1500, False), (1537, True), (3100, True), (7, True)])
+def test_cross_attention(ext, hip_device, max_len, fused):
+    """Cross mode over the 1500 encoder frames, plus lengths that take a partial and several 1536-key
+    rounds in the single-launch kernel."""
     from flash_whisper_amd.selftest import workspace
 
-    rng = np.random.default_rng(split_keys)
+    rng = np.random.default_rng(max_len)
     dev, heads = hip_device, 20
-    q, k, v = _attn_inputs(rng, heads, 1500)
+    q, k, v = _attn_inputs(rng, heads, max_len)
+    q = np.float16(q.astype(np.float32) * 2)  # sharper softmax than the N(0, 1) default
     out = torch.empty(heads * 64, dtype=torch.float16, device=dev)
-    ws = workspace(heads, 24)
-    ctr = torch.zeros(heads, dtype=torch.int32, device=dev)
-    ext.decode_attention_fused(h16(q, dev), h16(k, dev), h16(v, dev), out, None, None, None, *ws, ctr, 0.125,
-                               split_keys=split_keys)
-    ref = odec.attention(q.reshape(heads, 64).astype(np.float32), k, v, 1500, 0.125)
+    if fused:
+        ext.decode_attention_fused(h16(q, dev), h16(k, dev), h16(v, dev), out, None, None, None, 0.125)
+    else:
+        ext.decode_attention(h16(q, dev), h16(k, dev), h16(v, dev), out, None, None, None,
+                             *workspace(heads, -(-max_len // 64)), 0.125)
+    ref = odec.attention(q.reshape(heads, 64).astype(np.float32), k, v, max_len, 0.125)
     close_rel(np32(out), ref)
-    if split_keys == 64:
-        out2 = torch.empty_like(out)
-        ext.decode_attention(h16(q, dev), h16(k, dev), h16(v, dev), out2, None, None, None, *ws, 0.125)
-        assert torch.equal(out, out2)
 
 
 def _lm_setup(dev, seed=4):
@@ -194,10 +196,8 @@ def test_lm_head_argmax_bit_exact(ext, hip_device, fused):
     cur = torch.zeros(1, dtype=torch.long, device=dev)
     tsup = torch.from_numpy(sup).to(dev)
     if fused:
-        ctr = torch.zeros(1, dtype=torch.int32, device=dev)
         ext.lm_head_argmax_fused(h16(h, dev), None, h16(g1, dev), h16(b0, dev), 1e-5, w, tsup, best, tokens, state,
-                                 cur, 448, ctr)
-        assert int(ctr) == 0
+                                 cur, 448)
     else:
         y = torch.empty(1280, dtype=torch.float16, device=dev)
         th = h16(h, dev)
@@ -248,3 +248,42 @@ def test_selftest_passes(ext, hip_device):
     res = run_selftest(ext)
     bad = [c for c in res['checks'] if not c['ok']]
     assert res['ok'], bad
+
+
+@pytest.mark.parametrize('mode,length,split', [('self', 1, 64), ('self', 65, 64), ('self', 228, 64),
+                                               ('self', 448, 64), ('cross', 1500, 256), ('cross', 1500, 192),
+                                               ('self', 300, 128), ('self', 448, 256)])
+def test_split_attention_with_fused_combine_gemv(ext, hip_device, mode, length, split):
+    """attention_split + attn_out_gemv (combine in the GEMV prologue) must equal the reference-granularity
+    decode_attention (split + combine launches) followed by the GEMV, bit for bit at 64-key splits, and
+    match the oracle (attention, then the fp16 projection) within tolerance at any split size."""
+    from flash_whisper_amd.selftest import workspace
+    from oracle.common import f16
+
+    dev, heads = hip_device, 20
+    rng = np.random.default_rng(length + split)
+    max_len = 448 if mode == 'self' else 1500
+    q, k, v = _attn_inputs(rng, heads, max_len)
+    w = np.float16(0.02 * rng.standard_normal((1280, 1280)))
+    b = np.float16(0.02 * rng.standard_normal(1280))
+    ws = workspace(heads, -(-max_len // min(split, 64)))
+    args = [None, None, None]
+    k_ref, v_ref = k.copy(), v.copy()
+    if mode == 'self':
+        kn, vn = np.float16(rng.standard_normal((heads, 64))), np.float16(rng.standard_normal((heads, 64)))
+        args = [torch.tensor([length - 1, 0], device=dev), h16(kn, dev), h16(vn, dev)]
+        k_ref[:, length - 1], v_ref[:, length - 1] = kn, vn
+    tk, tv = h16(k, dev), h16(v, dev)
+    out = torch.empty(1280, dtype=torch.float16, device=dev)
+    ext.attention_split(h16(q, dev), tk, tv, *args, *ws, 0.125, split_keys=split)
+    ext.attn_out_gemv(*ws, args[0], heads, max_len, h16(w, dev), h16(b, dev), out, split_keys=split)
+    att = odec.attention(q.reshape(heads, 64).astype(np.float32), k_ref, v_ref, length, 0.125)
+    close_rel(np32(out), f16(w.astype(np.float32) @ att + b.astype(np.float32)))
+    if mode == 'self':
+        assert np.array_equal(tk.cpu().numpy(), k_ref) and np.array_equal(tv.cpu().numpy(), v_ref)
+    if split == 64 and mode == 'self':
+        tk2, tv2 = h16(k, dev), h16(v, dev)
+        attn, ref_out = torch.empty(1280, dtype=torch.float16, device=dev), torch.empty_like(out)
+        ext.decode_attention(h16(q, dev), tk2, tv2, attn, *args, *ws, 0.125)
+        ext.gemv(attn, h16(w, dev), h16(b, dev), ref_out)
+        assert torch.equal(out, ref_out)

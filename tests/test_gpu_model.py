@@ -103,6 +103,7 @@ def test_graph_replay_matches_eager(model, clip):
     assert res_graph2['token_ids'] == res_graph['token_ids']
 
 
+@torch.inference_mode()
 def test_fused_step_matches_reference_granularity_step(model, clip):
     model.transcribe(clip, max_new_tokens=1, stop_at_eos=False)  # fills cross K/V
     ids = {}
