@@ -40,6 +40,19 @@ def decode_step_bytes(dims, length):
     return weights + lm_head + cross + self_kv + 2 * 2 * d + dims.vocab
 
 
+def measured_traffic(path='profiles/lm_head_kernel_traffic.md'):
+    """HBM bytes per LM-head launch from the committed, copy-calibrated rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE passes), or None when that summary is absent."""
+    import pathlib
+    import re
+
+    f = pathlib.Path(__file__).resolve().parent / path
+    if not f.exists():
+        return None
+    m = re.search(r'^traffic_bytes_per_launch:\s*(\d+)', f.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
 def lm_head_bytes(dims):
     """Algorithmic bytes of one fused LM-head launch: the embedding, the suppress mask, h, x, gamma, beta."""
     return 2 * dims.vocab * dims.d_model + dims.vocab + 4 * 2 * dims.d_model
@@ -113,6 +126,8 @@ def main():
     ap.add_argument('--kernel-reps', type=int, default=60)
     ap.add_argument('--cpu-seconds', type=float, default=12.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--copy-calibration', action='store_true',
+                    help='also run 4 plain 256 MiB device copies (the reference kernel for PMC byte counters)')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py measures one GPU only (--gpus {args.gpus} requested): this build runs the batch-1 path on '
@@ -148,6 +163,13 @@ def main():
     model.record_events = False
 
     lm_us = time_lm_head(model, args.kernel_reps)
+    if args.copy_calibration:
+        src = torch.empty(128 << 20, dtype=torch.float16, device='cuda')
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     lm_bytes = lm_head_bytes(model.dims)
     lm_gbps = lm_bytes / (lm_us * 1e-6) / 1e9
 
@@ -173,7 +195,8 @@ def main():
         'n_tokens': rows[-1]['n_tokens'],
         'roofline': {'kernel': 'lm_head_kernel<true> (final LN + LM head GEMV + argmax; finalize is a separate 1-thread launch)',
                      'bound': 'hbm', 'achieved': round(lm_gbps, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
-                     'frac': round(lm_gbps / HBM_PEAK_GBPS, 4), 'traffic': None, 'us_per_launch': round(lm_us, 2),
+                     'frac': round(lm_gbps / HBM_PEAK_GBPS, 4), 'traffic': measured_traffic(),
+                     'traffic_source': 'profiles/lm_head_kernel_traffic.md', 'us_per_launch': round(lm_us, 2),
                      'bytes_per_launch': lm_bytes},
     }
     if not args.no_cpu_baseline:
