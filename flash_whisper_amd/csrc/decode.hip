@@ -10,35 +10,79 @@
 namespace fw {
 namespace {
 
+#ifndef FW_GEMV_WEIGHTS_NT
+#define FW_GEMV_WEIGHTS_NT 0  // decoder weights may stay resident in the 256 MB MALL
+#endif
+#ifndef FW_LM_HEAD_NT
+#define FW_LM_HEAD_NT 1
+#endif
+__device__ __forceinline__ uint4 ld_weights(const uint4* p) {
+#if FW_GEMV_WEIGHTS_NT
+  return ld_stream(p);
+#else
+  return *p;
+#endif
+}
+__device__ __forceinline__ uint4 ld_lm_head(const uint4* p) {
+#if FW_LM_HEAD_NT
+  return ld_stream(p);
+#else
+  return *p;
+#endif
+}
+
 // ------------------------------------------------------------------------------------------
 // Residual + LayerNorm prologue shared by add_layernorm, the fused LN+GEMV and the LM head.
 // Produces y = fp16(LN(r) * gamma + beta) for the 1280-wide hidden vector in `y_out` (LDS or
 // global), where r = fp16(a + b) (b may be null) and a, b are either (h, x) or the embedding rows
 // (embed[cur], pos_embed[pos]). Block 0 stores r to r_out when r_out is non-null.
 // ------------------------------------------------------------------------------------------
+// The inputs are loaded into registers by ln_load and consumed by ln_finish, so a kernel can issue
+// its other global loads (the weight rows) in between: vector-memory counters retire in order, and
+// inputs requested after the weights could not be used before the weights had arrived.
 template <int NT>
-__device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b, _Float16* r_out,
-                                            const _Float16* gamma, const _Float16* beta, float eps,
-                                            _Float16* y_out, float* red) {
-  constexpr int kPairs = kHidden / 2;
-  constexpr int kPer = (kPairs + NT - 1) / NT;
+struct LnRegs {
+  static constexpr int kPairs = kHidden / 2;
+  static constexpr int kPer = (kPairs + NT - 1) / NT;
+  h2v a[kPer], b[kPer], g[kPer], be[kPer];
+};
+
+template <int NT>
+__device__ __forceinline__ void ln_load(const _Float16* a, const _Float16* b, const _Float16* gamma,
+                                        const _Float16* beta, LnRegs<NT>& in) {
   const h2v* a2 = reinterpret_cast<const h2v*>(a);
   const h2v* b2 = reinterpret_cast<const h2v*>(b);
+  const h2v* g2 = reinterpret_cast<const h2v*>(gamma);
+  const h2v* be2 = reinterpret_cast<const h2v*>(beta);
+  const h2v zero = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
+#pragma unroll
+  for (int i = 0; i < LnRegs<NT>::kPer; ++i) {
+    const int idx = threadIdx.x + i * NT;
+    const bool ok = idx < LnRegs<NT>::kPairs;
+    in.a[i] = ok ? a2[idx] : zero;
+    in.b[i] = (ok && b2) ? b2[idx] : zero;
+    in.g[i] = ok ? g2[idx] : zero;
+    in.be[i] = ok ? be2[idx] : zero;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void ln_finish(const LnRegs<NT>& in, bool has_b, _Float16* r_out, float eps,
+                                          _Float16* y_out, float* red) {
+  constexpr int kPer = LnRegs<NT>::kPer;
   h2v* r2 = reinterpret_cast<h2v*>(r_out);
-  const int tid = threadIdx.x;
+  h2v* y2 = reinterpret_cast<h2v*>(y_out);
   float2 r[kPer];
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int idx = tid + i * NT;
+    const int idx = threadIdx.x + i * NT;
     r[i] = make_float2(0.f, 0.f);
-    if (idx < kPairs) {
-      const h2v av = a2[idx];
-      float rx = h2f(av.x), ry = h2f(av.y);
-      if (b2) {
-        const h2v bv = b2[idx];
-        rx = round_h(rx + h2f(bv.x));
-        ry = round_h(ry + h2f(bv.y));
+    if (idx < LnRegs<NT>::kPairs) {
+      float rx = h2f(in.a[i].x), ry = h2f(in.a[i].y);
+      if (has_b) {
+        rx = round_h(rx + h2f(in.b[i].x));
+        ry = round_h(ry + h2f(in.b[i].y));
       }
       r[i] = make_float2(rx, ry);
       sum += rx + ry;
@@ -54,28 +98,33 @@ __device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b
   float sq = 0.f;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int idx = tid + i * NT;
-    if (idx < kPairs) {
+    const int idx = threadIdx.x + i * NT;
+    if (idx < LnRegs<NT>::kPairs) {
       const float dx = r[i].x - mean, dy = r[i].y - mean;
       sq += dx * dx + dy * dy;
     }
   }
   const float var = block_sum<NT>(sq, red) * (1.0f / kHidden);
   const float inv = rsqrtf(var + eps);
-  const h2v* g2 = reinterpret_cast<const h2v*>(gamma);
-  const h2v* be2 = reinterpret_cast<const h2v*>(beta);
-  h2v* y2 = reinterpret_cast<h2v*>(y_out);
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int idx = tid + i * NT;
-    if (idx < kPairs) {
-      const h2v g = g2[idx], be = be2[idx];
+    const int idx = threadIdx.x + i * NT;
+    if (idx < LnRegs<NT>::kPairs) {
       h2v o;
-      o.x = f2h((r[i].x - mean) * inv * h2f(g.x) + h2f(be.x));
-      o.y = f2h((r[i].y - mean) * inv * h2f(g.y) + h2f(be.y));
+      o.x = f2h((r[i].x - mean) * inv * h2f(in.g[i].x) + h2f(in.be[i].x));
+      o.y = f2h((r[i].y - mean) * inv * h2f(in.g[i].y) + h2f(in.be[i].y));
       y2[idx] = o;
     }
   }
+}
+
+template <int NT>
+__device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b, _Float16* r_out,
+                                            const _Float16* gamma, const _Float16* beta, float eps,
+                                            _Float16* y_out, float* red) {
+  LnRegs<NT> in;
+  ln_load<NT>(a, b, gamma, beta, in);
+  ln_finish<NT>(in, b != nullptr, r_out, eps, y_out, red);
 }
 
 __device__ __forceinline__ void embed_rows(const int64_t* cur, const int64_t* state, const _Float16* embed,
@@ -161,51 +210,67 @@ __device__ __forceinline__ int active_splits(const int64_t* len_state, int max_l
 }
 
 // x[h * 64 + d] = fp16(sum_s acc[h, s, d] e^(m_s - M) / sum_s l_s e^(m_s - M)), splits with l = 0 skipped
-// (the arithmetic of the combine launch). Every partial a thread needs is requested before any is used.
+// (the arithmetic of the combine launch). combine_load requests every partial a thread needs;
+// combine_finish merges them once they have landed.
 template <int NT>
-__device__ __forceinline__ void combine_prologue(const CombineArgs& c, _Float16* x, float* wgt, float* den_lds) {
+struct CombineRegs {
+  static constexpr int kPer = (kHidden + NT - 1) / NT;
+  float pm[kMaxCombineSplits], pl[kMaxCombineSplits];
+  float pa[kPer][kMaxCombineSplits];
+  int active;
+};
+
+template <int NT>
+__device__ __forceinline__ void combine_load(const CombineArgs& c, CombineRegs<NT>& r) {
   constexpr int S = kMaxCombineSplits;
-  const int active = active_splits(c.len_state, c.max_len, c.split_keys, c.nsplit);
-  for (int h = threadIdx.x; h < c.heads; h += NT) {
-    float pm[S], pl[S];
+  r.active = active_splits(c.len_state, c.max_len, c.split_keys, c.nsplit);
+  const int h0 = threadIdx.x;  // threads below `heads` also own one head's weights
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      pm[s] = s < active ? c.part_m[h * c.nsplit + s] : -INFINITY;
-      pl[s] = s < active ? c.part_l[h * c.nsplit + s] : 0.f;
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < S; ++s) m = fmaxf(m, pm[s]);
-    float den = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const float w = pl[s] > 0.f ? __expf(pm[s] - m) : 0.f;
-      wgt[h * S + s] = w;
-      den = fmaf(pl[s], w, den);
-    }
-    den_lds[h] = den;
+  for (int s = 0; s < S; ++s) {
+    const bool ok = h0 < c.heads && s < r.active;
+    r.pm[s] = ok ? c.part_m[h0 * c.nsplit + s] : -INFINITY;
+    r.pl[s] = ok ? c.part_l[h0 * c.nsplit + s] : 0.f;
   }
-  constexpr int kPer = (kHidden + NT - 1) / NT;
-  float pa[kPer][S];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
+  for (int i = 0; i < CombineRegs<NT>::kPer; ++i) {
     const int j = threadIdx.x + i * NT;
     const int h = j / kHeadDim, d = j % kHeadDim;
 #pragma unroll
     for (int s = 0; s < S; ++s)
-      pa[i][s] = (j < c.heads * kHeadDim && s < active)
-                     ? c.part_acc[(static_cast<size_t>(h) * c.nsplit + s) * kHeadDim + d] : 0.f;
+      r.pa[i][s] = (j < c.heads * kHeadDim && s < r.active)
+                       ? c.part_acc[(static_cast<size_t>(h) * c.nsplit + s) * kHeadDim + d] : 0.f;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void combine_finish(const CombineArgs& c, const CombineRegs<NT>& r, _Float16* x,
+                                               float* wgt, float* den_lds) {
+  constexpr int S = kMaxCombineSplits;
+  static_assert(NT >= kMaxCombineHeads, "one thread per head computes the split weights");
+  if (threadIdx.x < c.heads) {
+    const int h = threadIdx.x;
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < S; ++s) m = fmaxf(m, r.pm[s]);
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float w = r.pl[s] > 0.f ? __expf(r.pm[s] - m) : 0.f;
+      wgt[h * S + s] = w;
+      den = fmaf(r.pl[s], w, den);
+    }
+    den_lds[h] = den;
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
+  for (int i = 0; i < CombineRegs<NT>::kPer; ++i) {
     const int j = threadIdx.x + i * NT;
     if (j < c.heads * kHeadDim) {
       const int h = j / kHeadDim;
       float num = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s)
-        if (wgt[h * S + s] != 0.f) num = fmaf(pa[i][s], wgt[h * S + s], num);
+        if (wgt[h * S + s] != 0.f) num = fmaf(r.pa[i][s], wgt[h * S + s], num);
       x[j] = f2h(num / den_lds[h]);
     }
   }
@@ -226,8 +291,17 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   __shared__ float inv_den[MODE == kModeCombine ? kMaxCombineHeads : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % RS::kLPR, rsel = lane / RS::kLPR;
-  // The weight rows do not depend on the input vector: request them first, so the prologue
-  // (LayerNorm or attention combine) runs while they are in flight.
+  // Order of requests: the prologue's inputs (small, on the critical path), then this block's weight
+  // rows, which do not depend on the input vector and stay in flight while the prologue computes.
+  LnRegs<NW * 64> lnr;
+  CombineRegs<MODE == kModeCombine ? NW * 64 : 64> cbr;
+  if constexpr (MODE == kModeLn) {
+    const _Float16 *a = ln.h, *b = ln.x;
+    if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b);
+    ln_load<NW * 64>(a, b, ln.gamma, ln.beta, lnr);
+  } else if constexpr (MODE == kModeCombine) {
+    combine_load<NW * 64>(cb, cbr);
+  }
   const int row0 = blockIdx.x * kRowsPerBlock + wave * RS::kRPW * U + rsel;
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
   uint4 wr[U][RS::kC];
@@ -237,18 +311,16 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
 #pragma unroll
     for (int c = 0; c < RS::kC; ++c) {
       wr[u][c] = make_uint4(0, 0, 0, 0);
-      if (row < n) wr[u][c] = ld_stream(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + RS::kLPR * c);
+      if (row < n) wr[u][c] = ld_weights(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + RS::kLPR * c);
     }
   }
   const uint4* xv;
   if constexpr (MODE == kModeLn) {
-    const _Float16 *a = ln.h, *b = ln.x;
-    if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b);
-    ln_prologue<NW * 64>(a, b, ln.h_out, ln.gamma, ln.beta, ln.eps, y_lds, red);
+    ln_finish<NW * 64>(lnr, ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
     __syncthreads();
     xv = reinterpret_cast<const uint4*>(y_lds);
   } else if constexpr (MODE == kModeCombine) {
-    combine_prologue<NW * 64>(cb, y_lds, wgt, inv_den);
+    combine_finish<NW * 64>(cb, cbr, y_lds, wgt, inv_den);
     __syncthreads();
     xv = reinterpret_cast<const uint4*>(y_lds);
   } else {
@@ -344,15 +416,17 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
 #pragma unroll
       for (int c = 0; c < RS::kC; ++c) {
         wr[u][c] = make_uint4(0, 0, 0, 0);
-        if (row < r_end) wr[u][c] = ld_stream(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + 32 * c);
+        if (row < r_end) wr[u][c] = ld_lm_head(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + 32 * c);
       }
     }
   };
+  LnRegs<kLmNW * 64> lnr;
+  if constexpr (LN) ln_load<kLmNW * 64>(ln.h, ln.x, ln.gamma, ln.beta, lnr);
   uint4 cur[kLmU][RS::kC];
   load(r_begin, cur);
 
   if constexpr (LN) {
-    ln_prologue<kLmNW * 64>(ln.h, ln.x, nullptr, ln.gamma, ln.beta, ln.eps, y_lds, red);
+    ln_finish<kLmNW * 64>(lnr, ln.x != nullptr, nullptr, ln.eps, y_lds, red);
   } else {
     for (int i = threadIdx.x; i < kHidden / 8; i += blockDim.x)
       reinterpret_cast<uint4*>(y_lds)[i] = reinterpret_cast<const uint4*>(yin)[i];
@@ -448,9 +522,38 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   const int split = blockIdx.x, head = blockIdx.y, nsplit = gridDim.x;
   const int slot = head * nsplit + split;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pos = attn_pos(a);
-  const int len = a.len_state ? pos + 1 : a.max_len;
+  const int ks = lane >> 3, c = lane & 7;
+  const size_t hoff = static_cast<size_t>(head) * a.max_len * kHeadDim;
+  _Float16* kh = a.k + hoff;
+  _Float16* vh = a.v + hoff;
+  const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + head * kHeadDim) : nullptr;
+  const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + head * kHeadDim) : nullptr;
+  // Every wave owns a fixed run of MAXP * 8 keys of the split. All loads are issued before the
+  // cached length is known (it arrives from device memory); keys past it are masked afterwards,
+  // so the length read and the K/V reads take one memory round trip together.
   const int begin = split * a.split_keys;
+  const int w0 = begin + wave * MAXP * 8;
+  const int wend = min(min(w0 + MAXP * 8, begin + a.split_keys), a.max_len);
+  const int64_t pos_raw = a.len_state ? a.len_state[0] : 0;
+  const uint4 qc = reinterpret_cast<const uint4*>(a.q + head * kHeadDim)[c];
+  uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
+  if (kn) {
+    knew = kn[c];
+    vnew = vn[c];
+  }
+  uint4 kr[MAXP], vr[MAXP];
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    const int j = w0 + p * 8 + ks;
+    kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
+    if (j < wend) {
+      kr[p] = reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim)[c];
+      vr[p] = reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
+    }
+  }
+  const int pos = a.len_state ? static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_len ? a.max_len - 1 : pos_raw))
+                              : -1;
+  const int len = a.len_state ? pos + 1 : a.max_len;
   const int n = min(a.split_keys, len - begin);
   if (n <= 0) {
     if (tid == 0) {
@@ -459,32 +562,18 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
     }
     return;
   }
-  const size_t hoff = static_cast<size_t>(head) * a.max_len * kHeadDim;
-  _Float16* kh = a.k + hoff;
-  _Float16* vh = a.v + hoff;
-  const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + head * kHeadDim) : nullptr;
-  const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + head * kHeadDim) : nullptr;
   if (kn && pos >= begin && pos < begin + n && tid < 16) {
     if (tid < 8)
-      reinterpret_cast<uint4*>(kh + static_cast<size_t>(pos) * kHeadDim)[tid] = kn[tid];
+      reinterpret_cast<uint4*>(kh + static_cast<size_t>(pos) * kHeadDim)[tid] = knew;
     else
-      reinterpret_cast<uint4*>(vh + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = vn[tid - 8];
+      reinterpret_cast<uint4*>(vh + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = vnew;
   }
-  const int ks = lane >> 3, c = lane & 7;
-  const uint4 qc = reinterpret_cast<const uint4*>(a.q + head * kHeadDim)[c];
-  // keys dealt to the 4 waves in equal multiples of 8; all K and V chunks requested up front
-  const int per_wave = ((n + 31) / 32) * 8;
-  const int w0 = begin + wave * per_wave;
-  const int w1 = min(w0 + per_wave, begin + n);
-  uint4 kr[MAXP], vr[MAXP];
+  const int w1 = min(wend, begin + n);
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
-    const int j = w0 + p * 8 + ks;
-    kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
-    if (j < w1) {
-      const bool fresh = kn && j == pos;
-      kr[p] = fresh ? kn[c] : reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim)[c];
-      vr[p] = fresh ? vn[c] : reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
+    if (kn && w0 + p * 8 + ks == pos) {  // the new row replaces the (stale) cached one
+      kr[p] = knew;
+      vr[p] = vnew;
     }
   }
   float sc[MAXP];
