@@ -36,7 +36,10 @@ SIGNATURES = {
     'fw_gemm': (c_int, [P, c_int, P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     'fw_conv1d': (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, P, c_int, P]),
     'fw_layernorm_rows': (c_int, [P, P, P, P, c_int, c_int, c_float, P]),
-    'fw_encoder_attention': (c_int, [P, P, c_int, c_int, P]),
+    'fw_encoder_vt_elems': (ctypes.c_longlong, [c_int, c_int]),
+    'fw_encoder_qkv': (c_int, [P, P, P, P, P, c_int, c_int, P]),
+    'fw_encoder_pack_vt': (c_int, [P, P, c_int, c_int, P]),
+    'fw_encoder_attention': (c_int, [P, P, P, c_int, c_int, P]),
     'fw_cross_kv': (c_int, [P, c_int, P, P, P, c_int, c_int, P]),
     'fw_synth_normal_f16': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float, P]),
     'fw_synth_normal_f16_host': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float]),

@@ -24,6 +24,9 @@ namespace {
 // ------------------------------------------------------------------------------------------
 constexpr int kBN = 128, kBK = 64;
 constexpr int kEpiCrossKV = 100;  // internal epilogue: scatter into [layers, 2, heads, t, 64]
+// Internal epilogue of the encoder q/k/v projection: q columns scaled as FW_EPI_SCALE_Q, k columns
+// stored as they are, v columns stored transposed into vt (the attention kernel's V layout).
+constexpr int kEpiQkvVt = 101;
 
 struct GemmArgs {
   const _Float16* a;
@@ -43,6 +46,9 @@ struct GemmArgs {
   int t_in, c_in;
   // cross K/V scatter
   int heads, t_len;
+  // q/k/v projection: transposed V, [heads * 64][vt_pad]
+  _Float16* vt;
+  int vt_pad;
 };
 
 __device__ __forceinline__ float epilogue_value(int epi, float acc, float b, const GemmArgs& g, int row, int col) {
@@ -64,6 +70,7 @@ __device__ __forceinline__ float epilogue_value(int epi, float acc, float b, con
       v = round_h(gelu_erf(v)) + h2f(g.res[static_cast<size_t>(row) * g.ldr + col]);
       break;
     case FW_EPI_SCALE_Q:
+    case kEpiQkvVt:
       if (col < g.q_cols) v = v * 0.125f;
       break;
     default:
@@ -152,7 +159,11 @@ __device__ __forceinline__ void gemm_mma(const u32x4* As, const u32x4* Bs, int w
 // source side: lane l fills LDS row r0 + l / 8, slot l % 8, so it fetches chunk (l % 8) ^ (row & 7).
 // The copies are issued from inline assembly: the compiler then does not guard every LDS read with
 // a wait for all outstanding copies, and the pipeline depth is set by the explicit vmcnt waits.
-constexpr int kDmaStages = 4;  // LDS ring depth: kDmaStages - 1 stages in flight
+// The LDS ring depth ST (ST - 1 stages in flight) is picked per tile height: 128-row tiles use two
+// 32 KB stages so that two blocks share a CU and hide each other's copy latency; 64-row tiles
+// (launched when there are fewer tiles than CUs) use four 24 KB stages in one block.
+template <int BM>
+constexpr int dma_stages() { return BM == 128 ? 2 : 4; }
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
@@ -168,6 +179,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// Waits until only the copies of the `ahead` most recently issued stages may still be in flight.
+template <int kPer, int A>
+__device__ __forceinline__ void wait_stages_ahead(int ahead) {
+  if constexpr (A == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= A) wait_vmcnt<A * kPer>();
+    else wait_stages_ahead<kPer, A - 1>(ahead);
+  }
+}
 
 template <int BM>
 __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
@@ -194,8 +216,38 @@ __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int
   }
 }
 
+// Position of key t in the transposed-V layout of the encoder attention (an involution: swaps bits 2
+// and 3 of t, so the 8 keys an MFMA lane pairs with P^T are one contiguous 16-byte chunk).
+__device__ __forceinline__ int vt_pos(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
+// v columns of the q/k/v projection -> vt[head * 64 + d][vt_pos(t)]; rows in [m, vt_pad) get zeros so
+// the padding keys of the last attention tile hold finite values.
+template <int kTM, int kTN>
+__device__ __forceinline__ void store_vt(const GemmArgs& g, const f16v (&acc)[kTM][kTN], int row_base,
+                                         int col_base, int lr, int lg) {
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int col = col_base + 32 * j + lr;
+    const float b = g.bias ? h2f(g.bias[col]) : 0.f;
+    _Float16* dst = g.vt + static_cast<size_t>(col - 2 * g.q_cols) * g.vt_pad;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int row0 = row_base + 32 * i + 8 * rq + 4 * lg;  // rows row0 .. row0 + 3 stay adjacent
+        if (row0 < g.vt_pad) {
+          h4v v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = row0 + e < g.m ? f2h(acc[i][j][4 * rq + e] + b) : static_cast<_Float16>(0.f);
+          *reinterpret_cast<h4v*>(dst + vt_pos(row0)) = v;
+        }
+      }
+  }
+}
+
 template <int BM, int EPI>
 __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
+  constexpr int kDmaStages = dma_stages<BM>();
   constexpr int kWM = BM / 2, kTM = kWM / 32, kTN = 2;
   constexpr int kStageBytes = (BM + kBN) * 128;
   constexpr int kPerStage = (BM / 8 / 4) + (kBN / 8 / 4);  // copies per thread per stage
@@ -224,10 +276,7 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
     if (s < kt_n) dma_stage<BM>(g, m0, n0, s * kBK, wave, lane, lds0 + s * kStageBytes);
   for (int kt = 0; kt < kt_n; ++kt) {
     // this thread's copies of stage kt have landed once at most the later in-flight stages remain
-    const int ahead = min(kDmaStages - 2, kt_n - 1 - kt);
-    if (ahead >= 2) wait_vmcnt<2 * kPerStage>();
-    else if (ahead == 1) wait_vmcnt<kPerStage>();
-    else wait_vmcnt<0>();
+    wait_stages_ahead<kPerStage, kDmaStages - 2>(min(kDmaStages - 2, kt_n - 1 - kt));
     barrier_only();  // stage kt visible to every wave; every wave is done with stage kt - 1
     const int nxt = kt + kDmaStages - 1;
     if (nxt < kt_n) dma_stage<BM>(g, m0, n0, nxt * kBK, wave, lane, lds0 + (nxt % kDmaStages) * kStageBytes);
@@ -235,6 +284,12 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
     gemm_mma<kTM, kTN>(As, As + BM * 8, wm, wn, lr, lg, acc);
   }
 
+  if constexpr (EPI == kEpiQkvVt) {
+    if (n0 >= 2 * g.q_cols) {  // a v column tile (q_cols % 128 == 0)
+      store_vt<kTM, kTN>(g, acc, m0 + wm, n0 + wn, lr, lg);
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
     const int col = n0 + wn + 32 * j + lr;
@@ -357,6 +412,7 @@ int launch_gemm_bm(const GemmArgs& g, int epi, hipStream_t s) {
     FW_GEMM_CASE(FW_EPI_BIAS_GELU_POS)
     FW_GEMM_CASE(FW_EPI_SCALE_Q)
     FW_GEMM_CASE(kEpiCrossKV)
+    FW_GEMM_CASE(kEpiQkvVt)
 #undef FW_GEMM_CASE
     default:
       return fw_fail(FW_EINVAL, "gemm: unknown epilogue %d", epi);
@@ -422,38 +478,72 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __r
 }
 
 // ------------------------------------------------------------------------------------------
-// Encoder self-attention, flash style. Block = (head, 64 queries), 2 waves of 32 queries each.
-// Per 64-key tile a wave computes S^T = K Q^T (keys x queries) with MFMA so that every lane holds
-// scores of a single query column: the online-softmax max/sum need one cross-lane step (lane ^ 32).
-// P^T is fed straight from the S^T accumulator layout as the B operand of O^T = V^T P^T; the
-// A operand V^T comes from an LDS copy of the V tile stored transposed, read with the same key
-// permutation, so no register shuffles are needed between the two products.
+// Encoder self-attention, flash style, non-causal, scale 1 (q is pre-scaled by the projection).
+// Block = (head, 128 queries): 4 waves of 32 queries each share one LDS ring of 64-key tiles. Per
+// tile a wave computes S^T = K Q^T (keys x queries) with MFMA, so that every lane holds the scores
+// of a single query column and the online-softmax max/sum need one cross-lane step (lane ^ 32).
+// P^T is fed straight from the S^T accumulator layout as the B operand of O^T = V^T P^T.
+//  - Inputs: q and k from the projection output qkv[seq, 3 * heads * 64]; V from a transposed copy
+//    vt[heads][64][seq_pad] written by the projection's epilogue, whose key order inside every
+//    16-key group has bits 2 and 3 of the key index swapped. With that order the 8 keys an MFMA
+//    A-operand lane needs for V^T are one contiguous 16-byte chunk, and they are the keys the
+//    same lane holds for P^T in the S^T accumulator (rows 8 (r / 4) + 4 g + (r % 4)).
+//  - K tiles (64 keys x 128 B) and V^T tiles (64 d x 128 B) arrive by direct-to-LDS copies into a
+//    ring of kEaStages stages, XOR-swizzled by 16-byte chunk like the GEMM tiles.
+//  - Block ids are remapped so that the query blocks of a head run on one XCD and its K/V stay in
+//    that XCD's L2.
 // ------------------------------------------------------------------------------------------
-constexpr int kAttnQ = 64, kAttnKV = 64, kVtStride = kAttnKV + 8;
+constexpr int kEaWaves = 4, kEaQ = 32 * kEaWaves, kEaKV = 64, kEaStages = 4;
+constexpr int kEaTileBytes = kEaKV * 128;  // one K tile or one V^T tile
 
-__global__ void __launch_bounds__(128) encoder_attention_kernel(const _Float16* __restrict__ qkv,
+__device__ __forceinline__ void ea_dma(const _Float16* kbase, int ld, const _Float16* vtbase, int seq_pad,
+                                       int seq, int kv0, int wave, int lane, uint32_t stage) {
+  const int rsub = lane >> 3, slot = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // K tile: wave fills 8-row blocks 2 wave and 2 wave + 1
+    const int blk = 2 * wave + i, row = blk * 8 + rsub;
+    const int key = min(kv0 + row, seq - 1);  // keys past seq are masked to -inf
+    dma16(kbase + static_cast<size_t>(key) * ld + (slot ^ (row & 7)) * 8,
+          __builtin_amdgcn_readfirstlane(stage + blk * 1024));
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // V^T tile: rows are head dims
+    const int blk = 2 * wave + i, d = blk * 8 + rsub;
+    dma16(vtbase + static_cast<size_t>(d) * seq_pad + kv0 + (slot ^ (d & 7)) * 8,
+          __builtin_amdgcn_readfirstlane(stage + kEaTileBytes + blk * 1024));
+  }
+}
+
+__global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* __restrict__ qkv,
+                                                                const _Float16* __restrict__ vt,
                                                                 _Float16* __restrict__ out, int seq, int heads) {
-  __shared__ __align__(16) _Float16 vt[kHeadDim][kVtStride];  // V tile transposed: [d][key]
-  const int head = blockIdx.y;
+  constexpr int kPerStage = 4;  // copies per thread per stage
+  __shared__ __align__(1024) u32x4 ring[kEaStages * 2 * kEaTileBytes / 16];
+
+  const int qblocks = (seq + kEaQ - 1) / kEaQ, nblk = qblocks * heads;
+  const int bid = blockIdx.x, full = (nblk / 8) * 8;
+  const int job = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+  const int head = job / qblocks, qb = job % qblocks;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, lg = lane >> 5;
-  const int ld = 3 * heads * kHeadDim;
-  const int q_row = blockIdx.x * kAttnQ + wave * 32 + lr;  // this lane's query column
-  const _Float16* qbase = qkv + head * kHeadDim;
+  const int ld = 3 * heads * kHeadDim, seq_pad = (seq + kEaKV - 1) / kEaKV * kEaKV;
+  const int q_row = qb * kEaQ + wave * 32 + lr;  // this lane's query column
   const _Float16* kbase = qkv + (heads + head) * kHeadDim;
-  const _Float16* vbase = qkv + (2 * heads + head) * kHeadDim;
+  const _Float16* vtbase = vt + static_cast<size_t>(head) * kHeadDim * seq_pad;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
 
   // Q^T as B operand: lane holds Q[q_row][16 s + 8 lg .. + 7] for s = 0..3.
   h8v qf[4];
+  {
+    const _Float16* qp = qkv + static_cast<size_t>(min(q_row, seq - 1)) * ld + head * kHeadDim + 8 * lg;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (q_row < seq) {
-      qf[s] = *reinterpret_cast<const h8v*>(qbase + static_cast<size_t>(q_row) * ld + 16 * s + 8 * lg);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = static_cast<_Float16>(0.f);
-    }
+    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const h8v*>(qp + 16 * s);
   }
+  const int nt = seq_pad / kEaKV;
+#pragma unroll
+  for (int st = 0; st < kEaStages - 1; ++st)
+    if (st < nt) ea_dma(kbase, ld, vtbase, seq_pad, seq, st * kEaKV, wave, lane, lds0 + st * 2 * kEaTileBytes);
+
   f16v o[2];  // O^T blocks: d in [0, 32) and [32, 64)
 #pragma unroll
   for (int b = 0; b < 2; ++b)
@@ -462,34 +552,27 @@ __global__ void __launch_bounds__(128) encoder_attention_kernel(const _Float16* 
   float m_run = -INFINITY, l_run = 0.f;
   constexpr float kLog2e = 1.4426950408889634f;
 
-  for (int kv0 = 0; kv0 < seq; kv0 += kAttnKV) {
-    __syncthreads();  // previous tile's vt reads are done
-    // Stage V tile transposed: 64 keys x 64 d; thread loads 16-byte chunks of V rows.
-    for (int c = tid; c < kAttnKV * 8; c += 128) {
-      const int key = c >> 3, d0 = (c & 7) * 8;
-      uint4 u = make_uint4(0, 0, 0, 0);
-      if (kv0 + key < seq) u = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(kv0 + key) * ld + d0);
-      const _Float16* hp = reinterpret_cast<const _Float16*>(&u);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt[d0 + e][key] = hp[e];
-    }
+  for (int t = 0; t < nt; ++t) {
+    wait_stages_ahead<kPerStage, kEaStages - 2>(min(kEaStages - 2, nt - 1 - t));
+    barrier_only();  // tile t visible to every wave; every wave is done with tile t - 1
+    const int nxt = t + kEaStages - 1;
+    if (nxt < nt)
+      ea_dma(kbase, ld, vtbase, seq_pad, seq, nxt * kEaKV, wave, lane, lds0 + (nxt % kEaStages) * 2 * kEaTileBytes);
+    const u32x4* kt = ring + (t % kEaStages) * (2 * kEaTileBytes / 16);
+    const u32x4* vtt = kt + kEaTileBytes / 16;
+    const int kv0 = t * kEaKV;
+
     // S^T = K Q^T for two 32-key blocks.
     f16v s[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
-      const int key = kv0 + 32 * b + lr;
+      const int row = 32 * b + lr;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        h8v kf;
-        if (key < seq) {
-          kf = *reinterpret_cast<const h8v*>(kbase + static_cast<size_t>(key) * ld + 16 * st + 8 * lg);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kf[e] = static_cast<_Float16>(0.f);
-        }
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[b], 0, 0, 0);
+        const u32x4 u = kt[swz(row, 2 * st + lg)];
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, u), qf[st], s[b], 0, 0, 0);
       }
     }
     // Mask keys beyond seq; running max over this lane's 32 scores and the partner lane.
@@ -498,21 +581,20 @@ __global__ void __launch_bounds__(128) encoder_attention_kernel(const _Float16* 
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kv0 + 32 * b + 8 * (r >> 2) + 4 * lg + (r & 3);
-        if (key >= seq) s[b][r] = -INFINITY;
+        if (kv0 + kEaKV > seq && kv0 + 32 * b + 8 * (r >> 2) + 4 * lg + (r & 3) >= seq) s[b][r] = -INFINITY;
         tmax = fmaxf(tmax, s[b][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
     const float m_new = fmaxf(m_run, tmax);
     const float corr = exp2f((m_run - m_new) * kLog2e);
+    const float mb = m_new * kLog2e;
     float psum = 0.f;
     h8v pf[2][2];  // P^T as B operand, [32-key block][k-step of 16 keys]
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f((s[b][r] - m_new) * kLog2e);
-        const _Float16 ph = f2h(p);
+        const _Float16 ph = f2h(exp2f(fmaf(s[b][r], kLog2e, -mb)));
         psum += h2f(ph);
         pf[b][r >> 3][r & 7] = ph;
       }
@@ -523,30 +605,17 @@ __global__ void __launch_bounds__(128) encoder_attention_kernel(const _Float16* 
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[b][r] *= corr;
-    __syncthreads();  // vt staged
-    // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]. For k-step (b, h) the lane half lg holds keys
-    // 32 b + 16 h + {4 lg .. 4 lg + 3} and 32 b + 16 h + 8 + {4 lg .. 4 lg + 3} (accumulator order).
+    // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]; k-step (b, hs) covers keys 32 b + 16 hs + [0, 16),
+    // whose transposed-layout chunk for lane half lg is chunk 4 b + 2 hs + lg of the V^T row.
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int hs = 0; hs < 2; ++hs) {
-        const int kb = 32 * b + 16 * hs + 4 * lg;
+      for (int hs = 0; hs < 2; ++hs)
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
-          const int d = 32 * db + lr;
-          h8v vf;
-          const uint2 lo = *reinterpret_cast<const uint2*>(&vt[d][kb]);
-          const uint2 hi = *reinterpret_cast<const uint2*>(&vt[d][kb + 8]);
-          const _Float16* lp = reinterpret_cast<const _Float16*>(&lo);
-          const _Float16* hp = reinterpret_cast<const _Float16*>(&hi);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            vf[e] = lp[e];
-            vf[4 + e] = hp[e];
-          }
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[b][hs], o[db], 0, 0, 0);
+          const u32x4 u = vtt[swz(32 * db + lr, 4 * b + 2 * hs + lg)];
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, u), pf[b][hs], o[db], 0, 0, 0);
         }
-      }
   }
   if (q_row >= seq) return;
   const float inv = 1.0f / l_run;
@@ -554,7 +623,24 @@ __global__ void __launch_bounds__(128) encoder_attention_kernel(const _Float16* 
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) orow[32 * db + 8 * (r >> 2) + 4 * lg + (r & 3)] = f2h(o[db][r] * inv);
+    for (int j = 0; j < 4; ++j) {
+      h4v v4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = f2h(o[db][4 * j + e] * inv);
+      *reinterpret_cast<h4v*>(orow + 32 * db + 8 * j + 4 * lg) = v4;
+    }
+}
+
+// Transposed V for the attention kernel from a projection output (qkv v columns).
+__global__ void __launch_bounds__(256) pack_vt_kernel(const _Float16* __restrict__ qkv, _Float16* __restrict__ vt,
+                                                      int seq, int heads) {
+  const int seq_pad = (seq + kEaKV - 1) / kEaKV * kEaKV;
+  const int i = blockIdx.x * 256 + threadIdx.x;  // over heads * 64 * seq_pad
+  if (i >= heads * kHeadDim * seq_pad) return;
+  const int pos = i % seq_pad, hd = i / seq_pad;  // hd = head * 64 + d
+  const int t = vt_pos(pos);
+  vt[i] = t < seq ? qkv[static_cast<size_t>(t) * 3 * heads * kHeadDim + 2 * heads * kHeadDim + hd]
+                  : static_cast<_Float16>(0.f);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -609,12 +695,44 @@ extern "C" int fw_layernorm_rows(const void* x, const void* gamma, const void* b
   return fw_check_launch("layernorm_rows");
 }
 
-extern "C" int fw_encoder_attention(const void* qkv, void* out, int seq, int heads, hipStream_t stream) {
-  if (!qkv || !out) return fw_fail(FW_EINVAL, "encoder_attention: null pointer");
+extern "C" long long fw_encoder_vt_elems(int seq, int heads) {
+  if (seq <= 0 || heads <= 0) return 0;
+  return static_cast<long long>(heads) * kHeadDim * ((seq + kEaKV - 1) / kEaKV * kEaKV);
+}
+
+extern "C" int fw_encoder_qkv(const void* y, const void* w, const void* bias, void* qkv, void* vt, int seq, int heads,
+                              hipStream_t stream) {
+  if (!y || !w || !qkv || !vt) return fw_fail(FW_EINVAL, "encoder_qkv: null pointer");
+  const int d = heads * kHeadDim;
+  if (seq <= 0 || heads <= 0 || d % kBN || d % kBK)
+    return fw_fail(FW_EINVAL, "encoder_qkv: need seq > 0 and heads * 64 a multiple of %d (seq=%d heads=%d)", kBN, seq,
+                   heads);
+  if (!aligned16(y) || !aligned16(w)) return fw_fail(FW_EINVAL, "encoder_qkv: y and w must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(vt) & 7u) return fw_fail(FW_EINVAL, "encoder_qkv: vt must be 8-byte aligned");
+  GemmArgs g{static_cast<const _Float16*>(y), d, static_cast<const _Float16*>(w), d,
+             static_cast<const _Float16*>(bias), static_cast<_Float16*>(qkv), 3 * d, nullptr, 0, seq, 3 * d, d, d,
+             0, 0, 0, heads, seq, static_cast<_Float16*>(vt), (seq + kEaKV - 1) / kEaKV * kEaKV};
+  return launch_gemm(g, kEpiQkvVt, stream);
+}
+
+extern "C" int fw_encoder_pack_vt(const void* qkv, void* vt, int seq, int heads, hipStream_t stream) {
+  if (!qkv || !vt) return fw_fail(FW_EINVAL, "encoder_pack_vt: null pointer");
+  if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_pack_vt: seq and heads must be positive");
+  const long long n = fw_encoder_vt_elems(seq, heads);
+  hipLaunchKernelGGL(pack_vt_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const _Float16*>(qkv), static_cast<_Float16*>(vt), seq, heads);
+  return fw_check_launch("encoder_pack_vt");
+}
+
+extern "C" int fw_encoder_attention(const void* qkv, const void* vt, void* out, int seq, int heads,
+                                    hipStream_t stream) {
+  if (!qkv || !vt || !out) return fw_fail(FW_EINVAL, "encoder_attention: null pointer");
   if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_attention: seq and heads must be positive");
-  if (!aligned16(qkv)) return fw_fail(FW_EINVAL, "encoder_attention: qkv must be 16-byte aligned");
-  hipLaunchKernelGGL(encoder_attention_kernel, dim3((seq + kAttnQ - 1) / kAttnQ, heads), dim3(128), 0, stream,
-                     static_cast<const _Float16*>(qkv), static_cast<_Float16*>(out), seq, heads);
+  if (!aligned16(qkv) || !aligned16(vt) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fw_fail(FW_EINVAL, "encoder_attention: qkv and vt must be 16-byte aligned, out 8-byte aligned");
+  const int blocks = (seq + kEaQ - 1) / kEaQ * heads;
+  hipLaunchKernelGGL(encoder_attention_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<const _Float16*>(qkv),
+                     static_cast<const _Float16*>(vt), static_cast<_Float16*>(out), seq, heads);
   return fw_check_launch("encoder_attention");
 }
 

@@ -15,6 +15,7 @@ constexpr int kHeadDim = 64;      // d_model / heads
 constexpr int kSplitKeys = 64;    // keys per split block (reference kSplitKeys)
 
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));

@@ -274,13 +274,44 @@ class WhisperExt:
         self._call('fw_layernorm_rows', x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(), x.size(0),
                    HIDDEN, float(eps), _stream())
 
-    def encoder_attention(self, qkv, out, heads):
+    def encoder_vt_workspace(self, seq, heads):
+        """Transposed-V buffer for encoder_qkv / encoder_pack_vt / encoder_attention (layout private)."""
+        n = self.lib.fw_encoder_vt_elems(seq, heads)
+        _require(n > 0, 'encoder_vt_workspace: seq and heads must be positive')
+        return torch.zeros(n, dtype=torch.float16, device='cuda')
+
+    def _check_vt(self, vt, seq, heads):
+        check_half(vt, 'vt')
+        _require(vt.numel() == self.lib.fw_encoder_vt_elems(seq, heads), 'vt must hold fw_encoder_vt_elems(seq, heads)')
+
+    def encoder_qkv(self, y, w, bias, qkv, vt, heads):
+        """q/k/v projection of an encoder layer: q (scaled by 1/8) and k into qkv, v into vt."""
+        for t, n in ((y, 'y'), (w, 'w'), (qkv, 'qkv')):
+            check_half(t, n)
+        seq, d = y.shape
+        _require(d == heads * HEAD_DIM and w.shape == (3 * d, d) and qkv.shape == (seq, 3 * d),
+                 'encoder_qkv shape mismatch')
+        if bias is not None:
+            check_half(bias, 'bias')
+        self._check_vt(vt, seq, heads)
+        self._call('fw_encoder_qkv', y.data_ptr(), w.data_ptr(), _ptr(bias), qkv.data_ptr(), vt.data_ptr(), seq, heads,
+                   _stream())
+
+    def encoder_pack_vt(self, qkv, vt, heads):
+        check_half(qkv, 'qkv')
+        seq = qkv.size(0)
+        _require(qkv.shape == (seq, 3 * heads * HEAD_DIM), 'encoder_pack_vt shape mismatch')
+        self._check_vt(vt, seq, heads)
+        self._call('fw_encoder_pack_vt', qkv.data_ptr(), vt.data_ptr(), seq, heads, _stream())
+
+    def encoder_attention(self, qkv, vt, out, heads):
         check_half(qkv, 'qkv')
         check_half(out, 'out')
         seq = qkv.size(0)
         _require(qkv.shape == (seq, 3 * heads * HEAD_DIM) and out.shape == (seq, heads * HEAD_DIM),
                  'encoder_attention shape mismatch')
-        self._call('fw_encoder_attention', qkv.data_ptr(), out.data_ptr(), seq, heads, _stream())
+        self._check_vt(vt, seq, heads)
+        self._call('fw_encoder_attention', qkv.data_ptr(), vt.data_ptr(), out.data_ptr(), seq, heads, _stream())
 
     def cross_kv(self, enc, w, bias, cross_kv):
         check_half(enc, 'enc')

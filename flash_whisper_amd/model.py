@@ -118,6 +118,7 @@ class CustomModel:
         self.ey = torch.empty(t, dm, dtype=half, device='cuda')        # LayerNorm output
         self.eqkv = torch.empty(t, 3 * dm, dtype=half, device='cuda')
         self.eattn = torch.empty(t, dm, dtype=half, device='cuda')
+        self.evt = self.ext.encoder_vt_workspace(t, self.heads)
         self.effn = torch.empty(t, d.ffn, dtype=half, device='cuda')
         self.enc_out = torch.empty(t, dm, dtype=half, device='cuda')
 
@@ -200,8 +201,8 @@ class CustomModel:
         ext.conv1d(self.x1, 2, self.conv2_wp, self.conv2_b, self.ex, EPI_BIAS_GELU_POS, res=self.enc_pos)
         for lay in self.enc_layers:
             ext.layernorm_rows(self.ex, lay.ln1[0], lay.ln1[1], self.ey, lay.ln1[2])
-            ext.gemm(self.ey, lay.qkv_w, lay.qkv_b, self.eqkv, EPI_SCALE_Q, q_cols=self.dims.d_model)
-            ext.encoder_attention(self.eqkv, self.eattn, nh)
+            ext.encoder_qkv(self.ey, lay.qkv_w, lay.qkv_b, self.eqkv, self.evt, nh)
+            ext.encoder_attention(self.eqkv, self.evt, self.eattn, nh)
             ext.gemm(self.eattn, lay.out_w, lay.out_b, self.ex, EPI_BIAS_RESID, res=self.ex)
             ext.layernorm_rows(self.ex, lay.ln2[0], lay.ln2[1], self.ey, lay.ln2[2])
             ext.gemm(self.ey, lay.fc1_w, lay.fc1_b, self.effn, EPI_BIAS_GELU)

@@ -152,9 +152,26 @@ int fw_conv1d(const void* x, int t_in, int c_in, int stride, const void* wp, con
 int fw_layernorm_rows(const void* x, const void* gamma, const void* beta, void* y, int rows, int n, float eps,
                       hipStream_t stream);
 
-/* Encoder self-attention (non-causal, scale 1: q is pre-scaled): qkv fp16[seq, 3 * heads * 64] as
- * [q | k | v] per row; out fp16[seq, heads * 64]. */
-int fw_encoder_attention(const void* qkv, void* out, int seq, int heads, hipStream_t stream);
+/* Element count of the transposed-V buffer `vt` of the encoder attention: heads * 64 * seq_pad,
+ * seq_pad = seq rounded up to a multiple of 64 (0 for non-positive arguments). The layout inside is
+ * private to this library: fill it with fw_encoder_qkv or fw_encoder_pack_vt. */
+long long fw_encoder_vt_elems(int seq, int heads);
+
+/* Encoder q/k/v projection of one layer (transformers modeling_whisper.py:309-311 with
+ * custom/model.py:81-91's [q; k; v] packing): y fp16[seq, heads * 64] times w fp16[3 * heads * 64,
+ * heads * 64] plus bias. q columns are scaled by 1/8 after the fp16 rounding (FW_EPI_SCALE_Q);
+ * q and k go to qkv fp16[seq, 3 * heads * 64] (its v columns are left untouched); v goes to vt
+ * (fw_encoder_vt_elems). heads * 64 % 128 == 0. */
+int fw_encoder_qkv(const void* y, const void* w, const void* bias, void* qkv, void* vt, int seq, int heads,
+                   hipStream_t stream);
+
+/* vt from the v columns of a q/k/v projection output qkv fp16[seq, 3 * heads * 64]. */
+int fw_encoder_pack_vt(const void* qkv, void* vt, int seq, int heads, hipStream_t stream);
+
+/* Encoder self-attention (transformers modeling_whisper.py:284-358, SDPA, non-causal, scale 1: q is
+ * pre-scaled): q and k from qkv fp16[seq, 3 * heads * 64] ([q | k | v] per row), v from vt;
+ * out fp16[seq, heads * 64]. */
+int fw_encoder_attention(const void* qkv, const void* vt, void* out, int seq, int heads, hipStream_t stream);
 
 /* Cross K/V for all decoder layers (custom/model.py:145-146) written straight into the cache layout:
  * enc fp16[t, 1280]; w fp16[layers * 2 * 1280, 1280] rows [k_0; v_0; k_1; v_1; ...];

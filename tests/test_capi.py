@@ -14,13 +14,14 @@ from conftest import ROOT
 
 def declared_symbols():
     text = (ROOT / 'include' / 'flash_whisper.h').read_text()
-    return sorted(set(re.findall(r'^\s*(?:const\s+)?\w+\*?\s+\**(fw_\w+)\s*\(', text, re.M)))
+    return sorted(set(re.findall(r'^\s*(?:const\s+)?(?:\w+\s+)*\w+\*?\s+\**(fw_\w+)\s*\(', text, re.M)))
 
 
 def test_header_declares_entry_points():
     syms = declared_symbols()
     for s in ('fw_lm_head_argmax', 'fw_argmax_finalize', 'fw_decode_attention', 'fw_add_layernorm',
-              'fw_log_mel', 'fw_gemm', 'fw_conv1d', 'fw_encoder_attention', 'fw_cross_kv'):
+              'fw_log_mel', 'fw_gemm', 'fw_conv1d', 'fw_encoder_qkv', 'fw_encoder_pack_vt', 'fw_encoder_attention',
+              'fw_encoder_vt_elems', 'fw_cross_kv'):
         assert s in syms
 
 
@@ -53,6 +54,10 @@ def test_validation_errors_return_einval(built_lib):
     rc = lib.fw_gemm(dummy, 1280, dummy, 1280, None, dummy, 1280, None, 0, 1500, 1280, 1280, 2, 0, None)
     assert rc == _lib.FW_EINVAL and b'needs res' in lib.fw_last_error()
     assert lib.fw_log_mel(dummy, 100, dummy, dummy, None, dummy, 100, None) == _lib.FW_EINVAL
+    rc = lib.fw_encoder_qkv(dummy, dummy, None, dummy, dummy, 1500, 3, None)  # 3 * 64 is not a multiple of 128
+    assert rc == _lib.FW_EINVAL and b'multiple of 128' in lib.fw_last_error()
+    assert lib.fw_encoder_attention(dummy, None, dummy, 1500, 20, None) == _lib.FW_EINVAL
+    assert lib.fw_encoder_vt_elems(1500, 20) == 20 * 64 * 1536 and lib.fw_encoder_vt_elems(0, 20) == 0
 
 
 def test_status_becomes_runtime_error(built_lib):

@@ -1,5 +1,5 @@
 """GPU parity of the encoder kernels (MFMA GEMM + epilogues, implicit-GEMM conv stem, row LayerNorm,
-flash encoder attention, cross K/V scatter) against the CPU oracle. Tolerance as in
+q/k/v projection with transposed V, flash encoder attention, cross K/V scatter) against the CPU oracle. Tolerance as in
 test_gpu_decode.close_rel: 2e-3 relative in fp16, elementwise with an rms floor."""
 
 import numpy as np
@@ -119,7 +119,8 @@ def _attn_ref(qkv, heads):
     return f16((p @ v).transpose(1, 0, 2).reshape(seq, d))
 
 
-@pytest.mark.parametrize('seq,heads,qscale', [(1500, 20, 0.125), (100, 2, 0.125), (1500, 20, 0.6), (33, 1, 0.3)])
+@pytest.mark.parametrize('seq,heads,qscale', [(1500, 20, 0.125), (100, 2, 0.125), (1500, 20, 0.6), (33, 1, 0.3),
+                                               (1496, 3, 0.2), (1, 2, 0.125), (64, 1, 0.5), (129, 2, 0.125)])
 def test_encoder_attention(ext, hip_device, seq, heads, qscale):
     dev = hip_device
     rng = np.random.default_rng(seq + heads)
@@ -127,8 +128,34 @@ def test_encoder_attention(ext, hip_device, seq, heads, qscale):
     qkv[:, :heads * 64] *= qscale  # q arrives pre-scaled; a larger scale sharpens the softmax
     qkv = np.float16(qkv)
     out = torch.empty(seq, heads * 64, dtype=torch.float16, device=dev)
-    ext.encoder_attention(h16(qkv, dev), out, heads)
+    tq = h16(qkv, dev)
+    vt = ext.encoder_vt_workspace(seq, heads)
+    vt.fill_(float('nan'))  # every element, padding included, must be rewritten
+    ext.encoder_pack_vt(tq, vt, heads)
+    assert not torch.isnan(vt).any()
+    ext.encoder_attention(tq, vt, out, heads)
     close_rel(np32(out), _attn_ref(qkv, heads))
+
+
+@pytest.mark.parametrize('m', [1500, 77, 1])
+def test_encoder_qkv_matches_gemm_and_pack(ext, hip_device, m):
+    """The fused q/k/v projection writes the FW_EPI_SCALE_Q GEMM's q and k columns and, for v, exactly
+    what fw_encoder_pack_vt makes of that GEMM's v columns (padding keys zero)."""
+    dev = hip_device
+    rng = np.random.default_rng(m)
+    y = h16(np.float16(rng.standard_normal((m, 1280))), dev)
+    w = h16(np.float16(0.02 * rng.standard_normal((3840, 1280))), dev)
+    b = h16(np.float16(0.02 * rng.standard_normal(3840)), dev)
+    ref = torch.empty(m, 3840, dtype=torch.float16, device=dev)
+    ext.gemm(y, w, b, ref, 5, q_cols=1280)
+    vt_ref = ext.encoder_vt_workspace(m, 20)
+    ext.encoder_pack_vt(ref, vt_ref, 20)
+    qkv = torch.full((m, 3840), 7.0, dtype=torch.float16, device=dev)
+    vt = torch.full_like(vt_ref, float('nan'))
+    ext.encoder_qkv(y, w, b, qkv, vt, 20)
+    assert torch.equal(qkv[:, :2560], ref[:, :2560])
+    assert torch.equal(qkv[:, 2560:], torch.full_like(qkv[:, 2560:], 7.0))  # v columns untouched
+    assert torch.equal(vt, vt_ref)
 
 
 def test_cross_kv_layout(ext, hip_device):
@@ -178,8 +205,8 @@ def test_encoder_layer_and_stem_vs_oracle(ext, hip_device):
     model.ex.copy_(torch.from_numpy(stem.astype(np.float16)))
     lay = model.enc_layers[0]
     ext.layernorm_rows(model.ex, lay.ln1[0], lay.ln1[1], model.ey, lay.ln1[2])
-    ext.gemm(model.ey, lay.qkv_w, lay.qkv_b, model.eqkv, 5, q_cols=1280)
-    ext.encoder_attention(model.eqkv, model.eattn, 20)
+    ext.encoder_qkv(model.ey, lay.qkv_w, lay.qkv_b, model.eqkv, model.evt, 20)
+    ext.encoder_attention(model.eqkv, model.evt, model.eattn, 20)
     ext.gemm(model.eattn, lay.out_w, lay.out_b, model.ex, 2, res=model.ex)
     ext.layernorm_rows(model.ex, lay.ln2[0], lay.ln2[1], model.ey, lay.ln2[2])
     ext.gemm(model.ey, lay.fc1_w, lay.fc1_b, model.effn, 1)
