@@ -29,7 +29,11 @@ COMMON_FLAGS = [
     '-Xarch_host', '-mfma',
 ]
 # The synthetic-weight generator must round identically on host and device: no FMA contraction.
-PER_FILE_FLAGS = {'synth.hip': ['-ffp-contract=off']}
+PER_FILE_FLAGS = {
+    'synth.hip': ['-ffp-contract=off'],
+    # MFMA results in VGPRs: the attention softmax reads every score and rescales O in place
+    'attention_enc.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form'],
+}
 
 
 def sources():

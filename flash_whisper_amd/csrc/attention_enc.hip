@@ -1,0 +1,236 @@
+// Whisper encoder self-attention for gfx950 (transformers models/whisper/modeling_whisper.py:284-358,
+// SDPA path, fp16 in and out, fp32 softmax and accumulation), plus the transposed-V packing it reads.
+// Built with MFMA results in VGPRs (-mllvm -amdgpu-mfma-vgpr-form): the softmax reads every score and
+// the O accumulators are rescaled in place, which in the AGPR form costs a register move per value.
+#include "lds_pipe.h"
+
+namespace fw {
+namespace {
+
+// ------------------------------------------------------------------------------------------
+// Encoder self-attention, flash style, non-causal, scale 1 (q is pre-scaled by the projection).
+// Block = (head, 128 queries): 4 waves of 32 queries each share one LDS ring of 64-key tiles. Per
+// tile a wave computes S^T = K Q^T (keys x queries) with MFMA, so that every lane holds the scores
+// of a single query column and the online-softmax max/sum need one cross-lane step (lane ^ 32).
+// P^T is fed straight from the S^T accumulator layout as the B operand of O^T = V^T P^T.
+//  - Inputs: q and k from the projection output qkv[seq, 3 * heads * 64]; V from a transposed copy
+//    vt[heads][64][seq_pad] written by the projection's epilogue, whose key order inside every
+//    16-key group has bits 2 and 3 of the key index swapped. With that order the 8 keys an MFMA
+//    A-operand lane needs for V^T are one contiguous 16-byte chunk, and they are the keys the
+//    same lane holds for P^T in the S^T accumulator (rows 8 (r / 4) + 4 g + (r % 4)).
+//  - K tiles (64 keys x 128 B) and V^T tiles (64 d x 128 B) arrive by direct-to-LDS copies into a
+//    ring of kEaStages stages, XOR-swizzled by 16-byte chunk like the GEMM tiles.
+//  - Block ids are remapped so that the query blocks of a head run on one XCD and its K/V stay in
+//    that XCD's L2.
+// ------------------------------------------------------------------------------------------
+constexpr int kEaWaves = 4, kEaQ = 32 * kEaWaves, kEaKV = 64, kEaStages = 4;
+constexpr int kEaTileBytes = kEaKV * 128;  // one K tile or one V^T tile
+
+__device__ __forceinline__ void ea_dma(const _Float16* kbase, int ld, const _Float16* vtbase, int seq_pad,
+                                       int seq, int kv0, int wave, int lane, uint32_t stage) {
+  const int rsub = lane >> 3, slot = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // K tile: wave fills 8-row blocks 2 wave and 2 wave + 1
+    const int blk = 2 * wave + i, row = blk * 8 + rsub;
+    const int key = min(kv0 + row, seq - 1);  // keys past seq are masked to -inf
+    dma16(kbase + static_cast<size_t>(key) * ld + (slot ^ (row & 7)) * 8,
+          __builtin_amdgcn_readfirstlane(stage + blk * 1024));
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // V^T tile: rows are head dims
+    const int blk = 2 * wave + i, d = blk * 8 + rsub;
+    dma16(vtbase + static_cast<size_t>(d) * seq_pad + kv0 + (slot ^ (d & 7)) * 8,
+          __builtin_amdgcn_readfirstlane(stage + kEaTileBytes + blk * 1024));
+  }
+}
+
+// Scores are kept in log2 units (x log2 e). The running max m used for p = exp2(s - m) is only moved
+// when some lane of the wave sees a score more than kEaSlack above it, so p stays in [0, 2^kEaSlack]
+// (exact in fp16's range) and the O/l rescale runs on few tiles instead of every tile.
+constexpr float kEaSlack = 8.f;
+
+struct EaState {
+  f16v o[2];  // O^T blocks: d in [0, 32) and [32, 64)
+  float m, l;
+};
+
+template <bool kMask>
+__device__ __forceinline__ void ea_tile(const u32x4* kt, const u32x4* vtt, const h8v (&qf)[4], int kv0, int seq,
+                                        int lr, int lg, EaState& st) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  // S^T = K Q^T for two 32-key blocks.
+  f16v s[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
+    const int row = 32 * b + lr;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const u32x4 u = kt[swz(row, 2 * k + lg)];
+      s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, u), qf[k], s[b], 0, 0, 0);
+    }
+  }
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if constexpr (kMask) {
+        if (kv0 + 32 * b + 8 * (r >> 2) + 4 * lg + (r & 3) >= seq) s[b][r] = -INFINITY;
+      }
+      tmax = fmaxf(tmax, s[b][r]);
+    }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * kLog2e;
+  if (__builtin_amdgcn_ballot_w64(tmax > st.m + kEaSlack)) {  // wave-uniform
+    const float m_new = fmaxf(st.m, tmax);
+    const float corr = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first tile (m = -inf)
+    st.l *= corr;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st.o[b][r] *= corr;
+    st.m = m_new;
+  }
+  h8v pf[2][2];  // P^T as B operand, [32-key block][k-step of 16 keys]
+  float psum = 0.f;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      h2v ph;
+      ph[0] = f2h(__builtin_amdgcn_exp2f(fmaf(s[b][r], kLog2e, -st.m)));
+      ph[1] = f2h(__builtin_amdgcn_exp2f(fmaf(s[b][r + 1], kLog2e, -st.m)));
+      psum = __builtin_amdgcn_fdot2(ph, h2v{static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)}, psum, false);
+      pf[b][r >> 3][r & 7] = ph[0];
+      pf[b][r >> 3][(r & 7) + 1] = ph[1];
+    }
+  st.l += psum + __shfl_xor(psum, 32, kWave);
+  // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]; k-step (b, hs) covers keys 32 b + 16 hs + [0, 16),
+  // whose transposed-layout chunk for lane half lg is chunk 4 b + 2 hs + lg of the V^T row.
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int hs = 0; hs < 2; ++hs)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const u32x4 u = vtt[swz(32 * db + lr, 4 * b + 2 * hs + lg)];
+        st.o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, u), pf[b][hs], st.o[db], 0, 0, 0);
+      }
+}
+
+__global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* __restrict__ qkv,
+                                                                const _Float16* __restrict__ vt,
+                                                                _Float16* __restrict__ out, int seq, int heads) {
+  constexpr int kPerStage = 4;  // copies per thread per stage
+  __shared__ __align__(1024) u32x4 ring[kEaStages * 2 * kEaTileBytes / 16];
+
+  const int qblocks = (seq + kEaQ - 1) / kEaQ, nblk = qblocks * heads;
+  const int bid = blockIdx.x, full = (nblk / 8) * 8;
+  const int job = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+  const int head = job / qblocks, qb = job % qblocks;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lg = lane >> 5;
+  const int ld = 3 * heads * kHeadDim, seq_pad = vt_pad(seq);
+  const int q_row = qb * kEaQ + wave * 32 + lr;  // this lane's query column
+  const _Float16* kbase = qkv + (heads + head) * kHeadDim;
+  const _Float16* vtbase = vt + static_cast<size_t>(head) * kHeadDim * seq_pad;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+
+  // Q^T as B operand: lane holds Q[q_row][16 s + 8 lg .. + 7] for s = 0..3.
+  h8v qf[4];
+  {
+    const _Float16* qp = qkv + static_cast<size_t>(min(q_row, seq - 1)) * ld + head * kHeadDim + 8 * lg;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qf[k] = *reinterpret_cast<const h8v*>(qp + 16 * k);
+  }
+  const int nt = seq_pad / kEaKV;
+#pragma unroll
+  for (int k = 0; k < kEaStages - 1; ++k)
+    if (k < nt) ea_dma(kbase, ld, vtbase, seq_pad, seq, k * kEaKV, wave, lane, lds0 + k * 2 * kEaTileBytes);
+
+  EaState st;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st.o[b][r] = 0.f;
+  st.m = -INFINITY;
+  st.l = 0.f;
+
+  // Returns tile t's K tile in the ring once every wave's copies of it have landed.
+  auto next_tile = [&](int t) {
+    wait_stages_ahead<kPerStage, kEaStages - 2>(min(kEaStages - 2, nt - 1 - t));
+    barrier_only();  // tile t visible to every wave; every wave is done with tile t - 1
+    const int nxt = t + kEaStages - 1;
+    if (nxt < nt)
+      ea_dma(kbase, ld, vtbase, seq_pad, seq, nxt * kEaKV, wave, lane, lds0 + (nxt % kEaStages) * 2 * kEaTileBytes);
+    return ring + (t % kEaStages) * (2 * kEaTileBytes / 16);
+  };
+  const int nfull = seq / kEaKV;  // tiles whose 64 keys are all valid; at most one partial tile follows
+  for (int t = 0; t < nfull; ++t) {
+    const u32x4* kt = next_tile(t);
+    ea_tile<false>(kt, kt + kEaTileBytes / 16, qf, t * kEaKV, seq, lr, lg, st);
+  }
+  if (nfull < nt) {
+    const u32x4* kt = next_tile(nfull);
+    ea_tile<true>(kt, kt + kEaTileBytes / 16, qf, nfull * kEaKV, seq, lr, lg, st);
+  }
+  if (q_row >= seq) return;
+  const float inv = 1.0f / st.l;
+  _Float16* orow = out + static_cast<size_t>(q_row) * heads * kHeadDim + head * kHeadDim;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h4v v4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = f2h(st.o[db][4 * j + e] * inv);
+      *reinterpret_cast<h4v*>(orow + 32 * db + 8 * j + 4 * lg) = v4;
+    }
+}
+
+// Transposed V for the attention kernel from a projection output (qkv v columns).
+__global__ void __launch_bounds__(256) pack_vt_kernel(const _Float16* __restrict__ qkv, _Float16* __restrict__ vt,
+                                                      int seq, int heads) {
+  const int seq_pad = vt_pad(seq);
+  const int i = blockIdx.x * 256 + threadIdx.x;  // over heads * 64 * seq_pad
+  if (i >= heads * kHeadDim * seq_pad) return;
+  const int pos = i % seq_pad, hd = i / seq_pad;  // hd = head * 64 + d
+  const int t = vt_pos(pos);
+  vt[i] = t < seq ? qkv[static_cast<size_t>(t) * 3 * heads * kHeadDim + 2 * heads * kHeadDim + hd]
+                  : static_cast<_Float16>(0.f);
+}
+
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+}  // namespace fw
+
+using namespace fw;
+
+extern "C" long long fw_encoder_vt_elems(int seq, int heads) {
+  if (seq <= 0 || heads <= 0) return 0;
+  return static_cast<long long>(heads) * kHeadDim * vt_pad(seq);
+}
+
+extern "C" int fw_encoder_pack_vt(const void* qkv, void* vt, int seq, int heads, hipStream_t stream) {
+  if (!qkv || !vt) return fw_fail(FW_EINVAL, "encoder_pack_vt: null pointer");
+  if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_pack_vt: seq and heads must be positive");
+  const long long n = fw_encoder_vt_elems(seq, heads);
+  hipLaunchKernelGGL(pack_vt_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const _Float16*>(qkv), static_cast<_Float16*>(vt), seq, heads);
+  return fw_check_launch("encoder_pack_vt");
+}
+
+extern "C" int fw_encoder_attention(const void* qkv, const void* vt, void* out, int seq, int heads,
+                                    hipStream_t stream) {
+  if (!qkv || !vt || !out) return fw_fail(FW_EINVAL, "encoder_attention: null pointer");
+  if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_attention: seq and heads must be positive");
+  if (!aligned(qkv, 16) || !aligned(vt, 16) || !aligned(out, 8))
+    return fw_fail(FW_EINVAL, "encoder_attention: qkv and vt must be 16-byte aligned, out 8-byte aligned");
+  const int blocks = (seq + kEaQ - 1) / kEaQ * heads;
+  hipLaunchKernelGGL(encoder_attention_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<const _Float16*>(qkv),
+                     static_cast<const _Float16*>(vt), static_cast<_Float16*>(out), seq, heads);
+  return fw_check_launch("encoder_attention");
+}

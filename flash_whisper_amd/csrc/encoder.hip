@@ -3,7 +3,7 @@
 // flash-style encoder self-attention. Semantics follow HF WhisperEncoder.forward in fp16
 // (transformers models/whisper/modeling_whisper.py:592-648, layer :379-414, attention :284-358):
 // every op output is rounded to fp16, accumulation is fp32.
-#include "fw_common.h"
+#include "lds_pipe.h"
 
 namespace fw {
 namespace {
@@ -79,8 +79,6 @@ __device__ __forceinline__ float epilogue_value(int epi, float acc, float b, con
   return v;
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
-
 // Workgroup barrier for LDS hand-off only: waits for this wave's LDS traffic, not for its global
 // loads (__syncthreads would also drain the prefetches that are meant to stay in flight).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -154,42 +152,12 @@ __device__ __forceinline__ void gemm_mma(const u32x4* As, const u32x4* Bs, int w
 }
 
 // ---- direct-to-LDS pipeline (plain GEMMs) ------------------------------------------------------
-// global_load_lds_dwordx4 writes one 16-byte chunk per lane straight into LDS at M0 + 16 * lane, so
-// a wave instruction fills 1 KB = 8 rows of a 64-wide k slice. The XOR swizzle is applied on the
-// source side: lane l fills LDS row r0 + l / 8, slot l % 8, so it fetches chunk (l % 8) ^ (row & 7).
-// The copies are issued from inline assembly: the compiler then does not guard every LDS read with
-// a wait for all outstanding copies, and the pipeline depth is set by the explicit vmcnt waits.
 // The LDS ring depth ST (ST - 1 stages in flight) is picked per tile height: 128-row tiles use two
 // 32 KB stages so that two blocks share a CU and hide each other's copy latency; 64-row tiles
 // (launched when there are fewer tiles than CUs) use four 24 KB stages in one block.
 template <int BM>
 constexpr int dma_stages() { return BM == 128 ? 2 : 4; }
 
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
-// Waits until only the copies of the `ahead` most recently issued stages may still be in flight.
-template <int kPer, int A>
-__device__ __forceinline__ void wait_stages_ahead(int ahead) {
-  if constexpr (A == 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (ahead >= A) wait_vmcnt<A * kPer>();
-    else wait_stages_ahead<kPer, A - 1>(ahead);
-  }
-}
 
 template <int BM>
 __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
@@ -215,10 +183,6 @@ __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int
           __builtin_amdgcn_readfirstlane(lds_stage + BM * 128 + blk * 1024));
   }
 }
-
-// Position of key t in the transposed-V layout of the encoder attention (an involution: swaps bits 2
-// and 3 of t, so the 8 keys an MFMA lane pairs with P^T are one contiguous 16-byte chunk).
-__device__ __forceinline__ int vt_pos(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
 
 // v columns of the q/k/v projection -> vt[head * 64 + d][vt_pos(t)]; rows in [m, vt_pad) get zeros so
 // the padding keys of the last attention tile hold finite values.
@@ -477,172 +441,6 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __r
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Encoder self-attention, flash style, non-causal, scale 1 (q is pre-scaled by the projection).
-// Block = (head, 128 queries): 4 waves of 32 queries each share one LDS ring of 64-key tiles. Per
-// tile a wave computes S^T = K Q^T (keys x queries) with MFMA, so that every lane holds the scores
-// of a single query column and the online-softmax max/sum need one cross-lane step (lane ^ 32).
-// P^T is fed straight from the S^T accumulator layout as the B operand of O^T = V^T P^T.
-//  - Inputs: q and k from the projection output qkv[seq, 3 * heads * 64]; V from a transposed copy
-//    vt[heads][64][seq_pad] written by the projection's epilogue, whose key order inside every
-//    16-key group has bits 2 and 3 of the key index swapped. With that order the 8 keys an MFMA
-//    A-operand lane needs for V^T are one contiguous 16-byte chunk, and they are the keys the
-//    same lane holds for P^T in the S^T accumulator (rows 8 (r / 4) + 4 g + (r % 4)).
-//  - K tiles (64 keys x 128 B) and V^T tiles (64 d x 128 B) arrive by direct-to-LDS copies into a
-//    ring of kEaStages stages, XOR-swizzled by 16-byte chunk like the GEMM tiles.
-//  - Block ids are remapped so that the query blocks of a head run on one XCD and its K/V stay in
-//    that XCD's L2.
-// ------------------------------------------------------------------------------------------
-constexpr int kEaWaves = 4, kEaQ = 32 * kEaWaves, kEaKV = 64, kEaStages = 4;
-constexpr int kEaTileBytes = kEaKV * 128;  // one K tile or one V^T tile
-
-__device__ __forceinline__ void ea_dma(const _Float16* kbase, int ld, const _Float16* vtbase, int seq_pad,
-                                       int seq, int kv0, int wave, int lane, uint32_t stage) {
-  const int rsub = lane >> 3, slot = lane & 7;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {  // K tile: wave fills 8-row blocks 2 wave and 2 wave + 1
-    const int blk = 2 * wave + i, row = blk * 8 + rsub;
-    const int key = min(kv0 + row, seq - 1);  // keys past seq are masked to -inf
-    dma16(kbase + static_cast<size_t>(key) * ld + (slot ^ (row & 7)) * 8,
-          __builtin_amdgcn_readfirstlane(stage + blk * 1024));
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {  // V^T tile: rows are head dims
-    const int blk = 2 * wave + i, d = blk * 8 + rsub;
-    dma16(vtbase + static_cast<size_t>(d) * seq_pad + kv0 + (slot ^ (d & 7)) * 8,
-          __builtin_amdgcn_readfirstlane(stage + kEaTileBytes + blk * 1024));
-  }
-}
-
-__global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* __restrict__ qkv,
-                                                                const _Float16* __restrict__ vt,
-                                                                _Float16* __restrict__ out, int seq, int heads) {
-  constexpr int kPerStage = 4;  // copies per thread per stage
-  __shared__ __align__(1024) u32x4 ring[kEaStages * 2 * kEaTileBytes / 16];
-
-  const int qblocks = (seq + kEaQ - 1) / kEaQ, nblk = qblocks * heads;
-  const int bid = blockIdx.x, full = (nblk / 8) * 8;
-  const int job = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-  const int head = job / qblocks, qb = job % qblocks;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 31, lg = lane >> 5;
-  const int ld = 3 * heads * kHeadDim, seq_pad = (seq + kEaKV - 1) / kEaKV * kEaKV;
-  const int q_row = qb * kEaQ + wave * 32 + lr;  // this lane's query column
-  const _Float16* kbase = qkv + (heads + head) * kHeadDim;
-  const _Float16* vtbase = vt + static_cast<size_t>(head) * kHeadDim * seq_pad;
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
-
-  // Q^T as B operand: lane holds Q[q_row][16 s + 8 lg .. + 7] for s = 0..3.
-  h8v qf[4];
-  {
-    const _Float16* qp = qkv + static_cast<size_t>(min(q_row, seq - 1)) * ld + head * kHeadDim + 8 * lg;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const h8v*>(qp + 16 * s);
-  }
-  const int nt = seq_pad / kEaKV;
-#pragma unroll
-  for (int st = 0; st < kEaStages - 1; ++st)
-    if (st < nt) ea_dma(kbase, ld, vtbase, seq_pad, seq, st * kEaKV, wave, lane, lds0 + st * 2 * kEaTileBytes);
-
-  f16v o[2];  // O^T blocks: d in [0, 32) and [32, 64)
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-  constexpr float kLog2e = 1.4426950408889634f;
-
-  for (int t = 0; t < nt; ++t) {
-    wait_stages_ahead<kPerStage, kEaStages - 2>(min(kEaStages - 2, nt - 1 - t));
-    barrier_only();  // tile t visible to every wave; every wave is done with tile t - 1
-    const int nxt = t + kEaStages - 1;
-    if (nxt < nt)
-      ea_dma(kbase, ld, vtbase, seq_pad, seq, nxt * kEaKV, wave, lane, lds0 + (nxt % kEaStages) * 2 * kEaTileBytes);
-    const u32x4* kt = ring + (t % kEaStages) * (2 * kEaTileBytes / 16);
-    const u32x4* vtt = kt + kEaTileBytes / 16;
-    const int kv0 = t * kEaKV;
-
-    // S^T = K Q^T for two 32-key blocks.
-    f16v s[2];
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[b][r] = 0.f;
-      const int row = 32 * b + lr;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const u32x4 u = kt[swz(row, 2 * st + lg)];
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, u), qf[st], s[b], 0, 0, 0);
-      }
-    }
-    // Mask keys beyond seq; running max over this lane's 32 scores and the partner lane.
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (kv0 + kEaKV > seq && kv0 + 32 * b + 8 * (r >> 2) + 4 * lg + (r & 3) >= seq) s[b][r] = -INFINITY;
-        tmax = fmaxf(tmax, s[b][r]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m_run, tmax);
-    const float corr = exp2f((m_run - m_new) * kLog2e);
-    const float mb = m_new * kLog2e;
-    float psum = 0.f;
-    h8v pf[2][2];  // P^T as B operand, [32-key block][k-step of 16 keys]
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const _Float16 ph = f2h(exp2f(fmaf(s[b][r], kLog2e, -mb)));
-        psum += h2f(ph);
-        pf[b][r >> 3][r & 7] = ph;
-      }
-    psum += __shfl_xor(psum, 32, kWave);
-    l_run = l_run * corr + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[b][r] *= corr;
-    // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]; k-step (b, hs) covers keys 32 b + 16 hs + [0, 16),
-    // whose transposed-layout chunk for lane half lg is chunk 4 b + 2 hs + lg of the V^T row.
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int hs = 0; hs < 2; ++hs)
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const u32x4 u = vtt[swz(32 * db + lr, 4 * b + 2 * hs + lg)];
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8v, u), pf[b][hs], o[db], 0, 0, 0);
-        }
-  }
-  if (q_row >= seq) return;
-  const float inv = 1.0f / l_run;
-  _Float16* orow = out + static_cast<size_t>(q_row) * heads * kHeadDim + head * kHeadDim;
-#pragma unroll
-  for (int db = 0; db < 2; ++db)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      h4v v4;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = f2h(o[db][4 * j + e] * inv);
-      *reinterpret_cast<h4v*>(orow + 32 * db + 8 * j + 4 * lg) = v4;
-    }
-}
-
-// Transposed V for the attention kernel from a projection output (qkv v columns).
-__global__ void __launch_bounds__(256) pack_vt_kernel(const _Float16* __restrict__ qkv, _Float16* __restrict__ vt,
-                                                      int seq, int heads) {
-  const int seq_pad = (seq + kEaKV - 1) / kEaKV * kEaKV;
-  const int i = blockIdx.x * 256 + threadIdx.x;  // over heads * 64 * seq_pad
-  if (i >= heads * kHeadDim * seq_pad) return;
-  const int pos = i % seq_pad, hd = i / seq_pad;  // hd = head * 64 + d
-  const int t = vt_pos(pos);
-  vt[i] = t < seq ? qkv[static_cast<size_t>(t) * 3 * heads * kHeadDim + 2 * heads * kHeadDim + hd]
-                  : static_cast<_Float16>(0.f);
-}
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -695,10 +493,6 @@ extern "C" int fw_layernorm_rows(const void* x, const void* gamma, const void* b
   return fw_check_launch("layernorm_rows");
 }
 
-extern "C" long long fw_encoder_vt_elems(int seq, int heads) {
-  if (seq <= 0 || heads <= 0) return 0;
-  return static_cast<long long>(heads) * kHeadDim * ((seq + kEaKV - 1) / kEaKV * kEaKV);
-}
 
 extern "C" int fw_encoder_qkv(const void* y, const void* w, const void* bias, void* qkv, void* vt, int seq, int heads,
                               hipStream_t stream) {
@@ -711,30 +505,11 @@ extern "C" int fw_encoder_qkv(const void* y, const void* w, const void* bias, vo
   if (reinterpret_cast<uintptr_t>(vt) & 7u) return fw_fail(FW_EINVAL, "encoder_qkv: vt must be 8-byte aligned");
   GemmArgs g{static_cast<const _Float16*>(y), d, static_cast<const _Float16*>(w), d,
              static_cast<const _Float16*>(bias), static_cast<_Float16*>(qkv), 3 * d, nullptr, 0, seq, 3 * d, d, d,
-             0, 0, 0, heads, seq, static_cast<_Float16*>(vt), (seq + kEaKV - 1) / kEaKV * kEaKV};
+             0, 0, 0, heads, seq, static_cast<_Float16*>(vt), vt_pad(seq)};
   return launch_gemm(g, kEpiQkvVt, stream);
 }
 
-extern "C" int fw_encoder_pack_vt(const void* qkv, void* vt, int seq, int heads, hipStream_t stream) {
-  if (!qkv || !vt) return fw_fail(FW_EINVAL, "encoder_pack_vt: null pointer");
-  if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_pack_vt: seq and heads must be positive");
-  const long long n = fw_encoder_vt_elems(seq, heads);
-  hipLaunchKernelGGL(pack_vt_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
-                     static_cast<const _Float16*>(qkv), static_cast<_Float16*>(vt), seq, heads);
-  return fw_check_launch("encoder_pack_vt");
-}
 
-extern "C" int fw_encoder_attention(const void* qkv, const void* vt, void* out, int seq, int heads,
-                                    hipStream_t stream) {
-  if (!qkv || !vt || !out) return fw_fail(FW_EINVAL, "encoder_attention: null pointer");
-  if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_attention: seq and heads must be positive");
-  if (!aligned16(qkv) || !aligned16(vt) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return fw_fail(FW_EINVAL, "encoder_attention: qkv and vt must be 16-byte aligned, out 8-byte aligned");
-  const int blocks = (seq + kEaQ - 1) / kEaQ * heads;
-  hipLaunchKernelGGL(encoder_attention_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<const _Float16*>(qkv),
-                     static_cast<const _Float16*>(vt), static_cast<_Float16*>(out), seq, heads);
-  return fw_check_launch("encoder_attention");
-}
 
 extern "C" int fw_cross_kv(const void* enc, int t, const void* w, const void* bias, void* cross_kv, int layers,
                            int heads, hipStream_t stream) {

@@ -1,0 +1,51 @@
+// Shared pieces of the LDS-staged MFMA kernels (encoder GEMM and encoder attention) for gfx950:
+// the 16-byte-chunk XOR swizzle of 128-byte LDS rows, direct global-to-LDS copies, explicit vmcnt
+// waits for a ring of copy stages, and the key order of the attention's transposed V.
+#pragma once
+#include "fw_common.h"
+
+namespace fw {
+
+// Chunk c of LDS row r (8 x 16-byte chunks per row) lives in slot c ^ (r & 7): the 8 rows a
+// quarter-wave reads for one MFMA operand hit 8 different bank groups.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+
+// global_load_lds_dwordx4 writes one 16-byte chunk per lane straight into LDS at M0 + 16 * lane, so
+// a wave instruction fills 1 KB = 8 rows of 128 bytes. The XOR swizzle is applied on the source
+// side: lane l fills LDS row r0 + l / 8, slot l % 8, so it fetches chunk (l % 8) ^ (row & 7).
+// The copies are issued from inline assembly: the compiler then does not guard every LDS read with
+// a wait for all outstanding copies, and the pipeline depth is set by the explicit vmcnt waits.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// Waits until only the copies of the `ahead` most recently issued stages may still be in flight.
+template <int kPer, int A>
+__device__ __forceinline__ void wait_stages_ahead(int ahead) {
+  if constexpr (A == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (ahead >= A) wait_vmcnt<A * kPer>();
+    else wait_stages_ahead<kPer, A - 1>(ahead);
+  }
+}
+
+// Keys per transposed-V row: seq rounded up to whole 64-key attention tiles.
+__host__ __device__ constexpr int vt_pad(int seq) { return (seq + 63) / 64 * 64; }
+
+// Position of key t in the transposed-V layout of the encoder attention (an involution: swaps bits 2
+// and 3 of t, so the 8 keys an MFMA lane pairs with P^T are one contiguous 16-byte chunk).
+__device__ __forceinline__ int vt_pos(int t) { return (t & ~12) | ((t & 4) << 1) | ((t & 8) >> 1); }
+
+}  // namespace fw
