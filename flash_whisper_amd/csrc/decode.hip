@@ -372,8 +372,17 @@ void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& 
 // last-block-done finalize needs a device-scope release per block, which on this part writes back
 // the L2 and costs far more than one extra launch.
 // ------------------------------------------------------------------------------------------
-constexpr int kLmNW = 4, kLmU = 2;
-constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // 16 rows per block iteration
+#ifndef FW_LM_NW
+#define FW_LM_NW 16
+#endif
+#ifndef FW_LM_U
+#define FW_LM_U 2
+#endif
+#ifndef FW_LM_BPC
+#define FW_LM_BPC 1
+#endif
+constexpr int kLmNW = FW_LM_NW, kLmU = FW_LM_U;
+constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // rows per block iteration
 
 struct FinArgs {
   int64_t* tokens;
@@ -476,7 +485,7 @@ int lm_head_grid(int vocab, int* rows_per_block) {
   if (hipGetDevice(&dev) == hipSuccess &&
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  const int max_blocks = cus * 4;
+  const int max_blocks = cus * FW_LM_BPC;
   const int iters = (vocab + max_blocks * kLmRowsIter - 1) / (max_blocks * kLmRowsIter);
   *rows_per_block = iters * kLmRowsIter;
   return (vocab + *rows_per_block - 1) / *rows_per_block;

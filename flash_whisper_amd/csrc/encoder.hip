@@ -49,7 +49,31 @@ struct GemmArgs {
   // q/k/v projection: transposed V, [heads * 64][vt_pad]
   _Float16* vt;
   int vt_pad;
+  // XCD tile grouping (0: none): the 8 XCDs split the tile grid into xm x xn rectangles
+  int xm, xn;
 };
+
+// Block -> output tile. Hardware deals workgroups round-robin over the 8 XCDs (block b runs on XCD
+// b % 8), each with its own L2. With a grouping, XCD x owns one (ntm / xm) x (ntn / xn) rectangle of
+// the tile grid, so each XCD fetches only its slices of A and W. Otherwise each XCD takes a contiguous
+// run of row-major tiles (the tail beyond a multiple of 8 keeps its id). Both maps are bijective.
+template <int BM>
+__device__ __forceinline__ void tile_origin(const GemmArgs& g, int& m0, int& n0) {
+  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM, bid = blockIdx.x;
+  int tm, tn;
+  if (g.xm) {
+    const int xcd = bid & 7, local = bid >> 3, mr = ntm / g.xm, nr = ntn / g.xn;
+    tm = (xcd / g.xn) * mr + local % mr;
+    tn = (xcd % g.xn) * nr + local / mr;
+  } else {
+    const int ntiles = ntn * ntm, full = (ntiles / 8) * 8;
+    const int tile = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+    tm = tile / ntn;
+    tn = tile % ntn;
+  }
+  m0 = tm * BM;
+  n0 = tn * kBN;
+}
 
 __device__ __forceinline__ float epilogue_value(int epi, float acc, float b, const GemmArgs& g, int row, int col) {
   float v = round_h(acc + b);
@@ -80,8 +104,14 @@ __device__ __forceinline__ float epilogue_value(int epi, float acc, float b, con
 }
 
 // Workgroup barrier for LDS hand-off only: waits for this wave's LDS traffic, not for its global
-// loads (__syncthreads would also drain the prefetches that are meant to stay in flight).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// loads (__syncthreads would also drain the prefetches that are meant to stay in flight). The
+// lgkmcnt(0) wait goes through the builtin (encoding: vmcnt 63, expcnt 7, lgkmcnt 0) so the compiler
+// knows every earlier LDS read has completed and adds no waits of its own for them afterwards; the
+// barrier itself stays an asm statement with a memory clobber so no LDS access moves across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+}
 
 template <int BM>
 struct GemmStage {
@@ -151,12 +181,53 @@ __device__ __forceinline__ void gemm_mma(const u32x4* As, const u32x4* Bs, int w
   }
 }
 
+// MFMA operand fragments of one 64-wide k stage for a wave: A rows wm + 32 i + lane % 32, B rows
+// wn + 32 j + lane % 32, k-step s covering k 16 s .. 16 s + 15.
+template <int kTM, int kTN>
+struct Frags {
+  h8v a[kBK / 16][kTM];
+  h8v b[kBK / 16][kTN];
+};
+
+template <int kTM, int kTN>
+__device__ __forceinline__ void load_frags(const u32x4* As, const u32x4* Bs, int wm, int wn, int lr, int lg,
+                                           Frags<kTM, kTN>& f) {
+#pragma unroll
+  for (int s = 0; s < kBK / 16; ++s) {
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) f.a[s][i] = __builtin_bit_cast(h8v, As[swz(wm + 32 * i + lr, 2 * s + lg)]);
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) f.b[s][j] = __builtin_bit_cast(h8v, Bs[swz(wn + 32 * j + lr, 2 * s + lg)]);
+  }
+}
+
+template <int kTM, int kTN>
+__device__ __forceinline__ void mma_frags(const Frags<kTM, kTN>& f, f16v (&acc)[kTM][kTN]) {
+#pragma unroll
+  for (int s = 0; s < kBK / 16; ++s)
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[s][i], f.b[s][j], acc[i][j], 0, 0, 0);
+}
+
 // ---- direct-to-LDS pipeline (plain GEMMs) ------------------------------------------------------
+// Per stage kt: wait until stage kt + 1 has landed, barrier (every wave also holds stage kt's operand
+// fragments in registers by then, so its LDS slot is free), refill that slot with stage kt + ST,
+// start the LDS reads of stage kt + 1's fragments, and run stage kt's MFMAs while they arrive. Copies
+// have ST - 1 stages of MFMA time to land and LDS read latency is hidden behind the MFMAs.
 // The LDS ring depth ST (ST - 1 stages in flight) is picked per tile height: 128-row tiles use two
 // 32 KB stages so that two blocks share a CU and hide each other's copy latency; 64-row tiles
 // (launched when there are fewer tiles than CUs) use four 24 KB stages in one block.
+#ifndef FW_ST128
+#define FW_ST128 2
+#endif
+#ifndef FW_ST64
+#define FW_ST64 4
+#endif
 template <int BM>
-constexpr int dma_stages() { return BM == 128 ? 2 : 4; }
+constexpr int dma_stages() { return BM == 128 ? FW_ST128 : FW_ST64; }
 
 
 template <int BM>
@@ -217,10 +288,8 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
   constexpr int kPerStage = (BM / 8 / 4) + (kBN / 8 / 4);  // copies per thread per stage
   __shared__ __align__(1024) u32x4 lds[kDmaStages * kStageBytes / 16];
 
-  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM, ntiles = ntn * ntm;
-  const int bid = blockIdx.x, full = (ntiles / 8) * 8;
-  const int tile = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-  const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * kBN;
+  int m0, n0;
+  tile_origin<BM>(g, m0, n0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave >> 1) * kWM, wn = (wave & 1) * 64;
   const int lr = lane & 31, lg = lane >> 5;
@@ -236,16 +305,33 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
 
   const int kt_n = g.k / kBK;
 #pragma unroll
-  for (int s = 0; s < kDmaStages - 1; ++s)
+  for (int s = 0; s < kDmaStages; ++s)
     if (s < kt_n) dma_stage<BM>(g, m0, n0, s * kBK, wave, lane, lds0 + s * kStageBytes);
-  for (int kt = 0; kt < kt_n; ++kt) {
-    // this thread's copies of stage kt have landed once at most the later in-flight stages remain
-    wait_stages_ahead<kPerStage, kDmaStages - 2>(min(kDmaStages - 2, kt_n - 1 - kt));
-    barrier_only();  // stage kt visible to every wave; every wave is done with stage kt - 1
-    const int nxt = kt + kDmaStages - 1;
-    if (nxt < kt_n) dma_stage<BM>(g, m0, n0, nxt * kBK, wave, lane, lds0 + (nxt % kDmaStages) * kStageBytes);
-    const u32x4* As = lds + (kt % kDmaStages) * (kStageBytes / 16);
-    gemm_mma<kTM, kTN>(As, As + BM * 8, wm, wn, lr, lg, acc);
+  auto slot = [&](int kt) { return lds + (kt % kDmaStages) * (kStageBytes / 16); };
+  Frags<kTM, kTN> fa, fb;
+  // this thread's copies of stage kt have landed once at most the later issued stages remain
+  wait_stages_ahead<kPerStage, kDmaStages - 1>(min(kDmaStages - 1, kt_n - 1));
+  barrier_only();
+  load_frags<kTM, kTN>(slot(0), slot(0) + BM * 8, wm, wn, lr, lg, fa);
+  // stage kt with a stage kt + 1 after it
+  auto step = [&](int kt, const Frags<kTM, kTN>& cur, Frags<kTM, kTN>& nxt) {
+    wait_stages_ahead<kPerStage, kDmaStages - 1>(min(kDmaStages - 2, kt_n - 2 - kt));
+    lds_barrier();  // own fragment reads of stage kt done; stage kt + 1 visible; slot kt free
+    if (kt + kDmaStages < kt_n)
+      dma_stage<BM>(g, m0, n0, (kt + kDmaStages) * kBK, wave, lane, lds0 + (kt % kDmaStages) * kStageBytes);
+    load_frags<kTM, kTN>(slot(kt + 1), slot(kt + 1) + BM * 8, wm, wn, lr, lg, nxt);
+    mma_frags<kTM, kTN>(cur, acc);
+  };
+  int kt = 0;
+  for (; kt + 2 < kt_n; kt += 2) {
+    step(kt, fa, fb);
+    step(kt + 1, fb, fa);
+  }
+  if (kt + 1 < kt_n) {
+    step(kt, fa, fb);
+    mma_frags<kTM, kTN>(fb, acc);
+  } else {
+    mma_frags<kTM, kTN>(fa, acc);
   }
 
   if constexpr (EPI == kEpiQkvVt) {
@@ -285,11 +371,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
   __shared__ __align__(16) u32x4 As0[BM * 8], As1[BM * 8];
   __shared__ __align__(16) u32x4 Bs0[kBN * 8], Bs1[kBN * 8];
 
-  // XCD-aware tile order (bijective: the tail beyond a multiple of 8 keeps its id)
-  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM, ntiles = ntn * ntm;
-  const int bid = blockIdx.x, full = (ntiles / 8) * 8;
-  const int tile = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
-  const int m0 = (tile / ntn) * BM, n0 = (tile % ntn) * kBN;
+  int m0, n0;
+  tile_origin<BM>(g, m0, n0);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave >> 1) * kWM, wn = (wave & 1) * 64;
@@ -347,10 +430,33 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
   }
 }
 
+#ifndef FW_XCD_GROUP
+#define FW_XCD_GROUP 1
+#endif
+// Picks the XCD rectangle grid that divides the tile grid and moves the fewest bytes into the L2s:
+// A is fetched once per column group (xn), W once per row group (xm).
+void choose_xcd_groups(GemmArgs& g, int bm) {
+  g.xm = g.xn = 0;
+  if (!FW_XCD_GROUP || g.conv_stride) return;
+  const int ntm = (g.m + bm - 1) / bm, ntn = g.n / kBN;
+  double best = 0;
+  for (int xm = 1; xm <= 8; xm *= 2) {
+    const int xn = 8 / xm;
+    if (ntm % xm || ntn % xn) continue;
+    const double bytes = static_cast<double>(xn) * g.m * g.k + static_cast<double>(xm) * g.n * g.k;
+    if (!g.xm || bytes < best) {
+      best = bytes;
+      g.xm = xm;
+      g.xn = xn;
+    }
+  }
+}
+
 template <int BM>
-int launch_gemm_bm(const GemmArgs& g, int epi, hipStream_t s) {
+int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
   const int tiles = (g.n / kBN) * ((g.m + BM - 1) / BM);
   const dim3 grid(tiles);
+  choose_xcd_groups(g, BM);
   if (g.conv_stride) {
     switch (epi) {
       case FW_EPI_BIAS: hipLaunchKernelGGL((gemm_kernel<BM, FW_EPI_BIAS, true>), grid, dim3(256), 0, s, g); break;
