@@ -9,8 +9,8 @@ in-memory waveform and stops at the token-id list (reference custom/model.py:179
 Reported metric: decode-step us (median GPU time per decoder step, HIP events around every 8-step graph
 replay inside the timed transcribes), its achieved HBM GB/s from the algorithmic bytes of a step, the
 30 s-clip E2E ms and TTFT. ``roofline`` covers the LM-head kernel (final LN + tied-embedding GEMV +
-argmax + finalize), timed standalone with HIP events over rotating copies of the 133 MB embedding so it
-streams from HBM as inside the step. ``cpu_baseline`` times the CPU oracle's decoder step on this host.
+argmax), timed standalone: a hipGraph of launches over rotating copies of the 133 MB embedding, so it
+streams from HBM as inside the step, between HIP events on the graph's stream. ``cpu_baseline`` times the CPU oracle's decoder step on this host.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -59,33 +59,37 @@ def lm_head_bytes(dims):
 
 
 def time_lm_head(model, reps, copies=3):
-    """Average us per launch of the fused LM-head kernel, HIP events on the launch stream, rotating over
-    `copies` embedding copies (>= 256 MB MALL) so each launch reads its weights from HBM."""
+    """Average us per launch of the LN + LM-head + argmax kernel alone (no finalize launch): `reps`
+    launches rotating over `copies` embedding copies (>= 256 MB, more than the MALL, so each launch
+    reads its weights from HBM) are captured in one hipGraph on a side stream and replayed between HIP
+    events recorded on that stream."""
     import torch
 
     ext, d = model.ext, model.dims
     tables = [model.lm_head] + [model.lm_head.clone() for _ in range(copies - 1)]
-    tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
-    state = torch.zeros(2, dtype=torch.long, device='cuda')
-    cur = torch.zeros(1, dtype=torch.long, device='cuda')
     best = torch.zeros(1, dtype=torch.long, device='cuda')
     g, b, eps = model.final_ln
     h, x = model.h[0], model.pending
+    stream = torch.cuda.Stream()
 
     def launch(i):
-        ext.lm_head_argmax_fused(h, x, g, b, eps, tables[i % copies], model.suppress, best, tokens, state, cur,
+        ext.lm_head_argmax_fused(h, x, g, b, eps, tables[i % copies], model.suppress, best, None, None, None,
                                  d.max_pos)
 
-    for i in range(2 * copies):
-        launch(i)
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(reps):
-        launch(i)
-    end.record(stream)
-    end.synchronize()
-    del tables
+    with torch.cuda.stream(stream):
+        for i in range(2 * copies):
+            launch(i)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(reps):
+                launch(i)
+        graph.replay()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        end.synchronize()
+    del tables, graph
     return start.elapsed_time(end) * 1e3 / reps
 
 
@@ -193,7 +197,7 @@ def main():
         'e2e_ms': round(med('e2e_s'), 3), 'ttft_ms': round(med('ttft_s'), 3), 'mel_ms': round(med('mel_s'), 3),
         'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
         'n_tokens': rows[-1]['n_tokens'],
-        'roofline': {'kernel': 'lm_head_kernel<true> (final LN + LM head GEMV + argmax; finalize is a separate 1-thread launch)',
+        'roofline': {'kernel': 'lm_head_kernel<true> (final LN + LM head GEMV + argmax)',
                      'bound': 'hbm', 'achieved': round(lm_gbps, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                      'frac': round(lm_gbps / HBM_PEAK_GBPS, 4), 'traffic': measured_traffic(),
                      'traffic_source': 'profiles/lm_head_kernel_traffic.md', 'us_per_launch': round(lm_us, 2),

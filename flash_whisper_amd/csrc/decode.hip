@@ -827,8 +827,9 @@ extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void*
                                        const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
                                        int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,
                                        hipStream_t stream) {
-  FW_REQUIRE(h && gamma && beta && w && suppress && best && tokens && state && cur,
-             "lm_head_argmax_fused: null pointer");
+  FW_REQUIRE(h && gamma && beta && w && suppress && best, "lm_head_argmax_fused: null pointer");
+  const bool finalize = tokens || state || cur;
+  FW_REQUIRE(!finalize || (tokens && state && cur), "lm_head_argmax_fused: tokens, state and cur must be given together");
   FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
   FW_REQUIRE(vocab > 0 && max_pos > 0, "vocab and max_pos must be positive");
   FW_REQUIRE(aligned16(w), "lm_head_argmax_fused: w must be 16-byte aligned");
@@ -840,7 +841,7 @@ extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void*
   hipLaunchKernelGGL(lm_head_kernel<true>, dim3(grid), dim3(kLmNW * 64), 0, stream, nullptr, ln,
                      static_cast<const _Float16*>(w), suppress, vocab, rpb, reinterpret_cast<unsigned long long*>(best));
   int rc = fw_check_launch("lm_head_argmax_fused");
-  if (rc != FW_OK) return rc;
+  if (rc != FW_OK || !finalize) return rc;
   FinArgs fin{tokens, state, cur, max_pos};
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<unsigned long long*>(best),
                      fin);

@@ -226,15 +226,25 @@ __device__ __forceinline__ void mma_frags(const Frags<kTM, kTN>& f, f16v (&acc)[
 #ifndef FW_ST64
 #define FW_ST64 4
 #endif
+#ifndef FW_ST256
+#define FW_ST256 3
+#endif
+#ifndef FW_MIN_TILES256
+#define FW_MIN_TILES256 128
+#endif
 template <int BM>
-constexpr int dma_stages() { return BM == 128 ? FW_ST128 : FW_ST64; }
+constexpr int dma_stages() { return BM == 256 ? FW_ST256 : BM == 128 ? FW_ST128 : FW_ST64; }
+// Waves per block: a 2-wide column of waves (64 output columns each) and BM / 64 rows of waves, at
+// least 2; each wave owns a (BM / rows) x 64 tile.
+template <int BM>
+constexpr int gemm_waves() { return BM >= 128 ? BM / 32 : 4; }
 
 
 template <int BM>
 __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
                                           uint32_t lds_stage) {
-  constexpr int kAInstr = BM / 8 / 4;    // wave instructions per A tile (8 rows each), per wave
-  constexpr int kBInstr = kBN / 8 / 4;
+  constexpr int kAInstr = BM / 8 / gemm_waves<BM>();  // wave instructions per A tile (8 rows each), per wave
+  constexpr int kBInstr = kBN / 8 / gemm_waves<BM>();
   const int rsub = lane >> 3, slot = lane & 7;
 #pragma unroll
   for (int i = 0; i < kAInstr; ++i) {
@@ -281,11 +291,11 @@ __device__ __forceinline__ void store_vt(const GemmArgs& g, const f16v (&acc)[kT
 }
 
 template <int BM, int EPI>
-__global__ void __launch_bounds__(256) gemm_dma_kernel(GemmArgs g) {
-  constexpr int kDmaStages = dma_stages<BM>();
-  constexpr int kWM = BM / 2, kTM = kWM / 32, kTN = 2;
+__global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArgs g) {
+  constexpr int kDmaStages = dma_stages<BM>(), kNW = gemm_waves<BM>();
+  constexpr int kWM = BM / (kNW / 2), kTM = kWM / 32, kTN = 2;
   constexpr int kStageBytes = (BM + kBN) * 128;
-  constexpr int kPerStage = (BM / 8 / 4) + (kBN / 8 / 4);  // copies per thread per stage
+  constexpr int kPerStage = (BM / 8 / kNW) + (kBN / 8 / kNW);  // copies per thread per stage
   __shared__ __align__(1024) u32x4 lds[kDmaStages * kStageBytes / 16];
 
   int m0, n0;
@@ -457,6 +467,7 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
   const int tiles = (g.n / kBN) * ((g.m + BM - 1) / BM);
   const dim3 grid(tiles);
   choose_xcd_groups(g, BM);
+  if constexpr (BM <= 128) {
   if (g.conv_stride) {
     switch (epi) {
       case FW_EPI_BIAS: hipLaunchKernelGGL((gemm_kernel<BM, FW_EPI_BIAS, true>), grid, dim3(256), 0, s, g); break;
@@ -471,10 +482,11 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
     }
     return fw_check_launch("conv1d");
   }
+  }
   switch (epi) {
 #define FW_GEMM_CASE(E) \
   case E:               \
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, E>), grid, dim3(256), 0, s, g); break;
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, E>), grid, dim3(gemm_waves<BM>() * 64), 0, s, g); break;
     FW_GEMM_CASE(FW_EPI_BIAS)
     FW_GEMM_CASE(FW_EPI_BIAS_GELU)
     FW_GEMM_CASE(FW_EPI_BIAS_RESID)
@@ -491,8 +503,13 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
 }
 
 // Fewer 128-row tiles than CUs leaves the chip idle: use 64-row tiles then.
+// 256-row tiles (8 waves, 48 KB stages) when they still cover half the CUs: they do twice the MFMA
+// work per byte staged of 128-row tiles. Fewer 128-row tiles than CUs leaves the chip idle: use
+// 64-row tiles then. The implicit-GEMM conv stays on the register-staged kernel (<= 128 rows).
 int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
+  const int tiles256 = (g.n / kBN) * ((g.m + 255) / 256);
   const int tiles128 = (g.n / kBN) * ((g.m + 127) / 128);
+  if (!g.conv_stride && tiles256 >= FW_MIN_TILES256) return launch_gemm_bm<256>(g, epi, s);
   if (tiles128 < 256) return launch_gemm_bm<64>(g, epi, s);
   return launch_gemm_bm<128>(g, epi, s);
 }

@@ -202,7 +202,8 @@ class WhisperExt:
                    w.size(0), _stream())
 
     def lm_head_argmax_fused(self, h, x, gamma, beta, eps, w, suppress, best, tokens, state, cur, max_pos):
-        """Final residual + LN + lm_head_argmax + argmax_finalize."""
+        """Final residual + LN + lm_head_argmax + argmax_finalize (finalize skipped when tokens, state and
+        cur are all None)."""
         for t, n in ((h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (w, 'w')):
             check_half(t, n)
         if x is not None:
@@ -210,11 +211,14 @@ class WhisperExt:
         _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
         _require(suppress.dtype == torch.bool and suppress.is_cuda and suppress.numel() == w.size(0),
                  'suppress must be bool [vocab]')
-        for t in (best, tokens, state, cur):
+        fin = (tokens, state, cur)
+        _require(all(t is None for t in fin) or all(t is not None for t in fin),
+                 'tokens, state and cur must be given together')
+        for t in (best,) + tuple(t for t in fin if t is not None):
             _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), 'tokens, state and cur must be int64')
         self._call('fw_lm_head_argmax_fused', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), float(eps),
-                   w.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN, best.data_ptr(), tokens.data_ptr(),
-                   state.data_ptr(), cur.data_ptr(), int(max_pos), _stream())
+                   w.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN, best.data_ptr(), _ptr(tokens),
+                   _ptr(state), _ptr(cur), int(max_pos), _stream())
 
     # ---- log-mel front end -------------------------------------------------------------
     def log_mel_workspace(self, n_samples, device='cuda'):

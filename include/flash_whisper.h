@@ -117,7 +117,8 @@ int fw_attn_out_gemv(const float* part_m, const float* part_l, const float* part
 
 /* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
  * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by
- * fw_argmax_finalize. best must be zero on entry and is left zero. */
+ * fw_argmax_finalize. best must be zero on entry and is left zero. With tokens, state and cur all
+ * NULL the finalize is skipped and best holds the packed winner, as after fw_lm_head_argmax. */
 int fw_lm_head_argmax_fused(const void* h, const void* x, const void* gamma, const void* beta, float eps,
                             const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
                             int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, hipStream_t stream);
