@@ -76,7 +76,7 @@ def time_lm_head(model, reps, copies=3):
         ext.lm_head_argmax_fused(h, x, g, b, eps, tables[i % copies], model.suppress, best, None, None, None,
                                  d.max_pos)
 
-    with torch.cuda.stream(stream):
+    with torch.inference_mode(), torch.cuda.stream(stream):
         for i in range(2 * copies):
             launch(i)
         graph = torch.cuda.CUDAGraph()
