@@ -353,13 +353,39 @@ void launch_gemv(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, con
   hipLaunchKernelGGL((gemv_kernel<K, NW, U, MODE, ACT>), dim3(grid), dim3(NW * 64), 0, s, x, ln, cb, w, b, out, n);
 }
 
+// Block shapes of the decode GEMVs (waves per block, row groups per wave), measured on MI355X over the
+// whole decoder step: large blocks (8-16 waves, 80-160 blocks) beat one small block per CU because the
+// prologue (LayerNorm or split-K combine) is repeated per block and its latency is the critical path.
+#ifndef FW_G5120_NW
+#define FW_G5120_NW 8  // LN + fc1 (5120 rows): 32 rows per block
+#endif
+#ifndef FW_G5120_U
+#define FW_G5120_U 2
+#endif
+#ifndef FW_G3840_NW
+#define FW_G3840_NW 8  // LN + q/k/v (3840 rows): 32 rows per block
+#endif
+#ifndef FW_G1280_NW
+#define FW_G1280_NW 8  // LN + cross q (1280 rows): 16 rows per block
+#endif
+#ifndef FW_GK5120_NW
+#define FW_GK5120_NW 8  // fc2 (K = 5120): 8 rows per block
+#endif
+#ifndef FW_GK5120_U
+#define FW_GK5120_U 1
+#endif
+#ifndef FW_CMB_NW
+#define FW_CMB_NW 16  // combine + out projection: 32 rows per block
+#endif
 template <int MODE, int ACT>
 void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w,
                         const _Float16* b, _Float16* out, int n, hipStream_t s) {
-  if (n >= 3840)
-    launch_gemv<kHidden, 4, 2, MODE, ACT>(x, ln, cb, w, b, out, n, s);
+  if (n >= 5120)
+    launch_gemv<kHidden, FW_G5120_NW, FW_G5120_U, MODE, ACT>(x, ln, cb, w, b, out, n, s);
+  else if (n >= 3840)
+    launch_gemv<kHidden, FW_G3840_NW, 2, MODE, ACT>(x, ln, cb, w, b, out, n, s);
   else
-    launch_gemv<kHidden, 2, 1, MODE, ACT>(x, ln, cb, w, b, out, n, s);
+    launch_gemv<kHidden, FW_G1280_NW, 1, MODE, ACT>(x, ln, cb, w, b, out, n, s);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -946,9 +972,9 @@ extern "C" int fw_gemv(const void* x, const void* w, const void* bias, void* out
       dispatch_gemv_1280<kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
   } else {
     if (act == FW_ACT_GELU)
-      launch_gemv<4 * kHidden, 4, 1, kModePlain, FW_ACT_GELU>(xp, ln, cb, wp, bp, op, n_out, stream);
+      launch_gemv<4 * kHidden, FW_GK5120_NW, FW_GK5120_U, kModePlain, FW_ACT_GELU>(xp, ln, cb, wp, bp, op, n_out, stream);
     else
-      launch_gemv<4 * kHidden, 4, 1, kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
+      launch_gemv<4 * kHidden, FW_GK5120_NW, FW_GK5120_U, kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
   }
   return fw_check_launch("gemv");
 }
@@ -1014,7 +1040,7 @@ extern "C" int fw_attn_out_gemv(const float* part_m, const float* part_l, const 
              "attn_out_gemv: at most %d splits (got %d) and %d heads", kMaxCombineSplits, nsplit, kMaxCombineHeads);
   FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * nsplit, "attn_out_gemv: workspace too small");
   const CombineArgs cb{part_m, part_l, part_acc, len_state, max_len, split_keys, nsplit, heads};
-  launch_gemv<kHidden, 4, 1, kModeCombine, FW_ACT_NONE>(nullptr, LnArgs{}, cb, static_cast<const _Float16*>(w),
+  launch_gemv<kHidden, FW_CMB_NW, 1, kModeCombine, FW_ACT_NONE>(nullptr, LnArgs{}, cb, static_cast<const _Float16*>(w),
                                                          static_cast<const _Float16*>(bias), static_cast<_Float16*>(out),
                                                          n_out, stream);
   return fw_check_launch("attn_out_gemv");
