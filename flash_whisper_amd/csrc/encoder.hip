@@ -236,8 +236,11 @@ template <int BM>
 constexpr int dma_stages() { return BM == 256 ? FW_ST256 : BM == 128 ? FW_ST128 : FW_ST64; }
 // Waves per block: a 2-wide column of waves (64 output columns each) and BM / 64 rows of waves, at
 // least 2; each wave owns a (BM / rows) x 64 tile.
+#ifndef FW_W256
+#define FW_W256 8
+#endif
 template <int BM>
-constexpr int gemm_waves() { return BM >= 128 ? BM / 32 : 4; }
+constexpr int gemm_waves() { return BM == 256 ? FW_W256 : 4; }
 
 
 template <int BM>

@@ -5,9 +5,11 @@ The drop-in for custom/model.py (``CustomModel``, custom/model.py:26-225): same 
 with the position kept on the device. Every kernel is this package's HIP code (csrc/); torch only
 allocates device memory, provides the stream and drives hipGraph capture/replay.
 
-Offline there is no checkpoint or tokenizer, so the constructor builds the Whisper-large-v3-turbo
-architecture with seeded random-init weights (flash_whisper_amd.weights) and fixed prompt/suppress ids
-(flash_whisper_amd.config); ``text`` is then empty.
+``model_id="synthetic"`` (the default) builds the Whisper-large-v3-turbo architecture with seeded
+random-init weights (flash_whisper_amd.weights) and fixed prompt/suppress ids (flash_whisper_amd.config);
+``text`` is then empty. Any other ``model_id`` is a local checkpoint directory or a hub id already in the
+local Hugging Face cache (flash_whisper_amd.checkpoint): its weights, generation config and tokenizer
+are used as the reference's from_pretrained path uses them, and nothing is downloaded.
 """
 
 import time
@@ -16,6 +18,7 @@ from types import SimpleNamespace
 import numpy as np
 import torch
 
+from . import checkpoint as C
 from . import weights as W
 from ._lib import (ACT_GELU, EPI_BIAS_GELU, EPI_BIAS_GELU_POS, EPI_BIAS_RESID, EPI_BIAS_RESID_CLAMP,
                    EPI_SCALE_Q)
@@ -34,8 +37,15 @@ class CustomModel:
                  capture=True):
         if not torch.cuda.is_available():
             raise RuntimeError('CustomModel requires a HIP device')
+        self._weights, self.tokenizer, self.checkpoint = None, None, None
         if model_id not in (None, SYNTHETIC):
-            raise NotImplementedError(f'no offline checkpoint loader for {model_id!r}; use model_id="synthetic"')
+            path = C.resolve(model_id, cache_dir)
+            dims = C.load_dims(path)
+            C.check_supported(dims)
+            self._weights = C.Weights(path)
+            self.tokenizer = C.load_tokenizer(path)
+            setup = setup or C.decode_setup(path, self.tokenizer, dims)
+            self.checkpoint = str(path)
         self.ext = load_ext()
         self.dims, self.seed = dims, seed
         self.setup = setup or DecodeSetup()
@@ -70,10 +80,13 @@ class CustomModel:
 
     # ---- weights -----------------------------------------------------------------------------
     def _param(self, name, out=None):
-        """Parameter `name` (HF naming) generated on the device, optionally into the view `out`."""
+        """Parameter `name` (HF naming) from the checkpoint, or generated on the device, optionally into
+        the view `out`."""
         shape, kind = self._specs[name]
         t = out if out is not None else torch.empty(shape, dtype=torch.float16, device='cuda')
         assert tuple(t.shape) == tuple(shape) and t.is_contiguous()
+        if self._weights is not None:
+            return t.copy_(self._weights.get(name, shape))
         return W.device_fill(t, name, kind, self.seed)
 
     def _ln(self, prefix):
@@ -127,6 +140,10 @@ class CustomModel:
         self.embed = self._param(f'{p}.embed_tokens.weight')      # tied with the LM head (custom/model.py:49-50)
         self.pos_embed = self._param(f'{p}.embed_positions.weight')
         self.lm_head = self.embed
+        if self._weights is not None and 'proj_out.weight' in self._weights:
+            self.lm_head = self._weights.get('proj_out.weight', (d.vocab, d.d_model)).cuda()
+            if torch.equal(self.lm_head, self.embed):
+                self.lm_head = self.embed
         self.layers = []
         dm = d.d_model
         self.cross_w = torch.empty(d.dec_layers * 2 * dm, dm, dtype=half, device='cuda')
@@ -385,7 +402,7 @@ class CustomModel:
         ttlt = time.perf_counter() - start
         decode_s = time.perf_counter() - decode_start
         detok_start = time.perf_counter()
-        text = ''  # no tokenizer offline
+        text = C.detokenize(self.tokenizer, token_ids)
         return {
             'text': text, 'token_ids': token_ids, 'ttft_s': ttft, 'ttlt_s': ttlt,
             'e2e_s': time.perf_counter() - start, 'mel_s': mel_s, 'encoder_s': encoder_s,
