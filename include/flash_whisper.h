@@ -138,7 +138,8 @@ int64_t fw_log_mel_ws_floats(int n_samples);
 
 /* out[m, n] <- epilogue(sum_k a[m, k] * w[n, k]) with fp32 accumulation on MFMA.
  * a fp16[m, lda], w fp16[n, ldw], out fp16[m, ldo], bias fp16[n], res fp16[m, ldr] (epilogues that read it).
- * k % 64 == 0, n % 64 == 0. q_cols is used by FW_EPI_SCALE_Q only. */
+ * k % 64 == 0, n % 128 == 0; lda, ldw, ldo, ldr multiples of 8; a, w 16-byte aligned, out, bias, res
+ * 8-byte aligned. q_cols is used by FW_EPI_SCALE_Q only. */
 int fw_gemm(const void* a, int lda, const void* w, int ldw, const void* bias, void* out, int ldo,
             const void* res, int ldr, int m, int n, int k, int epilogue, int q_cols, hipStream_t stream);
 
