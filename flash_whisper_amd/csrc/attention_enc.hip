@@ -9,7 +9,9 @@ namespace {
 
 // ------------------------------------------------------------------------------------------
 // Encoder self-attention, flash style, non-causal, scale 1 (q is pre-scaled by the projection).
-// Block = (head, 128 queries): 4 waves of 32 queries each share one LDS ring of 64-key tiles. Per
+// Block = (head, 128 queries), 8 waves: 4 query groups of 32 x 2 key halves (even / odd 64-key tiles),
+// so two waves share each SIMD and one's softmax overlaps the other's MFMAs; the halves' (m, l, O)
+// are merged through LDS at the end. All waves share one LDS ring whose stages hold a tile pair. Per
 // tile a wave computes S^T = K Q^T (keys x queries) with MFMA, so that every lane holds the scores
 // of a single query column and the online-softmax max/sum need one cross-lane step (lane ^ 32).
 // P^T is fed straight from the S^T accumulator layout as the B operand of O^T = V^T P^T.
@@ -23,9 +25,10 @@ namespace {
 //  - Block ids are remapped so that the query blocks of a head run on one XCD and its K/V stay in
 //    that XCD's L2.
 // ------------------------------------------------------------------------------------------
-constexpr int kEaWaves = 4, kEaQ = 32 * kEaWaves, kEaKV = 64, kEaStages = 4;
+constexpr int kEaQGroups = 4, kEaWaves = 2 * kEaQGroups, kEaQ = 32 * kEaQGroups, kEaKV = 64, kEaStages = 4;
 constexpr int kEaTileBytes = kEaKV * 128;  // one K tile or one V^T tile
 
+// The 4 waves of a key half fill one tile (K then V^T) of a ring stage; `wave` is 0..3 within the half.
 __device__ __forceinline__ void ea_dma(const _Float16* kbase, int ld, const _Float16* vtbase, int seq_pad,
                                        int seq, int kv0, int wave, int lane, uint32_t stage) {
   const int rsub = lane >> 3, slot = lane & 7;
@@ -119,20 +122,24 @@ __device__ __forceinline__ void ea_tile(const u32x4* kt, const u32x4* vtt, const
       }
 }
 
-__global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* __restrict__ qkv,
-                                                                const _Float16* __restrict__ vt,
-                                                                _Float16* __restrict__ out, int seq, int heads) {
-  constexpr int kPerStage = 4;  // copies per thread per stage
-  __shared__ __align__(1024) u32x4 ring[kEaStages * 2 * kEaTileBytes / 16];
+__global__ void __launch_bounds__(kEaWaves * 64) encoder_attention_kernel(const _Float16* __restrict__ qkv,
+                                                                         const _Float16* __restrict__ vt,
+                                                                         _Float16* __restrict__ out, int seq,
+                                                                         int heads) {
+  constexpr int kPerStage = 4;                       // copies per thread per stage
+  constexpr int kPairBytes = 2 * 2 * kEaTileBytes;   // K + V^T of two tiles
+  __shared__ __align__(1024) u32x4 ring[kEaStages * kPairBytes / 16];
+  static_assert(kEaStages * kPairBytes >= kEaQGroups * 64 * 34 * 4, "merge buffer fits in the ring");
 
   const int qblocks = (seq + kEaQ - 1) / kEaQ, nblk = qblocks * heads;
   const int bid = blockIdx.x, full = (nblk / 8) * 8;
   const int job = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
   const int head = job / qblocks, qb = job % qblocks;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wq = wave & (kEaQGroups - 1), half = wave / kEaQGroups;  // query group, key half (both wave-uniform)
   const int lr = lane & 31, lg = lane >> 5;
   const int ld = 3 * heads * kHeadDim, seq_pad = vt_pad(seq);
-  const int q_row = qb * kEaQ + wave * 32 + lr;  // this lane's query column
+  const int q_row = qb * kEaQ + wq * 32 + lr;  // this lane's query column
   const _Float16* kbase = qkv + (heads + head) * kHeadDim;
   const _Float16* vtbase = vt + static_cast<size_t>(head) * kHeadDim * seq_pad;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
@@ -144,10 +151,18 @@ __global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* 
 #pragma unroll
     for (int k = 0; k < 4; ++k) qf[k] = *reinterpret_cast<const h8v*>(qp + 16 * k);
   }
-  const int nt = seq_pad / kEaKV;
+  const int nt = seq_pad / kEaKV, npairs = (nt + 1) / 2;
+  // Stage p holds tiles 2p (half 0) and 2p + 1 (half 1). A half whose tile is past the end copies the
+  // last tile again, so every thread issues the same number of copies per stage (the vmcnt waits
+  // count this thread's own copies).
+  auto issue = [&](int p) {
+    const int t = min(2 * p + half, nt - 1);
+    ea_dma(kbase, ld, vtbase, seq_pad, seq, t * kEaKV, wq, lane,
+           lds0 + (p % kEaStages) * kPairBytes + half * 2 * kEaTileBytes);
+  };
 #pragma unroll
   for (int k = 0; k < kEaStages - 1; ++k)
-    if (k < nt) ea_dma(kbase, ld, vtbase, seq_pad, seq, k * kEaKV, wave, lane, lds0 + k * 2 * kEaTileBytes);
+    if (k < npairs) issue(k);
 
   EaState st;
 #pragma unroll
@@ -157,26 +172,45 @@ __global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* 
   st.m = -INFINITY;
   st.l = 0.f;
 
-  // Returns tile t's K tile in the ring once every wave's copies of it have landed.
-  auto next_tile = [&](int t) {
-    wait_stages_ahead<kPerStage, kEaStages - 2>(min(kEaStages - 2, nt - 1 - t));
-    barrier_only();  // tile t visible to every wave; every wave is done with tile t - 1
-    const int nxt = t + kEaStages - 1;
-    if (nxt < nt)
-      ea_dma(kbase, ld, vtbase, seq_pad, seq, nxt * kEaKV, wave, lane, lds0 + (nxt % kEaStages) * 2 * kEaTileBytes);
-    return ring + (t % kEaStages) * (2 * kEaTileBytes / 16);
+  // Returns this half's K tile of pair p once every wave's copies of the pair have landed.
+  auto next_pair = [&](int p) {
+    wait_stages_ahead<kPerStage, kEaStages - 2>(min(kEaStages - 2, npairs - 1 - p));
+    barrier_only();  // pair p visible to every wave; every wave is done with pair p - 1
+    if (p + kEaStages - 1 < npairs) issue(p + kEaStages - 1);
+    return ring + ((p % kEaStages) * kPairBytes + half * 2 * kEaTileBytes) / 16;
   };
-  const int nfull = seq / kEaKV;  // tiles whose 64 keys are all valid; at most one partial tile follows
-  for (int t = 0; t < nfull; ++t) {
-    const u32x4* kt = next_tile(t);
-    ea_tile<false>(kt, kt + kEaTileBytes / 16, qf, t * kEaKV, seq, lr, lg, st);
+  const int nfull = seq / kEaKV;  // tiles whose 64 keys are all valid; only the last tile may be partial
+  for (int p = 0; p < npairs - 1; ++p) {  // both tiles of these pairs are full
+    const u32x4* kt = next_pair(p);
+    ea_tile<false>(kt, kt + kEaTileBytes / 16, qf, (2 * p + half) * kEaKV, seq, lr, lg, st);
   }
-  if (nfull < nt) {
-    const u32x4* kt = next_tile(nfull);
-    ea_tile<true>(kt, kt + kEaTileBytes / 16, qf, nfull * kEaKV, seq, lr, lg, st);
+  {
+    const u32x4* kt = next_pair(npairs - 1);
+    const int t = 2 * (npairs - 1) + half;
+    if (t < nfull)
+      ea_tile<false>(kt, kt + kEaTileBytes / 16, qf, t * kEaKV, seq, lr, lg, st);
+    else if (t < nt)
+      ea_tile<true>(kt, kt + kEaTileBytes / 16, qf, t * kEaKV, seq, lr, lg, st);
   }
-  if (q_row >= seq) return;
-  const float inv = 1.0f / st.l;
+
+  // Merge the key halves: half 1 hands (m, l, O) through LDS to the wave of half 0 with the same
+  // query group; lane for lane the registers describe the same query and head dims.
+  lds_barrier();  // every wave is done with the ring
+  float* mbuf = reinterpret_cast<float*>(ring) + (wq * 64 + lane) * 34;
+  if (half == 1) {
+    mbuf[0] = st.m;
+    mbuf[1] = st.l;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mbuf[2 + 16 * b + r] = st.o[b][r];
+  }
+  lds_barrier();
+  if (half == 1 || q_row >= seq) return;
+  const float m1 = mbuf[0], l1 = mbuf[1];
+  const float m = fmaxf(st.m, m1);
+  const float a0 = __builtin_amdgcn_exp2f(st.m - m), a1 = __builtin_amdgcn_exp2f(m1 - m);  // m1 may be -inf
+  const float inv = 1.0f / (st.l * a0 + l1 * a1);
   _Float16* orow = out + static_cast<size_t>(q_row) * heads * kHeadDim + head * kHeadDim;
 #pragma unroll
   for (int db = 0; db < 2; ++db)
@@ -184,7 +218,10 @@ __global__ void __launch_bounds__(256) encoder_attention_kernel(const _Float16* 
     for (int j = 0; j < 4; ++j) {
       h4v v4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v4[e] = f2h(st.o[db][4 * j + e] * inv);
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * j + e;
+        v4[e] = f2h((st.o[db][r] * a0 + mbuf[2 + 16 * db + r] * a1) * inv);
+      }
       *reinterpret_cast<h4v*>(orow + 32 * db + 8 * j + 4 * lg) = v4;
     }
 }
@@ -230,7 +267,7 @@ extern "C" int fw_encoder_attention(const void* qkv, const void* vt, void* out, 
   if (!aligned(qkv, 16) || !aligned(vt, 16) || !aligned(out, 8))
     return fw_fail(FW_EINVAL, "encoder_attention: qkv and vt must be 16-byte aligned, out 8-byte aligned");
   const int blocks = (seq + kEaQ - 1) / kEaQ * heads;
-  hipLaunchKernelGGL(encoder_attention_kernel, dim3(blocks), dim3(256), 0, stream, static_cast<const _Float16*>(qkv),
+  hipLaunchKernelGGL(encoder_attention_kernel, dim3(blocks), dim3(kEaWaves * 64), 0, stream, static_cast<const _Float16*>(qkv),
                      static_cast<const _Float16*>(vt), static_cast<_Float16*>(out), seq, heads);
   return fw_check_launch("encoder_attention");
 }

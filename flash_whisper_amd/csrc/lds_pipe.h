@@ -41,6 +41,16 @@ __device__ __forceinline__ void wait_stages_ahead(int ahead) {
   }
 }
 
+// Workgroup barrier for LDS hand-off only: waits for this wave's LDS traffic, not for its global
+// loads (__syncthreads would also drain the prefetches that are meant to stay in flight). The
+// lgkmcnt(0) wait goes through the builtin (encoding: vmcnt 63, expcnt 7, lgkmcnt 0) so the compiler
+// knows every earlier LDS read has completed and adds no waits of its own for them afterwards; the
+// barrier itself stays an asm statement with a memory clobber so no LDS access moves across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // Keys per transposed-V row: seq rounded up to whole 64-key attention tiles.
 __host__ __device__ constexpr int vt_pad(int seq) { return (seq + 63) / 64 * 64; }
 
