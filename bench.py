@@ -93,6 +93,23 @@ def time_lm_head(model, reps, copies=3):
     return start.elapsed_time(end) * 1e3 / reps
 
 
+def serving_throughput(model, lanes, clips, tokens):
+    """Clips per second with `lanes` clips in flight (flash_whisper_amd.serve) against one at a time, on
+    `clips` seeded 30 s clips of `tokens` greedy tokens each (fixed length)."""
+    from flash_whisper_amd.audio import synthetic_clip
+    from flash_whisper_amd.serve import Scheduler
+
+    batch = [synthetic_clip(100 + i) for i in range(clips)]
+    out = {'lanes': lanes, 'clips': clips, 'tokens_per_clip': tokens}
+    for n in (1, lanes):
+        sched = Scheduler(model, lanes=n)
+        sched.transcribe_many(batch[:n], max_new_tokens=tokens, stop_at_eos=False)  # warm-up
+        res = sched.transcribe_many(batch, max_new_tokens=tokens, stop_at_eos=False)
+        out[f'clips_per_s_{n}_lane' + ('s' if n > 1 else '')] = round(clips / res[0]['wall_s'], 2)
+        del sched
+    return out
+
+
 def cpu_baseline(model, seconds):
     """The CPU oracle's decoder step (numpy fp32 with the reference's fp16 rounding points) on this host,
     on the GPU model's cross K/V, for a bounded number of steps."""
@@ -130,6 +147,7 @@ def main():
     ap.add_argument('--kernel-reps', type=int, default=60)
     ap.add_argument('--cpu-seconds', type=float, default=12.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--lanes', type=int, default=2, help='clips in flight for the serving-throughput extra (0: skip)')
     ap.add_argument('--copy-calibration', action='store_true',
                     help='also run 4 plain 256 MiB device copies (the reference kernel for PMC byte counters)')
     args = ap.parse_args()
@@ -167,6 +185,7 @@ def main():
     model.record_events = False
 
     lm_us = time_lm_head(model, args.kernel_reps)
+    serve = serving_throughput(model, args.lanes, 2 * args.lanes, args.tokens) if args.lanes > 1 else None
     if args.copy_calibration:
         src = torch.empty(128 << 20, dtype=torch.float16, device='cuda')
         dst = torch.empty_like(src)
@@ -203,6 +222,8 @@ def main():
                      'traffic_source': 'profiles/lm_head_kernel_traffic.md', 'us_per_launch': round(lm_us, 2),
                      'bytes_per_launch': lm_bytes},
     }
+    if serve is not None:
+        out['serving'] = serve
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(model, args.cpu_seconds)
     print(json.dumps(out), flush=True)

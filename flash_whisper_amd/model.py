@@ -64,11 +64,7 @@ class CustomModel:
         self._init_decoder()
 
         self.mel_filters = torch.from_numpy(mel_filters()).to(dev)
-        self.wave = torch.zeros(N_SAMPLES, device=dev)
-        self.wave_host = torch.zeros(N_SAMPLES, pin_memory=True)
-        self.mel32 = torch.zeros(d.n_mels, d.mel_frames, device=dev)
-        self.mel16 = torch.zeros(d.mel_frames, d.n_mels, dtype=half, device=dev)  # time-major encoder input
-        self.mel_ws = self.ext.log_mel_workspace(N_SAMPLES)
+        self._alloc_frontend_buffers()
 
         self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
         self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
@@ -77,6 +73,67 @@ class CustomModel:
             self.graph_one, self.graph_chunk = self._capture()
             self.graph_enc = self._capture_encoder()
         torch.cuda.synchronize()
+
+    # ---- per-lane buffers ---------------------------------------------------------------------
+    def _alloc_frontend_buffers(self):
+        d, dev, half = self.dims, 'cuda', torch.float16
+        self.wave = torch.zeros(N_SAMPLES, device=dev)
+        self.wave_host = torch.zeros(N_SAMPLES, pin_memory=True)
+        self.mel32 = torch.zeros(d.n_mels, d.mel_frames, device=dev)
+        self.mel16 = torch.zeros(d.mel_frames, d.n_mels, dtype=half, device=dev)  # time-major encoder input
+        self.mel_ws = self.ext.log_mel_workspace(N_SAMPLES)
+
+    def _alloc_encoder_buffers(self):
+        d, half = self.dims, torch.float16
+        t, dm = d.enc_len, d.d_model
+        self.x1 = torch.empty(d.mel_frames, dm, dtype=half, device='cuda')
+        self.ex = torch.empty(t, dm, dtype=half, device='cuda')        # residual stream
+        self.ey = torch.empty(t, dm, dtype=half, device='cuda')        # LayerNorm output
+        self.eqkv = torch.empty(t, 3 * dm, dtype=half, device='cuda')
+        self.eattn = torch.empty(t, dm, dtype=half, device='cuda')
+        self.evt = self.ext.encoder_vt_workspace(t, self.heads)
+        self.effn = torch.empty(t, d.ffn, dtype=half, device='cuda')
+        self.enc_out = torch.empty(t, dm, dtype=half, device='cuda')
+
+    def _alloc_decoder_buffers(self):
+        d, half = self.dims, torch.float16
+        dm = d.d_model
+        self.suppress = self.base_mask.clone()
+        self.self_kv = torch.zeros(d.dec_layers, 2, d.heads, d.max_pos, d.head_dim, dtype=half, device='cuda')
+        self.cross_kv = torch.zeros(d.dec_layers, 2, d.heads, d.enc_len, d.head_dim, dtype=half, device='cuda')
+        self.h = torch.zeros(2, dm, dtype=half, device='cuda')   # ping-pong residual stream
+        self.y = torch.zeros(1, dm, dtype=half, device='cuda')
+        self.qkv = torch.zeros(3 * dm, dtype=half, device='cuda')
+        self.q = torch.zeros(dm, dtype=half, device='cuda')
+        self.attn = torch.zeros(dm, dtype=half, device='cuda')
+        self.xo = torch.zeros(dm, dtype=half, device='cuda')
+        self.ffn = torch.zeros(d.ffn, dtype=half, device='cuda')
+        self.pending = torch.zeros(dm, dtype=half, device='cuda')
+        self.cur = torch.zeros(1, dtype=torch.long, device='cuda')
+        self.state = torch.zeros(2, dtype=torch.long, device='cuda')  # [position, generated count]
+        self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
+        self.best = torch.zeros(1, dtype=torch.long, device='cuda')
+        # split-K attention partials (both the fused step and the reference-granularity step)
+        self.workspace = workspace(d.heads, -(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, SELF_SPLIT, CROSS_SPLIT)))
+
+    @torch.inference_mode()
+    def new_lane(self):
+        """Another decode lane on the same weights: its own activations, caches, decoding state and
+        graphs, so several clips can be in flight at once on separate streams (flash_whisper_amd.serve)."""
+        lane = object.__new__(type(self))
+        lane.__dict__.update(self.__dict__)
+        lane.selftest = dict(self.selftest)
+        lane.chunk_events, lane.record_events = [], False
+        lane._alloc_frontend_buffers()
+        lane._alloc_encoder_buffers()
+        lane._alloc_decoder_buffers()
+        lane.graph_one = lane.graph_chunk = lane.graph_enc = None
+        if self.graph_chunk is not None:
+            lane.graph_one, lane.graph_chunk = lane._capture()
+        if self.graph_enc is not None:
+            lane.graph_enc = lane._capture_encoder()
+        torch.cuda.synchronize()
+        return lane
 
     # ---- weights -----------------------------------------------------------------------------
     def _param(self, name, out=None):
@@ -125,15 +182,7 @@ class CustomModel:
                 fc1_w=self._param(f'{p}.fc1.weight'), fc1_b=self._param(f'{p}.fc1.bias'),
                 fc2_w=self._param(f'{p}.fc2.weight'), fc2_b=self._param(f'{p}.fc2.bias')))
         self.enc_ln = self._ln(f'{e}.layer_norm')
-        t, dm, half = d.enc_len, d.d_model, torch.float16
-        self.x1 = torch.empty(d.mel_frames, dm, dtype=half, device='cuda')
-        self.ex = torch.empty(t, dm, dtype=half, device='cuda')        # residual stream
-        self.ey = torch.empty(t, dm, dtype=half, device='cuda')        # LayerNorm output
-        self.eqkv = torch.empty(t, 3 * dm, dtype=half, device='cuda')
-        self.eattn = torch.empty(t, dm, dtype=half, device='cuda')
-        self.evt = self.ext.encoder_vt_workspace(t, self.heads)
-        self.effn = torch.empty(t, d.ffn, dtype=half, device='cuda')
-        self.enc_out = torch.empty(t, dm, dtype=half, device='cuda')
+        self._alloc_encoder_buffers()
 
     def _init_decoder(self):
         d, p, half = self.dims, 'model.decoder', torch.float16
@@ -170,24 +219,7 @@ class CustomModel:
         self.base_mask[list(self.setup.suppress)] = True
         self.first_mask = self.base_mask.clone()
         self.first_mask[list(self.setup.begin_suppress)] = True
-        self.suppress = self.base_mask.clone()
-
-        self.self_kv = torch.zeros(d.dec_layers, 2, d.heads, d.max_pos, d.head_dim, dtype=half, device='cuda')
-        self.cross_kv = torch.zeros(d.dec_layers, 2, d.heads, d.enc_len, d.head_dim, dtype=half, device='cuda')
-        self.h = torch.zeros(2, dm, dtype=half, device='cuda')   # ping-pong residual stream
-        self.y = torch.zeros(1, dm, dtype=half, device='cuda')
-        self.qkv = torch.zeros(3 * dm, dtype=half, device='cuda')
-        self.q = torch.zeros(dm, dtype=half, device='cuda')
-        self.attn = torch.zeros(dm, dtype=half, device='cuda')
-        self.xo = torch.zeros(dm, dtype=half, device='cuda')
-        self.ffn = torch.zeros(d.ffn, dtype=half, device='cuda')
-        self.pending = torch.zeros(dm, dtype=half, device='cuda')
-        self.cur = torch.zeros(1, dtype=torch.long, device='cuda')
-        self.state = torch.zeros(2, dtype=torch.long, device='cuda')  # [position, generated count]
-        self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
-        self.best = torch.zeros(1, dtype=torch.long, device='cuda')
-        # split-K attention partials (both the fused step and the reference-granularity step)
-        self.workspace = workspace(d.heads, -(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, SELF_SPLIT, CROSS_SPLIT)))
+        self._alloc_decoder_buffers()
 
     # ---- front end ---------------------------------------------------------------------------
     def _log_mel(self, wave):
@@ -344,34 +376,32 @@ class CustomModel:
                 self._step()
 
     # ---- per-clip ------------------------------------------------------------------------------
-    @torch.inference_mode()
-    def transcribe(self, audio, max_new_tokens=None, stop_at_eos=True):
-        """custom/model.py:173-225. ``max_new_tokens``/``stop_at_eos`` select the fixed-length mode used
-        for the synthetic benchmark (224 tokens, no EOS stop); the defaults are the reference's."""
+    def _check_audio(self, audio, max_new_tokens):
+        """custom/model.py:175-178; returns the token budget."""
         if not isinstance(audio, np.ndarray) or audio.dtype != np.float32 or audio.ndim != 1:
             raise ValueError('audio must be a one-dimensional float32 NumPy array')
         if not 0 < audio.size <= N_SAMPLES or not np.isfinite(audio).all():
             raise ValueError('audio must contain finite samples and be between 0 and 30 seconds')
-        max_new = self.max_new if max_new_tokens is None else min(int(max_new_tokens), self.max_new)
-        torch.cuda.synchronize()
-        start = time.perf_counter()
+        return self.max_new if max_new_tokens is None else min(int(max_new_tokens), self.max_new)
 
+    # The three stages below only enqueue work on the current stream (no host synchronisation), so a
+    # scheduler can drive several lanes at once; transcribe() synchronises between them for its timings.
+    def _enqueue_mel(self, audio):
+        """Zero-padded waveform through the pinned staging buffer, then the HIP log-mel."""
         host = self.wave_host.numpy()
         host[:audio.size] = audio
         host[audio.size:] = 0.0
         self.wave.copy_(self.wave_host, non_blocking=True)
         self._log_mel(self.wave)
-        torch.cuda.synchronize()
-        mel_s = time.perf_counter() - start
 
+    def _enqueue_encoder(self):
         if self.graph_enc is not None:
             self.graph_enc.replay()
         else:
             self._encode()
-        torch.cuda.synchronize()
-        encoder_s = time.perf_counter() - start - mel_s
 
-        decode_start = time.perf_counter()
+    def _enqueue_prompt(self):
+        """The prompt steps (custom/model.py:196-207): afterwards tokens[0] is the first generated token."""
         self.state.zero_()
         last = len(self.prompt) - 1
         for i, token in enumerate(self.prompt):
@@ -383,6 +413,25 @@ class CustomModel:
                 self.suppress.copy_(self.base_mask)
             else:
                 self.state[1].zero_()  # predictions made inside the prompt are discarded
+
+    @torch.inference_mode()
+    def transcribe(self, audio, max_new_tokens=None, stop_at_eos=True):
+        """custom/model.py:173-225. ``max_new_tokens``/``stop_at_eos`` select the fixed-length mode used
+        for the synthetic benchmark (224 tokens, no EOS stop); the defaults are the reference's."""
+        max_new = self._check_audio(audio, max_new_tokens)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+
+        self._enqueue_mel(audio)
+        torch.cuda.synchronize()
+        mel_s = time.perf_counter() - start
+
+        self._enqueue_encoder()
+        torch.cuda.synchronize()
+        encoder_s = time.perf_counter() - start - mel_s
+
+        decode_start = time.perf_counter()
+        self._enqueue_prompt()
         token_ids = [int(self.tokens[0])]
         ttft = time.perf_counter() - start
         self.chunk_events = []

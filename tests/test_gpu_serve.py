@@ -1,0 +1,29 @@
+"""Several clips in flight on separate lanes and streams (flash_whisper_amd.serve) must produce exactly
+the token ids of one-at-a-time CustomModel.transcribe, in fixed-length and EOS-stopping modes."""
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope='module')
+def model(hip_device):
+    from flash_whisper_amd.model import CustomModel
+
+    return CustomModel(seed=0, selftest=False)
+
+
+@pytest.mark.parametrize('lanes,stop_at_eos', [(2, False), (3, True)])
+def test_lanes_match_sequential_transcribe(model, lanes, stop_at_eos):
+    from flash_whisper_amd.audio import synthetic_clip
+    from flash_whisper_amd.serve import Scheduler
+
+    clips = [synthetic_clip(s) for s in (0, 1, 2, 3)]
+    clips[3] = clips[3][:5 * 16000]  # a short clip too
+    ref = [model.transcribe(c, max_new_tokens=30, stop_at_eos=stop_at_eos)['token_ids'] for c in clips]
+    sched = Scheduler(model, lanes=lanes)
+    out = sched.transcribe_many(clips, max_new_tokens=30, stop_at_eos=stop_at_eos)
+    assert [r['token_ids'] for r in out] == ref
+    assert all(r['wall_s'] >= r['e2e_s'] > 0 for r in out)
+    # the lanes stay usable one at a time
+    assert sched.lanes[-1].transcribe(clips[0], max_new_tokens=30, stop_at_eos=stop_at_eos)['token_ids'] == ref[0]
