@@ -1,6 +1,6 @@
 // Whisper encoder kernels for gfx950: an MFMA GEMM with fused epilogues (also used as an
-// implicit-GEMM conv1d and for the decoder cross K/V projection), a row LayerNorm and a
-// flash-style encoder self-attention. Semantics follow HF WhisperEncoder.forward in fp16
+// implicit-GEMM conv1d and for the decoder cross K/V projection) and a row LayerNorm; the encoder
+// self-attention is in attention_enc.hip. Semantics follow HF WhisperEncoder.forward in fp16
 // (transformers models/whisper/modeling_whisper.py:592-648, layer :379-414, attention :284-358):
 // every op output is rounded to fp16, accumulation is fp32.
 #include "lds_pipe.h"
@@ -9,15 +9,18 @@ namespace fw {
 namespace {
 
 // ------------------------------------------------------------------------------------------
-// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 64, 4 waves in a 2 x 2
-// arrangement, each wave (BM/2) x 64 built from v_mfma_f32_32x32x16_f16 tiles.
+// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 64 with BM in {256, 128, 64};
+// waves in a (BM / 64 or 2) x 2 arrangement, each wave a (64 or 32) x 64 tile of
+// v_mfma_f32_32x32x16_f16 products.
 //  - LDS: one [rows][64] fp16 tile per operand and stage, 8 x 16-byte chunks per row, chunk c of
 //    row r stored in slot c ^ (r & 7), so the 8 rows a quarter-wave reads for one MFMA operand hit
 //    8 different bank groups (conflict-free ds_read_b128).
-//  - Pipeline: two LDS buffers and two register staging sets. Stage kt + 2 is requested from global
-//    memory while stage kt feeds the MFMAs, so each load has two stages of MFMA work to arrive in.
+//  - Plain GEMMs (gemm_dma_kernel): global -> LDS copies into a ring of stages, operand fragments
+//    double-buffered in registers (see the pipeline notes above that kernel).
+//  - Implicit-GEMM conv (gemm_kernel): the A tile is gathered from the time-major input through
+//    registers (two staging sets, two LDS buffers), since its rows are shifted time windows.
 //  - Tile order: hardware deals blocks round-robin over the 8 XCDs; the block id is remapped so each
-//    XCD works on a contiguous run of row-major tiles that share A row panels in its L2.
+//    XCD works on its own part of the tile grid and its L2 sees only that part's operand panels.
 // MFMA 32x32x16 f16 operand layout (lane l, g = l / 32):
 //   A: lane holds A[l % 32][8g .. 8g + 7]      B: lane holds B[8g .. 8g + 7][l % 32]
 //   C: acc[r] = C[8 (r / 4) + 4 g + (r % 4)][l % 32], r = 0 .. 15
@@ -226,9 +229,11 @@ __device__ __forceinline__ void mma_frags(const Frags<kTM, kTN>& f, f16v (&acc)[
 // fragments in registers by then, so its LDS slot is free), refill that slot with stage kt + ST,
 // start the LDS reads of stage kt + 1's fragments, and run stage kt's MFMAs while they arrive. Copies
 // have ST - 1 stages of MFMA time to land and LDS read latency is hidden behind the MFMAs.
-// The LDS ring depth ST (ST - 1 stages in flight) is picked per tile height: 128-row tiles use two
-// 32 KB stages so that two blocks share a CU and hide each other's copy latency; 64-row tiles
-// (launched when there are fewer tiles than CUs) use four 24 KB stages in one block.
+// The LDS ring depth ST is picked per tile height: 256-row tiles use three 48 KB stages (one 8-wave
+// block per CU); 128-row tiles two 32 KB stages so that two blocks share a CU and hide each other's
+// copy latency; 64-row tiles (launched when 128-row tiles would leave CUs idle) four 24 KB stages.
+// Tuning knobs (defaults measured on MI355X): ring depths per tile height, the minimum number of
+// 256-row tiles for that shape, waves per 256-row block, and the XCD rectangle grouping.
 #ifndef FW_ST128
 #define FW_ST128 2
 #endif
@@ -250,7 +255,6 @@ constexpr int dma_stages() { return BM == 256 ? FW_ST256 : BM == 128 ? FW_ST128 
 #endif
 template <int BM>
 constexpr int gemm_waves() { return BM == 256 ? FW_W256 : 4; }
-
 
 template <int BM>
 __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
