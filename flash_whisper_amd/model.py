@@ -68,9 +68,9 @@ class CustomModel:
 
         self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
         self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
-        self.graph_one = self.graph_chunk = self.graph_enc = None
+        self.graph_one = self.graph_chunk = self.graph_prefix = self.graph_enc = None
         if capture:
-            self.graph_one, self.graph_chunk = self._capture()
+            self.graph_one, self.graph_chunk, self.graph_prefix = self._capture()
             self.graph_enc = self._capture_encoder()
         torch.cuda.synchronize()
 
@@ -127,9 +127,9 @@ class CustomModel:
         lane._alloc_frontend_buffers()
         lane._alloc_encoder_buffers()
         lane._alloc_decoder_buffers()
-        lane.graph_one = lane.graph_chunk = lane.graph_enc = None
+        lane.graph_one = lane.graph_chunk = lane.graph_prefix = lane.graph_enc = None
         if self.graph_chunk is not None:
-            lane.graph_one, lane.graph_chunk = lane._capture()
+            lane.graph_one, lane.graph_chunk, lane.graph_prefix = lane._capture()
         if self.graph_enc is not None:
             lane.graph_enc = lane._capture_encoder()
         torch.cuda.synchronize()
@@ -288,11 +288,12 @@ class CustomModel:
             torch.cuda.synchronize()
 
     # ---- decoder -----------------------------------------------------------------------------
-    def _step(self):
+    def _step(self, lm_head=True):
         """One decoder token, entirely on the device (custom/model.py:107-123) in 34 launches:
         per layer [LN1+QKV] [self-attn split-K + KV write] [combine + out] [LN2+cross-q]
         [cross-attn split-K] [combine + cross-out] [LN3+fc1+GELU] [fc2], then
-        [final LN + LM head + argmax] [finalize]."""
+        [final LN + LM head + argmax] [finalize]. Without `lm_head` (prompt tokens whose prediction
+        is discarded) the step ends after the layers and only advances the position."""
         ext, d, dm = self.ext, self.dims, self.dims.d_model
         ws = self.workspace
         q, k_new, v_new = self.qkv[:dm], self.qkv[dm:2 * dm], self.qkv[2 * dm:]
@@ -316,6 +317,9 @@ class CustomModel:
             ext.ln_gemv(self.h[b], self.xo, self.h[a], g, be, eps, *lay.fc1, self.ffn, act=ACT_GELU)
             ext.gemv(self.ffn, *lay.fc2, self.pending)
             a, b = b, a
+        if not lm_head:
+            self.state[0].add_(1)
+            return
         g, be, eps = self.final_ln
         ext.lm_head_argmax_fused(self.h[b], self.pending, g, be, eps, self.lm_head, self.suppress, self.best,
                                  self.tokens, self.state, self.cur, self.max_pos)
@@ -348,7 +352,8 @@ class CustomModel:
         ext.argmax_finalize(self.best, self.tokens, self.state, self.cur, self.max_pos)
 
     def _capture(self):
-        """Warm-up, then 1-step and CHUNK-step decoder graphs (custom/model.py:125-141)."""
+        """Warm-up, then 1-step and CHUNK-step decoder graphs (custom/model.py:125-141), plus a 1-step
+        graph without the LM head for the prompt tokens before the last."""
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -356,24 +361,24 @@ class CustomModel:
                 self._step()
         torch.cuda.current_stream().wait_stream(side)
         graphs = []
-        for steps in (1, CHUNK):
+        for steps, lm_head in ((1, True), (CHUNK, True), (1, False)):
             self.state.zero_()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 for _ in range(steps):
-                    self._step()
+                    self._step(lm_head)
             graphs.append(graph)
         torch.cuda.synchronize()
         self.self_kv.zero_()
         self.state.zero_()
         return graphs
 
-    def _replay(self, graph, steps):
+    def _replay(self, graph, steps, lm_head=True):
         if graph is not None:
             graph.replay()
         else:
             for _ in range(steps):
-                self._step()
+                self._step(lm_head)
 
     # ---- per-clip ------------------------------------------------------------------------------
     def _check_audio(self, audio, max_new_tokens):
@@ -401,18 +406,19 @@ class CustomModel:
             self._encode()
 
     def _enqueue_prompt(self):
-        """The prompt steps (custom/model.py:196-207): afterwards tokens[0] is the first generated token."""
+        """The prompt steps (custom/model.py:196-207): afterwards tokens[0] is the first generated token.
+        The reference runs full steps and discards the predictions made inside the prompt; here the
+        tokens before the last run without the LM head (same K/V cache rows, same final token)."""
         self.state.zero_()
         last = len(self.prompt) - 1
         for i, token in enumerate(self.prompt):
             self.cur.fill_(token)
-            if i == last:
-                self.suppress.copy_(self.first_mask)
+            if i < last:
+                self._replay(self.graph_prefix, 1, lm_head=False)
+                continue
+            self.suppress.copy_(self.first_mask)
             self._replay(self.graph_one, 1)
-            if i == last:
-                self.suppress.copy_(self.base_mask)
-            else:
-                self.state[1].zero_()  # predictions made inside the prompt are discarded
+            self.suppress.copy_(self.base_mask)
 
     @torch.inference_mode()
     def transcribe(self, audio, max_new_tokens=None, stop_at_eos=True):

@@ -92,12 +92,12 @@ def test_decoder_teacher_forced_vs_oracle(model, clip):
 
 def test_graph_replay_matches_eager(model, clip):
     res_graph = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
-    g1, gc = model.graph_one, model.graph_chunk
+    g1, gc, gp = model.graph_one, model.graph_chunk, model.graph_prefix
     try:
-        model.graph_one = model.graph_chunk = None
+        model.graph_one = model.graph_chunk = model.graph_prefix = None
         res_eager = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
     finally:
-        model.graph_one, model.graph_chunk = g1, gc
+        model.graph_one, model.graph_chunk, model.graph_prefix = g1, gc, gp
     assert res_graph['token_ids'] == res_eager['token_ids']
     res_graph2 = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
     assert res_graph2['token_ids'] == res_graph['token_ids']
