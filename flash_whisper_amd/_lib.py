@@ -30,6 +30,12 @@ SIGNATURES = {
     'fw_decode_attention_fused': (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_float, P]),
     'fw_attention_split': (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, c_int64, c_float, P]),
     'fw_attn_out_gemv': (c_int, [P, P, P, c_int64, P, c_int, c_int, c_int, P, P, P, c_int, P]),
+    'fw_gemv_batch': (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    'fw_ln_gemv_batch': (c_int, [P, P, P, P, P, c_float, P, P, P, P, c_int, c_int, P, P, P, c_int, c_int, c_int, c_int,
+                                 P]),
+    'fw_attention_split_batch': (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, P, P, P, c_int64, c_float, c_int, c_int,
+                                         c_int, P]),
+    'fw_attn_out_gemv_batch': (c_int, [P, P, P, c_int64, P, c_int, c_int, c_int, P, P, P, c_int, c_int, P]),
     'fw_lm_head_argmax_fused': (c_int, [P, P, P, P, c_float, P, P, c_int, c_int, P, P, P, P, c_int, P]),
     'fw_log_mel': (c_int, [P, c_int, P, P, P, P, c_int64, P]),
     'fw_log_mel_ws_floats': (c_int64, [c_int]),

@@ -127,10 +127,11 @@ __device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b
   ln_finish<NT>(in, b != nullptr, r_out, eps, y_out, red);
 }
 
+// Token and position embedding rows of vector v of a batch: token cur[v] at position state[0] + v.
 __device__ __forceinline__ void embed_rows(const int64_t* cur, const int64_t* state, const _Float16* embed,
                                            const _Float16* pos_embed, int vocab, int max_pos, const _Float16** a,
-                                           const _Float16** b) {
-  int64_t tok = cur[0], pos = state[0];
+                                           const _Float16** b, int v = 0) {
+  int64_t tok = cur[v], pos = state[0] + v;
   tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
   pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
   *a = embed + tok * kHidden;
@@ -197,14 +198,27 @@ struct CombineArgs {
   int split_keys;
   int nsplit;
   int heads;
+  int pos_offset;  // vector v of a batch attends at position len_state[0] + v
+
+  // The partials of vector v of a batch (laid out vector-major, heads * nsplit slots each).
+  __device__ CombineArgs vec(int v) const {
+    CombineArgs c = *this;
+    const size_t slots = static_cast<size_t>(heads) * nsplit;
+    c.part_m += v * slots;
+    c.part_l += v * slots;
+    c.part_acc += v * slots * kHeadDim;
+    c.pos_offset = v;
+    return c;
+  }
 };
 
 constexpr int kMaxCombineSplits = 8;   // splits per head the combine prologue merges
 constexpr int kMaxCombineHeads = 32;
 
-__device__ __forceinline__ int active_splits(const int64_t* len_state, int max_len, int split_keys, int nsplit) {
+__device__ __forceinline__ int active_splits(const int64_t* len_state, int max_len, int split_keys, int nsplit,
+                                             int pos_offset = 0) {
   if (!len_state) return nsplit;
-  int64_t p = len_state[0];
+  int64_t p = len_state[0] + pos_offset;
   p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
   return static_cast<int>((p + split_keys) / split_keys);  // ceil((p + 1) / split_keys)
 }
@@ -223,7 +237,7 @@ struct CombineRegs {
 template <int NT>
 __device__ __forceinline__ void combine_load(const CombineArgs& c, CombineRegs<NT>& r) {
   constexpr int S = kMaxCombineSplits;
-  r.active = active_splits(c.len_state, c.max_len, c.split_keys, c.nsplit);
+  r.active = active_splits(c.len_state, c.max_len, c.split_keys, c.nsplit, c.pos_offset);
   const int h0 = threadIdx.x;  // threads below `heads` also own one head's weights
 #pragma unroll
   for (int s = 0; s < S; ++s) {
@@ -278,14 +292,21 @@ __device__ __forceinline__ void combine_finish(const CombineArgs& c, const Combi
 
 constexpr int kModePlain = 0, kModeLn = 1, kModeCombine = 2;
 
-template <int K, int NW, int U, int MODE, int ACT>
+// Stands in for a missing bias: a load from it replaces a branch around the bias load (a branch
+// whose join would wait for every load issued before it).
+__device__ _Float16 g_zero_half = static_cast<_Float16>(0.f);
+
+// NV input vectors (a batch of decoder positions, NV <= kMaxBatch) share every weight row load: vector
+// v reads x / h / h_out at offset v * K and writes out + v * n; its LN or combine prologue is that of
+// a single-vector launch, so each vector's result is bit-identical to NV separate launches.
+template <int K, int NW, int U, int MODE, int ACT, int NV = 1>
 __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restrict__ xin, LnArgs ln, CombineArgs cb,
                                                        const _Float16* __restrict__ w,
                                                        const _Float16* __restrict__ bias, _Float16* __restrict__ out,
                                                        int n) {
   using RS = RowSplit<K>;
   constexpr int kRowsPerBlock = NW * RS::kRPW * U;
-  __shared__ __align__(16) _Float16 y_lds[MODE != kModePlain ? K : 8];
+  __shared__ __align__(16) _Float16 y_lds[MODE != kModePlain ? NV * K : 8];
   __shared__ float red[NW];
   __shared__ float wgt[MODE == kModeCombine ? kMaxCombineHeads * kMaxCombineSplits : 1];
   __shared__ float inv_den[MODE == kModeCombine ? kMaxCombineHeads : 1];
@@ -293,64 +314,102 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   const int sub = lane % RS::kLPR, rsel = lane / RS::kLPR;
   // Order of requests: the prologue's inputs (small, on the critical path), then this block's weight
   // rows, which do not depend on the input vector and stay in flight while the prologue computes.
-  LnRegs<NW * 64> lnr;
-  CombineRegs<MODE == kModeCombine ? NW * 64 : 64> cbr;
+  LnRegs<NW * 64> lnr[MODE == kModeLn ? NV : 1];
+  CombineRegs<MODE == kModeCombine ? NW * 64 : 64> cbr;  // one vector at a time
   if constexpr (MODE == kModeLn) {
-    const _Float16 *a = ln.h, *b = ln.x;
-    if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b);
-    ln_load<NW * 64>(a, b, ln.gamma, ln.beta, lnr);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const _Float16* a = ln.h ? ln.h + v * kHidden : nullptr;
+      const _Float16* b = ln.x ? ln.x + v * kHidden : nullptr;
+      if (ln.cur) embed_rows(ln.cur, ln.state, ln.embed, ln.pos_embed, ln.vocab, ln.max_pos, &a, &b, v);
+      ln_load<NW * 64>(a, b, ln.gamma, ln.beta, lnr[v]);
+    }
   } else if constexpr (MODE == kModeCombine) {
-    combine_load<NW * 64>(cb, cbr);
+    combine_load<NW * 64>(NV > 1 ? cb.vec(0) : cb, cbr);
   }
   const int row0 = blockIdx.x * kRowsPerBlock + wave * RS::kRPW * U + rsel;
+  // Rows past n load row n - 1 (their results are never stored): no load sits under a lane mask,
+  // so none of them forces a wait for the loads before it. The bias is requested first, so waiting
+  // for it never waits for a weight row.
+  _Float16 braw[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) braw[u] = *(bias ? bias + min(row0 + u * RS::kRPW, n - 1) : &g_zero_half);
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
   uint4 wr[U][RS::kC];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int row = row0 + u * RS::kRPW;
+    const size_t row = min(row0 + u * RS::kRPW, n - 1);
 #pragma unroll
-    for (int c = 0; c < RS::kC; ++c) {
-      wr[u][c] = make_uint4(0, 0, 0, 0);
-      if (row < n) wr[u][c] = ld_weights(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + RS::kLPR * c);
-    }
+    for (int c = 0; c < RS::kC; ++c) wr[u][c] = ld_weights(w4 + row * RS::kChunksRow + sub + RS::kLPR * c);
   }
   const uint4* xv;
   if constexpr (MODE == kModeLn) {
-    ln_finish<NW * 64>(lnr, ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      ln_finish<NW * 64>(lnr[v], ln.cur != nullptr || ln.x != nullptr, ln.h_out ? ln.h_out + v * kHidden : nullptr,
+                         ln.eps, y_lds + v * K, red);
     __syncthreads();
     xv = reinterpret_cast<const uint4*>(y_lds);
   } else if constexpr (MODE == kModeCombine) {
-    combine_finish<NW * 64>(cb, cbr, y_lds, wgt, inv_den);
-    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (v > 0) combine_load<NW * 64>(cb.vec(v), cbr);
+      combine_finish<NW * 64>(NV > 1 ? cb.vec(v) : cb, cbr, y_lds + v * K, wgt, inv_den);
+      __syncthreads();  // y visible; wgt / inv_den free for the next vector
+    }
     xv = reinterpret_cast<const uint4*>(y_lds);
   } else {
     xv = reinterpret_cast<const uint4*>(xin);
   }
-  uint4 xr[RS::kC];
+  uint4 xr[NV][RS::kC];
 #pragma unroll
-  for (int c = 0; c < RS::kC; ++c) xr[c] = xv[sub + RS::kLPR * c];
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int c = 0; c < RS::kC; ++c) xr[v][c] = xv[v * (K / 8) + sub + RS::kLPR * c];
 
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int row = row0 + u * RS::kRPW;
-    float acc = 0.f;
+    const float b = h2f(braw[u]);
 #pragma unroll
-    for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[u][c], xr[c], acc);
-    acc = group_sum<RS::kLPR>(acc);
-    if (sub == 0 && row < n) {
-      float v = acc + (bias ? h2f(bias[row]) : 0.f);
-      if constexpr (ACT == FW_ACT_GELU) v = gelu_erf(round_h(v));
-      out[row] = f2h(v);
+    for (int v = 0; v < NV; ++v) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[u][c], xr[v][c], acc);
+      acc = group_sum<RS::kLPR>(acc);
+      // every lane finishes the row and one lane stores; the empty asm pins y (and with it the
+      // bias) outside the store's lane mask, where the bias request would otherwise be sunk to
+      float y = acc + b;
+      if constexpr (ACT == FW_ACT_GELU) y = gelu_erf(round_h(y));
+      asm volatile("" : "+v"(y));
+      if (sub == 0 && row < n) out[static_cast<size_t>(v) * n + row] = f2h(y);
     }
   }
 }
 
-template <int K, int NW, int U, int MODE, int ACT>
+constexpr int kMaxBatch = 4;  // decoder positions per batched launch (the 4-token prompt)
+
+template <int K, int NW, int U, int MODE, int ACT, int NV = 1>
 void launch_gemv(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w, const _Float16* b,
                  _Float16* out, int n, hipStream_t s) {
   constexpr int kRows = NW * RowSplit<K>::kRPW * U;
   const int grid = (n + kRows - 1) / kRows;
-  hipLaunchKernelGGL((gemv_kernel<K, NW, U, MODE, ACT>), dim3(grid), dim3(NW * 64), 0, s, x, ln, cb, w, b, out, n);
+  hipLaunchKernelGGL((gemv_kernel<K, NW, U, MODE, ACT, NV>), dim3(grid), dim3(NW * 64), 0, s, x, ln, cb, w, b, out, n);
+}
+
+// A batch of nv (1..kMaxBatch) vectors, one row group per wave (the batch runs once per clip, for the
+// prompt, so registers for up to 4 input vectors matter more than the row-group depth). NW is that of
+// the single-vector launch of the same weights: the LayerNorm prologue reduces over the block's
+// threads, and the same block size keeps each vector's result bit-identical to a single-vector step.
+template <int K, int NW, int MODE, int ACT>
+void launch_gemv_batch(int nv, const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w,
+                       const _Float16* b, _Float16* out, int n, hipStream_t s) {
+  switch (nv) {
+    case 1: launch_gemv<K, NW, 1, MODE, ACT, 1>(x, ln, cb, w, b, out, n, s); break;
+    case 2: launch_gemv<K, NW, 1, MODE, ACT, 2>(x, ln, cb, w, b, out, n, s); break;
+    case 3: launch_gemv<K, NW, 1, MODE, ACT, 3>(x, ln, cb, w, b, out, n, s); break;
+    default: launch_gemv<K, NW, 1, MODE, ACT, 4>(x, ln, cb, w, b, out, n, s); break;
+  }
 }
 
 // Block shapes of the decode GEMVs (waves per block, row groups per wave), measured on MI355X over the
@@ -386,6 +445,19 @@ void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& 
     launch_gemv<kHidden, FW_G3840_NW, 2, MODE, ACT>(x, ln, cb, w, b, out, n, s);
   else
     launch_gemv<kHidden, FW_G1280_NW, 1, MODE, ACT>(x, ln, cb, w, b, out, n, s);
+}
+
+template <int MODE, int ACT>
+void dispatch_gemv_1280_batch(int nv, const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w,
+                              const _Float16* b, _Float16* out, int n, hipStream_t s) {
+  if (nv == 1)
+    dispatch_gemv_1280<MODE, ACT>(x, ln, cb, w, b, out, n, s);
+  else if (n >= 5120)
+    launch_gemv_batch<kHidden, FW_G5120_NW, MODE, ACT>(nv, x, ln, cb, w, b, out, n, s);
+  else if (n >= 3840)
+    launch_gemv_batch<kHidden, FW_G3840_NW, MODE, ACT>(nv, x, ln, cb, w, b, out, n, s);
+  else
+    launch_gemv_batch<kHidden, FW_G1280_NW, MODE, ACT>(nv, x, ln, cb, w, b, out, n, s);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -443,22 +515,23 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
   const int r_begin = blockIdx.x * rows_per_block;
   const int r_end = min(vocab, r_begin + rows_per_block);
 
-  auto load = [&](int base, uint4 (&wr)[kLmU][RS::kC]) {
+  // Rows past r_end load row r_end - 1 and are masked when scored: no load sits under a lane mask,
+  // so the wait for one batch never includes the batch requested after it.
+  auto load = [&](int base, uint4 (&wr)[kLmU][RS::kC], uint32_t (&sp)[kLmU]) {
     const int row0 = base + wave * 2 * kLmU + rsel;
 #pragma unroll
     for (int u = 0; u < kLmU; ++u) {
-      const int row = row0 + 2 * u;
+      const size_t row = min(row0 + 2 * u, r_end - 1);
 #pragma unroll
-      for (int c = 0; c < RS::kC; ++c) {
-        wr[u][c] = make_uint4(0, 0, 0, 0);
-        if (row < r_end) wr[u][c] = ld_lm_head(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + 32 * c);
-      }
+      for (int c = 0; c < RS::kC; ++c) wr[u][c] = ld_lm_head(w4 + row * RS::kChunksRow + sub + 32 * c);
+      sp[u] = suppress[row];
     }
   };
   LnRegs<kLmNW * 64> lnr;
   if constexpr (LN) ln_load<kLmNW * 64>(ln.h, ln.x, ln.gamma, ln.beta, lnr);
-  uint4 cur[kLmU][RS::kC];
-  load(r_begin, cur);
+  uint4 wa[kLmU][RS::kC], wb[kLmU][RS::kC];
+  uint32_t sa[kLmU], sb[kLmU];
+  load(r_begin, wa, sa);
 
   if constexpr (LN) {
     ln_finish<kLmNW * 64>(lnr, ln.x != nullptr, nullptr, ln.eps, y_lds, red);
@@ -472,29 +545,26 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
   for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(y_lds)[sub + 32 * c];
 
   unsigned long long mine = 0;
-  for (int base = r_begin; base < r_end; base += kLmRowsIter) {
-    uint4 next[kLmU][RS::kC];
-    const bool more = base + kLmRowsIter < r_end;
-    if (more) load(base + kLmRowsIter, next);
+  auto score = [&](int base, const uint4 (&wr)[kLmU][RS::kC], const uint32_t (&sp)[kLmU]) {
     const int row0 = base + wave * 2 * kLmU + rsel;
 #pragma unroll
     for (int u = 0; u < kLmU; ++u) {
       const int row = row0 + 2 * u;
       float acc = 0.f;
 #pragma unroll
-      for (int c = 0; c < RS::kC; ++c) acc = dot8(cur[u][c], xr[c], acc);
-      acc = group_sum<32>(acc);
-      if (sub == 0 && row < r_end && !suppress[row]) {
-        const unsigned long long sc = pack_score(round_h(acc), row);
-        mine = sc > mine ? sc : mine;
-      }
+      for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[u][c], xr[c], acc);
+      acc = group_sum<32>(acc);  // every lane of the row holds the sum
+      const unsigned long long sc = pack_score(round_h(acc), row);
+      if (row < r_end && !sp[u] && sc > mine) mine = sc;
     }
-    if (more) {
-#pragma unroll
-      for (int u = 0; u < kLmU; ++u)
-#pragma unroll
-        for (int c = 0; c < RS::kC; ++c) cur[u][c] = next[u][c];
-    }
+  };
+  // two register buffers in turn: batch i + 1 is in flight while batch i is scored
+  for (int base = r_begin; base < r_end; base += 2 * kLmRowsIter) {
+    const int b1 = base + kLmRowsIter, b2 = base + 2 * kLmRowsIter;
+    if (b1 < r_end) load(b1, wb, sb);
+    score(base, wa, sa);
+    if (b2 < r_end) load(b2, wa, sa);
+    if (b1 < r_end) score(b1, wb, sb);
   }
   if (sub == 0) block_best[wave * 2 + rsel] = mine;
   __syncthreads();
@@ -542,6 +612,10 @@ struct AttnArgs {
   float* part_l;
   float* part_acc;
   _Float16* out;
+  // batches of queries (split kernel, grid.z): query z is q + z * q_stride at position len_state[0] + z,
+  // and its fresh K/V row is k_new / v_new + z * kv_stride
+  int q_stride;
+  int kv_stride;
 };
 
 __device__ __forceinline__ int attn_pos(const AttnArgs& a) {
@@ -550,19 +624,24 @@ __device__ __forceinline__ int attn_pos(const AttnArgs& a) {
   return static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
 }
 
-template <int MAXP>
+// BATCH: a batch of queries (grid.z, the prompt) takes the fresh K/V rows of the batch's earlier
+// queries straight from k_new / v_new: their cache rows are written by other blocks of the same
+// launch, so a cache row at or past the batch's first position is never trusted. The single-query
+// instantiation carries none of this code.
+template <int MAXP, bool BATCH>
 __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   __shared__ float wm[4], wl[4];
   __shared__ float wacc[4][kHeadDim];
-  const int split = blockIdx.x, head = blockIdx.y, nsplit = gridDim.x;
-  const int slot = head * nsplit + split;
+  const int split = blockIdx.x, head = blockIdx.y, nsplit = gridDim.x, qv = BATCH ? blockIdx.z : 0;
+  const int slot = (qv * gridDim.y + head) * nsplit + split;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ks = lane >> 3, c = lane & 7;
   const size_t hoff = static_cast<size_t>(head) * a.max_len * kHeadDim;
   _Float16* kh = a.k + hoff;
   _Float16* vh = a.v + hoff;
-  const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + head * kHeadDim) : nullptr;
-  const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + head * kHeadDim) : nullptr;
+  const size_t kv_off = BATCH ? static_cast<size_t>(qv) * a.kv_stride : 0;
+  const uint4* kn = a.k_new ? reinterpret_cast<const uint4*>(a.k_new + kv_off + head * kHeadDim) : nullptr;
+  const uint4* vn = a.v_new ? reinterpret_cast<const uint4*>(a.v_new + kv_off + head * kHeadDim) : nullptr;
   // Every wave owns a fixed run of MAXP * 8 keys of the split. All loads are issued before the
   // cached length is known (it arrives from device memory); keys past it are masked afterwards,
   // so the length read and the K/V reads take one memory round trip together.
@@ -570,7 +649,8 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   const int w0 = begin + wave * MAXP * 8;
   const int wend = min(min(w0 + MAXP * 8, begin + a.split_keys), a.max_len);
   const int64_t pos_raw = a.len_state ? a.len_state[0] : 0;
-  const uint4 qc = reinterpret_cast<const uint4*>(a.q + head * kHeadDim)[c];
+  const size_t q_off = BATCH ? static_cast<size_t>(qv) * a.q_stride : 0;
+  const uint4 qc = reinterpret_cast<const uint4*>(a.q + q_off + head * kHeadDim)[c];
   uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
   if (kn) {
     knew = kn[c];
@@ -586,8 +666,9 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
       vr[p] = reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
     }
   }
-  const int pos = a.len_state ? static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_len ? a.max_len - 1 : pos_raw))
-                              : -1;
+  const int pos0 = a.len_state ? static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_len ? a.max_len - 1 : pos_raw))
+                               : -1;
+  const int pos = a.len_state ? (BATCH ? min(pos0 + qv, a.max_len - 1) : pos0) : -1;
   const int len = a.len_state ? pos + 1 : a.max_len;
   const int n = min(a.split_keys, len - begin);
   if (n <= 0) {
@@ -606,9 +687,14 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   const int w1 = min(wend, begin + n);
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
-    if (kn && w0 + p * 8 + ks == pos) {  // the new row replaces the (stale) cached one
+    const int j = w0 + p * 8 + ks;
+    if (kn && j == pos) {  // the new row replaces the (stale) cached one
       kr[p] = knew;
       vr[p] = vnew;
+    } else if (BATCH && kn && j >= pos0 && j < pos) {  // an earlier query of the batch: its fresh row
+      const size_t r = static_cast<size_t>(j - pos0) * a.kv_stride + head * kHeadDim;
+      kr[p] = reinterpret_cast<const uint4*>(a.k_new + r)[c];
+      vr[p] = reinterpret_cast<const uint4*>(a.v_new + r)[c];
     }
   }
   float sc[MAXP];
@@ -675,14 +761,23 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   }
 }
 
-int launch_attn_split(const AttnArgs& a, int nsplit, int heads, hipStream_t s) {
-  const dim3 grid(nsplit, heads);
-  if (a.split_keys <= 64)
-    hipLaunchKernelGGL(attn_split_kernel<2>, grid, dim3(256), 0, s, a);
-  else if (a.split_keys <= 128)
-    hipLaunchKernelGGL(attn_split_kernel<4>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(attn_split_kernel<8>, grid, dim3(256), 0, s, a);
+int launch_attn_split(const AttnArgs& a, int nsplit, int heads, hipStream_t s, int nq = 1) {
+  const dim3 grid(nsplit, heads, nq);
+  if (nq == 1) {
+    if (a.split_keys <= 64)
+      hipLaunchKernelGGL((attn_split_kernel<2, false>), grid, dim3(256), 0, s, a);
+    else if (a.split_keys <= 128)
+      hipLaunchKernelGGL((attn_split_kernel<4, false>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((attn_split_kernel<8, false>), grid, dim3(256), 0, s, a);
+  } else {
+    if (a.split_keys <= 64)
+      hipLaunchKernelGGL((attn_split_kernel<2, true>), grid, dim3(256), 0, s, a);
+    else if (a.split_keys <= 128)
+      hipLaunchKernelGGL((attn_split_kernel<4, true>), grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((attn_split_kernel<8, true>), grid, dim3(256), 0, s, a);
+  }
   return fw_check_launch("attention split");
 }
 
@@ -894,7 +989,7 @@ static int attention_common(const void* q, void* k, void* v, void* out, const in
              "decode_attention: q, k, v, k_new, v_new must be 16-byte aligned");
   *a = AttnArgs{static_cast<const _Float16*>(q), static_cast<_Float16*>(k), static_cast<_Float16*>(v),
                 static_cast<const _Float16*>(k_new), static_cast<const _Float16*>(v_new), len_state, max_len,
-                kSplitKeys, 0.f, nullptr, nullptr, nullptr, static_cast<_Float16*>(out)};
+                kSplitKeys, 0.f, nullptr, nullptr, nullptr, static_cast<_Float16*>(out), 0, 0};
   return FW_OK;
 }
 
@@ -952,12 +1047,13 @@ extern "C" int fw_embed(const int64_t* cur, const int64_t* state, const void* em
   return fw_check_launch("embed");
 }
 
-extern "C" int fw_gemv(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
-                       hipStream_t stream) {
+static int gemv_impl(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act, int nv,
+                     hipStream_t stream) {
   FW_REQUIRE(x && w && out, "gemv: null pointer");
   FW_REQUIRE(n_out > 0, "gemv: n_out must be positive");
   FW_REQUIRE(k_in == kHidden || k_in == 4 * kHidden, "gemv: k_in must be 1280 or 5120");
   FW_REQUIRE(act == FW_ACT_NONE || act == FW_ACT_GELU, "gemv: unknown activation %d", act);
+  FW_REQUIRE(nv >= 1 && nv <= kMaxBatch, "gemv: nv must be in [1, %d]", kMaxBatch);
   FW_REQUIRE(aligned16(x) && aligned16(w), "gemv: x and w must be 16-byte aligned");
   const auto* xp = static_cast<const _Float16*>(x);
   const auto* wp = static_cast<const _Float16*>(w);
@@ -967,23 +1063,39 @@ extern "C" int fw_gemv(const void* x, const void* w, const void* bias, void* out
   const CombineArgs cb{};
   if (k_in == kHidden) {
     if (act == FW_ACT_GELU)
-      dispatch_gemv_1280<kModePlain, FW_ACT_GELU>(xp, ln, cb, wp, bp, op, n_out, stream);
+      dispatch_gemv_1280_batch<kModePlain, FW_ACT_GELU>(nv, xp, ln, cb, wp, bp, op, n_out, stream);
     else
-      dispatch_gemv_1280<kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
-  } else {
+      dispatch_gemv_1280_batch<kModePlain, FW_ACT_NONE>(nv, xp, ln, cb, wp, bp, op, n_out, stream);
+  } else if (nv == 1) {
     if (act == FW_ACT_GELU)
       launch_gemv<4 * kHidden, FW_GK5120_NW, FW_GK5120_U, kModePlain, FW_ACT_GELU>(xp, ln, cb, wp, bp, op, n_out, stream);
     else
       launch_gemv<4 * kHidden, FW_GK5120_NW, FW_GK5120_U, kModePlain, FW_ACT_NONE>(xp, ln, cb, wp, bp, op, n_out, stream);
+  } else {
+    if (act == FW_ACT_GELU)
+      launch_gemv_batch<4 * kHidden, FW_GK5120_NW, kModePlain, FW_ACT_GELU>(nv, xp, ln, cb, wp, bp, op, n_out, stream);
+    else
+      launch_gemv_batch<4 * kHidden, FW_GK5120_NW, kModePlain, FW_ACT_NONE>(nv, xp, ln, cb, wp, bp, op, n_out, stream);
   }
   return fw_check_launch("gemv");
 }
 
-extern "C" int fw_ln_gemv(const void* h, const void* x, void* h_out, const void* gamma, const void* beta, float eps,
-                          const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed,
-                          int vocab, int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in,
-                          int act, hipStream_t stream) {
+extern "C" int fw_gemv(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
+                       hipStream_t stream) {
+  return gemv_impl(x, w, bias, out, n_out, k_in, act, 1, stream);
+}
+
+extern "C" int fw_gemv_batch(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
+                             int nv, hipStream_t stream) {
+  return gemv_impl(x, w, bias, out, n_out, k_in, act, nv, stream);
+}
+
+static int ln_gemv_impl(const void* h, const void* x, void* h_out, const void* gamma, const void* beta, float eps,
+                        const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                        int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in, int act, int nv,
+                        hipStream_t stream) {
   FW_REQUIRE(gamma && beta && w && out, "ln_gemv: null pointer");
+  FW_REQUIRE(nv >= 1 && nv <= kMaxBatch, "ln_gemv: nv must be in [1, %d]", kMaxBatch);
   FW_REQUIRE(k_in == kHidden, "ln_gemv: k_in must be %d", kHidden);
   FW_REQUIRE(n_out > 0, "ln_gemv: n_out must be positive");
   FW_REQUIRE(act == FW_ACT_NONE || act == FW_ACT_GELU, "ln_gemv: unknown activation %d", act);
@@ -1002,46 +1114,109 @@ extern "C" int fw_ln_gemv(const void* h, const void* x, void* h_out, const void*
   auto* op = static_cast<_Float16*>(out);
   const CombineArgs cb{};
   if (act == FW_ACT_GELU)
-    dispatch_gemv_1280<kModeLn, FW_ACT_GELU>(nullptr, ln, cb, wp, bp, op, n_out, stream);
+    dispatch_gemv_1280_batch<kModeLn, FW_ACT_GELU>(nv, nullptr, ln, cb, wp, bp, op, n_out, stream);
   else
-    dispatch_gemv_1280<kModeLn, FW_ACT_NONE>(nullptr, ln, cb, wp, bp, op, n_out, stream);
+    dispatch_gemv_1280_batch<kModeLn, FW_ACT_NONE>(nv, nullptr, ln, cb, wp, bp, op, n_out, stream);
   return fw_check_launch("ln_gemv");
 }
 
-extern "C" int fw_attention_split(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
-                                  const void* v_new, int heads, int max_len, int split_keys, float* part_m,
-                                  float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream) {
+extern "C" int fw_ln_gemv(const void* h, const void* x, void* h_out, const void* gamma, const void* beta, float eps,
+                          const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed,
+                          int vocab, int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in,
+                          int act, hipStream_t stream) {
+  return ln_gemv_impl(h, x, h_out, gamma, beta, eps, cur, state, embed, pos_embed, vocab, max_pos, w, bias, out, n_out,
+                      k_in, act, 1, stream);
+}
+
+extern "C" int fw_ln_gemv_batch(const void* h, const void* x, void* h_out, const void* gamma, const void* beta,
+                                float eps, const int64_t* cur, const int64_t* state, const void* embed,
+                                const void* pos_embed, int vocab, int max_pos, const void* w, const void* bias,
+                                void* out, int n_out, int k_in, int act, int nv, hipStream_t stream) {
+  return ln_gemv_impl(h, x, h_out, gamma, beta, eps, cur, state, embed, pos_embed, vocab, max_pos, w, bias, out, n_out,
+                      k_in, act, nv, stream);
+}
+
+static int attention_split_impl(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
+                                const void* v_new, int heads, int max_len, int split_keys, float* part_m,
+                                float* part_l, float* part_acc, int64_t ws_slots, float scale, int nq, int q_stride,
+                                int kv_stride, hipStream_t stream) {
   AttnArgs a;
   int rc = attention_common(q, k, v, nullptr, len_state, k_new, v_new, heads, max_len, &a);
   if (rc != FW_OK) return rc;
   FW_REQUIRE(part_m && part_l && part_acc, "attention_split: null workspace");
   FW_REQUIRE(split_keys >= 8 && split_keys <= 256 && split_keys % 8 == 0,
              "split_keys must be a multiple of 8 in [8, 256]");
+  FW_REQUIRE(nq >= 1 && nq <= kMaxBatch, "attention_split: nq must be in [1, %d]", kMaxBatch);
+  if (nq > 1) {
+    FW_REQUIRE(q_stride >= heads * kHeadDim && q_stride % 8 == 0,
+               "attention_split: q_stride must be a multiple of 8 and at least heads * 64");
+    FW_REQUIRE(!k_new || (kv_stride >= heads * kHeadDim && kv_stride % 8 == 0),
+               "attention_split: kv_stride must be a multiple of 8 and at least heads * 64");
+  }
   const int nsplit = (max_len + split_keys - 1) / split_keys;
-  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * nsplit, "workspace too small for %d splits", nsplit);
+  FW_REQUIRE(ws_slots >= static_cast<int64_t>(nq) * heads * nsplit, "workspace too small for %d x %d splits", nq,
+             nsplit);
   a.out = nullptr;
   a.split_keys = split_keys;
   a.scale = scale;
   a.part_m = part_m;
   a.part_l = part_l;
   a.part_acc = part_acc;
-  return launch_attn_split(a, nsplit, heads, stream);
+  a.q_stride = nq > 1 ? q_stride : 0;
+  a.kv_stride = nq > 1 && k_new ? kv_stride : 0;
+  return launch_attn_split(a, nsplit, heads, stream, nq);
 }
 
-extern "C" int fw_attn_out_gemv(const float* part_m, const float* part_l, const float* part_acc, int64_t ws_slots,
-                                const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
-                                const void* bias, void* out, int n_out, hipStream_t stream) {
+extern "C" int fw_attention_split(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
+                                  const void* v_new, int heads, int max_len, int split_keys, float* part_m,
+                                  float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream) {
+  return attention_split_impl(q, k, v, len_state, k_new, v_new, heads, max_len, split_keys, part_m, part_l, part_acc,
+                              ws_slots, scale, 1, 0, 0, stream);
+}
+
+extern "C" int fw_attention_split_batch(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
+                                        const void* v_new, int heads, int max_len, int split_keys, float* part_m,
+                                        float* part_l, float* part_acc, int64_t ws_slots, float scale, int nq,
+                                        int q_stride, int kv_stride, hipStream_t stream) {
+  return attention_split_impl(q, k, v, len_state, k_new, v_new, heads, max_len, split_keys, part_m, part_l, part_acc,
+                              ws_slots, scale, nq, q_stride, kv_stride, stream);
+}
+
+static int attn_out_gemv_impl(const float* part_m, const float* part_l, const float* part_acc, int64_t ws_slots,
+                              const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
+                              const void* bias, void* out, int n_out, int nv, hipStream_t stream) {
   FW_REQUIRE(part_m && part_l && part_acc && w && out, "attn_out_gemv: null pointer");
+  FW_REQUIRE(nv >= 1 && nv <= kMaxBatch, "attn_out_gemv: nv must be in [1, %d]", kMaxBatch);
   FW_REQUIRE(heads * kHeadDim == kHidden, "attn_out_gemv: heads * 64 must be %d", kHidden);
   FW_REQUIRE(max_len > 0 && split_keys >= 8 && n_out > 0, "attn_out_gemv: bad sizes");
   FW_REQUIRE(aligned16(w), "attn_out_gemv: w must be 16-byte aligned");
   const int nsplit = (max_len + split_keys - 1) / split_keys;
   FW_REQUIRE(nsplit <= kMaxCombineSplits && heads <= kMaxCombineHeads,
              "attn_out_gemv: at most %d splits (got %d) and %d heads", kMaxCombineSplits, nsplit, kMaxCombineHeads);
-  FW_REQUIRE(ws_slots >= static_cast<int64_t>(heads) * nsplit, "attn_out_gemv: workspace too small");
-  const CombineArgs cb{part_m, part_l, part_acc, len_state, max_len, split_keys, nsplit, heads};
-  launch_gemv<kHidden, FW_CMB_NW, 1, kModeCombine, FW_ACT_NONE>(nullptr, LnArgs{}, cb, static_cast<const _Float16*>(w),
-                                                         static_cast<const _Float16*>(bias), static_cast<_Float16*>(out),
-                                                         n_out, stream);
+  FW_REQUIRE(ws_slots >= static_cast<int64_t>(nv) * heads * nsplit, "attn_out_gemv: workspace too small");
+  const CombineArgs cb{part_m, part_l, part_acc, len_state, max_len, split_keys, nsplit, heads, 0};
+  const auto* wp = static_cast<const _Float16*>(w);
+  const auto* bp = static_cast<const _Float16*>(bias);
+  auto* op = static_cast<_Float16*>(out);
+  if (nv == 1)
+    launch_gemv<kHidden, FW_CMB_NW, 1, kModeCombine, FW_ACT_NONE>(nullptr, LnArgs{}, cb, wp, bp, op, n_out, stream);
+  else
+    launch_gemv_batch<kHidden, FW_CMB_NW, kModeCombine, FW_ACT_NONE>(nv, nullptr, LnArgs{}, cb, wp, bp, op, n_out,
+                                                                     stream);
   return fw_check_launch("attn_out_gemv");
+}
+
+extern "C" int fw_attn_out_gemv(const float* part_m, const float* part_l, const float* part_acc, int64_t ws_slots,
+                                const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
+                                const void* bias, void* out, int n_out, hipStream_t stream) {
+  return attn_out_gemv_impl(part_m, part_l, part_acc, ws_slots, len_state, heads, max_len, split_keys, w, bias, out,
+                            n_out, 1, stream);
+}
+
+extern "C" int fw_attn_out_gemv_batch(const float* part_m, const float* part_l, const float* part_acc,
+                                      int64_t ws_slots, const int64_t* len_state, int heads, int max_len,
+                                      int split_keys, const void* w, const void* bias, void* out, int n_out, int nv,
+                                      hipStream_t stream) {
+  return attn_out_gemv_impl(part_m, part_l, part_acc, ws_slots, len_state, heads, max_len, split_keys, w, bias, out,
+                            n_out, nv, stream);
 }

@@ -22,6 +22,7 @@ from ._lib import ACT_GELU, ACT_NONE, EPI_BIAS  # noqa: F401  (re-exported const
 from .config import SPLIT_KEYS
 
 HIDDEN, HEAD_DIM = 1280, 64
+MAX_BATCH = 4  # decoder positions per batched launch (the prompt)
 
 
 def _stream():
@@ -41,6 +42,15 @@ def check_half(t, name):
     """Reference check_half (whisper_kernels.cu:272-274)."""
     _require(isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous() and t.dtype == torch.float16,
              f'{name} must be contiguous CUDA fp16')
+
+
+def _check_rows(t, name, cols):
+    """A [rows, cols] fp16 CUDA view with unit column stride and a 16-byte-aligned row stride; returns rows."""
+    _require(isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float16 and t.dim() == 2
+             and t.size(1) == cols and t.stride(1) == 1 and (t.size(0) == 1 or t.stride(0) >= cols)
+             and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0,
+             f'{name} must be a CUDA fp16 [rows, {cols}] view with unit column stride and 16-byte aligned rows')
+    return t.size(0)
 
 
 def _check(t, name, dtype, what):
@@ -126,36 +136,54 @@ class WhisperExt:
         self._call('fw_embed', cur.data_ptr(), state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(),
                    embed.size(0), pos_embed.size(0), h.data_ptr(), HIDDEN, _stream())
 
-    def gemv(self, x, w, bias, out, act=ACT_NONE):
+    def gemv(self, x, w, bias, out, act=ACT_NONE, nv=1):
+        """out = act(w x + b); with nv > 1, x and out hold nv rows (a batch of decoder positions)."""
         check_half(x, 'x')
         check_half(w, 'w')
         check_half(out, 'out')
-        _require(w.dim() == 2 and x.numel() == w.size(1) and out.numel() == w.size(0), 'gemv shape mismatch')
+        _require(1 <= nv <= MAX_BATCH, f'nv must be in [1, {MAX_BATCH}]')
+        _require(w.dim() == 2 and x.numel() == nv * w.size(1) and out.numel() == nv * w.size(0),
+                 'gemv shape mismatch')
         if bias is not None:
             check_half(bias, 'bias')
             _require(bias.numel() == w.size(0), 'bias must be [n_out]')
-        self._call('fw_gemv', x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), w.size(1), act,
-                   _stream())
+        args = (x.data_ptr(), w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), w.size(1), act)
+        if nv == 1:
+            self._call('fw_gemv', *args, _stream())
+        else:
+            self._call('fw_gemv_batch', *args, nv, _stream())
 
-    def ln_gemv(self, h, x, h_out, gamma, beta, eps, w, bias, out, act=ACT_NONE, embed=None):
-        """r = fp16(h + x) -> h_out; y = LN(r); out = act(w y + b). embed = (cur, state, table, pos_table)."""
+    def ln_gemv(self, h, x, h_out, gamma, beta, eps, w, bias, out, act=ACT_NONE, embed=None, nv=1):
+        """r = fp16(h + x) -> h_out; y = LN(r); out = act(w y + b). embed = (cur, state, table, pos_table).
+        With nv > 1, h, x, h_out and out hold nv rows and cur nv tokens (positions state[0] + v)."""
         for t, n in ((gamma, 'gamma'), (beta, 'beta'), (w, 'w'), (out, 'out')):
             check_half(t, n)
-        _require(w.dim() == 2 and w.size(1) == HIDDEN and out.numel() == w.size(0), 'ln_gemv shape mismatch')
+        _require(1 <= nv <= MAX_BATCH, f'nv must be in [1, {MAX_BATCH}]')
+        _require(w.dim() == 2 and w.size(1) == HIDDEN and out.numel() == nv * w.size(0), 'ln_gemv shape mismatch')
         cur = state = table = pos_table = None
         if embed is not None:
             cur, state, table, pos_table = embed
             check_half(table, 'embed')
             check_half(pos_table, 'pos_embed')
+            _check(cur, 'cur', torch.int64, 'int64')
+            _require(cur.numel() >= nv, 'embedding mode needs nv tokens in cur')
         else:
             check_half(h, 'h')
-        for t, n in ((x, 'x'), (h_out, 'h_out'), (bias, 'bias')):
+            _require(h.numel() == nv * HIDDEN, 'h must hold nv rows of the hidden size')
+        for t, n in ((x, 'x'), (h_out, 'h_out')):
             if t is not None:
                 check_half(t, n)
-        self._call('fw_ln_gemv', _ptr(h), _ptr(x), _ptr(h_out), gamma.data_ptr(), beta.data_ptr(), float(eps),
-                   _ptr(cur), _ptr(state), _ptr(table), _ptr(pos_table),
-                   0 if table is None else table.size(0), 0 if pos_table is None else pos_table.size(0),
-                   w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), HIDDEN, act, _stream())
+                _require(t.numel() == nv * HIDDEN, f'{n} must hold nv rows of the hidden size')
+        if bias is not None:
+            check_half(bias, 'bias')
+        args = (_ptr(h), _ptr(x), _ptr(h_out), gamma.data_ptr(), beta.data_ptr(), float(eps),
+                _ptr(cur), _ptr(state), _ptr(table), _ptr(pos_table),
+                0 if table is None else table.size(0), 0 if pos_table is None else pos_table.size(0),
+                w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0), HIDDEN, act)
+        if nv == 1:
+            self._call('fw_ln_gemv', *args, _stream())
+        else:
+            self._call('fw_ln_gemv_batch', *args, nv, _stream())
 
     def decode_attention_fused(self, q, k, v, out, len_state, k_new, v_new, scale):
         """decode_attention in a single launch (one block per head, no workspace)."""
@@ -183,23 +211,57 @@ class WhisperExt:
                    _ptr(v_new), heads, max_len, int(split_keys), part_m.data_ptr(), part_l.data_ptr(),
                    part_acc.data_ptr(), slots, float(scale), _stream())
 
-    def attn_out_gemv(self, part_m, part_l, part_acc, len_state, heads, max_len, w, bias, out, split_keys=SPLIT_KEYS):
-        """Combine of attention_split partials + output projection: out = fp16(w . combine + bias)."""
+    def attention_split_batch(self, q, k, v, len_state, k_new, v_new, part_m, part_l, part_acc, scale,
+                              split_keys=SPLIT_KEYS):
+        """attention_split for nq = q.size(0) queries at positions len_state[0] + z (self mode). q, k_new
+        and v_new are [nq, heads * 64] row views (the row stride may exceed the row, e.g. slices of a
+        packed q/k/v batch); partials land query-major for attn_out_gemv(nv=nq)."""
+        check_half(k, 'k')
+        check_half(v, 'v')
+        _require(k.dim() == 3 and k.size(2) == HEAD_DIM and k.shape == v.shape, 'k, v must be [heads, max_len, 64]')
+        heads, max_len = k.size(0), k.size(1)
+        nq = _check_rows(q, 'q', heads * HEAD_DIM)
+        _require(1 <= nq <= MAX_BATCH, f'at most {MAX_BATCH} queries')
+        _require((k_new is None) == (v_new is None) == (len_state is None),
+                 'len_state, k_new and v_new must be given together')
+        kv_stride = 0
+        if k_new is not None:
+            _require(_check_rows(k_new, 'k_new', heads * HEAD_DIM) == nq == _check_rows(v_new, 'v_new', heads * HEAD_DIM)
+                     and k_new.stride(0) == v_new.stride(0), 'k_new, v_new must be [nq, heads * 64] with one stride')
+            _require(len_state.dtype == torch.int64 and len_state.is_cuda, 'len_state must be CUDA int64')
+            kv_stride = k_new.stride(0)
+        for t in (part_m, part_l, part_acc):
+            _require(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32,
+                     'workspace must be contiguous CUDA fp32')
+        slots = min(part_m.numel(), part_l.numel(), part_acc.numel() // HEAD_DIM)
+        _require(slots >= nq * heads * -(-max_len // split_keys), 'workspace too small')
+        self._call('fw_attention_split_batch', q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(len_state),
+                   _ptr(k_new), _ptr(v_new), heads, max_len, int(split_keys), part_m.data_ptr(), part_l.data_ptr(),
+                   part_acc.data_ptr(), slots, float(scale), nq, q.stride(0), kv_stride, _stream())
+
+    def attn_out_gemv(self, part_m, part_l, part_acc, len_state, heads, max_len, w, bias, out, split_keys=SPLIT_KEYS,
+                      nv=1):
+        """Combine of attention_split partials + output projection: out = fp16(w . combine + bias); with
+        nv > 1 the partials of attention_split_batch, out nv rows."""
         for t in (part_m, part_l, part_acc):
             _require(t.is_cuda and t.is_contiguous() and t.dtype == torch.float32,
                      'workspace must be contiguous CUDA fp32')
         check_half(w, 'w')
         check_half(out, 'out')
-        _require(w.dim() == 2 and w.size(1) == heads * HEAD_DIM == HIDDEN and out.numel() == w.size(0),
+        _require(1 <= nv <= MAX_BATCH, f'nv must be in [1, {MAX_BATCH}]')
+        _require(w.dim() == 2 and w.size(1) == heads * HEAD_DIM == HIDDEN and out.numel() == nv * w.size(0),
                  'attn_out_gemv shape mismatch')
         if bias is not None:
             check_half(bias, 'bias')
         if len_state is not None:
             _require(len_state.dtype == torch.int64 and len_state.is_cuda, 'len_state must be CUDA int64')
         slots = min(part_m.numel(), part_l.numel(), part_acc.numel() // HEAD_DIM)
-        self._call('fw_attn_out_gemv', part_m.data_ptr(), part_l.data_ptr(), part_acc.data_ptr(), slots,
-                   _ptr(len_state), heads, int(max_len), int(split_keys), w.data_ptr(), _ptr(bias), out.data_ptr(),
-                   w.size(0), _stream())
+        args = (part_m.data_ptr(), part_l.data_ptr(), part_acc.data_ptr(), slots, _ptr(len_state), heads,
+                int(max_len), int(split_keys), w.data_ptr(), _ptr(bias), out.data_ptr(), w.size(0))
+        if nv == 1:
+            self._call('fw_attn_out_gemv', *args, _stream())
+        else:
+            self._call('fw_attn_out_gemv_batch', *args, nv, _stream())
 
     def lm_head_argmax_fused(self, h, x, gamma, beta, eps, w, suppress, best, tokens, state, cur, max_pos):
         """Final residual + LN + lm_head_argmax + argmax_finalize (finalize skipped when tokens, state and

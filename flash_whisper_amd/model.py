@@ -24,7 +24,7 @@ from ._lib import (ACT_GELU, EPI_BIAS_GELU, EPI_BIAS_GELU_POS, EPI_BIAS_RESID, E
                    EPI_SCALE_Q)
 from .audio import mel_filters
 from .config import CHUNK, N_SAMPLES, SAMPLE_RATE, SPLIT_KEYS, TURBO, DecodeSetup
-from .ext import load_ext
+from .ext import MAX_BATCH, load_ext
 from .selftest import run_selftest, workspace
 
 SYNTHETIC = 'synthetic'
@@ -54,6 +54,7 @@ class CustomModel:
         self.scale = d.head_dim ** -0.5
         self.max_pos, self.enc_len = d.max_pos, d.enc_len
         self.prompt = list(self.setup.prompt)
+        self.batch_prompt = 2 <= len(self.prompt) <= MAX_BATCH   # the prompt in one batched pass
         self.max_new = self.max_pos - len(self.prompt)
         self.eos = set(self.setup.eos)
         self.record_events = False   # time every chunk replay with HIP events (bench.py)
@@ -68,9 +69,9 @@ class CustomModel:
 
         self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
         self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
-        self.graph_one = self.graph_chunk = self.graph_prefix = self.graph_enc = None
+        self.graph_one = self.graph_chunk = self.graph_prompt = self.graph_enc = None
         if capture:
-            self.graph_one, self.graph_chunk, self.graph_prefix = self._capture()
+            self.graph_one, self.graph_chunk, self.graph_prompt = self._capture()
             self.graph_enc = self._capture_encoder()
         torch.cuda.synchronize()
 
@@ -113,8 +114,20 @@ class CustomModel:
         self.state = torch.zeros(2, dtype=torch.long, device='cuda')  # [position, generated count]
         self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
         self.best = torch.zeros(1, dtype=torch.long, device='cuda')
-        # split-K attention partials (both the fused step and the reference-granularity step)
-        self.workspace = workspace(d.heads, -(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, SELF_SPLIT, CROSS_SPLIT)))
+        # split-K attention partials (the fused step, the reference-granularity step and the batched
+        # prompt, whose n queries take n times the splits of one)
+        n = len(self.prompt) if self.batch_prompt else 1
+        splits = max(-(-max(d.max_pos, d.enc_len) // min(SPLIT_KEYS, SELF_SPLIT, CROSS_SPLIT)),
+                     n * -(-d.max_pos // SELF_SPLIT), n * -(-d.enc_len // CROSS_SPLIT))
+        self.workspace = workspace(d.heads, splits)
+        if self.batch_prompt:   # the prompt's n positions side by side
+            self.prompt_ids = torch.tensor(self.prompt, dtype=torch.long, device='cuda')
+            self.hb = torch.zeros(2, n, dm, dtype=half, device='cuda')
+            self.qkvb = torch.zeros(n, 3 * dm, dtype=half, device='cuda')
+            self.qb = torch.zeros(n, dm, dtype=half, device='cuda')
+            self.xob = torch.zeros(n, dm, dtype=half, device='cuda')
+            self.ffnb = torch.zeros(n, d.ffn, dtype=half, device='cuda')
+            self.pendingb = torch.zeros(n, dm, dtype=half, device='cuda')
 
     @torch.inference_mode()
     def new_lane(self):
@@ -127,9 +140,9 @@ class CustomModel:
         lane._alloc_frontend_buffers()
         lane._alloc_encoder_buffers()
         lane._alloc_decoder_buffers()
-        lane.graph_one = lane.graph_chunk = lane.graph_prefix = lane.graph_enc = None
+        lane.graph_one = lane.graph_chunk = lane.graph_prompt = lane.graph_enc = None
         if self.graph_chunk is not None:
-            lane.graph_one, lane.graph_chunk, lane.graph_prefix = lane._capture()
+            lane.graph_one, lane.graph_chunk, lane.graph_prompt = lane._capture()
         if self.graph_enc is not None:
             lane.graph_enc = lane._capture_encoder()
         torch.cuda.synchronize()
@@ -324,6 +337,41 @@ class CustomModel:
         ext.lm_head_argmax_fused(self.h[b], self.pending, g, be, eps, self.lm_head, self.suppress, self.best,
                                  self.tokens, self.state, self.cur, self.max_pos)
 
+    def _prefill(self):
+        """The whole prompt (custom/model.py:196-207) in one pass: each layer runs its 8 launches once
+        for the n prompt positions (batched GEMVs share every weight load; the self attention of
+        position v sees the fresh K/V rows of positions < v of the same launch), then the final LN,
+        LM head and argmax on the last position. K/V cache rows, state and the first token are those
+        of n sequential steps (each position's arithmetic is that of a single step)."""
+        ext, d, dm, n = self.ext, self.dims, self.dims.d_model, len(self.prompt)
+        ws = self.workspace
+        qkv, hb, pend = self.qkvb, self.hb, self.pendingb
+        q, k_new, v_new = qkv[:, :dm], qkv[:, dm:2 * dm], qkv[:, 2 * dm:]
+        a, b = 0, 1
+        for i, lay in enumerate(self.layers):
+            g, be, eps = lay.ln1
+            if i == 0:
+                ext.ln_gemv(None, None, hb[a], g, be, eps, lay.qkv_w, lay.qkv_b, qkv,
+                            embed=(self.prompt_ids, self.state, self.embed, self.pos_embed), nv=n)
+            else:
+                ext.ln_gemv(hb[b], pend, hb[a], g, be, eps, lay.qkv_w, lay.qkv_b, qkv, nv=n)
+            ext.attention_split_batch(q, self.self_kv[i, 0], self.self_kv[i, 1], self.state, k_new, v_new, *ws,
+                                      self.scale, SELF_SPLIT)
+            ext.attn_out_gemv(*ws, self.state, d.heads, d.max_pos, *lay.out, self.xob, SELF_SPLIT, nv=n)
+            g, be, eps = lay.ln2
+            ext.ln_gemv(hb[a], self.xob, hb[b], g, be, eps, *lay.cross_q, self.qb, nv=n)
+            ext.attention_split_batch(self.qb, self.cross_kv[i, 0], self.cross_kv[i, 1], None, None, None, *ws,
+                                      self.scale, CROSS_SPLIT)
+            ext.attn_out_gemv(*ws, None, d.heads, d.enc_len, *lay.cross_out, self.xob, CROSS_SPLIT, nv=n)
+            g, be, eps = lay.ln3
+            ext.ln_gemv(hb[b], self.xob, hb[a], g, be, eps, *lay.fc1, self.ffnb, act=ACT_GELU, nv=n)
+            ext.gemv(self.ffnb, *lay.fc2, pend, nv=n)
+            a, b = b, a
+        self.state[0].add_(n - 1)
+        g, be, eps = self.final_ln
+        ext.lm_head_argmax_fused(hb[b][n - 1], pend[n - 1], g, be, eps, self.lm_head, self.suppress, self.best,
+                                 self.tokens, self.state, self.cur, self.max_pos)
+
     def _step_reference(self):
         """The same step at the reference's op granularity (embed, add_layernorm, GEMV, split+combine
         attention, lm_head_argmax, argmax_finalize); used to check the fused step."""
@@ -352,21 +400,26 @@ class CustomModel:
         ext.argmax_finalize(self.best, self.tokens, self.state, self.cur, self.max_pos)
 
     def _capture(self):
-        """Warm-up, then 1-step and CHUNK-step decoder graphs (custom/model.py:125-141), plus a 1-step
-        graph without the LM head for the prompt tokens before the last."""
+        """Warm-up, then 1-step and CHUNK-step decoder graphs (custom/model.py:125-141), plus the prompt
+        graph: the batched prompt pass, or (prompts that do not batch) a 1-step graph without the LM
+        head for the prompt tokens before the last."""
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(3):
                 self._step()
+            if self.batch_prompt:
+                self.state.zero_()
+                self._prefill()
         torch.cuda.current_stream().wait_stream(side)
         graphs = []
-        for steps, lm_head in ((1, True), (CHUNK, True), (1, False)):
+        prompt_fn = self._prefill if self.batch_prompt else (lambda: self._step(lm_head=False))
+        for steps, fn in ((1, self._step), (CHUNK, self._step), (1, prompt_fn)):
             self.state.zero_()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
                 for _ in range(steps):
-                    self._step(lm_head)
+                    fn()
             graphs.append(graph)
         torch.cuda.synchronize()
         self.self_kv.zero_()
@@ -405,16 +458,26 @@ class CustomModel:
         else:
             self._encode()
 
-    def _enqueue_prompt(self):
+    def _enqueue_prompt(self, batched=None):
         """The prompt steps (custom/model.py:196-207): afterwards tokens[0] is the first generated token.
         The reference runs full steps and discards the predictions made inside the prompt; here the
-        tokens before the last run without the LM head (same K/V cache rows, same final token)."""
+        whole prompt runs as one batched pass (``_prefill``), or, for prompts that do not batch (or
+        ``batched=False``), the tokens before the last run as steps without the LM head. Both leave the
+        same K/V cache rows, state and first token."""
         self.state.zero_()
+        if self.batch_prompt and batched is not False:
+            self.suppress.copy_(self.first_mask)
+            if self.graph_prompt is not None:
+                self.graph_prompt.replay()
+            else:
+                self._prefill()
+            self.suppress.copy_(self.base_mask)
+            return
         last = len(self.prompt) - 1
         for i, token in enumerate(self.prompt):
             self.cur.fill_(token)
             if i < last:
-                self._replay(self.graph_prefix, 1, lm_head=False)
+                self._replay(None if self.batch_prompt else self.graph_prompt, 1, lm_head=False)
                 continue
             self.suppress.copy_(self.first_mask)
             self._replay(self.graph_one, 1)

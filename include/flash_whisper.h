@@ -115,6 +115,38 @@ int fw_attn_out_gemv(const float* part_m, const float* part_l, const float* part
                      const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
                      const void* bias, void* out, int n_out, hipStream_t stream);
 
+/* ---- batched prompt (no reference counterpart: custom/model.py:196-207 runs the prompt one
+ *      token per step; these run its nv <= 4 positions through each layer in one launch per op) --- */
+
+/* fw_gemv on nv input vectors: x holds nv rows of k_in, out nv rows of n_out. Each row's result is
+ * bit-identical to fw_gemv on that row. */
+int fw_gemv_batch(const void* x, const void* w, const void* bias, void* out, int n_out, int k_in, int act, int nv,
+                  hipStream_t stream);
+
+/* fw_ln_gemv on nv vectors: h, x, h_out hold nv rows of 1280, out nv rows of n_out. Embedding mode
+ * takes token cur[v] at position state[0] + v for vector v. Each vector's results are bit-identical
+ * to fw_ln_gemv on it. */
+int fw_ln_gemv_batch(const void* h, const void* x, void* h_out, const void* gamma, const void* beta, float eps,
+                     const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                     int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in, int act, int nv,
+                     hipStream_t stream);
+
+/* fw_attention_split for nq queries: query z is q + z * q_stride (elements) and, in self mode, sits at
+ * position len_state[0] + z with its fresh K/V row at k_new / v_new + z * kv_stride; it attends to the
+ * cached rows before len_state[0] and to the fresh rows of queries 0..z, and its row is written to the
+ * cache. Partials are laid out query-major (nq * heads * splits slots), ready for
+ * fw_attn_out_gemv_batch. Strides are multiples of 8 and at least heads * 64; nq <= 4. */
+int fw_attention_split_batch(const void* q, void* k, void* v, const int64_t* len_state, const void* k_new,
+                             const void* v_new, int heads, int max_len, int split_keys, float* part_m, float* part_l,
+                             float* part_acc, int64_t ws_slots, float scale, int nq, int q_stride, int kv_stride,
+                             hipStream_t stream);
+
+/* fw_attn_out_gemv on the partials of nv queries from fw_attention_split_batch: vector v combines
+ * the splits of position len_state[0] + v (self mode); out holds nv rows of n_out. */
+int fw_attn_out_gemv_batch(const float* part_m, const float* part_l, const float* part_acc, int64_t ws_slots,
+                           const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
+                           const void* bias, void* out, int n_out, int nv, hipStream_t stream);
+
 /* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
  * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by
  * fw_argmax_finalize. best must be zero on entry and is left zero. With tokens, state and cur all

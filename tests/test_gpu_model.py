@@ -92,15 +92,43 @@ def test_decoder_teacher_forced_vs_oracle(model, clip):
 
 def test_graph_replay_matches_eager(model, clip):
     res_graph = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
-    g1, gc, gp = model.graph_one, model.graph_chunk, model.graph_prefix
+    g1, gc, gp = model.graph_one, model.graph_chunk, model.graph_prompt
     try:
-        model.graph_one = model.graph_chunk = model.graph_prefix = None
+        model.graph_one = model.graph_chunk = model.graph_prompt = None
         res_eager = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
     finally:
-        model.graph_one, model.graph_chunk, model.graph_prefix = g1, gc, gp
+        model.graph_one, model.graph_chunk, model.graph_prompt = g1, gc, gp
     assert res_graph['token_ids'] == res_eager['token_ids']
     res_graph2 = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)
     assert res_graph2['token_ids'] == res_graph['token_ids']
+
+
+@torch.inference_mode()
+def test_batched_prompt_matches_sequential_steps(model, clip):
+    """The prompt as one batched pass (graph and eager) leaves the same K/V cache, state, current token
+    and first generated token as the prompt run one position per step."""
+    assert model.batch_prompt
+    model.transcribe(clip, max_new_tokens=1, stop_at_eos=False)  # fills cross K/V
+    results = {}
+    for name in ('sequential', 'graph', 'eager'):
+        model.self_kv.zero_()
+        model.tokens.zero_()
+        if name == 'eager':
+            g, model.graph_prompt = model.graph_prompt, None
+            try:
+                model._enqueue_prompt()
+            finally:
+                model.graph_prompt = g
+        else:
+            model._enqueue_prompt(batched=name != 'sequential')
+        torch.cuda.synchronize()
+        results[name] = (model.self_kv.clone(), model.state.clone(), model.cur.clone(), model.tokens[:1].clone())
+    ref = results['sequential']
+    assert int(ref[1][0]) == len(model.prompt) and int(ref[1][1]) == 1
+    for name in ('graph', 'eager'):
+        for a, b in zip(results[name], ref):
+            assert torch.equal(a, b), name
+    assert torch.equal(model.suppress, model.base_mask)
 
 
 @torch.inference_mode()
