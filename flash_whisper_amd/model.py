@@ -113,6 +113,7 @@ class CustomModel:
         self.cur = torch.zeros(1, dtype=torch.long, device='cuda')
         self.state = torch.zeros(2, dtype=torch.long, device='cuda')  # [position, generated count]
         self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
+        self.tokens_host = torch.zeros(d.max_pos, dtype=torch.long, pin_memory=True)
         self.best = torch.zeros(1, dtype=torch.long, device='cuda')
         # split-K attention partials (the fused step, the reference-granularity step and the batched
         # prompt, whose n queries take n times the splits of one)
@@ -483,6 +484,26 @@ class CustomModel:
             self._replay(self.graph_one, 1)
             self.suppress.copy_(self.base_mask)
 
+    def _publish(self, n0, n):
+        """Queues a copy of tokens[n0:n0 + n] into the pinned host mirror, then an event."""
+        self.tokens_host[n0:n0 + n].copy_(self.tokens[n0:n0 + n], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        return ev
+
+    def _queue_chunk(self, i):
+        """Replays the CHUNK-step graph for chunk i (tokens 1 + i * CHUNK ...) and publishes its tokens."""
+        if self.record_events:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+            self._replay(self.graph_chunk, CHUNK)
+            ev[1].record()
+            self.chunk_events.append(ev)
+        else:
+            self._replay(self.graph_chunk, CHUNK)
+        n0 = 1 + i * CHUNK
+        return self._publish(n0, max(0, min(CHUNK, self.max_pos - n0)))
+
     @torch.inference_mode()
     def transcribe(self, audio, max_new_tokens=None, stop_at_eos=True):
         """custom/model.py:173-225. ``max_new_tokens``/``stop_at_eos`` select the fixed-length mode used
@@ -500,20 +521,28 @@ class CustomModel:
         encoder_s = time.perf_counter() - start - mel_s
 
         decode_start = time.perf_counter()
+        # The reference replays a chunk, then reads its tokens before replaying the next
+        # (custom/model.py:208-215). Here the next chunk is already queued while the host reads the
+        # previous one (an asynchronous copy of its token slice into pinned memory, then an event), so
+        # the GPU never waits for the host. The ids are the same: a chunk queued past an EOS only
+        # decodes tokens that are never read, and no chunk is queued past the token budget.
         self._enqueue_prompt()
-        token_ids = [int(self.tokens[0])]
+        host = self.tokens_host
+        self._publish(0, 1).synchronize()
+        token_ids = [int(host[0])]
         ttft = time.perf_counter() - start
         self.chunk_events = []
-        while (not stop_at_eos or token_ids[-1] not in self.eos) and len(token_ids) < max_new:
-            if self.record_events:
-                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                ev[0].record()
-                self._replay(self.graph_chunk, CHUNK)
-                ev[1].record()
-                self.chunk_events.append(ev)
-            else:
-                self._replay(self.graph_chunk, CHUNK)
-            for token in self.tokens[len(token_ids):len(token_ids) + CHUNK].tolist():
+        n_chunks = -(-(max_new - 1) // CHUNK)
+        done = stop_at_eos and token_ids[0] in self.eos
+        queued = [] if done else [self._queue_chunk(i) for i in range(min(2, n_chunks))]
+        for i in range(n_chunks):
+            if (stop_at_eos and token_ids[-1] in self.eos) or len(token_ids) >= max_new:
+                break
+            queued.pop(0).synchronize()
+            if i + 2 < n_chunks:
+                queued.append(self._queue_chunk(i + 2))
+            n0 = 1 + i * CHUNK
+            for token in host[n0:n0 + CHUNK].tolist():
                 token_ids.append(token)
                 if (stop_at_eos and token in self.eos) or len(token_ids) >= max_new:
                     break

@@ -195,9 +195,12 @@ def test_lm_head_argmax_bit_exact(ext, hip_device, fused):
     state = torch.tensor([3, 0], device=dev)
     cur = torch.zeros(1, dtype=torch.long, device=dev)
     tsup = torch.from_numpy(sup).to(dev)
-    if fused:
-        ext.lm_head_argmax_fused(h16(h, dev), None, h16(g1, dev), h16(b0, dev), 1e-5, w, tsup, best, tokens, state,
-                                 cur, 448)
+    if fused:  # three steps in a row: each finalizes and leaves best zero for the next
+        for i in range(3):
+            ext.lm_head_argmax_fused(h16(h, dev), None, h16(g1, dev), h16(b0, dev), 1e-5, w, tsup, best, tokens,
+                                     state, cur, 448)
+            assert tokens[:i + 1].tolist() == [tok_ref] * (i + 1) and state.tolist() == [4 + i, 1 + i]
+        state[:] = torch.tensor([4, 1])
     else:
         y = torch.empty(1280, dtype=torch.float16, device=dev)
         th = h16(h, dev)
@@ -205,7 +208,7 @@ def test_lm_head_argmax_bit_exact(ext, hip_device, fused):
         ext.lm_head_argmax(y, w, tsup, best)
         ext.argmax_finalize(best, tokens, state, cur, 448)
     assert int(tokens[0]) == tok_ref
-    assert int(cur) == tok_ref and state.tolist() == [4, 1] and int(best) == 0
+    assert int(cur) == tok_ref and state.tolist() == [4, 1] and not best.any()
 
 
 def test_lm_head_ties_and_suppression(ext, hip_device):
