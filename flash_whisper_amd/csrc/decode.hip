@@ -463,12 +463,12 @@ void dispatch_gemv_1280_batch(int nv, const _Float16* x, const LnArgs& ln, const
 // ------------------------------------------------------------------------------------------
 // LM head + argmax (reference lm_head_argmax_kernel, whisper_kernels.cu:28-86): rows of the tied
 // embedding are streamed once; each row's fp32 dot is rounded to fp16, packed with its index and
-// max-reduced to one 64-bit atomicMax per block. The logits vector is never written. Each block owns
-// a contiguous row range; its first 16 rows are requested before the (optional) final-LayerNorm
-// prologue and every iteration prefetches the next 16 rows, so two row groups are in flight per wave.
-// The finalize step (reference argmax_finalize_kernel, :88-100) is a separate 1-thread launch: a
-// last-block-done finalize needs a device-scope release per block, which on this part writes back
-// the L2 and costs far more than one extra launch.
+// max-reduced to one 64-bit atomicMax per block. The logits vector is never written. Blocks take
+// 64-row batches round-robin; a block's first batch is requested before the (optional)
+// final-LayerNorm prologue and the next batch is always in flight while one is scored (two register
+// buffers per wave). The finalize step (reference argmax_finalize_kernel, :88-100) is a separate
+// 1-thread launch: a last-block-done finalize needs a device-scope release per block, which on this
+// part writes back the L2 and costs more than the extra launch (measured +2.8 us per decode step).
 // ------------------------------------------------------------------------------------------
 #ifndef FW_LM_NW
 #define FW_LM_NW 16
@@ -479,6 +479,7 @@ void dispatch_gemv_1280_batch(int nv, const _Float16* x, const LnArgs& ln, const
 #ifndef FW_LM_BPC
 #define FW_LM_BPC 1
 #endif
+
 constexpr int kLmNW = FW_LM_NW, kLmU = FW_LM_U;
 constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // rows per block iteration
 
@@ -504,7 +505,7 @@ template <bool LN>
 __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __restrict__ yin, LnArgs ln,
                                                              const _Float16* __restrict__ w,
                                                              const uint8_t* __restrict__ suppress, int vocab,
-                                                             int rows_per_block, unsigned long long* best) {
+                                                             unsigned long long* best) {
   using RS = RowSplit<kHidden>;
   __shared__ __align__(16) _Float16 y_lds[kHidden];
   __shared__ float red[kLmNW];
@@ -512,8 +513,11 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane & 31, rsel = lane >> 5;
   const uint4* w4 = reinterpret_cast<const uint4*>(w);
-  const int r_begin = blockIdx.x * rows_per_block;
-  const int r_end = min(vocab, r_begin + rows_per_block);
+  // Batches of kLmRowsIter rows are dealt to the blocks round-robin: batch k of this block starts at
+  // row (k * gridDim.x + blockIdx.x) * kLmRowsIter, so at any moment the grid streams one contiguous
+  // stretch of the table.
+  const int r_end = vocab;
+  auto base_of = [&](int k) { return (k * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) * kLmRowsIter; };
 
   // Rows past r_end load row r_end - 1 and are masked when scored: no load sits under a lane mask,
   // so the wait for one batch never includes the batch requested after it.
@@ -531,7 +535,7 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
   if constexpr (LN) ln_load<kLmNW * 64>(ln.h, ln.x, ln.gamma, ln.beta, lnr);
   uint4 wa[kLmU][RS::kC], wb[kLmU][RS::kC];
   uint32_t sa[kLmU], sb[kLmU];
-  load(r_begin, wa, sa);
+  load(base_of(0), wa, sa);
 
   if constexpr (LN) {
     ln_finish<kLmNW * 64>(lnr, ln.x != nullptr, nullptr, ln.eps, y_lds, red);
@@ -559,8 +563,8 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
     }
   };
   // two register buffers in turn: batch i + 1 is in flight while batch i is scored
-  for (int base = r_begin; base < r_end; base += 2 * kLmRowsIter) {
-    const int b1 = base + kLmRowsIter, b2 = base + 2 * kLmRowsIter;
+  for (int k = 0; base_of(k) < r_end; k += 2) {
+    const int base = base_of(k), b1 = base_of(k + 1), b2 = base_of(k + 2);
     if (b1 < r_end) load(b1, wb, sb);
     score(base, wa, sa);
     if (b2 < r_end) load(b2, wa, sa);
@@ -576,15 +580,15 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __r
   }
 }
 
-int lm_head_grid(int vocab, int* rows_per_block) {
+int lm_head_grid(int vocab) {
   int dev = 0, cus = 256;
   if (hipGetDevice(&dev) == hipSuccess &&
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     cus = 256;
-  const int max_blocks = cus * FW_LM_BPC;
-  const int iters = (vocab + max_blocks * kLmRowsIter - 1) / (max_blocks * kLmRowsIter);
-  *rows_per_block = iters * kLmRowsIter;
-  return (vocab + *rows_per_block - 1) / *rows_per_block;
+  // as few batches per block as the CUs allow, then as few blocks as that count needs
+  const int batches = (vocab + kLmRowsIter - 1) / kLmRowsIter;
+  const int per = (batches + cus * FW_LM_BPC - 1) / (cus * FW_LM_BPC);
+  return (batches + per - 1) / per;
 }
 
 __global__ void argmax_finalize_kernel(unsigned long long* best, FinArgs fin) { finalize_token(best, fin); }
@@ -936,10 +940,9 @@ extern "C" int fw_lm_head_argmax(const void* y, const void* w, const uint8_t* su
   FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
   FW_REQUIRE(vocab > 0, "vocab must be positive");
   FW_REQUIRE(aligned16(y) && aligned16(w), "lm_head_argmax: y and w must be 16-byte aligned");
-  int rpb = 0;
-  const int grid = lm_head_grid(vocab, &rpb);
+  const int grid = lm_head_grid(vocab);
   hipLaunchKernelGGL(lm_head_kernel<false>, dim3(grid), dim3(kLmNW * 64), 0, stream, static_cast<const _Float16*>(y),
-                     LnArgs{}, static_cast<const _Float16*>(w), suppress, vocab, rpb,
+                     LnArgs{}, static_cast<const _Float16*>(w), suppress, vocab,
                      reinterpret_cast<unsigned long long*>(best));
   return fw_check_launch("lm_head_argmax");
 }
@@ -954,13 +957,12 @@ extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void*
   FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
   FW_REQUIRE(vocab > 0 && max_pos > 0, "vocab and max_pos must be positive");
   FW_REQUIRE(aligned16(w), "lm_head_argmax_fused: w must be 16-byte aligned");
-  int rpb = 0;
-  const int grid = lm_head_grid(vocab, &rpb);
+  const int grid = lm_head_grid(vocab);
   LnArgs ln{static_cast<const _Float16*>(h), static_cast<const _Float16*>(x), nullptr,
             static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta), eps, nullptr, nullptr,
             nullptr, nullptr, 0, 0};
   hipLaunchKernelGGL(lm_head_kernel<true>, dim3(grid), dim3(kLmNW * 64), 0, stream, nullptr, ln,
-                     static_cast<const _Float16*>(w), suppress, vocab, rpb, reinterpret_cast<unsigned long long*>(best));
+                     static_cast<const _Float16*>(w), suppress, vocab, reinterpret_cast<unsigned long long*>(best));
   int rc = fw_check_launch("lm_head_argmax_fused");
   if (rc != FW_OK || !finalize) return rc;
   FinArgs fin{tokens, state, cur, max_pos};
