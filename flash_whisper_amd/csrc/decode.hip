@@ -413,8 +413,9 @@ void launch_gemv_batch(int nv, const _Float16* x, const LnArgs& ln, const Combin
 }
 
 // Block shapes of the decode GEMVs (waves per block, row groups per wave), measured on MI355X over the
-// whole decoder step: large blocks (8-16 waves, 80-160 blocks) beat one small block per CU because the
-// prologue (LayerNorm or split-K combine) is repeated per block and its latency is the critical path.
+// whole decoder step (alternating runs of each shape on one device): large blocks (8-12 waves, 54-160
+// blocks) beat one small block per CU because the prologue (LayerNorm or split-K combine) is repeated
+// per block and its latency is the critical path; 4- and 16-wave blocks were slower everywhere.
 #ifndef FW_G5120_NW
 #define FW_G5120_NW 8  // LN + fc1 (5120 rows): 32 rows per block
 #endif
@@ -422,7 +423,10 @@ void launch_gemv_batch(int nv, const _Float16* x, const LnArgs& ln, const Combin
 #define FW_G5120_U 2
 #endif
 #ifndef FW_G3840_NW
-#define FW_G3840_NW 8  // LN + q/k/v (3840 rows): 32 rows per block
+#define FW_G3840_NW 8  // LN + q/k/v (3840 rows): 16 rows per block
+#endif
+#ifndef FW_G3840_U
+#define FW_G3840_U 1
 #endif
 #ifndef FW_G1280_NW
 #define FW_G1280_NW 8  // LN + cross q (1280 rows): 16 rows per block
@@ -434,7 +438,7 @@ void launch_gemv_batch(int nv, const _Float16* x, const LnArgs& ln, const Combin
 #define FW_GK5120_U 1
 #endif
 #ifndef FW_CMB_NW
-#define FW_CMB_NW 16  // combine + out projection: 32 rows per block
+#define FW_CMB_NW 12  // combine + out projection: 24 rows per block
 #endif
 template <int MODE, int ACT>
 void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w,
@@ -442,7 +446,7 @@ void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& 
   if (n >= 5120)
     launch_gemv<kHidden, FW_G5120_NW, FW_G5120_U, MODE, ACT>(x, ln, cb, w, b, out, n, s);
   else if (n >= 3840)
-    launch_gemv<kHidden, FW_G3840_NW, 2, MODE, ACT>(x, ln, cb, w, b, out, n, s);
+    launch_gemv<kHidden, FW_G3840_NW, FW_G3840_U, MODE, ACT>(x, ln, cb, w, b, out, n, s);
   else
     launch_gemv<kHidden, FW_G1280_NW, 1, MODE, ACT>(x, ln, cb, w, b, out, n, s);
 }
