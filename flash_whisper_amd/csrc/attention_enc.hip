@@ -36,13 +36,13 @@ __device__ __forceinline__ void ea_dma(const _Float16* kbase, int ld, const _Flo
   for (int i = 0; i < 2; ++i) {  // K tile: wave fills 8-row blocks 2 wave and 2 wave + 1
     const int blk = 2 * wave + i, row = blk * 8 + rsub;
     const int key = min(kv0 + row, seq - 1);  // keys past seq are masked to -inf
-    dma16(kbase + static_cast<size_t>(key) * ld + (slot ^ (row & 7)) * 8,
+    dma16(kbase + static_cast<size_t>(key) * ld + swz_slot(row, slot) * 8,
           __builtin_amdgcn_readfirstlane(stage + blk * 1024));
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {  // V^T tile: rows are head dims
     const int blk = 2 * wave + i, d = blk * 8 + rsub;
-    dma16(vtbase + static_cast<size_t>(d) * seq_pad + kv0 + (slot ^ (d & 7)) * 8,
+    dma16(vtbase + static_cast<size_t>(d) * seq_pad + kv0 + swz_slot(d, slot) * 8,
           __builtin_amdgcn_readfirstlane(stage + kEaTileBytes + blk * 1024));
   }
 }

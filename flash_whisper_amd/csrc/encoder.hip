@@ -13,8 +13,10 @@ namespace {
 // waves in a (BM / 64 or 2) x 2 arrangement, each wave a (64 or 32) x 64 tile of
 // v_mfma_f32_32x32x16_f16 products.
 //  - LDS: one [rows][64] fp16 tile per operand and stage, 8 x 16-byte chunks per row, chunk c of
-//    row r stored in slot c ^ (r & 7), so the 8 rows a quarter-wave reads for one MFMA operand hit
-//    8 different bank groups (conflict-free ds_read_b128).
+//    row r stored in slot swz_slot(r, c) = c ^ ((r >> 1) & 7), so the 16 rows a 16-lane group reads
+//    for one MFMA operand cover all 64 banks (conflict-free ds_read_b128).
+//  - Epilogues: bias, GELU (erfc by a Chebyshev fit, one fp16 ulp of the exact-erf GELU at most),
+//    residual, fp16 clamp, the q scale, the cross K/V scatter and the transposed-V store.
 //  - Plain GEMMs (gemm_dma_kernel): global -> LDS copies into a ring of stages, operand fragments
 //    double-buffered in registers (see the pipeline notes above that kernel).
 //  - Implicit-GEMM conv (gemm_kernel): the A tile is gathered from the time-major input through
@@ -82,13 +84,38 @@ constexpr bool epi_reads_res(int epi) {
   return epi == FW_EPI_BIAS_RESID || epi == FW_EPI_BIAS_RESID_CLAMP || epi == FW_EPI_BIAS_GELU_POS;
 }
 
+// erfc(z) for z >= 0 by the Chebyshev fit of Press et al., Numerical Recipes in C (2nd ed.), 6.2
+// ("erfcc"): erfc(z) = t exp(-z^2 - 1.26551223 + t (1.00002368 + ... + t 0.17087277)),
+// t = 1 / (1 + z / 2), fractional error below 1.2e-7 everywhere. The GELU built on it,
+// 0.5 x erfc(-x / sqrt 2), is then accurate in relative terms on both tails and is rounded to
+// fp16 (relative step 2^-11), so it can differ from an exact-erf GELU by one fp16 ulp only next to
+// a rounding boundary. It costs a third of the library erff in the GEMM epilogue.
+__device__ __forceinline__ float erfc_nr(float z) {
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(t, p, -0.82215223f);
+  p = fmaf(t, p, 1.48851587f);
+  p = fmaf(t, p, -1.13520398f);
+  p = fmaf(t, p, 0.27886807f);
+  p = fmaf(t, p, -0.18628806f);
+  p = fmaf(t, p, 0.09678418f);
+  p = fmaf(t, p, 0.37409196f);
+  p = fmaf(t, p, 1.00002368f);
+  p = fmaf(t, p, -1.26551223f);
+  return t * __builtin_amdgcn_exp2f((p - z * z) * 1.4426950408889634f);
+}
+__device__ __forceinline__ float gelu_enc(float x) {
+  const float c = erfc_nr(fabsf(x) * 0.70710678118654752f);  // erfc(|x| / sqrt 2)
+  return 0.5f * x * (x >= 0.0f ? 2.0f - c : c);
+}
+
 // Output value before the final fp16 rounding; `res` is the residual / position operand of the
 // epilogues that read one.
 __device__ __forceinline__ float epilogue_apply(int epi, float acc, float b, float res, int col, int q_cols) {
   float v = round_h(acc + b);
   switch (epi) {
     case FW_EPI_BIAS_GELU:
-      v = gelu_erf(v);
+      v = gelu_enc(v);
       break;
     case FW_EPI_BIAS_RESID:
       v = res + v;
@@ -100,7 +127,7 @@ __device__ __forceinline__ float epilogue_apply(int epi, float acc, float b, flo
       break;
     }
     case FW_EPI_BIAS_GELU_POS:
-      v = round_h(gelu_erf(v)) + res;
+      v = round_h(gelu_enc(v)) + res;
       break;
     case FW_EPI_SCALE_Q:
     case kEpiQkvVt:
@@ -267,7 +294,7 @@ __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int
     const int blk = wave * kAInstr + i;  // 8-row block of the tile
     const int row = blk * 8 + rsub;
     const int gm = min(m0 + row, g.m - 1);  // rows past m are computed and never stored
-    const int chunk = slot ^ (row & 7);
+    const int chunk = swz_slot(row, slot);
     dma16(g.a + static_cast<size_t>(gm) * g.lda + k0 + chunk * 8,
           __builtin_amdgcn_readfirstlane(lds_stage + blk * 1024));
   }
@@ -275,7 +302,7 @@ __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int
   for (int i = 0; i < kBInstr; ++i) {
     const int blk = wave * kBInstr + i;
     const int row = blk * 8 + rsub;
-    const int chunk = slot ^ (row & 7);
+    const int chunk = swz_slot(row, slot);
     dma16(g.w + static_cast<size_t>(n0 + row) * g.ldw + k0 + chunk * 8,
           __builtin_amdgcn_readfirstlane(lds_stage + BM * 128 + blk * 1024));
   }

@@ -6,13 +6,20 @@
 
 namespace fw {
 
-// Chunk c of LDS row r (8 x 16-byte chunks per row) lives in slot c ^ (r & 7): the 8 rows a
-// quarter-wave reads for one MFMA operand hit 8 different bank groups.
-__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + (chunk ^ (row & 7)); }
+// Chunk c of LDS row r (8 x 16-byte chunks per row) lives in slot c ^ ((r >> 1) & 7). An MFMA
+// operand read has lane i on row r0 + i; with 64 four-byte banks (256 bytes) a 16-lane group then
+// covers every (r & 1, slot) pair once, i.e. all 64 banks. The row-only XOR (c ^ (r & 7), shift 0)
+// put rows r and r + 8 of a group on the same banks; the shift took the 1280-column encoder GEMM
+// (K = 5120) from 43 to 36 us and the q/k/v projection from 30 to 28 us on MI355X.
+#ifndef FW_SWZ_SHIFT
+#define FW_SWZ_SHIFT 1
+#endif
+__device__ __forceinline__ int swz_slot(int row, int chunk) { return chunk ^ ((row >> FW_SWZ_SHIFT) & 7); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + swz_slot(row, chunk); }
 
 // global_load_lds_dwordx4 writes one 16-byte chunk per lane straight into LDS at M0 + 16 * lane, so
 // a wave instruction fills 1 KB = 8 rows of 128 bytes. The XOR swizzle is applied on the source
-// side: lane l fills LDS row r0 + l / 8, slot l % 8, so it fetches chunk (l % 8) ^ (row & 7).
+// side: lane l fills LDS row r0 + l / 8, slot l % 8, so it fetches chunk swz_slot(row, l % 8).
 // The copies are issued from inline assembly: the compiler then does not guard every LDS read with
 // a wait for all outstanding copies, and the pipeline depth is set by the explicit vmcnt waits.
 #pragma clang diagnostic push

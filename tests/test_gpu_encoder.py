@@ -64,6 +64,33 @@ def test_gemm_epilogues(ext, hip_device, m, n, k, epi):
     close_rel(np32(out), ref, scale=scale)
 
 
+def _f16_order(v):
+    """fp16 values -> integers in value order (adjacent fp16 numbers differ by 1)."""
+    bits = np.asarray(v, np.float16).view(np.int16).astype(np.int32)
+    return np.where(bits < 0, -(bits & 0x7FFF), bits)
+
+
+def test_gelu_epilogue_within_one_ulp(ext, hip_device):
+    """The GELU epilogue (erfc by a Chebyshev fit) against an exact GELU, 0.5 x erfc(-x / sqrt 2) in
+    float64, on 16384 fp16 inputs spanning both tails, passed through the GEMM unchanged (identity
+    weights): every output within one fp16 ulp, and nearly all of them equal."""
+    from scipy.special import erfc
+
+    dev = hip_device
+    rng = np.random.default_rng(11)
+    x = np.concatenate([np.linspace(-12, 12, 8192), rng.standard_normal(4096) * 3,
+                        np.float16(rng.standard_normal(4096)) * 1e-3]).astype(np.float16)
+    a = x.reshape(128, 128)
+    out = torch.empty(128, 128, dtype=torch.float16, device=dev)
+    ext.gemm(h16(a, dev), h16(np.eye(128), dev), None, out, 1)
+    x64 = x.astype(np.float64)
+    ref = np.float16(0.5 * x64 * erfc(-x64 / np.sqrt(2.0)))
+    got = np.float16(np32(out).reshape(-1))
+    d = np.abs(_f16_order(got) - _f16_order(ref))
+    assert d.max() <= 1, (x[d.argmax()], got[d.argmax()], ref[d.argmax()])
+    assert (d == 0).mean() > 0.995
+
+
 def test_gemm_row_strided_views(ext, hip_device):
     """a, out given as column slices of wider matrices (leading dimension > k / n)."""
     dev = hip_device
