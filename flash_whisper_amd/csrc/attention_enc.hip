@@ -84,7 +84,7 @@ __device__ __forceinline__ void ea_tile(const u32x4* kt, const u32x4* vtt, const
       }
       tmax = fmaxf(tmax, s[b][r]);
     }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * kLog2e;
+  tmax = xor_max<32>(tmax) * kLog2e;
   if (__builtin_amdgcn_ballot_w64(tmax > st.m + kEaSlack)) {  // wave-uniform
     const float m_new = fmaxf(st.m, tmax);
     const float corr = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first tile (m = -inf)
@@ -108,7 +108,7 @@ __device__ __forceinline__ void ea_tile(const u32x4* kt, const u32x4* vtt, const
       pf[b][r >> 3][r & 7] = ph[0];
       pf[b][r >> 3][(r & 7) + 1] = ph[1];
     }
-  st.l += psum + __shfl_xor(psum, 32, kWave);
+  st.l += xor_add<32>(psum);
   // O^T[d][q] += sum_keys V^T[d][key] P^T[key][q]; k-step (b, hs) covers keys 32 b + 16 hs + [0, 16),
   // whose transposed-layout chunk for lane half lg is chunk 4 b + 2 hs + lg of the V^T row.
 #pragma unroll

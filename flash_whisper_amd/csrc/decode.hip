@@ -730,14 +730,10 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
       }
     }
   }
-  psum += __shfl_xor(psum, 8, kWave);
-  psum += __shfl_xor(psum, 16, kWave);
-  psum += __shfl_xor(psum, 32, kWave);
+  psum = xor_add<32>(xor_add<16>(xor_add<8>(psum)));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    acc[t] += __shfl_xor(acc[t], 8, kWave);
-    acc[t] += __shfl_xor(acc[t], 16, kWave);
-    acc[t] += __shfl_xor(acc[t], 32, kWave);
+    acc[t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[t])));
   }
   if (lane == 0) {
     wm[wave] = mx;
@@ -888,17 +884,13 @@ __global__ void __launch_bounds__(kHeadWaves * 64) attn_head_kernel(AttnArgs a) 
       }
     }
     // psum is replicated over the 8 lanes of a key group: sum one lane per group
-    psum += __shfl_xor(psum, 8, kWave);
-    psum += __shfl_xor(psum, 16, kWave);
-    psum += __shfl_xor(psum, 32, kWave);
+    psum = xor_add<32>(xor_add<16>(xor_add<8>(psum)));
     l_run = l_run * corr + psum;
     m_run = m_new;
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    acc[t] += __shfl_xor(acc[t], 8, kWave);
-    acc[t] += __shfl_xor(acc[t], 16, kWave);
-    acc[t] += __shfl_xor(acc[t], 32, kWave);
+    acc[t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[t])));
   }
   if (lane == 0) {
     wm[wave] = m_run;

@@ -29,17 +29,84 @@ __device__ __forceinline__ float h2f(_Float16 x) { return static_cast<float>(x);
 __device__ __forceinline__ _Float16 f2h(float x) { return static_cast<_Float16>(x); }  // round-to-nearest-even
 __device__ __forceinline__ float round_h(float x) { return static_cast<float>(static_cast<_Float16>(x)); }
 
-// Butterfly sum over `width` consecutive lanes (width a power of two <= 64).
+// Butterfly steps between lane l and lane l ^ O without the LDS crossbar (a ds_bpermute costs an LDS
+// round trip per step): O = 1, 2 are DPP quad permutes; O = 4, 8 are two DPP row shifts, each
+// writing the 4-lane banks whose partner lies on its side; O = 16, 32 use v_permlane16_swap /
+// v_permlane32_swap, which trade row pairs / wave halves between two copies of the value, so that
+// the two results hold, lane by lane, the value and its partner. Every step combines the same two
+// operands as a __shfl_xor step would.
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+  static_assert(O == 1 || O == 2 || O == 4 || O == 8, "DPP partner for O <= 8");
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (O == 1) {
+    r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (O == 2) {
+    r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (O == 4) {
+    r = __builtin_amdgcn_update_dpp(0, x, 0x104, 0xF, 0x5, false);  // banks 0, 2 <- lane + 4 (row_shl:4)
+    r = __builtin_amdgcn_update_dpp(r, x, 0x114, 0xF, 0xA, false);  // banks 1, 3 <- lane - 4 (row_shr:4)
+  } else {
+    r = __builtin_amdgcn_update_dpp(0, x, 0x108, 0xF, 0x3, false);  // banks 0, 1 <- lane + 8 (row_shl:8)
+    r = __builtin_amdgcn_update_dpp(r, x, 0x118, 0xF, 0xC, false);  // banks 2, 3 <- lane - 8 (row_shr:8)
+  }
+  return __builtin_bit_cast(float, r);
+}
+// {v, v[l ^ O]} in some order per lane, for O = 16 or 32. Issued as inline assembly: the compiler's
+// builtins for these swaps hand back the first register for both results. The leading s_nop covers
+// the wait states a swap needs after the VALU write of its operands.
+template <int O>
+__device__ __forceinline__ void xor_pair(float v, float& a, float& b) {
+  static_assert(O == 16 || O == 32, "row / half swaps");
+  a = v;
+  b = v;
+  if constexpr (O == 16)
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  else
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+template <int O>
+__device__ __forceinline__ float xor_add(float v) {
+  if constexpr (O >= 16) {
+    float a, b;
+    xor_pair<O>(v, a, b);
+    return a + b;
+  } else {
+    return v + xor_lane<O>(v);
+  }
+}
+template <int O>
+__device__ __forceinline__ float xor_max(float v) {
+  if constexpr (O >= 16) {
+    float a, b;
+    xor_pair<O>(v, a, b);
+    return fmaxf(a, b);
+  } else {
+    return fmaxf(v, xor_lane<O>(v));
+  }
+}
+
+// Butterfly sum / max over `width` consecutive lanes (width a power of two <= 64), partners taken in
+// the order width / 2, ..., 2, 1.
 template <int kWidth>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = kWidth / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  if constexpr (kWidth >= 64) v = xor_add<32>(v);
+  if constexpr (kWidth >= 32) v = xor_add<16>(v);
+  if constexpr (kWidth >= 16) v = xor_add<8>(v);
+  if constexpr (kWidth >= 8) v = xor_add<4>(v);
+  if constexpr (kWidth >= 4) v = xor_add<2>(v);
+  if constexpr (kWidth >= 2) v = xor_add<1>(v);
   return v;
 }
 template <int kWidth>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = kWidth / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  if constexpr (kWidth >= 64) v = xor_max<32>(v);
+  if constexpr (kWidth >= 32) v = xor_max<16>(v);
+  if constexpr (kWidth >= 16) v = xor_max<8>(v);
+  if constexpr (kWidth >= 8) v = xor_max<4>(v);
+  if constexpr (kWidth >= 4) v = xor_max<2>(v);
+  if constexpr (kWidth >= 2) v = xor_max<1>(v);
   return v;
 }
 
