@@ -604,11 +604,22 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __r
   const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
   const bool valid = row < rows;
   const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(valid ? row : 0) * kHidden);
+  // gamma and beta are requested with the row, not after the two reductions
+  const uint4* g4 = reinterpret_cast<const uint4*>(gamma);
+  const uint4* b4 = reinterpret_cast<const uint4*>(beta);
+  uint4 xu[kC], gu[kC], bu[kC];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) xu[c] = xr[sub + 32 * c];
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    gu[c] = g4[sub + 32 * c];
+    bu[c] = b4[sub + 32 * c];
+  }
   float v[kC * 8];
   float sum = 0.f;
 #pragma unroll
   for (int c = 0; c < kC; ++c) {
-    const uint4 u = xr[sub + 32 * c];
+    const uint4 u = xu[c];
     const _Float16* hp = reinterpret_cast<const _Float16*>(&u);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -624,20 +635,18 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __r
     sq += d * d;
   }
   const float inv = rsqrtf(group_sum<32>(sq) * (1.0f / kHidden) + eps);
-  if (!valid) return;
-  const uint4* g4 = reinterpret_cast<const uint4*>(gamma);
-  const uint4* b4 = reinterpret_cast<const uint4*>(beta);
-  uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(row) * kHidden);
+  uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(valid ? row : 0) * kHidden);
 #pragma unroll
   for (int c = 0; c < kC; ++c) {
-    const uint4 gu = g4[sub + 32 * c], bu = b4[sub + 32 * c];
-    const _Float16* gp = reinterpret_cast<const _Float16*>(&gu);
-    const _Float16* bp = reinterpret_cast<const _Float16*>(&bu);
+    const _Float16* gp = reinterpret_cast<const _Float16*>(&gu[c]);
+    const _Float16* bp = reinterpret_cast<const _Float16*>(&bu[c]);
     uint4 o;
     _Float16* op = reinterpret_cast<_Float16*>(&o);
 #pragma unroll
     for (int e = 0; e < 8; ++e) op[e] = f2h((v[c * 8 + e] - mean) * inv * h2f(gp[e]) + h2f(bp[e]));
-    yr[sub + 32 * c] = o;
+    // computed outside the store's lane mask, so the gamma / beta requests are not sunk into it
+    asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
+    if (valid) yr[sub + 32 * c] = o;
   }
 }
 
