@@ -8,9 +8,11 @@ in-memory waveform and stops at the token-id list (reference custom/model.py:179
 
 Reported metric: decode-step us (median GPU time per decoder step, HIP events around every 8-step graph
 replay inside the timed transcribes), its achieved HBM GB/s from the algorithmic bytes of a step, the
-30 s-clip E2E ms and TTFT. ``roofline`` covers the LM-head kernel (final LN + tied-embedding GEMV +
-argmax), timed standalone: a hipGraph of launches over rotating copies of the 133 MB embedding, so it
-streams from HBM as inside the step, between HIP events on the graph's stream. ``cpu_baseline`` times the CPU oracle's decoder step on this host.
+30 s-clip E2E ms and TTFT. ``roofline`` covers the step's LM-head kernel (final LN + int8 pre-pass over
+the tied embedding + exact fp16 logits of the candidate rows + argmax; ``--fp16-lm-head`` decodes with
+the fp16 LM-head kernel instead, same tokens), timed standalone: a hipGraph of launches over rotating
+copies of its table, so it streams from HBM as inside the step, between HIP events on the graph's
+stream. ``cpu_baseline`` times the CPU oracle's decoder step on this host.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -25,22 +27,25 @@ import time
 
 METRIC = 'decode-step µs + achieved HBM GB/s; 30 s-clip E2E ms & TTFT, batch 1'
 HBM_PEAK_GBPS = 8000.0
+LM_KERNEL = {False: 'lm_head_kernel<true> (final LN + LM head GEMV + argmax)',
+             True: 'lm_head_q8_kernel<true> (final LN + int8 pre-pass over the LM head + exact fp16 candidates + argmax)'}
+LM_TRAFFIC = {False: 'profiles/lm_head_kernel_traffic.md', True: 'profiles/lm_head_q8_kernel_traffic.md'}
 
 
-def decode_step_bytes(dims, length):
+def decode_step_bytes(dims, length, q8=False):
     """Algorithmic HBM bytes of one decoder step attending over `length` cached positions: every decoder
     weight, bias and LayerNorm vector once, the tied 51866 x 1280 LM head once, the cross K/V of all
     layers, the self K/V rows 0..length-1 of all layers, the two embedding rows and the suppress mask."""
     d, f, L = dims.d_model, dims.ffn, dims.dec_layers
     per_layer = 2 * (3 * d * d + 3 * d * d + 2 * d * f) + 2 * (3 * d + d + d + d + f + d) + 2 * 6 * d
     weights = L * per_layer + 2 * 2 * d  # + final LN
-    lm_head = 2 * dims.vocab * d
+    lm_head = (dims.vocab * d + 8 * dims.vocab) if q8 else 2 * dims.vocab * d
     cross = L * 2 * dims.heads * dims.enc_len * dims.head_dim * 2
     self_kv = L * 2 * dims.heads * length * dims.head_dim * 2
     return weights + lm_head + cross + self_kv + 2 * 2 * d + dims.vocab
 
 
-def measured_traffic(path='profiles/lm_head_kernel_traffic.md'):
+def measured_traffic(path):
     """HBM bytes per LM-head launch from the committed, copy-calibrated rocprofv3 PMC summary
     (FETCH_SIZE and WRITE_SIZE passes), or None when that summary is absent."""
     import pathlib
@@ -53,28 +58,42 @@ def measured_traffic(path='profiles/lm_head_kernel_traffic.md'):
     return int(m.group(1)) if m else None
 
 
-def lm_head_bytes(dims):
-    """Algorithmic bytes of one fused LM-head launch: the embedding, the suppress mask, h, x, gamma, beta."""
-    return 2 * dims.vocab * dims.d_model + dims.vocab + 4 * 2 * dims.d_model
+def lm_head_bytes(dims, q8):
+    """Algorithmic bytes of one fused LM-head launch. fp16 kernel: the embedding, the suppress mask, h, x,
+    gamma, beta. int8 pre-pass kernel: the int8 table, its per-row scale and error bound (8 B a row),
+    the mask and the four vectors; the fp16 rows of the candidates it re-scores (a few per block,
+    data-dependent) are not counted."""
+    vec = dims.vocab + 4 * 2 * dims.d_model
+    return (dims.vocab * dims.d_model + 8 * dims.vocab + vec) if q8 else (2 * dims.vocab * dims.d_model + vec)
 
 
-def time_lm_head(model, reps, copies=3):
+def time_lm_head(model, reps, q8):
     """Average us per launch of the LN + LM-head + argmax kernel alone (no finalize launch): `reps`
-    launches rotating over `copies` embedding copies (>= 256 MB, more than the MALL, so each launch
-    reads its weights from HBM) are captured in one hipGraph on a side stream and replayed between HIP
+    launches rotating over copies of its table (>= 256 MB in all, more than the MALL, so each launch
+    reads its table from HBM) are captured in one hipGraph on a side stream and replayed between HIP
     events recorded on that stream."""
     import torch
 
     ext, d = model.ext, model.dims
-    tables = [model.lm_head] + [model.lm_head.clone() for _ in range(copies - 1)]
+    copies = 5 if q8 else 3
+    if q8:
+        tables = [(model.lm_q8, model.lm_meta)] + [(model.lm_q8.clone(), model.lm_meta.clone())
+                                                   for _ in range(copies - 1)]
+    else:
+        tables = [model.lm_head] + [model.lm_head.clone() for _ in range(copies - 1)]
     best = torch.zeros(1, dtype=torch.long, device='cuda')
     g, b, eps = model.final_ln
     h, x = model.h[0], model.pending
     stream = torch.cuda.Stream()
 
     def launch(i):
-        ext.lm_head_argmax_fused(h, x, g, b, eps, tables[i % copies], model.suppress, best, None, None, None,
-                                 d.max_pos)
+        if q8:
+            wq, meta = tables[i % copies]
+            ext.lm_head_argmax_q8(h, x, g, b, eps, model.lm_head, wq, meta, model.suppress, best, None, None, None,
+                                  d.max_pos)
+        else:
+            ext.lm_head_argmax_fused(h, x, g, b, eps, tables[i % copies], model.suppress, best, None, None, None,
+                                     d.max_pos)
 
     with torch.inference_mode(), torch.cuda.stream(stream):
         for i in range(2 * copies):
@@ -148,6 +167,8 @@ def main():
     ap.add_argument('--cpu-seconds', type=float, default=12.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--lanes', type=int, default=2, help='clips in flight for the serving-throughput extra (0: skip)')
+    ap.add_argument('--fp16-lm-head', action='store_true',
+                    help='decode with the fp16 LM-head kernel instead of the int8 pre-pass one (same tokens)')
     ap.add_argument('--copy-calibration', action='store_true',
                     help='also run 4 plain 256 MiB device copies (the reference kernel for PMC byte counters)')
     args = ap.parse_args()
@@ -163,7 +184,7 @@ def main():
     from flash_whisper_amd.config import CHUNK
     from flash_whisper_amd.model import CustomModel
 
-    model = CustomModel(seed=0)
+    model = CustomModel(seed=0, lm_q8=not args.fp16_lm_head)
     if not model.selftest['ok']:
         print(f'selftest failed: {[c for c in model.selftest["checks"] if not c["ok"]]}', file=sys.stderr)
         sys.exit(1)
@@ -184,7 +205,9 @@ def main():
     elapsed = time.perf_counter() - t0
     model.record_events = False
 
-    lm_us = time_lm_head(model, args.kernel_reps)
+    q8 = model.use_lm_q8
+    lm_us = time_lm_head(model, args.kernel_reps, q8)
+    lm16_us = time_lm_head(model, args.kernel_reps, False) if q8 else lm_us
     serve = serving_throughput(model, args.lanes, 2 * args.lanes, args.tokens) if args.lanes > 1 else None
     if args.copy_calibration:
         src = torch.empty(128 << 20, dtype=torch.float16, device='cuda')
@@ -193,12 +216,13 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    lm_bytes = lm_head_bytes(model.dims)
+    lm_bytes = lm_head_bytes(model.dims, q8)
     lm_gbps = lm_bytes / (lm_us * 1e-6) / 1e9
 
     # mean cached length over the decode: positions 4 .. 4 + tokens - 1 attend over pos + 1 keys
     lengths = np.arange(len(model.prompt) + 1, len(model.prompt) + args.tokens + 1)
-    step_bytes = float(np.mean([decode_step_bytes(model.dims, int(L)) for L in lengths]))
+    step_bytes = float(np.mean([decode_step_bytes(model.dims, int(L), q8) for L in lengths]))
+    ref_step_bytes = float(np.mean([decode_step_bytes(model.dims, int(L)) for L in lengths]))
     med_step = statistics.median(step_us)
     step_gbps = step_bytes / (med_step * 1e-6) / 1e9
     med = lambda k: statistics.median(r[k] for r in rows) * 1e3
@@ -212,15 +236,16 @@ def main():
                                f'{args.tokens} greedy tokens (8-step decoder hipGraph)',
                    'clip_s': 30, 'tokens': args.tokens, 'batch': 1},
         'decode_step_us': round(med_step, 2), 'decode_step_bytes': int(step_bytes),
+        'decode_step_bytes_fp16_head': int(ref_step_bytes),
         'decode_step_hbm_gbps': round(step_gbps, 1), 'decode_step_roofline_frac': round(step_gbps / HBM_PEAK_GBPS, 4),
         'e2e_ms': round(med('e2e_s'), 3), 'ttft_ms': round(med('ttft_s'), 3), 'mel_ms': round(med('mel_s'), 3),
         'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
         'n_tokens': rows[-1]['n_tokens'],
-        'roofline': {'kernel': 'lm_head_kernel<true> (final LN + LM head GEMV + argmax)',
-                     'bound': 'hbm', 'achieved': round(lm_gbps, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
-                     'frac': round(lm_gbps / HBM_PEAK_GBPS, 4), 'traffic': measured_traffic(),
-                     'traffic_source': 'profiles/lm_head_kernel_traffic.md', 'us_per_launch': round(lm_us, 2),
-                     'bytes_per_launch': lm_bytes},
+        'roofline': {'kernel': LM_KERNEL[q8], 'bound': 'hbm', 'achieved': round(lm_gbps, 1),
+                     'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(lm_gbps / HBM_PEAK_GBPS, 4),
+                     'traffic': measured_traffic(LM_TRAFFIC[q8]), 'traffic_source': LM_TRAFFIC[q8],
+                     'us_per_launch': round(lm_us, 2), 'bytes_per_launch': lm_bytes,
+                     'fp16_head_us_per_launch': round(lm16_us, 2)},
     }
     if serve is not None:
         out['serving'] = serve

@@ -37,6 +37,8 @@ SIGNATURES = {
                                          c_int, P]),
     'fw_attn_out_gemv_batch': (c_int, [P, P, P, c_int64, P, c_int, c_int, c_int, P, P, P, c_int, c_int, P]),
     'fw_lm_head_argmax_fused': (c_int, [P, P, P, P, c_float, P, P, c_int, c_int, P, P, P, P, c_int, P]),
+    'fw_lm_head_q8_pack': (c_int, [P, c_int, c_int, P, P, P]),
+    'fw_lm_head_argmax_q8': (c_int, [P, P, P, P, c_float, P, P, P, P, c_int, c_int, P, P, P, P, c_int, P]),
     'fw_log_mel': (c_int, [P, c_int, P, P, P, P, c_int64, P]),
     'fw_log_mel_ws_floats': (c_int64, [c_int]),
     'fw_gemm': (c_int, [P, c_int, P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),

@@ -598,6 +598,263 @@ int lm_head_grid(int vocab) {
 __global__ void argmax_finalize_kernel(unsigned long long* best, FinArgs fin) { finalize_token(best, fin); }
 
 // ------------------------------------------------------------------------------------------
+// LM head with an int8 pre-pass: the packed winner of lm_head_kernel, bit for bit, from about half
+// of its HBM bytes. The embedding is also kept as int8 rows q_v with a per-row scale s_v and a per-row
+// bound e_v >= || E_v - s_v q_v ||_2 (lm_q8_pack_kernel). Each block, over its 256 rows:
+//  1. scores them on the int8 table. y is quantized per block to integers y_int of step t
+//     (|y_int| <= 127 * 128), split into two int8 digits, so q_v . y_int is an exact integer dot
+//     (v_dot4_i32_i8) and A_v = s_v t (q_v . y_int) takes one fp64 rounding. With eta = y - t y_int,
+//     |Ehat_v| <= 127 s_v sqrt(1280) + e_v =: nE_v (a bound on |E_v| and |s_v q_v|) and
+//     g = 1280 * 2^-24 / (1 - 1280 * 2^-24), the fp32 logit X_v that lm_head_kernel computes obeys
+//       |A_v - X_v| <= r_v = |y| e_v + (|eta| + g |y|) nE_v
+//     (quantization of E, quantization of y, and the fp32 rounding of X_v, whose dot has at most 45
+//     roundings, each at most 2^-24 of the sum of |products| <= |y| |E_v|); r_v is inflated by 2^-20
+//     and the bounds A_v -+ r_v are rounded outward to fp32;
+//  2. takes T = max(A_v - r_v) over its unsuppressed rows. Some row has X >= T, so the block's winner w
+//     has fp16(X_w) >= fp16(T) and X_w >= T - (two fp16 spacings at T) >= thr(T) (below): every row
+//     with A_v + r_v >= thr is a candidate, and every row that ties the winner is one too;
+//  3. computes each candidate's logit with exactly the lane split and summation order of
+//     lm_head_kernel, packs it as that kernel does and sends the block maximum to best with one
+//     atomicMax. The maximum over blocks is then that of lm_head_kernel.
+// Candidates are typically 0-15 of a block's 256 rows for fp16 logits of unit scale; when every logit
+// is equal (y = 0) all rows are candidates and the block reads its fp16 rows as lm_head_kernel does.
+// ------------------------------------------------------------------------------------------
+constexpr int kQ8RowsPerBlock = kLmRowsIter * 4;  // 4 batches of 64 rows, dealt round-robin
+constexpr int kQ8Chunks = kHidden / 16;           // 16-byte int8 chunks per row (80)
+constexpr int kQ8Lpr = 16;                        // lanes per row in the int8 pass
+constexpr int kQ8C = kQ8Chunks / kQ8Lpr;          // chunks per lane (5)
+constexpr int kQ8YMax = 127 * 128;                // |y_int| bound: digits hi in [-127, 127], lo in [-64, 63]
+constexpr float kQ8Gamma = 7.7e-5f;               // >= 1280 * 2^-24 / (1 - 1280 * 2^-24)
+static_assert(kLmNW * 64 / kQ8Lpr == kLmRowsIter, "one int8 row per 16 lanes per batch");
+
+__device__ __forceinline__ int xor_add_i16(int v) {
+  // integer butterfly over 16 lanes (partners 8, 4, 2, 1), exact
+  v += __builtin_bit_cast(int, xor_lane<8>(__builtin_bit_cast(float, v)));
+  v += __builtin_bit_cast(int, xor_lane<4>(__builtin_bit_cast(float, v)));
+  v += __builtin_bit_cast(int, xor_lane<2>(__builtin_bit_cast(float, v)));
+  v += __builtin_bit_cast(int, xor_lane<1>(__builtin_bit_cast(float, v)));
+  return v;
+}
+
+__device__ __forceinline__ int dot16_i8(const uint4& a, const uint4& b, int acc) {
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.x), static_cast<int>(b.x), acc, false);
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.y), static_cast<int>(b.y), acc, false);
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.z), static_cast<int>(b.z), acc, false);
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.w), static_cast<int>(b.w), acc, false);
+  return acc;
+}
+
+// Smallest X that can still tie or beat a row whose fp32 logit is at least T once both are rounded to
+// fp16 (round to nearest even; logits at or beyond 65520 round to +-inf and tie there).
+__device__ __forceinline__ float q8_threshold(float t) {
+  if (!(t > -65504.0f)) return -INFINITY;  // also NaN: keep every row
+  return fminf(t - (fabsf(t) * 0x1p-9f + 0x1p-23f), 65504.0f);
+}
+
+__global__ void __launch_bounds__(256) lm_q8_pack_kernel(const _Float16* __restrict__ w, int vocab,
+                                                         int8_t* __restrict__ wq, float2* __restrict__ meta) {
+  constexpr int kPer = kHidden / 64;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= vocab) return;  // wave-uniform
+  const _Float16* wr = w + static_cast<size_t>(row) * kHidden;
+  float v[kPer];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    v[i] = h2f(wr[lane + 64 * i]);
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = group_max<64>(amax);
+  const float s = amax / 127.0f;
+  const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+  double err = 0.0;
+  int8_t* qr = wq + static_cast<size_t>(row) * kHidden;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const float q = fminf(fmaxf(rintf(v[i] * inv), -127.f), 127.f);
+    qr[lane + 64 * i] = static_cast<int8_t>(q);
+    const double d = static_cast<double>(v[i]) - static_cast<double>(s) * static_cast<double>(q);
+    err = fma(d, d, err);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) err += __shfl_xor(err, o);
+  if (lane == 0) meta[row] = make_float2(s, __double2float_ru(sqrt(err) * (1.0 + 0x1p-40)));
+}
+
+template <bool LN>
+__global__ void __launch_bounds__(kLmNW * 64) lm_head_q8_kernel(const _Float16* __restrict__ yin, LnArgs ln,
+                                                                const _Float16* __restrict__ w,
+                                                                const int8_t* __restrict__ wq,
+                                                                const float2* __restrict__ meta,
+                                                                const uint8_t* __restrict__ suppress, int vocab,
+                                                                unsigned long long* best) {
+  __shared__ __align__(16) _Float16 y_lds[kHidden];
+  __shared__ __align__(16) int8_t yhi[kHidden];
+  __shared__ __align__(16) int8_t ylo[kHidden];
+  __shared__ float red[kLmNW];
+  __shared__ float ub_lds[kQ8RowsPerBlock];
+  __shared__ int cand[kQ8RowsPerBlock];
+  __shared__ int ncand;
+  __shared__ unsigned long long block_best[kLmNW * 2];
+  constexpr int kNT = kLmNW * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane & (kQ8Lpr - 1), rsel = lane / kQ8Lpr;  // 4 rows per wave
+  const uint4* wq4 = reinterpret_cast<const uint4*>(wq);
+  auto base_of = [&](int k) { return (k * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) * kLmRowsIter; };
+
+  struct Batch {
+    uint4 w[kQ8C];
+    float2 m;
+    uint32_t sp;
+  };
+  // Rows past vocab load row vocab - 1 (no load under a lane mask) and are dropped when scored.
+  auto load = [&](int base, Batch& b) {
+    const size_t row = min(base + wave * 4 + rsel, vocab - 1);
+#pragma unroll
+    for (int c = 0; c < kQ8C; ++c) b.w[c] = ld_lm_head(wq4 + row * kQ8Chunks + sub + kQ8Lpr * c);
+    b.m = meta[row];
+    b.sp = suppress[row];
+  };
+  LnRegs<kNT> lnr;
+  if constexpr (LN) ln_load<kNT>(ln.h, ln.x, ln.gamma, ln.beta, lnr);
+  if (tid == 0) ncand = 0;
+  // the first two batches are requested before the LayerNorm and y statistics, which take several
+  // block reductions; the other two are requested as soon as a register buffer frees up
+  Batch ba, bb;
+  load(base_of(0), ba);
+  load(base_of(1), bb);
+
+  if constexpr (LN) {
+    ln_finish<kNT>(lnr, ln.x != nullptr, nullptr, ln.eps, y_lds, red);
+  } else {
+    for (int i = tid; i < kHidden / 8; i += kNT)
+      reinterpret_cast<uint4*>(y_lds)[i] = reinterpret_cast<const uint4*>(yin)[i];
+  }
+  __syncthreads();
+  // y statistics (same values and reduction order in every block): max |y|, |y|^2, then the
+  // quantization y_int = rint(y / t) into two int8 digits and |eta|^2 = |y - t y_int|^2.
+  constexpr int kPairs = kHidden / 2;
+  const bool has_pair = tid < kPairs;
+  h2v yp = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
+  if (has_pair) yp = reinterpret_cast<const h2v*>(y_lds)[tid];
+  const float y0 = h2f(yp.x), y1 = h2f(yp.y);
+  float amax = group_max<64>(fmaxf(fabsf(y0), fabsf(y1)));
+  if (lane == 0) red[wave] = amax;
+  __syncthreads();
+  amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < kLmNW; ++i) amax = fmaxf(amax, red[i]);
+  __syncthreads();
+  const float t = amax > 0.f ? amax / static_cast<float>(kQ8YMax) : 1.0f;
+  const float tinv = amax > 0.f ? static_cast<float>(kQ8YMax) / amax : 0.f;
+  const float i0 = fminf(fmaxf(rintf(y0 * tinv), -kQ8YMax), kQ8YMax);
+  const float i1 = fminf(fmaxf(rintf(y1 * tinv), -kQ8YMax), kQ8YMax);
+  const float e0 = fmaf(-t, i0, y0), e1 = fmaf(-t, i1, y1);
+  if (has_pair) {
+    const int n0 = static_cast<int>(i0), n1 = static_cast<int>(i1);
+    const int h0 = (n0 + 64) >> 7, h1 = (n1 + 64) >> 7;  // floor division; lo digits in [-64, 63]
+    yhi[2 * tid] = static_cast<int8_t>(h0);
+    yhi[2 * tid + 1] = static_cast<int8_t>(h1);
+    ylo[2 * tid] = static_cast<int8_t>(n0 - 128 * h0);
+    ylo[2 * tid + 1] = static_cast<int8_t>(n1 - 128 * h1);
+  }
+  const float ysq = block_sum<kNT>(y0 * y0 + y1 * y1, red);
+  const float esq = block_sum<kNT>(e0 * e0 + e1 * e1, red);  // its barriers also publish the digits
+  // upper bounds: fp32 sums of <= 1280 non-negative terms are within 1280 * 2^-24 < 2^-10 relative
+  const double ny = static_cast<double>(sqrtf(ysq)) * (1.0 + 0x1p-9);
+  const double neta = static_cast<double>(sqrtf(esq)) * (1.0 + 0x1p-9);
+  const double nE_per_s = 127.0 * sqrt(static_cast<double>(kHidden)) * (1.0 + 0x1p-30);
+  uint4 dh[kQ8C], dl[kQ8C];
+#pragma unroll
+  for (int c = 0; c < kQ8C; ++c) {
+    dh[c] = reinterpret_cast<const uint4*>(yhi)[sub + kQ8Lpr * c];
+    dl[c] = reinterpret_cast<const uint4*>(ylo)[sub + kQ8Lpr * c];
+  }
+
+  float lb_max = -INFINITY;
+  auto score = [&](int k, const Batch& b) {
+    const int slot_row = wave * 4 + rsel;
+    const int row = base_of(k) + slot_row;
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int c = 0; c < kQ8C; ++c) {
+      ah = dot16_i8(b.w[c], dh[c], ah);
+      al = dot16_i8(b.w[c], dl[c], al);
+    }
+    ah = xor_add_i16(ah);
+    al = xor_add_i16(al);
+    const double a = static_cast<double>(b.m.x) * static_cast<double>(t) *
+                     static_cast<double>(128ll * ah + al);
+    const double nE = static_cast<double>(b.m.x) * nE_per_s + static_cast<double>(b.m.y);
+    const double r = (ny * static_cast<double>(b.m.y) + (neta + static_cast<double>(kQ8Gamma) * ny) * nE) *
+                     (1.0 + 0x1p-20);
+    const bool live = row < vocab && !b.sp;
+    const float ub = live ? __double2float_ru(a + r) : -INFINITY;
+    const float lb = live ? __double2float_rd(a - r) : -INFINITY;
+    lb_max = fmaxf(lb_max, lb);
+    if (sub == 0) ub_lds[k * kLmRowsIter + slot_row] = ub;
+  };
+  // 4 batches, two register buffers in turn
+  score(0, ba);
+  load(base_of(2), ba);
+  score(1, bb);
+  load(base_of(3), bb);
+  score(2, ba);
+  score(3, bb);
+
+  lb_max = group_max<64>(lb_max);
+  if (lane == 0) red[wave] = lb_max;
+  __syncthreads();  // also publishes ub_lds
+  float tb = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kLmNW; ++i) tb = fmaxf(tb, red[i]);
+  const float thr = q8_threshold(tb);
+  if (tid < kQ8RowsPerBlock) {
+    const int row = base_of(tid / kLmRowsIter) + tid % kLmRowsIter;
+    const float ub = ub_lds[tid];
+    if (row < vocab && ub != -INFINITY && !(ub < thr)) cand[atomicAdd(&ncand, 1)] = row;
+  }
+  __syncthreads();
+
+  // exact logits of the candidates: the lane split and order of lm_head_kernel
+  using RS = RowSplit<kHidden>;
+  const int sub32 = lane & 31, rsel32 = lane >> 5;
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(y_lds)[sub32 + 32 * c];
+  const int nc = ncand;
+  unsigned long long mine = 0;
+  for (int i0c = wave * 2; i0c < nc; i0c += kLmNW * 2) {
+    const int i = i0c + rsel32;
+    const int row = cand[i < nc ? i : i0c];
+    uint4 wr[RS::kC];
+#pragma unroll
+    for (int c = 0; c < RS::kC; ++c) wr[c] = ld_lm_head(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub32 + 32 * c);
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < RS::kC; ++c) acc = dot8(wr[c], xr[c], acc);
+    acc = group_sum<32>(acc);
+    const unsigned long long sc = pack_score(round_h(acc), row);
+    if (i < nc && sc > mine) mine = sc;
+  }
+  if (sub32 == 0) block_best[wave * 2 + rsel32] = mine;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long m = 0;
+#pragma unroll
+    for (int i = 0; i < kLmNW * 2; ++i) m = block_best[i] > m ? block_best[i] : m;
+    if (m) atomicMax(best, m);
+  }
+}
+
+int lm_head_q8_grid(int vocab) {
+  const int batches = (vocab + kLmRowsIter - 1) / kLmRowsIter;
+  return (batches + 3) / 4;
+}
+
+// ------------------------------------------------------------------------------------------
 // Split-K single-query attention (flash-decoding; reference decode_attention_split_kernel,
 // whisper_kernels.cu:102-189). Block (split, head) covers split_keys keys. A key row is 64 fp16 =
 // 8 lanes x 16 bytes, so one wave scores 8 keys per pass and a 256-thread block 32 keys. Scores,
@@ -965,6 +1222,42 @@ extern "C" int fw_lm_head_argmax_fused(const void* h, const void* x, const void*
   hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<unsigned long long*>(best),
                      fin);
   return fw_check_launch("lm_head_argmax_fused finalize");
+}
+
+extern "C" int fw_lm_head_q8_pack(const void* w, int vocab, int hidden, void* wq, float* meta, hipStream_t stream) {
+  FW_REQUIRE(w && wq && meta, "lm_head_q8_pack: null pointer");
+  FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
+  FW_REQUIRE(vocab > 0, "vocab must be positive");
+  FW_REQUIRE((reinterpret_cast<uintptr_t>(meta) & 7u) == 0, "lm_head_q8_pack: meta must be 8-byte aligned");
+  hipLaunchKernelGGL(lm_q8_pack_kernel, dim3((vocab + 3) / 4), dim3(256), 0, stream, static_cast<const _Float16*>(w),
+                     vocab, static_cast<int8_t*>(wq), reinterpret_cast<float2*>(meta));
+  return fw_check_launch("lm_head_q8_pack");
+}
+
+extern "C" int fw_lm_head_argmax_q8(const void* h, const void* x, const void* gamma, const void* beta, float eps,
+                                    const void* w, const void* wq, const float* meta, const uint8_t* suppress,
+                                    int vocab, int hidden, uint64_t* best, int64_t* tokens, int64_t* state,
+                                    int64_t* cur, int max_pos, hipStream_t stream) {
+  FW_REQUIRE(h && gamma && beta && w && wq && meta && suppress && best, "lm_head_argmax_q8: null pointer");
+  const bool finalize = tokens || state || cur;
+  FW_REQUIRE(!finalize || (tokens && state && cur), "lm_head_argmax_q8: tokens, state and cur must be given together");
+  FW_REQUIRE(hidden == kHidden, "hidden size must be %d", kHidden);
+  FW_REQUIRE(vocab > 0 && max_pos > 0, "vocab and max_pos must be positive");
+  FW_REQUIRE(aligned16(w) && aligned16(wq) && (reinterpret_cast<uintptr_t>(meta) & 7u) == 0,
+             "lm_head_argmax_q8: w and wq must be 16-byte aligned, meta 8-byte aligned");
+  LnArgs ln{static_cast<const _Float16*>(h), static_cast<const _Float16*>(x), nullptr,
+            static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta), eps, nullptr, nullptr,
+            nullptr, nullptr, 0, 0};
+  hipLaunchKernelGGL(lm_head_q8_kernel<true>, dim3(lm_head_q8_grid(vocab)), dim3(kLmNW * 64), 0, stream, nullptr, ln,
+                     static_cast<const _Float16*>(w), static_cast<const int8_t*>(wq),
+                     reinterpret_cast<const float2*>(meta), suppress, vocab,
+                     reinterpret_cast<unsigned long long*>(best));
+  int rc = fw_check_launch("lm_head_argmax_q8");
+  if (rc != FW_OK || !finalize) return rc;
+  FinArgs fin{tokens, state, cur, max_pos};
+  hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, stream, reinterpret_cast<unsigned long long*>(best),
+                     fin);
+  return fw_check_launch("lm_head_argmax_q8 finalize");
 }
 
 extern "C" int fw_argmax_finalize(uint64_t* best, int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,

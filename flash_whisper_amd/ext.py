@@ -282,6 +282,47 @@ class WhisperExt:
                    w.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN, best.data_ptr(), _ptr(tokens),
                    _ptr(state), _ptr(cur), int(max_pos), _stream())
 
+    def lm_head_q8_table(self, w):
+        """Allocates and fills the int8 table of w for lm_head_argmax_q8 (init time): (wq, meta)."""
+        wq = torch.empty(w.size(0), HIDDEN, dtype=torch.int8, device=w.device)
+        meta = torch.empty(w.size(0), 2, dtype=torch.float32, device=w.device)
+        self.lm_head_q8_pack(w, wq, meta)
+        return wq, meta
+
+    def lm_head_q8_pack(self, w, wq, meta):
+        """Fills wq int8 [vocab, 1280] and meta fp32 [vocab, 2] (scale, error bound) from w."""
+        check_half(w, 'w')
+        _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
+        vocab = w.size(0)
+        _check(wq, 'wq', torch.int8, 'int8')
+        _check(meta, 'meta', torch.float32, 'fp32')
+        _require(tuple(wq.shape) == (vocab, HIDDEN) and tuple(meta.shape) == (vocab, 2),
+                 'wq must be [vocab, 1280] and meta [vocab, 2]')
+        self._call('fw_lm_head_q8_pack', w.data_ptr(), vocab, HIDDEN, wq.data_ptr(), meta.data_ptr(), _stream())
+        return wq, meta
+
+    def lm_head_argmax_q8(self, h, x, gamma, beta, eps, w, wq, meta, suppress, best, tokens, state, cur, max_pos):
+        """lm_head_argmax_fused with the same result, bit for bit, from the int8 table (wq, meta) of w."""
+        for t, n in ((h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (w, 'w')):
+            check_half(t, n)
+        if x is not None:
+            check_half(x, 'x')
+        _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
+        _check(wq, 'wq', torch.int8, 'int8')
+        _check(meta, 'meta', torch.float32, 'fp32')
+        _require(tuple(wq.shape) == tuple(w.shape) and tuple(meta.shape) == (w.size(0), 2),
+                 'wq must match w and meta be [vocab, 2]')
+        _require(suppress.dtype == torch.bool and suppress.is_cuda and suppress.numel() == w.size(0),
+                 'suppress must be bool [vocab]')
+        fin = (tokens, state, cur)
+        _require(all(t is None for t in fin) or all(t is not None for t in fin),
+                 'tokens, state and cur must be given together')
+        for t in (best,) + tuple(t for t in fin if t is not None):
+            _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), 'tokens, state and cur must be int64')
+        self._call('fw_lm_head_argmax_q8', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), float(eps),
+                   w.data_ptr(), wq.data_ptr(), meta.data_ptr(), suppress.data_ptr(), w.size(0), HIDDEN,
+                   best.data_ptr(), _ptr(tokens), _ptr(state), _ptr(cur), int(max_pos), _stream())
+
     # ---- log-mel front end -------------------------------------------------------------
     def log_mel_workspace(self, n_samples, device='cuda'):
         return torch.empty(int(self.lib.fw_log_mel_ws_floats(int(n_samples))), dtype=torch.float32, device=device)

@@ -34,7 +34,7 @@ SELF_SPLIT, CROSS_SPLIT = 64, 256  # keys per split block of the decoder's self 
 class CustomModel:
     @torch.inference_mode()
     def __init__(self, model_id=SYNTHETIC, cache_dir=None, *, seed=0, dims=TURBO, setup=None, selftest=True,
-                 capture=True):
+                 capture=True, lm_q8=True):
         if not torch.cuda.is_available():
             raise RuntimeError('CustomModel requires a HIP device')
         self._weights, self.tokenizer, self.checkpoint = None, None, None
@@ -58,6 +58,7 @@ class CustomModel:
         self.max_new = self.max_pos - len(self.prompt)
         self.eos = set(self.setup.eos)
         self.record_events = False   # time every chunk replay with HIP events (bench.py)
+        self.use_lm_q8 = lm_q8       # LM head with the int8 pre-pass (same token as the fp16 head)
         self.chunk_events = []
 
         self._specs = W.spec_map(dims)
@@ -207,6 +208,8 @@ class CustomModel:
             self.lm_head = self._weights.get('proj_out.weight', (d.vocab, d.d_model)).cuda()
             if torch.equal(self.lm_head, self.embed):
                 self.lm_head = self.embed
+        # int8 copy of the LM head for the pre-pass LM-head kernel (same token, about half the bytes)
+        self.lm_q8, self.lm_meta = self.ext.lm_head_q8_table(self.lm_head)
         self.layers = []
         dm = d.d_model
         self.cross_w = torch.empty(d.dec_layers * 2 * dm, dm, dtype=half, device='cuda')
@@ -334,9 +337,7 @@ class CustomModel:
         if not lm_head:
             self.state[0].add_(1)
             return
-        g, be, eps = self.final_ln
-        ext.lm_head_argmax_fused(self.h[b], self.pending, g, be, eps, self.lm_head, self.suppress, self.best,
-                                 self.tokens, self.state, self.cur, self.max_pos)
+        self._lm_head(self.h[b], self.pending)
 
     def _prefill(self):
         """The whole prompt (custom/model.py:196-207) in one pass: each layer runs its 8 launches once
@@ -369,9 +370,18 @@ class CustomModel:
             ext.gemv(self.ffnb, *lay.fc2, pend, nv=n)
             a, b = b, a
         self.state[0].add_(n - 1)
+        self._lm_head(hb[b][n - 1], pend[n - 1])
+
+    def _lm_head(self, h, x):
+        """Final residual + LN + LM head + argmax + finalize (custom/model.py:121-123): the int8
+        pre-pass kernel (bit-identical token) unless ``use_lm_q8`` is off."""
         g, be, eps = self.final_ln
-        ext.lm_head_argmax_fused(hb[b][n - 1], pend[n - 1], g, be, eps, self.lm_head, self.suppress, self.best,
-                                 self.tokens, self.state, self.cur, self.max_pos)
+        if self.use_lm_q8:
+            self.ext.lm_head_argmax_q8(h, x, g, be, eps, self.lm_head, self.lm_q8, self.lm_meta, self.suppress,
+                                       self.best, self.tokens, self.state, self.cur, self.max_pos)
+        else:
+            self.ext.lm_head_argmax_fused(h, x, g, be, eps, self.lm_head, self.suppress, self.best, self.tokens,
+                                          self.state, self.cur, self.max_pos)
 
     def _step_reference(self):
         """The same step at the reference's op granularity (embed, add_layernorm, GEMV, split+combine

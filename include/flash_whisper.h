@@ -155,6 +155,23 @@ int fw_lm_head_argmax_fused(const void* h, const void* x, const void* gamma, con
                             const void* w, const uint8_t* suppress, int vocab, int hidden, uint64_t* best,
                             int64_t* tokens, int64_t* state, int64_t* cur, int max_pos, hipStream_t stream);
 
+/* int8 copy of an LM-head table for fw_lm_head_argmax_q8 (no reference counterpart; built once per
+ * weight load): per row v of w fp16[vocab, hidden], meta[2v] = s_v = max|w_v| / 127 (fp32),
+ * wq[v, :] = clamp(rint(w_v / s_v), -127, 127) (int8), meta[2v + 1] = an fp32 upper bound of
+ * || w_v - s_v wq[v, :] ||_2. wq int8[vocab, hidden], meta fp32[2 * vocab]. hidden == 1280. */
+int fw_lm_head_q8_pack(const void* w, int vocab, int hidden, void* wq, float* meta, hipStream_t stream);
+
+/* fw_lm_head_argmax_fused with the same arguments and the same result, bit for bit, reading the int8
+ * table (wq, meta from fw_lm_head_q8_pack of this w) instead of all of w. Replaces lm_head_argmax +
+ * argmax_finalize (whisper_kernels.cu:28-100, custom/model.py:121-123): each block scores its rows on
+ * the int8 table with an exact integer dot, bounds every fp32 logit from both sides, and evaluates only
+ * the rows that can tie or beat its best lower bound on w, with the arithmetic of fw_lm_head_argmax.
+ * w, wq 16-byte aligned, meta 8-byte aligned. */
+int fw_lm_head_argmax_q8(const void* h, const void* x, const void* gamma, const void* beta, float eps,
+                         const void* w, const void* wq, const float* meta, const uint8_t* suppress, int vocab,
+                         int hidden, uint64_t* best, int64_t* tokens, int64_t* state, int64_t* cur, int max_pos,
+                         hipStream_t stream);
+
 /* ---- log-mel front end (custom/model.py:93-98) ------------------------------------------- */
 
 /* wave fp32[n_samples] (n_samples = 480000; already zero padded) -> out fp32[128, n_frames]

@@ -1,0 +1,119 @@
+"""CPU check of the soundness argument behind the LM head's int8 pre-pass (lm_head_q8_kernel in
+flash_whisper_amd/csrc/decode.hip): with the kernel's quantization of the table and of y, its radius
+r_v and its threshold rule, the row that wins the fp16-logit argmax (lowest index on ties) is always a
+candidate. The fp32 logits are formed in two different summation orders (numpy's float32 matmul and a
+pairwise float32 sum), and the argmax is taken over the fp16-rounded logits as the oracle does
+(oracle.decoder.masked_argmax). Cases: random tables at several scales, planted ties, near-ties below
+an fp16 ulp, y = 0, and logits past the fp16 range."""
+
+import numpy as np
+
+from oracle.decoder import masked_argmax
+
+D = 1280
+GAMMA = 7.7e-5  # >= D * 2^-24 / (1 - D * 2^-24), as in the kernel
+YMAX = 127 * 128
+
+
+def pack_table(w):
+    """int8 rows, fp32 scales and fp32 error bounds, as lm_q8_pack_kernel builds them."""
+    w = np.asarray(w, np.float32)
+    amax = np.abs(w).max(1)
+    s = (amax / np.float32(127)).astype(np.float32)
+    inv = np.where(amax > 0, np.float32(127) / np.where(amax > 0, amax, 1), 0).astype(np.float32)
+    q = np.clip(np.rint(w * inv[:, None]), -127, 127)
+    err = np.sqrt(((w.astype(np.float64) - s[:, None].astype(np.float64) * q) ** 2).sum(1))
+    e = np.nextafter(err.astype(np.float32), np.float32(np.inf))  # rounded up
+    return q, s, e
+
+
+def threshold(t):
+    if not t > -65504.0:
+        return -np.inf
+    return min(t - (abs(t) * 2.0 ** -9 + 2.0 ** -23), 65504.0)
+
+
+def candidates(q, s, e, y, live, radius_scale=1.0):
+    y = np.asarray(y, np.float32)
+    amax = np.abs(y).max()
+    t = np.float32(amax / YMAX) if amax > 0 else np.float32(1)
+    tinv = np.float32(YMAX / amax) if amax > 0 else np.float32(0)
+    yi = np.clip(np.rint(y * tinv), -YMAX, YMAX)
+    eta = y.astype(np.float64) - np.float64(t) * yi
+    ny = np.sqrt((y.astype(np.float64) ** 2).sum()) * (1 + 2 ** -9)
+    neta = np.sqrt((eta ** 2).sum()) * (1 + 2 ** -9)
+    a = s.astype(np.float64) * np.float64(t) * (q @ yi)            # exact integer dot, then scaled
+    n_e = s.astype(np.float64) * 127 * np.sqrt(D) * (1 + 2 ** -30) + e
+    r = (ny * e + (neta + GAMMA * ny) * n_e) * (1 + 2 ** -20) * radius_scale
+    ub = np.where(live, a + r, -np.inf)
+    lb = np.where(live, a - r, -np.inf)
+    thr = threshold(lb.max())
+    return np.nonzero(live & ~(ub < thr))[0]
+
+
+def fp16_argmax_two_orders(w, y, sup):
+    w32, y32 = np.asarray(w, np.float32), np.asarray(y, np.float32)
+    x1 = w32 @ y32                                                   # BLAS order
+    x2 = (w32 * y32).reshape(len(w32), 32, 40).sum(2, dtype=np.float32).sum(1, dtype=np.float32)
+    with np.errstate(over='ignore'):
+        return [masked_argmax(np.float32(np.float16(x)), sup) for x in (x1, x2)]
+
+
+def check(w, y, sup):
+    q, s, e = pack_table(w)
+    cand = set(candidates(q, s, e, y, ~sup).tolist())
+    for win in fp16_argmax_two_orders(w, y, sup):
+        assert win in cand, (win, len(cand))
+    return len(cand)
+
+
+def test_random_tables_all_scales():
+    rng = np.random.default_rng(0)
+    counts = []
+    for trial in range(12):
+        v = 2000
+        w = np.float16(rng.standard_normal((v, D)) * 0.02 * (10.0 ** rng.uniform(-2, 1)))
+        y = np.float16(rng.standard_normal(D) * (10.0 ** rng.uniform(-1, 1.5)))
+        sup = rng.random(v) < 0.02
+        counts.append(check(w, y, sup))
+    assert max(counts) < 200  # the pre-pass does filter: a few rows of 2000, not all
+
+
+def test_ties_near_ties_and_degenerate_inputs():
+    rng = np.random.default_rng(1)
+    w = np.float16(0.02 * rng.standard_normal((1500, D)))
+    y = np.float16(rng.standard_normal(D))
+    w[[10, 700, 1499]] = np.float16(0.05 * np.sign(y.astype(np.float32)))   # exact ties
+    sup = np.zeros(1500, bool)
+    check(w, y, sup)
+    sup[10] = True
+    check(w, y, sup)
+    base = np.float16(0.03 * rng.standard_normal(D))                       # near-ties below one ulp
+    for k in range(200, 400):
+        r = base.copy()
+        idx = rng.choice(D, 3, replace=False)
+        r[idx] = np.nextafter(r[idx], np.float16(np.inf) if k % 2 else np.float16(-np.inf))
+        w[k] = r
+    check(w, np.float16(np.sign(base.astype(np.float32)) * np.abs(y.astype(np.float32))), np.zeros(1500, bool))
+    assert check(w, np.zeros(D, np.float16), np.zeros(1500, bool)) == 1500  # y = 0: all rows tie
+    big = np.full(D, 60000, np.float16)                                     # +-inf logits
+    check(w, big, np.zeros(1500, bool))
+    check(np.float16(np.full((300, D), -0.01)), big, np.zeros(300, bool))
+
+
+def test_planted_mistake_is_caught():
+    """Without the radius (ranking by the int8 estimate A_v alone) the winner escapes among near-tied
+    rows, so the checks above would catch a radius that is too small."""
+    rng = np.random.default_rng(2)
+    sup = np.zeros(3000, bool)
+    missed = 0
+    for trial in range(10):
+        w = np.float16(0.02 * rng.standard_normal((3000, D)))
+        y = np.float16(rng.standard_normal(D))
+        best = w[np.argmax(w.astype(np.float32) @ y.astype(np.float32))].astype(np.float64)
+        w[:64] = np.float16(best + 1e-4 * rng.standard_normal((64, D)))  # 64 rows within a few fp16 ulps
+        q, s, e = pack_table(w)
+        win = fp16_argmax_two_orders(w, y, sup)[0]
+        assert win in set(candidates(q, s, e, y, ~sup).tolist())
+        missed += win not in set(candidates(q, s, e, y, ~sup, radius_scale=0.0).tolist())
+    assert missed > 0
