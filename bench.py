@@ -166,7 +166,7 @@ def main():
     ap.add_argument('--kernel-reps', type=int, default=60)
     ap.add_argument('--cpu-seconds', type=float, default=12.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--lanes', type=int, default=2, help='clips in flight for the serving-throughput extra (0: skip)')
+    ap.add_argument('--lanes', type=int, default=4, help='clips in flight for the serving-throughput extra (0: skip)')
     ap.add_argument('--fp16-lm-head', action='store_true',
                     help='decode with the fp16 LM-head kernel instead of the int8 pre-pass one (same tokens)')
     ap.add_argument('--copy-calibration', action='store_true',

@@ -893,10 +893,10 @@ __device__ __forceinline__ int attn_pos(const AttnArgs& a) {
 // queries straight from k_new / v_new: their cache rows are written by other blocks of the same
 // launch, so a cache row at or past the batch's first position is never trusted. The single-query
 // instantiation carries none of this code.
-template <int MAXP, bool BATCH>
-__global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
-  __shared__ float wm[4], wl[4];
-  __shared__ float wacc[4][kHeadDim];
+template <int MAXP, bool BATCH, int NW = 4>
+__global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnArgs a) {
+  __shared__ float wm[NW], wl[NW];
+  __shared__ float wacc[NW][kHeadDim];
   const int split = blockIdx.x, head = blockIdx.y, nsplit = gridDim.x, qv = BATCH ? blockIdx.z : 0;
   const int slot = (qv * gridDim.y + head) * nsplit + split;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1004,10 +1004,10 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   if (tid < kHeadDim) {
     float m = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) m = fmaxf(m, wm[w]);
+    for (int w = 0; w < NW; ++w) m = fmaxf(m, wm[w]);
     float l = 0.f, o = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       if (wl[w] > 0.f) {
         const float wgt = __expf(wm[w] - m);
         l = fmaf(wl[w], wgt, l);
@@ -1022,22 +1022,28 @@ __global__ void __launch_bounds__(256) attn_split_kernel(AttnArgs a) {
   }
 }
 
+// Splits of up to 256 keys (the cross attention): FW_ATTN256_P passes of 8 keys per wave, 32 / P
+// waves. 4 waves of 64 keys measured 0.9 us faster per decoder step than 8 waves of 32 on MI355X.
+#ifndef FW_ATTN256_P
+#define FW_ATTN256_P 8
+#endif
 int launch_attn_split(const AttnArgs& a, int nsplit, int heads, hipStream_t s, int nq = 1) {
   const dim3 grid(nsplit, heads, nq);
+  constexpr int kP256 = FW_ATTN256_P, kW256 = 32 / FW_ATTN256_P;
   if (nq == 1) {
     if (a.split_keys <= 64)
       hipLaunchKernelGGL((attn_split_kernel<2, false>), grid, dim3(256), 0, s, a);
     else if (a.split_keys <= 128)
       hipLaunchKernelGGL((attn_split_kernel<4, false>), grid, dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL((attn_split_kernel<8, false>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((attn_split_kernel<kP256, false, kW256>), grid, dim3(kW256 * 64), 0, s, a);
   } else {
     if (a.split_keys <= 64)
       hipLaunchKernelGGL((attn_split_kernel<2, true>), grid, dim3(256), 0, s, a);
     else if (a.split_keys <= 128)
       hipLaunchKernelGGL((attn_split_kernel<4, true>), grid, dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL((attn_split_kernel<8, true>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((attn_split_kernel<kP256, true, kW256>), grid, dim3(kW256 * 64), 0, s, a);
   }
   return fw_check_launch("attention split");
 }
