@@ -522,15 +522,18 @@ class CustomModel:
         torch.cuda.synchronize()
         start = time.perf_counter()
 
+        # The stages are enqueued back to back and timed with HIP events: the reference synchronises
+        # the host after the front end and after the encoder to read its stage times
+        # (custom/model.py:182-190), which leaves the GPU idle for a host round trip before each next
+        # stage. mel_s counts from the host start to the end of the log-mel on the GPU timeline.
+        stage = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        stage[0].record()
+        enqueue_s = time.perf_counter() - start
         self._enqueue_mel(audio)
-        torch.cuda.synchronize()
-        mel_s = time.perf_counter() - start
-
+        stage[1].record()
         self._enqueue_encoder()
-        torch.cuda.synchronize()
-        encoder_s = time.perf_counter() - start - mel_s
+        stage[2].record()
 
-        decode_start = time.perf_counter()
         # The reference replays a chunk, then reads its tokens before replaying the next
         # (custom/model.py:208-215). Here the next chunk is already queued while the host reads the
         # previous one (an asynchronous copy of its token slice into pinned memory, then an event), so
@@ -541,6 +544,8 @@ class CustomModel:
         self._publish(0, 1).synchronize()
         token_ids = [int(host[0])]
         ttft = time.perf_counter() - start
+        mel_s = enqueue_s + stage[0].elapsed_time(stage[1]) * 1e-3
+        encoder_s = stage[1].elapsed_time(stage[2]) * 1e-3
         self.chunk_events = []
         n_chunks = -(-(max_new - 1) // CHUNK)
         done = stop_at_eos and token_ids[0] in self.eos
@@ -557,7 +562,7 @@ class CustomModel:
                 if (stop_at_eos and token in self.eos) or len(token_ids) >= max_new:
                     break
         ttlt = time.perf_counter() - start
-        decode_s = time.perf_counter() - decode_start
+        decode_s = ttlt - mel_s - encoder_s  # from the end of the encoder on the GPU timeline
         detok_start = time.perf_counter()
         text = C.detokenize(self.tokenizer, token_ids)
         return {

@@ -164,3 +164,7 @@ def test_short_clip_and_timing_dict(model, clip):
                 'n_tokens'):
         assert key in res
     assert 0 < res['ttft_s'] <= res['ttlt_s'] <= res['e2e_s']
+    # stage times on the GPU timeline: front end, encoder, then the decode up to the last token
+    assert 0 < res['mel_s'] and 0 < res['encoder_s'] and 0 < res['decode_s']
+    assert res['mel_s'] + res['encoder_s'] < res['ttft_s']
+    assert abs(res['mel_s'] + res['encoder_s'] + res['decode_s'] - res['ttlt_s']) < 1e-6
