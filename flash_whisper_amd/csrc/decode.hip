@@ -118,6 +118,95 @@ __device__ __forceinline__ void ln_finish(const LnRegs<NT>& in, bool has_b, _Flo
   }
 }
 
+// ln_finish for NV vectors at once: the vectors' sums share each reduction round (two barriers in all
+// instead of four per vector). Every value is reduced in the order block_sum uses (the wave butterfly,
+// then the wave partials in wave order), so each vector's result is that of ln_finish on it alone.
+// red holds 2 * NV * (NT / 64) floats.
+template <int NT, int NV>
+__device__ __forceinline__ void ln_finish_multi(const LnRegs<NT> (&in)[NV], bool has_b, _Float16* r_out, float eps,
+                                                _Float16* y_out, float* red) {
+  constexpr int kPer = LnRegs<NT>::kPer, kWaves = NT / kWave;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  float2 r[NV][kPer];
+  float part[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    h2v* r2 = r_out ? reinterpret_cast<h2v*>(r_out + v * kHidden) : nullptr;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      r[v][i] = make_float2(0.f, 0.f);
+      if (idx < LnRegs<NT>::kPairs) {
+        float rx = h2f(in[v].a[i].x), ry = h2f(in[v].a[i].y);
+        if (has_b) {
+          rx = round_h(rx + h2f(in[v].b[i].x));
+          ry = round_h(ry + h2f(in[v].b[i].y));
+        }
+        r[v][i] = make_float2(rx, ry);
+        sum += rx + ry;
+        if (r2 && blockIdx.x == 0) {
+          h2v o;
+          o.x = f2h(rx);
+          o.y = f2h(ry);
+          r2[idx] = o;
+        }
+      }
+    }
+    part[v] = group_sum<kWave>(sum);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) red[v * kWaves + wave] = part[v];
+  }
+  __syncthreads();
+  float mean[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += red[v * kWaves + w];
+    mean[v] = s * (1.0f / kHidden);
+  }
+  float* red2 = red + NV * kWaves;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < LnRegs<NT>::kPairs) {
+        const float dx = r[v][i].x - mean[v], dy = r[v][i].y - mean[v];
+        sq += dx * dx + dy * dy;
+      }
+    }
+    part[v] = group_sum<kWave>(sq);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) red2[v * kWaves + wave] = part[v];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += red2[v * kWaves + w];
+    const float inv = rsqrtf(s * (1.0f / kHidden) + eps);
+    h2v* y2 = reinterpret_cast<h2v*>(y_out + v * kHidden);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      if (idx < LnRegs<NT>::kPairs) {
+        h2v o;
+        o.x = f2h((r[v][i].x - mean[v]) * inv * h2f(in[v].g[i].x) + h2f(in[v].be[i].x));
+        o.y = f2h((r[v][i].y - mean[v]) * inv * h2f(in[v].g[i].y) + h2f(in[v].be[i].y));
+        y2[idx] = o;
+      }
+    }
+  }
+}
+
 template <int NT>
 __device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b, _Float16* r_out,
                                             const _Float16* gamma, const _Float16* beta, float eps,
@@ -307,7 +396,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   using RS = RowSplit<K>;
   constexpr int kRowsPerBlock = NW * RS::kRPW * U;
   __shared__ __align__(16) _Float16 y_lds[MODE != kModePlain ? NV * K : 8];
-  __shared__ float red[NW];
+  __shared__ float red[MODE == kModeLn && NV > 1 ? 2 * NV * NW : NW];
   __shared__ float wgt[MODE == kModeCombine ? kMaxCombineHeads * kMaxCombineSplits : 1];
   __shared__ float inv_den[MODE == kModeCombine ? kMaxCombineHeads : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -315,7 +404,8 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   // Order of requests: the prologue's inputs (small, on the critical path), then this block's weight
   // rows, which do not depend on the input vector and stay in flight while the prologue computes.
   LnRegs<NW * 64> lnr[MODE == kModeLn ? NV : 1];
-  CombineRegs<MODE == kModeCombine ? NW * 64 : 64> cbr;  // one vector at a time
+  // one vector at a time; a batch keeps the next vector's partials in flight while one is merged
+  CombineRegs<MODE == kModeCombine ? NW * 64 : 64> cbr[MODE == kModeCombine && NV > 1 ? 2 : 1];
   if constexpr (MODE == kModeLn) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
@@ -325,7 +415,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
       ln_load<NW * 64>(a, b, ln.gamma, ln.beta, lnr[v]);
     }
   } else if constexpr (MODE == kModeCombine) {
-    combine_load<NW * 64>(NV > 1 ? cb.vec(0) : cb, cbr);
+    combine_load<NW * 64>(NV > 1 ? cb.vec(0) : cb, cbr[0]);
   }
   const int row0 = blockIdx.x * kRowsPerBlock + wave * RS::kRPW * U + rsel;
   // Rows past n load row n - 1 (their results are never stored): no load sits under a lane mask,
@@ -344,17 +434,17 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   }
   const uint4* xv;
   if constexpr (MODE == kModeLn) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v)
-      ln_finish<NW * 64>(lnr[v], ln.cur != nullptr || ln.x != nullptr, ln.h_out ? ln.h_out + v * kHidden : nullptr,
-                         ln.eps, y_lds + v * K, red);
+    if constexpr (NV == 1)
+      ln_finish<NW * 64>(lnr[0], ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
+    else
+      ln_finish_multi<NW * 64, NV>(lnr, ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
     __syncthreads();
     xv = reinterpret_cast<const uint4*>(y_lds);
   } else if constexpr (MODE == kModeCombine) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      if (v > 0) combine_load<NW * 64>(cb.vec(v), cbr);
-      combine_finish<NW * 64>(NV > 1 ? cb.vec(v) : cb, cbr, y_lds + v * K, wgt, inv_den);
+      if (v + 1 < NV) combine_load<NW * 64>(cb.vec(v + 1), cbr[(v + 1) & 1]);
+      combine_finish<NW * 64>(NV > 1 ? cb.vec(v) : cb, cbr[v & 1], y_lds + v * K, wgt, inv_den);
       __syncthreads();  // y visible; wgt / inv_den free for the next vector
     }
     xv = reinterpret_cast<const uint4*>(y_lds);
