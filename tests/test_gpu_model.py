@@ -168,3 +168,22 @@ def test_short_clip_and_timing_dict(model, clip):
     assert 0 < res['mel_s'] and 0 < res['encoder_s'] and 0 < res['decode_s']
     assert res['mel_s'] + res['encoder_s'] < res['ttft_s']
     assert abs(res['mel_s'] + res['encoder_s'] + res['decode_s'] - res['ttlt_s']) < 1e-6
+
+
+def test_eos_stop_and_token_cap(model, clip):
+    """custom/model.py:208-215: the token list ends with the first EOS (included), a first token that is
+    EOS ends decoding at once, and without an EOS the list stops at max_pos - len(prompt) tokens."""
+    ref = model.transcribe(clip, max_new_tokens=40, stop_at_eos=False)['token_ids']
+    saved = model.eos
+    try:
+        for k in (0, 7, 8, 9, 23):  # first token, inside a chunk, at and after chunk boundaries
+            eos = ref[k]
+            model.eos = {eos}
+            ids = model.transcribe(clip)['token_ids']
+            assert ids == ref[:ref.index(eos) + 1], k
+        model.eos = {-1}  # never produced
+        ids = model.transcribe(clip)['token_ids']
+        assert len(ids) == model.max_new == model.max_pos - len(model.prompt)
+        assert ids[:40] == ref
+    finally:
+        model.eos = saved

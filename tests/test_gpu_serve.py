@@ -20,10 +20,21 @@ def test_lanes_match_sequential_transcribe(model, lanes, stop_at_eos):
 
     clips = [synthetic_clip(s) for s in (0, 1, 2, 3)]
     clips[3] = clips[3][:5 * 16000]  # a short clip too
-    ref = [model.transcribe(c, max_new_tokens=30, stop_at_eos=stop_at_eos)['token_ids'] for c in clips]
-    sched = Scheduler(model, lanes=lanes)
-    out = sched.transcribe_many(clips, max_new_tokens=30, stop_at_eos=stop_at_eos)
-    assert [r['token_ids'] for r in out] == ref
-    assert all(r['wall_s'] >= r['e2e_s'] > 0 for r in out)
-    # the lanes stay usable one at a time
-    assert sched.lanes[-1].transcribe(clips[0], max_new_tokens=30, stop_at_eos=stop_at_eos)['token_ids'] == ref[0]
+    saved = set(model.eos)
+    try:
+        if stop_at_eos:  # an EOS that the first clip produces at its 13th token, so that clip stops early
+            first = model.transcribe(clips[0], max_new_tokens=30, stop_at_eos=False)['token_ids']
+            model.eos.clear()
+            model.eos.add(first[12])  # in place: the lanes share this set
+        ref = [model.transcribe(c, max_new_tokens=30, stop_at_eos=stop_at_eos)['token_ids'] for c in clips]
+        if stop_at_eos:
+            assert len(ref[0]) <= 13 and ref[0][-1] in model.eos
+        sched = Scheduler(model, lanes=lanes)
+        out = sched.transcribe_many(clips, max_new_tokens=30, stop_at_eos=stop_at_eos)
+        assert [r['token_ids'] for r in out] == ref
+        assert all(r['wall_s'] >= r['e2e_s'] > 0 for r in out)
+        # the lanes stay usable one at a time
+        assert sched.lanes[-1].transcribe(clips[0], max_new_tokens=30, stop_at_eos=stop_at_eos)['token_ids'] == ref[0]
+    finally:
+        model.eos.clear()
+        model.eos.update(saved)
