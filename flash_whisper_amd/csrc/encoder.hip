@@ -270,18 +270,25 @@ __device__ __forceinline__ void mma_frags(const Frags<kTM, kTN>& f, f16v (&acc)[
 #ifndef FW_ST256
 #define FW_ST256 3
 #endif
+#ifndef FW_ST192
+#define FW_ST192 3
+#endif
 #ifndef FW_MIN_TILES256
 #define FW_MIN_TILES256 128
 #endif
 template <int BM>
-constexpr int dma_stages() { return BM == 256 ? FW_ST256 : BM == 128 ? FW_ST128 : FW_ST64; }
-// Waves per block: a 2-wide column of waves (64 output columns each) and BM / 64 rows of waves, at
-// least 2; each wave owns a (BM / rows) x 64 tile.
+constexpr int dma_stages() {
+  return BM == 256 ? FW_ST256 : BM == 192 ? FW_ST192 : BM == 128 ? FW_ST128 : FW_ST64;
+}
+// Waves per block, in gemm_wave_cols columns (kBN / cols output columns each) and waves / cols rows;
+// each wave owns a (BM / rows) x (kBN / cols) tile. 192-row tiles use 2 x 4 waves of 96 x 32.
 #ifndef FW_W256
 #define FW_W256 8
 #endif
 template <int BM>
-constexpr int gemm_waves() { return BM == 256 ? FW_W256 : 4; }
+constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 ? 8 : 4; }
+template <int BM>
+constexpr int gemm_wave_cols() { return BM == 192 ? 4 : 2; }
 
 template <int BM>
 __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
@@ -335,8 +342,9 @@ __device__ __forceinline__ void store_vt(const GemmArgs& g, const f16v (&acc)[kT
 
 template <int BM, int EPI>
 __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArgs g) {
-  constexpr int kDmaStages = dma_stages<BM>(), kNW = gemm_waves<BM>();
-  constexpr int kWM = BM / (kNW / 2), kTM = kWM / 32, kTN = 2;
+  constexpr int kDmaStages = dma_stages<BM>(), kNW = gemm_waves<BM>(), kNWN = gemm_wave_cols<BM>();
+  constexpr int kWM = BM / (kNW / kNWN), kTM = kWM / 32, kTN = kBN / kNWN / 32;
+  static_assert(kWM % 32 == 0 && kTN >= 1 && BM % (8 * kNW) == 0, "wave tiling");
   constexpr int kStageBytes = (BM + kBN) * 128;
   constexpr int kPerStage = (BM / 8 / kNW) + (kBN / 8 / kNW);  // copies per thread per stage
   // Transposed accumulators (8-byte epilogue accesses) pay off on the 64-row tiles of the 1280-column
@@ -347,7 +355,7 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
   int m0, n0;
   tile_origin<BM>(g, m0, n0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave >> 1) * kWM, wn = (wave & 1) * 64;
+  const int wm = (wave / kNWN) * kWM, wn = (wave % kNWN) * (kBN / kNWN);
   const int lr = lane & 31, lg = lane >> 5;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
 
@@ -579,13 +587,21 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
   return fw_check_launch("gemm");
 }
 
-// Fewer 128-row tiles than CUs leaves the chip idle: use 64-row tiles then.
 // 256-row tiles (8 waves, 48 KB stages) when they still cover half the CUs: they do twice the MFMA
-// work per byte staged of 128-row tiles. Fewer 128-row tiles than CUs leaves the chip idle: use
-// 64-row tiles then. The implicit-GEMM conv stays on the register-staged kernel (<= 128 rows).
+// work per byte staged of 128-row tiles. When 256-row tiles would leave a quarter of the CUs idle and
+// 192-row tiles still fit in one pass (q/k/v: 180 -> 240 tiles), 192-row tiles: each SIMD then does
+// 3/4 of the MFMA work and each CU stages 5/6 of the bytes (4.90 -> 4.78 ms per encoder on MI355X).
+// Fewer 128-row tiles than CUs leaves the chip idle: use 64-row tiles then. The implicit-GEMM conv
+// stays on the register-staged kernel (<= 128 rows).
+#ifndef FW_USE192
+#define FW_USE192 1
+#endif
 int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
   const int tiles256 = (g.n / kBN) * ((g.m + 255) / 256);
+  const int tiles192 = (g.n / kBN) * ((g.m + 191) / 192);
   const int tiles128 = (g.n / kBN) * ((g.m + 127) / 128);
+  if (FW_USE192 && !g.conv_stride && tiles256 < 192 && tiles256 >= FW_MIN_TILES256 && tiles192 <= 256)
+    return launch_gemm_bm<192>(g, epi, s);
   if (!g.conv_stride && tiles256 >= FW_MIN_TILES256) return launch_gemm_bm<256>(g, epi, s);
   if (tiles128 < 256) return launch_gemm_bm<64>(g, epi, s);
   return launch_gemm_bm<128>(g, epi, s);

@@ -43,11 +43,12 @@ def _gemm_ref(a, w, b, epi, res=None, q_cols=0):
     return v, scale
 
 
-# shapes cover the 256-, 128- and 64-row tile paths, a single k stage and partial last tiles
+# shapes cover the 256-, 192-, 128- and 64-row tile paths, a single k stage and partial last tiles
+# (192-row tiles: 1500 x 3840 and 1200 x 4096)
 @pytest.mark.parametrize('m,n,k,epi', [(1500, 3840, 1280, 5), (1500, 1280, 1280, 2), (1500, 5120, 1280, 1),
                                        (1500, 1280, 5120, 3), (1500, 1280, 1280, 0), (77, 128, 64, 0),
                                        (1500, 1280, 1280, 4), (300, 8192, 64, 0), (513, 16384, 192, 1),
-                                       (1100, 2560, 128, 0)])
+                                       (1100, 2560, 128, 0), (1200, 4096, 128, 1)])
 def test_gemm_epilogues(ext, hip_device, m, n, k, epi):
     dev = hip_device
     rng = np.random.default_rng(m + n + k + epi)
