@@ -9,9 +9,9 @@ namespace fw {
 namespace {
 
 // ------------------------------------------------------------------------------------------
-// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 64 with BM in {256, 128, 64};
-// waves in a (BM / 64 or 2) x 2 arrangement, each wave a (64 or 32) x 64 tile of
-// v_mfma_f32_32x32x16_f16 products.
+// GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 64 with BM in
+// {256, 192, 128, 64}; waves in a (BM / 64 or 2) x 2 arrangement, each wave a (64 or 32) x 64 tile of
+// v_mfma_f32_32x32x16_f16 products (192-row tiles: 2 x 4 waves of 96 x 32).
 //  - LDS: one [rows][64] fp16 tile per operand and stage, 8 x 16-byte chunks per row, chunk c of
 //    row r stored in slot swz_slot(r, c) = c ^ ((r >> 1) & 7), so the 16 rows a 16-lane group reads
 //    for one MFMA operand cover all 64 banks (conflict-free ds_read_b128).
@@ -19,8 +19,10 @@ namespace {
 //    residual, fp16 clamp, the q scale, the cross K/V scatter and the transposed-V store.
 //  - Plain GEMMs (gemm_dma_kernel): global -> LDS copies into a ring of stages, operand fragments
 //    double-buffered in registers (see the pipeline notes above that kernel).
-//  - Implicit-GEMM conv (gemm_kernel): the A tile is gathered from the time-major input through
-//    registers (two staging sets, two LDS buffers), since its rows are shifted time windows.
+//  - Implicit-GEMM conv: a 64-wide k stage of A row m is 64 contiguous channels of input row
+//    m * stride + tap - 1, so long-k convs use the same direct-to-LDS pipeline (padding rows copy
+//    from a zero row); short-k convs gather the A tile through registers (gemm_kernel: two staging
+//    sets, two LDS buffers).
 //  - Tile order: hardware deals blocks round-robin over the 8 XCDs; the block id is remapped so each
 //    XCD works on its own part of the tile grid and its L2 sees only that part's operand panels.
 // MFMA 32x32x16 f16 operand layout (lane l, g = l / 32):
@@ -290,20 +292,33 @@ constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 ? 8 : 4; }
 template <int BM>
 constexpr int gemm_wave_cols() { return BM == 192 ? 4 : 2; }
 
-template <int BM>
+// Source of the implicit conv's zero padding rows: a k stage of one A row is 64 halves.
+__device__ __align__(16) _Float16 g_zero_row[kBK];
+
+// CONV: implicit conv1d (k = 3, pad 1). A 64-wide k stage lies inside one tap (c_in % 64 == 0), so A
+// row m of the stage is 64 contiguous channels of input row m * stride + tap - 1, or zeros outside
+// [0, t_in).
+template <int BM, bool CONV = false>
 __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int k0, int wave, int lane,
                                           uint32_t lds_stage) {
   constexpr int kAInstr = BM / 8 / gemm_waves<BM>();  // wave instructions per A tile (8 rows each), per wave
   constexpr int kBInstr = kBN / 8 / gemm_waves<BM>();
   const int rsub = lane >> 3, slot = lane & 7;
+  const int tap = CONV ? k0 / g.c_in : 0, ch0 = CONV ? k0 - tap * g.c_in : 0;
 #pragma unroll
   for (int i = 0; i < kAInstr; ++i) {
     const int blk = wave * kAInstr + i;  // 8-row block of the tile
     const int row = blk * 8 + rsub;
     const int gm = min(m0 + row, g.m - 1);  // rows past m are computed and never stored
     const int chunk = swz_slot(row, slot);
-    dma16(g.a + static_cast<size_t>(gm) * g.lda + k0 + chunk * 8,
-          __builtin_amdgcn_readfirstlane(lds_stage + blk * 1024));
+    const _Float16* src;
+    if constexpr (CONV) {
+      const int r = gm * g.conv_stride + tap - 1;
+      src = (r >= 0 && r < g.t_in) ? g.a + static_cast<size_t>(r) * g.c_in + ch0 + chunk * 8 : g_zero_row + chunk * 8;
+    } else {
+      src = g.a + static_cast<size_t>(gm) * g.lda + k0 + chunk * 8;
+    }
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_stage + blk * 1024));
   }
 #pragma unroll
   for (int i = 0; i < kBInstr; ++i) {
@@ -340,7 +355,7 @@ __device__ __forceinline__ void store_vt(const GemmArgs& g, const f16v (&acc)[kT
   }
 }
 
-template <int BM, int EPI>
+template <int BM, int EPI, bool CONV = false>
 __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArgs g) {
   constexpr int kDmaStages = dma_stages<BM>(), kNW = gemm_waves<BM>(), kNWN = gemm_wave_cols<BM>();
   constexpr int kWM = BM / (kNW / kNWN), kTM = kWM / 32, kTN = kBN / kNWN / 32;
@@ -370,7 +385,7 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
   const int kt_n = g.k / kBK;
 #pragma unroll
   for (int s = 0; s < kDmaStages; ++s)
-    if (s < kt_n) dma_stage<BM>(g, m0, n0, s * kBK, wave, lane, lds0 + s * kStageBytes);
+    if (s < kt_n) dma_stage<BM, CONV>(g, m0, n0, s * kBK, wave, lane, lds0 + s * kStageBytes);
   auto slot = [&](int kt) { return lds + (kt % kDmaStages) * (kStageBytes / 16); };
   Frags<kTM, kTN> fa, fb;
   // this thread's copies of stage kt have landed once at most the later issued stages remain
@@ -382,7 +397,7 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
     wait_stages_ahead<kPerStage, kDmaStages - 1>(min(kDmaStages - 2, kt_n - 2 - kt));
     lds_barrier();  // own fragment reads of stage kt done; stage kt + 1 visible; slot kt free
     if (kt + kDmaStages < kt_n)
-      dma_stage<BM>(g, m0, n0, (kt + kDmaStages) * kBK, wave, lane, lds0 + (kt % kDmaStages) * kStageBytes);
+      dma_stage<BM, CONV>(g, m0, n0, (kt + kDmaStages) * kBK, wave, lane, lds0 + (kt % kDmaStages) * kStageBytes);
     load_frags<kTM, kTN>(slot(kt + 1), slot(kt + 1) + BM * 8, wm, wn, lr, lg, nxt);
     mma_frags<kTM, kTN, kT>(cur, acc);
   };
@@ -552,6 +567,24 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
   const int tiles = (g.n / kBN) * ((g.m + BM - 1) / BM);
   const dim3 grid(tiles);
   choose_xcd_groups(g, BM);
+  // Implicit convs with a long k (the stride-2 1280 -> 1280 stem conv, k = 3840) use the direct-to-LDS
+  // pipeline (75 -> 37 us); with a short k (the 128 -> 1280 conv, k = 384: six stages) the ring's
+  // fill and drain dominate and the register-staged kernel, whose small LDS footprint keeps two
+  // blocks per CU, is faster (15 us against 18-19 us).
+  if (g.conv_stride && g.k >= 1024) {
+    switch (epi) {
+#define FW_CONV_CASE(E) \
+  case E:               \
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, E, true>), grid, dim3(gemm_waves<BM>() * 64), 0, s, g); break;
+      FW_CONV_CASE(FW_EPI_BIAS)
+      FW_CONV_CASE(FW_EPI_BIAS_GELU)
+      FW_CONV_CASE(FW_EPI_BIAS_GELU_POS)
+#undef FW_CONV_CASE
+      default:
+        return fw_fail(FW_EINVAL, "conv1d: unsupported epilogue %d", epi);
+    }
+    return fw_check_launch("conv1d");
+  }
   if constexpr (BM <= 128) {
   if (g.conv_stride) {
     switch (epi) {
