@@ -331,27 +331,42 @@ __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int
 }
 
 // v columns of the q/k/v projection -> vt[head * 64 + d][vt_pos(t)]; rows in [m, vt_pad) get zeros so
-// the padding keys of the last attention tile hold finite values.
-template <int kTM, int kTN>
-__device__ __forceinline__ void store_vt(const GemmArgs& g, const f16v (&acc)[kTM][kTN], int row_base,
-                                         int col_base, int lr, int lg) {
+// the padding keys of the last attention tile hold finite values. The tile is transposed through LDS
+// (the operand ring is free once every wave has left the main loop): each lane puts its 4-row runs
+// into a [128 columns][BM] staging tile, already in vt_pos order (tiles start at multiples of 64 and
+// vt_pos permutes within 16-key groups), and the block then writes each column's BM keys as whole
+// 16-byte chunks instead of one 8-byte store per 4 keys and column.
+template <int BM, int kTM, int kTN>
+__device__ __forceinline__ void store_vt(const GemmArgs& g, const f16v (&acc)[kTM][kTN], int m0, int n0, int wm,
+                                         int wn, int lr, int lg, u32x4* lds) {
+  constexpr int kStride = BM + 8;  // halves per staged column (16-byte aligned rows)
+  static_assert(kBN * kStride * 2 <= dma_stages<BM>() * (BM + kBN) * 128, "staging tile must fit the ring");
+  _Float16* t = reinterpret_cast<_Float16*>(lds);
+  __syncthreads();  // every wave has read its last operand fragments from the ring
 #pragma unroll
   for (int j = 0; j < kTN; ++j) {
-    const int col = col_base + 32 * j + lr;
-    const float b = g.bias ? h2f(g.bias[col]) : 0.f;
-    _Float16* dst = g.vt + static_cast<size_t>(col - 2 * g.q_cols) * g.vt_pad;
+    const int cl = wn + 32 * j + lr;
+    const float b = g.bias ? h2f(g.bias[n0 + cl]) : 0.f;
 #pragma unroll
     for (int i = 0; i < kTM; ++i)
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq) {
-        const int row0 = row_base + 32 * i + 8 * rq + 4 * lg;  // rows row0 .. row0 + 3 stay adjacent
-        if (row0 < g.vt_pad) {
-          h4v v;
+        const int rl = wm + 32 * i + 8 * rq + 4 * lg;  // rows rl .. rl + 3 stay adjacent under vt_pos
+        h4v v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = row0 + e < g.m ? f2h(acc[i][j][4 * rq + e] + b) : static_cast<_Float16>(0.f);
-          *reinterpret_cast<h4v*>(dst + vt_pos(row0)) = v;
-        }
+        for (int e = 0; e < 4; ++e) v[e] = m0 + rl + e < g.m ? f2h(acc[i][j][4 * rq + e] + b) : static_cast<_Float16>(0.f);
+        *reinterpret_cast<h4v*>(t + cl * kStride + vt_pos(rl)) = v;
       }
+  }
+  __syncthreads();
+  constexpr int kChunks = BM / 8;  // 16-byte chunks per staged column
+  _Float16* dst = g.vt + static_cast<size_t>(n0 - 2 * g.q_cols) * g.vt_pad;
+  for (int c = threadIdx.x; c < kBN * kChunks; c += blockDim.x) {
+    const int cl = c / kChunks, ch = c - cl * kChunks;
+    const int pos = m0 + ch * 8;
+    if (pos < g.vt_pad)
+      *reinterpret_cast<u32x4*>(dst + static_cast<size_t>(cl) * g.vt_pad + pos) =
+          *reinterpret_cast<const u32x4*>(t + cl * kStride + ch * 8);
   }
 }
 
@@ -445,8 +460,8 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
     return;
   }
   if constexpr (EPI == kEpiQkvVt) {
-    if (n0 >= 2 * g.q_cols) {  // a v column tile (q_cols % 128 == 0)
-      store_vt<kTM, kTN>(g, acc, m0 + wm, n0 + wn, lr, lg);
+    if (n0 >= 2 * g.q_cols) {  // a v column tile (q_cols % 128 == 0): the branch is uniform per block
+      store_vt<BM, kTM, kTN>(g, acc, m0, n0, wm, wn, lr, lg, lds);
       return;
     }
   }
