@@ -716,6 +716,7 @@ constexpr int kQ8C = kQ8Chunks / kQ8Lpr;          // chunks per lane (5)
 constexpr int kQ8YMax = 127 * 128;                // |y_int| bound: digits hi in [-127, 127], lo in [-64, 63]
 constexpr float kQ8Gamma = 7.7e-5f;               // >= 1280 * 2^-24 / (1 - 1280 * 2^-24)
 static_assert(kLmNW * 64 / kQ8Lpr == kLmRowsIter, "one int8 row per 16 lanes per batch");
+static_assert(kLmNW * 64 >= kHidden / 2, "the y statistics and digits take one thread per pair of y values");
 
 __device__ __forceinline__ int xor_add_i16(int v) {
   // integer butterfly over 16 lanes (partners 8, 4, 2, 1), exact
