@@ -129,7 +129,7 @@ def serving_throughput(model, lanes, clips, tokens):
     return out
 
 
-def cpu_baseline(model, seconds):
+def cpu_baseline(model, seconds, tokens):
     """The CPU oracle's decoder step (numpy fp32 with the reference's fp16 rounding points) on this host,
     on the GPU model's cross K/V, for a bounded number of steps."""
     import numpy as np
@@ -142,9 +142,11 @@ def cpu_baseline(model, seconds):
     params = weights.host_params(d, model.seed, names)
     oracle = DecoderOracle(params, d, model.cross_kv.float().cpu().numpy())
     del params
+    # the workload's step positions: the prompt and then the generated tokens (0 .. prompt + tokens - 1)
+    n_steps = min(d.max_pos, len(model.prompt) + tokens - 1)
     tok, pos, times = model.prompt[0], 0, []
     t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end and len(times) < 64:
+    while time.perf_counter() < t_end and len(times) < n_steps:
         t0 = time.perf_counter()
         logits = oracle.step(tok, pos)
         times.append(time.perf_counter() - t0)
@@ -250,7 +252,7 @@ def main():
     if serve is not None:
         out['serving'] = serve
     if not args.no_cpu_baseline:
-        out['cpu_baseline'] = cpu_baseline(model, args.cpu_seconds)
+        out['cpu_baseline'] = cpu_baseline(model, args.cpu_seconds, args.tokens)
     print(json.dumps(out), flush=True)
 
 
