@@ -27,6 +27,7 @@ import time
 
 METRIC = 'decode-step µs + achieved HBM GB/s; 30 s-clip E2E ms & TTFT, batch 1'
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 LM_KERNEL = {False: 'lm_head_kernel<true> (final LN + LM head GEMV + argmax)',
              True: 'lm_head_q8_kernel<true> (final LN + int8 pre-pass over the LM head + exact fp16 candidates + argmax)'}
 LM_TRAFFIC = {False: 'profiles/lm_head_kernel_traffic.md', True: 'profiles/lm_head_q8_kernel_traffic.md'}
@@ -43,6 +44,16 @@ def decode_step_bytes(dims, length, q8=False):
     cross = L * 2 * dims.heads * dims.enc_len * dims.head_dim * 2
     self_kv = L * 2 * dims.heads * length * dims.head_dim * 2
     return weights + lm_head + cross + self_kv + 2 * 2 * d + dims.vocab
+
+
+def encoder_flops(dims):
+    """Algorithmic FLOPs of the encoder stage: the conv stem (conv1 over 2 x enc_len frames, conv2 with
+    stride 2), every layer's q/k/v, attention (Q K^T and P V), out, fc1 and fc2 products, and the cross
+    K/V projection of all decoder layers (2.313 TFLOP for whisper-large-v3-turbo)."""
+    t, d, f = dims.enc_len, dims.d_model, dims.ffn
+    stem = 2 * (2 * t) * d * (3 * dims.n_mels) + 2 * t * d * (3 * d)
+    layer = 2 * t * (3 * d) * d + 2 * 2 * t * t * d + 2 * t * d * d + 2 * 2 * t * f * d
+    return stem + dims.enc_layers * layer + 2 * t * (dims.dec_layers * 2 * d) * d
 
 
 def measured_traffic(path):
@@ -242,6 +253,9 @@ def main():
         'decode_step_hbm_gbps': round(step_gbps, 1), 'decode_step_roofline_frac': round(step_gbps / HBM_PEAK_GBPS, 4),
         'e2e_ms': round(med('e2e_s'), 3), 'ttft_ms': round(med('ttft_s'), 3), 'mel_ms': round(med('mel_s'), 3),
         'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
+        'encoder_tflops': round(encoder_flops(model.dims) / (med('encoder_s') * 1e-3) / 1e12, 1),
+        'encoder_mfma_frac': round(encoder_flops(model.dims) / (med('encoder_s') * 1e-3) / 1e12
+                                   / MFMA_FP16_PEAK_TFLOPS, 4),
         'n_tokens': rows[-1]['n_tokens'],
         'roofline': {'kernel': LM_KERNEL[q8], 'bound': 'hbm', 'achieved': round(lm_gbps, 1),
                      'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(lm_gbps / HBM_PEAK_GBPS, 4),
