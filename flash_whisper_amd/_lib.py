@@ -44,6 +44,8 @@ SIGNATURES = {
     'fw_gemm': (c_int, [P, c_int, P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     'fw_conv1d': (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, P, c_int, P]),
     'fw_layernorm_rows': (c_int, [P, P, P, P, c_int, c_int, c_float, P]),
+    'fw_gemm_splitk': (c_int, [P, c_int, P, c_int, P, c_int, c_int, c_int, c_int, P]),
+    'fw_layernorm_rows_residual': (c_int, [P, c_int, P, P, P, P, P, c_int, c_int, c_float, c_int, P]),
     'fw_encoder_vt_elems': (ctypes.c_longlong, [c_int, c_int]),
     'fw_encoder_qkv': (c_int, [P, P, P, P, P, c_int, c_int, P]),
     'fw_encoder_pack_vt': (c_int, [P, P, c_int, c_int, P]),

@@ -34,6 +34,9 @@ constexpr int kEpiCrossKV = 100;  // internal epilogue: scatter into [layers, 2,
 // Internal epilogue of the encoder q/k/v projection: q columns scaled as FW_EPI_SCALE_Q, k columns
 // stored as they are, v columns stored transposed into vt (the attention kernel's V layout).
 constexpr int kEpiQkvVt = 101;
+// Internal epilogue of the split-k products: split s (blockIdx.x / tiles) covers k in [s k, (s + 1) k)
+// and stores its fp32 sums to part[s][m][n]; the row kernel that follows adds the splits.
+constexpr int kEpiPartial = 102;
 
 struct GemmArgs {
   const _Float16* a;
@@ -58,6 +61,9 @@ struct GemmArgs {
   int vt_pad;
   // XCD tile grouping (0: none): the 8 XCDs split the tile grid into xm x xn rectangles
   int xm, xn;
+  // split-k products (kEpiPartial): number of splits and the fp32 partial sums [splits][m][n]
+  int splits;
+  float* part;
 };
 
 // Block -> output tile. Hardware deals workgroups round-robin over the 8 XCDs (block b runs on XCD
@@ -66,7 +72,8 @@ struct GemmArgs {
 // run of row-major tiles (the tail beyond a multiple of 8 keeps its id). Both maps are bijective.
 template <int BM>
 __device__ __forceinline__ void tile_origin(const GemmArgs& g, int& m0, int& n0) {
-  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM, bid = blockIdx.x;
+  const int ntn = g.n / kBN, ntm = (g.m + BM - 1) / BM;
+  const int bid = g.splits > 1 ? static_cast<int>(blockIdx.x) % (ntn * ntm) : static_cast<int>(blockIdx.x);
   int tm, tn;
   if (g.xm) {
     const int xcd = bid & 7, local = bid >> 3, mr = ntm / g.xm, nr = ntn / g.xn;
@@ -259,12 +266,12 @@ __device__ __forceinline__ void mma_frags(const Frags<kTM, kTN>& f, f16v (&acc)[
 // start the LDS reads of stage kt + 1's fragments, and run stage kt's MFMAs while they arrive. Copies
 // have ST - 1 stages of MFMA time to land and LDS read latency is hidden behind the MFMAs.
 // The LDS ring depth ST is picked per tile height: 256-row tiles use three 48 KB stages (one 8-wave
-// block per CU); 128-row tiles two 32 KB stages so that two blocks share a CU and hide each other's
-// copy latency; 64-row tiles (launched when 128-row tiles would leave CUs idle) four 24 KB stages.
+// block per CU); 128-row tiles (8 waves of 32 x 64; the split-k products) four 32 KB stages; 64-row
+// tiles (launched when 128-row tiles would leave CUs idle) four 24 KB stages.
 // Tuning knobs (defaults measured on MI355X): ring depths per tile height, the minimum number of
 // 256-row tiles for that shape, waves per 256-row block, and the XCD rectangle grouping.
 #ifndef FW_ST128
-#define FW_ST128 2
+#define FW_ST128 4
 #endif
 #ifndef FW_ST64
 #define FW_ST64 4
@@ -283,12 +290,13 @@ constexpr int dma_stages() {
   return BM == 256 ? FW_ST256 : BM == 192 ? FW_ST192 : BM == 128 ? FW_ST128 : FW_ST64;
 }
 // Waves per block, in gemm_wave_cols columns (kBN / cols output columns each) and waves / cols rows;
-// each wave owns a (BM / rows) x (kBN / cols) tile. 192-row tiles use 2 x 4 waves of 96 x 32.
+// each wave owns a (BM / rows) x (kBN / cols) tile. 192-row tiles use 2 x 4 waves of 96 x 32 and
+// 128-row tiles 4 x 2 waves of 32 x 64.
 #ifndef FW_W256
 #define FW_W256 8
 #endif
 template <int BM>
-constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 ? 8 : 4; }
+constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 || BM == 128 ? 8 : 4; }
 template <int BM>
 constexpr int gemm_wave_cols() { return BM == 192 ? 4 : 2; }
 
@@ -384,6 +392,12 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
 
   int m0, n0;
   tile_origin<BM>(g, m0, n0);
+  int split = 0;
+  if constexpr (EPI == kEpiPartial) {  // this block's k range: [split k, (split + 1) k) of the rows
+    split = static_cast<int>(blockIdx.x) / ((g.n / kBN) * ((g.m + BM - 1) / BM));
+    g.a += static_cast<size_t>(split) * g.k;
+    g.w += static_cast<size_t>(split) * g.k;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave / kNWN) * kWM, wn = (wave % kNWN) * (kBN / kNWN);
   const int lr = lane & 31, lg = lane >> 5;
@@ -475,7 +489,9 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lg + (r & 3);
         if (row < g.m) {
-          if constexpr (EPI == kEpiCrossKV) {
+          if constexpr (EPI == kEpiPartial) {
+            g.part[(static_cast<size_t>(split) * g.m + row) * g.n + col] = acc[i][j][r];
+          } else if constexpr (EPI == kEpiCrossKV) {
             const int d = col & 63, lhk = col >> 6;
             const size_t o = (static_cast<size_t>(lhk) * g.t_len + row) * 64 + d;
             g.out[o] = f2h(acc[i][j][r] + b);
@@ -658,50 +674,25 @@ int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
 // ------------------------------------------------------------------------------------------
 // Row LayerNorm over 1280 columns: 32 lanes per row (5 x 16-byte chunks each), 8 rows per block.
 // ------------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __restrict__ x,
-                                                             const _Float16* __restrict__ gamma,
-                                                             const _Float16* __restrict__ beta,
-                                                             _Float16* __restrict__ y, int rows, float eps) {
-  constexpr int kC = kHidden / 8 / 32;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane & 31;
-  const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
-  const bool valid = row < rows;
-  const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(valid ? row : 0) * kHidden);
-  // gamma and beta are requested with the row, not after the two reductions
-  const uint4* g4 = reinterpret_cast<const uint4*>(gamma);
-  const uint4* b4 = reinterpret_cast<const uint4*>(beta);
-  uint4 xu[kC], gu[kC], bu[kC];
-#pragma unroll
-  for (int c = 0; c < kC; ++c) xu[c] = xr[sub + 32 * c];
-#pragma unroll
-  for (int c = 0; c < kC; ++c) {
-    gu[c] = g4[sub + 32 * c];
-    bu[c] = b4[sub + 32 * c];
-  }
-  float v[kC * 8];
+constexpr int kLnC = kHidden / 8 / 32;  // 16-byte fp16 chunks per lane of a row
+
+// LayerNorm of one row held as v[] (this lane's elements: chunks sub + 32 c) with gamma / beta chunks
+// gu / bu, written to yr when valid.
+__device__ __forceinline__ void ln_row_finish(const float (&v)[kLnC * 8], const uint4 (&gu)[kLnC],
+                                              const uint4 (&bu)[kLnC], float eps, uint4* yr, bool valid, int sub) {
   float sum = 0.f;
 #pragma unroll
-  for (int c = 0; c < kC; ++c) {
-    const uint4 u = xu[c];
-    const _Float16* hp = reinterpret_cast<const _Float16*>(&u);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[c * 8 + e] = h2f(hp[e]);
-      sum += v[c * 8 + e];
-    }
-  }
+  for (int i = 0; i < kLnC * 8; ++i) sum += v[i];
   const float mean = group_sum<32>(sum) * (1.0f / kHidden);
   float sq = 0.f;
 #pragma unroll
-  for (int i = 0; i < kC * 8; ++i) {
+  for (int i = 0; i < kLnC * 8; ++i) {
     const float d = v[i] - mean;
     sq += d * d;
   }
   const float inv = rsqrtf(group_sum<32>(sq) * (1.0f / kHidden) + eps);
-  uint4* yr = reinterpret_cast<uint4*>(y + static_cast<size_t>(valid ? row : 0) * kHidden);
 #pragma unroll
-  for (int c = 0; c < kC; ++c) {
+  for (int c = 0; c < kLnC; ++c) {
     const _Float16* gp = reinterpret_cast<const _Float16*>(&gu[c]);
     const _Float16* bp = reinterpret_cast<const _Float16*>(&bu[c]);
     uint4 o;
@@ -712,6 +703,105 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __r
     asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
     if (valid) yr[sub + 32 * c] = o;
   }
+}
+
+__global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __restrict__ x,
+                                                             const _Float16* __restrict__ gamma,
+                                                             const _Float16* __restrict__ beta,
+                                                             _Float16* __restrict__ y, int rows, float eps) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 31;
+  const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
+  const bool valid = row < rows;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(valid ? row : 0) * kHidden);
+  // gamma and beta are requested with the row, not after the two reductions
+  const uint4* g4 = reinterpret_cast<const uint4*>(gamma);
+  const uint4* b4 = reinterpret_cast<const uint4*>(beta);
+  uint4 xu[kLnC], gu[kLnC], bu[kLnC];
+#pragma unroll
+  for (int c = 0; c < kLnC; ++c) xu[c] = xr[sub + 32 * c];
+#pragma unroll
+  for (int c = 0; c < kLnC; ++c) {
+    gu[c] = g4[sub + 32 * c];
+    bu[c] = b4[sub + 32 * c];
+  }
+  float v[kLnC * 8];
+#pragma unroll
+  for (int c = 0; c < kLnC; ++c) {
+    const _Float16* hp = reinterpret_cast<const _Float16*>(&xu[c]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[c * 8 + e] = h2f(hp[e]);
+  }
+  ln_row_finish(v, gu, bu, eps, reinterpret_cast<uint4*>(y + static_cast<size_t>(valid ? row : 0) * kHidden), valid,
+                sub);
+}
+
+// The end of a split-k product followed by a LayerNorm: the split sums part[0 .. 1] of row r are added
+// (in split order), then the residual epilogue of fw_gemm (FW_EPI_BIAS_RESID, or with CLAMP
+// FW_EPI_BIAS_RESID_CLAMP) updates h[r] in place, and y[r] <- LN(h[r]) exactly as layernorm_rows_kernel.
+template <bool CLAMP>
+__global__ void __launch_bounds__(256) residual_layernorm_rows_kernel(const float* __restrict__ part,
+                                                                      const _Float16* __restrict__ bias,
+                                                                      _Float16* h,
+                                                                      const _Float16* __restrict__ gamma,
+                                                                      const _Float16* __restrict__ beta,
+                                                                      _Float16* __restrict__ y, int rows, float eps) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 31;
+  const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
+  const bool valid = row < rows;
+  const size_t r0 = static_cast<size_t>(valid ? row : 0) * kHidden;
+  const size_t split_stride = static_cast<size_t>(rows) * kHidden;
+  const float4* p0 = reinterpret_cast<const float4*>(part + r0);
+  const float4* p1 = reinterpret_cast<const float4*>(part + split_stride + r0);
+  uint4* hr = reinterpret_cast<uint4*>(h + r0);
+  const uint4* g4 = reinterpret_cast<const uint4*>(gamma);
+  const uint4* b4 = reinterpret_cast<const uint4*>(beta);
+  const uint4* bi4 = reinterpret_cast<const uint4*>(bias);
+  uint4 hu[kLnC], gu[kLnC], bu[kLnC], biu[kLnC];
+  float4 a0[kLnC][2], a1[kLnC][2];
+#pragma unroll
+  for (int c = 0; c < kLnC; ++c) {
+    const int q = sub + 32 * c;  // this lane's 8-element chunk
+    a0[c][0] = p0[2 * q];
+    a0[c][1] = p0[2 * q + 1];
+    a1[c][0] = p1[2 * q];
+    a1[c][1] = p1[2 * q + 1];
+    hu[c] = hr[q];
+  }
+#pragma unroll
+  for (int c = 0; c < kLnC; ++c) {
+    gu[c] = g4[sub + 32 * c];
+    bu[c] = b4[sub + 32 * c];
+    biu[c] = bi4[sub + 32 * c];
+  }
+  float v[kLnC * 8];
+#pragma unroll
+  for (int c = 0; c < kLnC; ++c) {
+    const _Float16* rp = reinterpret_cast<const _Float16*>(&hu[c]);
+    const _Float16* bp = reinterpret_cast<const _Float16*>(&biu[c]);
+    const float* s0 = reinterpret_cast<const float*>(&a0[c][0]);
+    const float* s1 = reinterpret_cast<const float*>(&a1[c][0]);
+    uint4 o;
+    _Float16* op = reinterpret_cast<_Float16*>(&o);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float acc = s0[e] + s1[e];
+      float t = round_h(acc + h2f(bp[e]));
+      if constexpr (CLAMP) {
+        t = round_h(h2f(rp[e]) + t);
+        const float lim = 65504.0f - 1000.0f;
+        t = fminf(fmaxf(t, -lim), lim);
+      } else {
+        t = round_h(h2f(rp[e]) + t);
+      }
+      op[e] = f2h(t);
+      v[c * 8 + e] = t;
+    }
+    asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
+    if (valid) hr[sub + 32 * c] = o;
+  }
+  ln_row_finish(v, gu, bu, eps, reinterpret_cast<uint4*>(y + r0), valid, sub);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -767,6 +857,55 @@ extern "C" int fw_layernorm_rows(const void* x, const void* gamma, const void* b
                      static_cast<const _Float16*>(x), static_cast<const _Float16*>(gamma),
                      static_cast<const _Float16*>(beta), static_cast<_Float16*>(y), rows, eps);
   return fw_check_launch("layernorm_rows");
+}
+
+extern "C" int fw_gemm_splitk(const void* a, int lda, const void* w, int ldw, float* part, int m, int n, int k,
+                              int splits, hipStream_t stream) {
+  if (!a || !w || !part) return fw_fail(FW_EINVAL, "gemm_splitk: null pointer");
+  if (splits != 2) return fw_fail(FW_EINVAL, "gemm_splitk: splits must be 2");
+  if (m <= 0 || n <= 0 || n % kBN || k <= 0 || k % (splits * kBK))
+    return fw_fail(FW_EINVAL, "gemm_splitk: need m > 0, n %% %d == 0, k %% %d == 0 (m=%d n=%d k=%d)", kBN,
+                   splits * kBK, m, n, k);
+  if (lda < k || ldw < k || lda % 8 || ldw % 8 || !aligned16(a) || !aligned16(w) || !aligned16(part))
+    return fw_fail(FW_EINVAL, "gemm_splitk: leading dimensions must cover k and be multiples of 8; 16-byte aligned");
+  GemmArgs g{};
+  g.a = static_cast<const _Float16*>(a);
+  g.lda = lda;
+  g.w = static_cast<const _Float16*>(w);
+  g.ldw = ldw;
+  g.m = m;
+  g.n = n;
+  g.k = k / splits;  // per split
+  g.splits = splits;
+  g.part = part;
+  const int tiles = (n / kBN) * ((m + 127) / 128);
+  hipLaunchKernelGGL((gemm_dma_kernel<128, kEpiPartial>), dim3(splits * tiles), dim3(gemm_waves<128>() * 64), 0,
+                     stream, g);
+  return fw_check_launch("gemm_splitk");
+}
+
+extern "C" int fw_layernorm_rows_residual(const float* part, int splits, const void* bias, void* h,
+                                          const void* gamma, const void* beta, void* y, int rows, int n, float eps,
+                                          int epilogue, hipStream_t stream) {
+  if (!part || !bias || !h || !gamma || !beta || !y) return fw_fail(FW_EINVAL, "layernorm_rows_residual: null pointer");
+  if (splits != 2) return fw_fail(FW_EINVAL, "layernorm_rows_residual: splits must be 2");
+  if (n != kHidden || rows <= 0) return fw_fail(FW_EINVAL, "layernorm_rows_residual: n must be %d", kHidden);
+  if (epilogue != FW_EPI_BIAS_RESID && epilogue != FW_EPI_BIAS_RESID_CLAMP)
+    return fw_fail(FW_EINVAL, "layernorm_rows_residual: epilogue must be a residual epilogue");
+  if (!aligned16(part) || !aligned16(bias) || !aligned16(h) || !aligned16(gamma) || !aligned16(beta) || !aligned16(y))
+    return fw_fail(FW_EINVAL, "layernorm_rows_residual: tensors must be 16-byte aligned");
+  const dim3 grid((rows + 7) / 8);
+  if (epilogue == FW_EPI_BIAS_RESID_CLAMP)
+    hipLaunchKernelGGL(residual_layernorm_rows_kernel<true>, grid, dim3(256), 0, stream, part,
+                       static_cast<const _Float16*>(bias), static_cast<_Float16*>(h),
+                       static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta),
+                       static_cast<_Float16*>(y), rows, eps);
+  else
+    hipLaunchKernelGGL(residual_layernorm_rows_kernel<false>, grid, dim3(256), 0, stream, part,
+                       static_cast<const _Float16*>(bias), static_cast<_Float16*>(h),
+                       static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta),
+                       static_cast<_Float16*>(y), rows, eps);
+  return fw_check_launch("layernorm_rows_residual");
 }
 
 

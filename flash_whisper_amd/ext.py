@@ -381,6 +381,29 @@ class WhisperExt:
         self._call('fw_layernorm_rows', x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(), x.size(0),
                    HIDDEN, float(eps), _stream())
 
+    def gemm_splitk(self, a, w, part, splits=2):
+        """part[s] <- the fp32 product of a and w^T over the s-th k half (a [m, k], w [n, k], part [2, m, n])."""
+        check_half(a, 'a')
+        check_half(w, 'w')
+        _check(part, 'part', torch.float32, 'float32')
+        m, k = a.shape
+        n = w.size(0)
+        _require(a.dim() == 2 and w.dim() == 2 and w.size(1) == k and part.shape == (splits, m, n),
+                 'gemm_splitk shape mismatch')
+        self._call('fw_gemm_splitk', a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), part.data_ptr(), m, n, k,
+                   int(splits), _stream())
+
+    def layernorm_rows_residual(self, part, bias, h, gamma, beta, y, eps, epilogue):
+        """h <- residual epilogue(part[0] + part[1], bias) in place, then y <- LN(h) (part from gemm_splitk)."""
+        for t, n in ((bias, 'bias'), (h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (y, 'y')):
+            check_half(t, n)
+        _check(part, 'part', torch.float32, 'float32')
+        rows = h.size(0)
+        _require(h.dim() == 2 and h.size(1) == HIDDEN and y.shape == h.shape and part.shape == (2, rows, HIDDEN),
+                 'layernorm_rows_residual shape mismatch')
+        self._call('fw_layernorm_rows_residual', part.data_ptr(), 2, bias.data_ptr(), h.data_ptr(), gamma.data_ptr(),
+                   beta.data_ptr(), y.data_ptr(), rows, HIDDEN, float(eps), int(epilogue), _stream())
+
     def encoder_vt_workspace(self, seq, heads):
         """Transposed-V buffer for encoder_qkv / encoder_pack_vt / encoder_attention (layout private)."""
         n = self.lib.fw_encoder_vt_elems(seq, heads)

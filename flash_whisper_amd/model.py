@@ -95,6 +95,7 @@ class CustomModel:
         self.eattn = torch.empty(t, dm, dtype=half, device='cuda')
         self.evt = self.ext.encoder_vt_workspace(t, self.heads)
         self.effn = torch.empty(t, d.ffn, dtype=half, device='cuda')
+        self.epart = torch.empty(2, t, dm, dtype=torch.float32, device='cuda')  # fc2's two k-half sums
         self.enc_out = torch.empty(t, dm, dtype=half, device='cuda')
 
     def _alloc_decoder_buffers(self):
@@ -265,15 +266,23 @@ class CustomModel:
         ext, nh = self.ext, self.heads
         ext.conv1d(self.mel16, 1, self.conv1_wp, self.conv1_b, self.x1, EPI_BIAS_GELU)
         ext.conv1d(self.x1, 2, self.conv2_wp, self.conv2_b, self.ex, EPI_BIAS_GELU_POS, res=self.enc_pos)
+        prev = None
         for lay in self.enc_layers:
-            ext.layernorm_rows(self.ex, lay.ln1[0], lay.ln1[1], self.ey, lay.ln1[2])
+            if prev is None:
+                ext.layernorm_rows(self.ex, lay.ln1[0], lay.ln1[1], self.ey, lay.ln1[2])
+            else:  # the previous layer's fc2 residual (clamped), then this layer's first LayerNorm
+                ext.layernorm_rows_residual(self.epart, prev.fc2_b, self.ex, lay.ln1[0], lay.ln1[1], self.ey,
+                                            lay.ln1[2], EPI_BIAS_RESID_CLAMP)
             ext.encoder_qkv(self.ey, lay.qkv_w, lay.qkv_b, self.eqkv, self.evt, nh)
             ext.encoder_attention(self.eqkv, self.evt, self.eattn, nh)
             ext.gemm(self.eattn, lay.out_w, lay.out_b, self.ex, EPI_BIAS_RESID, res=self.ex)
             ext.layernorm_rows(self.ex, lay.ln2[0], lay.ln2[1], self.ey, lay.ln2[2])
             ext.gemm(self.ey, lay.fc1_w, lay.fc1_b, self.effn, EPI_BIAS_GELU)
-            ext.gemm(self.effn, lay.fc2_w, lay.fc2_b, self.ex, EPI_BIAS_RESID_CLAMP, res=self.ex)
-        ext.layernorm_rows(self.ex, self.enc_ln[0], self.enc_ln[1], self.enc_out, self.enc_ln[2])
+            # fc2 (k = 5120) as two k halves: 240 blocks of 128-row tiles instead of 64-row ones
+            ext.gemm_splitk(self.effn, lay.fc2_w, self.epart)
+            prev = lay
+        ext.layernorm_rows_residual(self.epart, prev.fc2_b, self.ex, self.enc_ln[0], self.enc_ln[1], self.enc_out,
+                                    self.enc_ln[2], EPI_BIAS_RESID_CLAMP)
         ext.cross_kv(self.enc_out, self.cross_w, self.cross_b, self.cross_kv)
         return self.enc_out
 

@@ -199,6 +199,22 @@ int fw_gemm(const void* a, int lda, const void* w, int ldw, const void* bias, vo
 int fw_conv1d(const void* x, int t_in, int c_in, int stride, const void* wp, const void* bias, void* out,
               int c_out, const void* res, int epilogue, hipStream_t stream);
 
+/* Split-k product (no reference counterpart: the encoder's fc2 Linear, transformers
+ * modeling_whisper.py:405-407, computed as two k halves so that 1500 x 1280 outputs still fill the
+ * CUs): part[s][m][n] <- sum over k' in [s k / 2, (s + 1) k / 2) of a[m, k'] * w[n, k'] in fp32, for
+ * s < splits = 2. a fp16[m, lda], w fp16[n, ldw]; part fp32 [2][m][n]; n % 128 == 0, k % 128 == 0. */
+int fw_gemm_splitk(const void* a, int lda, const void* w, int ldw, float* part, int m, int n, int k, int splits,
+                   hipStream_t stream);
+
+/* The end of a split-k product and the next LayerNorm in one launch (no reference counterpart): for
+ * each row r, acc = part[0][r] + part[1][r], then h[r] <- the residual epilogue of fw_gemm with that
+ * acc (epilogue FW_EPI_BIAS_RESID or FW_EPI_BIAS_RESID_CLAMP: fp16(acc + bias) added to h[r] in fp16,
+ * clamped to +-64504 with the latter), then y[r] <- fp16(LN(h[r]) * gamma + beta) as fw_layernorm_rows.
+ * part fp32 [2][rows][1280] from fw_gemm_splitk; h fp16[rows, 1280] updated in place; splits == 2. */
+int fw_layernorm_rows_residual(const float* part, int splits, const void* bias, void* h, const void* gamma,
+                               const void* beta, void* y, int rows, int n, float eps, int epilogue,
+                               hipStream_t stream);
+
 /* Row LayerNorm: y[r] <- fp16(LN(x[r]) * gamma + beta) for r < rows, n == 1280 (F.layer_norm on fp16). */
 int fw_layernorm_rows(const void* x, const void* gamma, const void* beta, void* y, int rows, int n, float eps,
                       hipStream_t stream);

@@ -57,6 +57,12 @@ def test_validation_errors_return_einval(built_lib):
     rc = lib.fw_encoder_qkv(dummy, dummy, None, dummy, dummy, 1500, 3, None)  # 3 * 64 is not a multiple of 128
     assert rc == _lib.FW_EINVAL and b'multiple of 128' in lib.fw_last_error()
     assert lib.fw_encoder_attention(dummy, None, dummy, 1500, 20, None) == _lib.FW_EINVAL
+    rc = lib.fw_gemm_splitk(dummy, 5120, dummy, 5120, dummy, 1500, 1280, 5120, 3, None)
+    assert rc == _lib.FW_EINVAL and b'splits must be 2' in lib.fw_last_error()
+    rc = lib.fw_gemm_splitk(dummy, 5120, dummy, 5120, dummy, 1500, 1280, 5056, 2, None)  # k not a multiple of 128
+    assert rc == _lib.FW_EINVAL
+    rc = lib.fw_layernorm_rows_residual(dummy, 2, dummy, dummy, dummy, dummy, dummy, 1500, 1280, 1e-5, 0, None)
+    assert rc == _lib.FW_EINVAL and b'residual epilogue' in lib.fw_last_error()
     assert lib.fw_encoder_vt_elems(1500, 20) == 20 * 64 * 1536 and lib.fw_encoder_vt_elems(0, 20) == 0
 
 

@@ -92,6 +92,40 @@ def test_gelu_epilogue_within_one_ulp(ext, hip_device):
     assert (d == 0).mean() > 0.995
 
 
+@pytest.mark.parametrize('epi', [2, 3])  # FW_EPI_BIAS_RESID, FW_EPI_BIAS_RESID_CLAMP
+def test_splitk_residual_layernorm_matches_fused_path(ext, hip_device, epi):
+    """fc2 as two k halves (fw_gemm_splitk) finished by fw_layernorm_rows_residual: the partial sums add
+    up to the fp32 product, and the updated residual and its LayerNorm match the one-pass GEMM with
+    the same residual epilogue followed by fw_layernorm_rows (within the fp16 tolerance: only the fp32
+    summation order differs), on the encoder's fc2 shape (1500 rows: a partial last 128-row tile)."""
+    dev = hip_device
+    rng = np.random.default_rng(epi)
+    m, n, k = 1500, 1280, 5120
+    a = np.float16(0.5 * rng.standard_normal((m, k)))
+    w = np.float16(0.02 * rng.standard_normal((n, k)))
+    b = np.float16(0.02 * rng.standard_normal(n))
+    res = np.float16(rng.standard_normal((m, n)))
+    g, be = h16(1 + 0.1 * rng.standard_normal(n), dev), h16(0.1 * rng.standard_normal(n), dev)
+    ta, tw, tb = h16(a, dev), h16(w, dev), h16(b, dev)
+    part = torch.full((2, m, n), float('nan'), dtype=torch.float32, device=dev)
+    ext.gemm_splitk(ta, tw, part)
+    prod = a.astype(np.float64) @ w.astype(np.float64).T
+    close_rel(np32(part[0] + part[1]), prod, rtol=1e-4)
+    h_ref = h16(res, dev)
+    ext.gemm(ta, tw, tb, h_ref, epi, res=h_ref)
+    y_ref = torch.empty_like(h_ref)
+    ext.layernorm_rows(h_ref, g, be, y_ref, 1e-5)
+    h = h16(res, dev)
+    y = torch.full_like(h, float('nan'))
+    ext.layernorm_rows_residual(part, tb, h, g, be, y, 1e-5, epi)
+    close_rel(np32(h), np32(h_ref), scale=np.abs(res.astype(np.float32)) + np.abs(prod))
+    close_rel(np32(y), np32(y_ref))
+    # the LayerNorm of the updated residual is exactly fw_layernorm_rows of it
+    y2 = torch.empty_like(h)
+    ext.layernorm_rows(h, g, be, y2, 1e-5)
+    assert torch.equal(y, y2)
+
+
 def test_gemm_row_strided_views(ext, hip_device):
     """a, out given as column slices of wider matrices (leading dimension > k / n)."""
     dev = hip_device
