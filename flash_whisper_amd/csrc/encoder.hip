@@ -672,9 +672,15 @@ int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Row LayerNorm over 1280 columns: 32 lanes per row (5 x 16-byte chunks each), 8 rows per block.
+// Row LayerNorm over 1280 columns: 32 lanes per row (5 x 16-byte chunks each), kLnRows = kLnThreads / 32 rows per block.
 // ------------------------------------------------------------------------------------------
 constexpr int kLnC = kHidden / 8 / 32;  // 16-byte fp16 chunks per lane of a row
+#ifndef FW_LN_THREADS
+#define FW_LN_THREADS 256
+#endif
+constexpr int kLnThreads = FW_LN_THREADS;  // threads per row-LayerNorm block: 32 lanes per row
+constexpr int kLnRows = kLnThreads / 32;
+static_assert(kLnThreads % 64 == 0 && kLnThreads <= 256, "whole waves, within the launch bounds");
 
 // LayerNorm of one row held as v[] (this lane's elements: chunks sub + 32 c) with gamma / beta chunks
 // gu / bu, written to yr when valid.
@@ -711,7 +717,7 @@ __global__ void __launch_bounds__(256) layernorm_rows_kernel(const _Float16* __r
                                                              _Float16* __restrict__ y, int rows, float eps) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane & 31;
-  const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
+  const int row = blockIdx.x * kLnRows + wave * 2 + (lane >> 5);
   const bool valid = row < rows;
   const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<size_t>(valid ? row : 0) * kHidden);
   // gamma and beta are requested with the row, not after the two reductions
@@ -748,7 +754,7 @@ __global__ void __launch_bounds__(256) residual_layernorm_rows_kernel(const floa
                                                                       _Float16* __restrict__ y, int rows, float eps) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane & 31;
-  const int row = blockIdx.x * 8 + wave * 2 + (lane >> 5);
+  const int row = blockIdx.x * kLnRows + wave * 2 + (lane >> 5);
   const bool valid = row < rows;
   const size_t r0 = static_cast<size_t>(valid ? row : 0) * kHidden;
   const size_t split_stride = static_cast<size_t>(rows) * kHidden;
@@ -853,7 +859,7 @@ extern "C" int fw_layernorm_rows(const void* x, const void* gamma, const void* b
   if (n != kHidden || rows <= 0) return fw_fail(FW_EINVAL, "layernorm_rows: n must be %d", kHidden);
   if (!aligned16(x) || !aligned16(y) || !aligned16(gamma) || !aligned16(beta))
     return fw_fail(FW_EINVAL, "layernorm_rows: tensors must be 16-byte aligned");
-  hipLaunchKernelGGL(layernorm_rows_kernel, dim3((rows + 7) / 8), dim3(256), 0, stream,
+  hipLaunchKernelGGL(layernorm_rows_kernel, dim3((rows + kLnRows - 1) / kLnRows), dim3(kLnThreads), 0, stream,
                      static_cast<const _Float16*>(x), static_cast<const _Float16*>(gamma),
                      static_cast<const _Float16*>(beta), static_cast<_Float16*>(y), rows, eps);
   return fw_check_launch("layernorm_rows");
@@ -894,14 +900,14 @@ extern "C" int fw_layernorm_rows_residual(const float* part, int splits, const v
     return fw_fail(FW_EINVAL, "layernorm_rows_residual: epilogue must be a residual epilogue");
   if (!aligned16(part) || !aligned16(bias) || !aligned16(h) || !aligned16(gamma) || !aligned16(beta) || !aligned16(y))
     return fw_fail(FW_EINVAL, "layernorm_rows_residual: tensors must be 16-byte aligned");
-  const dim3 grid((rows + 7) / 8);
+  const dim3 grid((rows + kLnRows - 1) / kLnRows);
   if (epilogue == FW_EPI_BIAS_RESID_CLAMP)
-    hipLaunchKernelGGL(residual_layernorm_rows_kernel<true>, grid, dim3(256), 0, stream, part,
+    hipLaunchKernelGGL(residual_layernorm_rows_kernel<true>, grid, dim3(kLnThreads), 0, stream, part,
                        static_cast<const _Float16*>(bias), static_cast<_Float16*>(h),
                        static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta),
                        static_cast<_Float16*>(y), rows, eps);
   else
-    hipLaunchKernelGGL(residual_layernorm_rows_kernel<false>, grid, dim3(256), 0, stream, part,
+    hipLaunchKernelGGL(residual_layernorm_rows_kernel<false>, grid, dim3(kLnThreads), 0, stream, part,
                        static_cast<const _Float16*>(bias), static_cast<_Float16*>(h),
                        static_cast<const _Float16*>(gamma), static_cast<const _Float16*>(beta),
                        static_cast<_Float16*>(y), rows, eps);
