@@ -21,7 +21,7 @@ import json
 import os
 from pathlib import Path
 
-from .config import BEGIN_SUPPRESS_IDS, EOS_IDS, SUPPRESS_IDS, DecodeSetup, WhisperDims
+from .config import DecodeSetup, WhisperDims
 
 PROMPT_TOKENS = ('<|startoftranscript|>', '<|en|>', '<|transcribe|>', '<|notimestamps|>')  # custom/model.py:22
 WEIGHT_FILE = 'model.safetensors'
@@ -133,8 +133,18 @@ def load_tokenizer(path):
     return Tokenizer.from_file(str(f))
 
 
+def _ids(value):
+    """A token-id list from a config value: null is empty, a single id is a one-element list."""
+    if value is None:
+        return ()
+    return tuple(value) if isinstance(value, (list, tuple)) else (value,)
+
+
 def decode_setup(path, tokenizer, dims):
-    """Prompt, EOS and suppress ids as the reference derives them (custom/model.py:44-46,57-61)."""
+    """Prompt, EOS and suppress ids as the reference derives them (custom/model.py:44-46,57-61): from
+    the generation config, whose fields transformers fills from config.json when the checkpoint has
+    no generation_config.json; a missing or null suppress list is empty (``gen.suppress_tokens or []``),
+    and a missing EOS id means no EOS stop."""
     prompt = None
     if tokenizer is not None:
         ids = [tokenizer.token_to_id(t) for t in PROMPT_TOKENS]
@@ -143,10 +153,10 @@ def decode_setup(path, tokenizer, dims):
     cfg = json.loads((Path(path) / 'config.json').read_text())
     gen_file = Path(path) / 'generation_config.json'
     gen = json.loads(gen_file.read_text()) if gen_file.is_file() else {}
-    eos = gen.get('eos_token_id', cfg.get('eos_token_id'))
-    eos = EOS_IDS if eos is None else (tuple(eos) if isinstance(eos, list) else (eos,))
-    suppress = tuple(gen['suppress_tokens']) if 'suppress_tokens' in gen else SUPPRESS_IDS
-    begin = tuple(gen['begin_suppress_tokens']) if 'begin_suppress_tokens' in gen else BEGIN_SUPPRESS_IDS
+    field = lambda key: gen[key] if key in gen else cfg.get(key)
+    eos = gen.get('eos_token_id')
+    eos = _ids(cfg.get('eos_token_id') if eos is None else eos)
+    suppress, begin = _ids(field('suppress_tokens')), _ids(field('begin_suppress_tokens'))
     if prompt is None:
         raise CheckpointError('the prompt tokens need tokenizer.json with ' + ', '.join(PROMPT_TOKENS))
     for name, ids in (('prompt', prompt), ('eos', eos), ('suppress', suppress), ('begin_suppress', begin)):

@@ -797,7 +797,8 @@ __global__ void __launch_bounds__(256) residual_layernorm_rows_kernel(const floa
       if constexpr (CLAMP) {
         t = round_h(h2f(rp[e]) + t);
         const float lim = 65504.0f - 1000.0f;
-        t = fminf(fmaxf(t, -lim), lim);
+        // the LayerNorm below reads the stored fp16 value: the bound itself rounds to 64512
+        t = round_h(fminf(fmaxf(t, -lim), lim));
       } else {
         t = round_h(h2f(rp[e]) + t);
       }

@@ -260,19 +260,26 @@ class CustomModel:
         return float((mel32 - ref).abs().max())
 
     # ---- encoder -----------------------------------------------------------------------------
-    def _encode(self):
+    def _encode(self, hook=None):
         """Conv stem + 32 layers + final LN, then the cross K/V of every decoder layer written straight
-        into self.cross_kv (custom/model.py:143-147; transformers modeling_whisper.py:592-648)."""
+        into self.cross_kv (custom/model.py:143-147; transformers modeling_whisper.py:592-648).
+        ``hook(i, x)``, if given, is called (at enqueue time) as soon as the residual stream ``x`` holds
+        the stem output (i = -1) or the output of layer i; it lets a caller read every layer of this
+        exact launch sequence."""
         ext, nh = self.ext, self.heads
         ext.conv1d(self.mel16, 1, self.conv1_wp, self.conv1_b, self.x1, EPI_BIAS_GELU)
         ext.conv1d(self.x1, 2, self.conv2_wp, self.conv2_b, self.ex, EPI_BIAS_GELU_POS, res=self.enc_pos)
+        if hook:
+            hook(-1, self.ex)
         prev = None
-        for lay in self.enc_layers:
+        for i, lay in enumerate(self.enc_layers):
             if prev is None:
                 ext.layernorm_rows(self.ex, lay.ln1[0], lay.ln1[1], self.ey, lay.ln1[2])
             else:  # the previous layer's fc2 residual (clamped), then this layer's first LayerNorm
                 ext.layernorm_rows_residual(self.epart, prev.fc2_b, self.ex, lay.ln1[0], lay.ln1[1], self.ey,
                                             lay.ln1[2], EPI_BIAS_RESID_CLAMP)
+                if hook:
+                    hook(i - 1, self.ex)
             ext.encoder_qkv(self.ey, lay.qkv_w, lay.qkv_b, self.eqkv, self.evt, nh)
             ext.encoder_attention(self.eqkv, self.evt, self.eattn, nh)
             ext.gemm(self.eattn, lay.out_w, lay.out_b, self.ex, EPI_BIAS_RESID, res=self.ex)
@@ -283,6 +290,8 @@ class CustomModel:
             prev = lay
         ext.layernorm_rows_residual(self.epart, prev.fc2_b, self.ex, self.enc_ln[0], self.enc_ln[1], self.enc_out,
                                     self.enc_ln[2], EPI_BIAS_RESID_CLAMP)
+        if hook:
+            hook(len(self.enc_layers) - 1, self.ex)
         ext.cross_kv(self.enc_out, self.cross_w, self.cross_b, self.cross_kv)
         return self.enc_out
 

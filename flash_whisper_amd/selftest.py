@@ -1,140 +1,215 @@
-"""In-process kernel checks against PyTorch fp32 math on the GPU (the drop-in for custom/selftest.py).
+"""Kernel self-checks run when a model is built (the drop-in for custom/selftest.py).
 
-``run_selftest(ext)`` runs the same checks and tolerances as the reference (custom/selftest.py:32-88):
-add_layernorm vs F.layer_norm (<= 2e-2), self attention at lengths {1, 63, 64, 65, 200, 448} with the
-KV write exact (tolerance 0), cross attention over 1500 keys (<= 1e-2), and the LM head argmax whose
-chosen fp32 logit must be within 1e-3 of the maximum with the finalize bookkeeping intact. It adds the
-same checks for the fused ops this build's decoder step uses. ``python -m custom.selftest --out DIR``
-writes selftest.json like the reference's ``main`` (:91-101).
+Gate interface, kept as the reference defines it (custom/selftest.py:15-19,22-23,32-101):
+``run_selftest(ext)`` returns ``{'ok': bool, 'checks': [{'name', 'max_err', 'ok'}, ...]}``, ``ok`` being
+true only when every check is; the reference's check names and tolerances are kept (add_layernorm
+2e-2; decode_attention_self_<L> and decode_attention_cross 1e-2; kv_write_<L> exact; lm_head_argmax:
+the chosen row's logit within 1e-3 of the best unsuppressed one, with the finalize bookkeeping intact);
+``workspace(heads, splits)`` sizes the split-K partials; ``python -m custom.selftest --out DIR``
+writes ``DIR/selftest.json``.
+
+How the checks are made here: every input is drawn on the host from one seeded numpy generator and
+uploaded, and every reference is computed on the host in float64, so no device math library takes part
+in judging a kernel. The checks are grouped by kernel family (``FAMILIES``); each family is a
+generator of ``(name, error, tolerance)`` triples. Besides the reference's checks, each fused kernel of
+this build's decoder step is compared with the unfused ops it replaces: LN + GEMV, the one-launch
+attention, the fused final LN + LM head + finalize, and the LM head with the int8 pre-pass (which must
+pick the same token, bit for bit, as the fp16 head).
 """
 
 import argparse
 import json
+import math
 from pathlib import Path
 
+import numpy as np
 import torch
-import torch.nn.functional as F
 
 from .config import SPLIT_KEYS
 
 HIDDEN, HEADS, HEAD_DIM, VOCAB = 1280, 20, 64, 51866
+MAX_POS, ENC_LEN = 448, 1500
+SELF_LENGTHS = (1, 63, 64, 65, 200, 448)
+EPS = 1e-5
+
+# tolerances of the reference gate (custom/selftest.py:44,57,64,72,86); 0 means bit for bit
+TOL_LAYERNORM, TOL_ATTENTION, TOL_ARGMAX_GAP, EXACT = 2e-2, 1e-2, 1e-3, 0.0
 
 
 def workspace(heads, splits, device='cuda'):
-    """fp32 partials (max, exp-sum, value sum) for the split-K attention kernels."""
-    return (torch.empty(heads * splits, device=device), torch.empty(heads * splits, device=device),
-            torch.empty(heads * splits * HEAD_DIM, device=device))
+    """fp32 split-K attention partials: running max and exp-sum per (head, split), and the
+    unnormalised value sum per (head, split, dim)."""
+    m = torch.empty(heads * splits, device=device)
+    return m, torch.empty_like(m), torch.empty(heads * splits * HEAD_DIM, device=device)
 
 
-def _check(name, err, tol):
-    return {'name': name, 'max_err': float(err), 'ok': bool(err <= tol)}
+class _Inputs:
+    """Seeded host inputs (fp16 values) and their device copies."""
+
+    def __init__(self, seed=0):
+        self.rng = np.random.default_rng(seed)
+
+    def draw(self, *shape, std=1.0):
+        return (self.rng.standard_normal(shape, dtype=np.float32) * std).astype(np.float16)
+
+    @staticmethod
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    @staticmethod
+    def host(t):
+        return t.detach().float().cpu().numpy().astype(np.float64)
 
 
-def _attention_ref(q, k, v, length, scale):
-    # fp32 math path; bmm operands made contiguous first
-    qf = q.float().unsqueeze(1)                                 # [h, 1, d]
-    kt = k[:, :length].float().transpose(1, 2).contiguous()     # [h, d, l]
-    s = torch.bmm(qf, kt) * scale                               # [h, 1, l]
-    return torch.bmm(s.softmax(-1), v[:, :length].float().contiguous()).squeeze(1)
+def _ln64(r, gamma, beta):
+    r = np.asarray(r, np.float64)
+    mu = r.mean(-1, keepdims=True)
+    var = ((r - mu) ** 2).mean(-1, keepdims=True)
+    return (r - mu) / np.sqrt(var + EPS) * np.asarray(gamma, np.float64) + np.asarray(beta, np.float64)
+
+
+def _attn64(q, k, v, length, scale):
+    """q [H, D], k/v [H, >=length, D] -> softmax(q k^T * scale) v over the first `length` keys, [H * D]."""
+    k, v = np.asarray(k[:, :length], np.float64), np.asarray(v[:, :length], np.float64)
+    s = np.einsum('hd,hld->hl', np.asarray(q, np.float64), k) * scale
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum('hl,hld->hd', p, v).reshape(-1)
+
+
+def _maxdiff(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def _finalize_state():
+    dev = 'cuda'
+    return (torch.zeros(1, dtype=torch.long, device=dev), torch.zeros(8, dtype=torch.long, device=dev),
+            torch.tensor([3, 0], dtype=torch.long, device=dev), torch.zeros(1, dtype=torch.long, device=dev))
+
+
+def _layernorm_family(ext, inp):
+    h, x = inp.draw(1, HIDDEN), inp.draw(1, HIDDEN)
+    gamma, beta = inp.draw(HIDDEN), inp.draw(HIDDEN)
+    th, tx, tg, tb = inp.dev(h), inp.dev(x), inp.dev(gamma), inp.dev(beta)
+    h_before = th.clone()
+    y = torch.empty_like(th)
+    ext.add_layernorm(th, tx, tg, tb, y, EPS)
+    r = (h.astype(np.float32) + x.astype(np.float32)).astype(np.float16)  # the fp16 residual
+    err = max(_maxdiff(inp.host(y), _ln64(r, gamma, beta)), _maxdiff(inp.host(th), r))
+    yield 'add_layernorm', err, TOL_LAYERNORM
+    # residual + LN + GEMV in one launch == add_layernorm followed by the GEMV
+    w, b = inp.dev(inp.draw(3 * HIDDEN, HIDDEN, std=0.02)), inp.dev(inp.draw(3 * HIDDEN, std=0.02))
+    fused, unfused = (torch.empty(3 * HIDDEN, dtype=torch.float16, device='cuda') for _ in range(2))
+    h_out = torch.empty_like(th)
+    ext.ln_gemv(h_before, tx, h_out, tg, tb, EPS, w, b, fused)
+    ext.gemv(y, w, b, unfused)
+    yield 'ln_gemv_vs_unfused', max(float((fused - unfused).abs().max()), float((h_out - th).abs().max())), EXACT
+
+
+def _self_attention_family(ext, inp):
+    scale = HEAD_DIM ** -0.5
+    ws = workspace(HEADS, -(-ENC_LEN // SPLIT_KEYS))
+    for length in SELF_LENGTHS:
+        pos = length - 1
+        q = inp.draw(HEADS, HEAD_DIM)
+        k, v = inp.draw(HEADS, MAX_POS, HEAD_DIM), inp.draw(HEADS, MAX_POS, HEAD_DIM)
+        k_new, v_new = inp.draw(HEADS, 1, HEAD_DIM), inp.draw(HEADS, 1, HEAD_DIM)
+        k_want, v_want = k.copy(), v.copy()   # the cache after the fused write of row `pos`
+        k_want[:, pos], v_want[:, pos] = k_new[:, 0], v_new[:, 0]
+        ref = _attn64(q, k_want, v_want, length, scale)
+        state = inp.dev(np.array([pos, 0], np.int64))
+        tq, tkn, tvn = inp.dev(q.reshape(-1)), inp.dev(k_new), inp.dev(v_new)
+        for tag, launch in (('', lambda tk, tv, out: ext.decode_attention(tq, tk, tv, out, state, tkn, tvn, *ws, scale)),
+                            ('fused_', lambda tk, tv, out: ext.decode_attention_fused(tq, tk, tv, out, state, tkn,
+                                                                                      tvn, scale))):
+            tk, tv = inp.dev(k), inp.dev(v)
+            out = torch.empty_like(tq)
+            launch(tk, tv, out)
+            yield f'decode_attention_{tag}self_{length}', _maxdiff(inp.host(out), ref), TOL_ATTENTION
+            # the new row is written, and nothing else in the cache moves
+            yield f'kv_write_{tag}{length}', max(_maxdiff(inp.host(tk), k_want), _maxdiff(inp.host(tv), v_want)), EXACT
+
+
+def _cross_attention_family(ext, inp):
+    scale = HEAD_DIM ** -0.5
+    ws = workspace(HEADS, -(-ENC_LEN // SPLIT_KEYS))
+    q = inp.draw(HEADS, HEAD_DIM)
+    k, v = inp.draw(HEADS, ENC_LEN, HEAD_DIM), inp.draw(HEADS, ENC_LEN, HEAD_DIM)
+    ref = _attn64(q, k, v, ENC_LEN, scale)
+    tq, tk, tv = inp.dev(q.reshape(-1)), inp.dev(k), inp.dev(v)
+    out = torch.empty_like(tq)
+    ext.decode_attention(tq, tk, tv, out, None, None, None, *ws, scale)
+    yield 'decode_attention_cross', _maxdiff(inp.host(out), ref), TOL_ATTENTION
+    out = torch.empty_like(tq)
+    ext.decode_attention_fused(tq, tk, tv, out, None, None, None, scale)
+    yield 'decode_attention_fused_cross', _maxdiff(inp.host(out), ref), TOL_ATTENTION
+
+
+def _lm_head_family(ext, inp):
+    w = inp.draw(VOCAB, HIDDEN, std=0.02)
+    suppress = inp.rng.random(VOCAB) < 0.01
+    tw, tsup = inp.dev(w), inp.dev(suppress)
+    w32 = w.astype(np.float32)
+
+    # the reference op pair: LM head argmax into `best`, then finalize. The kernel's contract is the
+    # argmax of fp16-rounded logits (lowest index on ties), so the reference logits are rounded too and
+    # a correct pick has gap 0.
+    y = inp.draw(HIDDEN)
+    logits = (w32 @ y.astype(np.float32)).astype(np.float16).astype(np.float64)
+    logits = np.where(suppress, -np.inf, logits)
+    best, tokens, state, cur = _finalize_state()
+    ext.lm_head_argmax(inp.dev(y[None]), tw, tsup, best)
+    ext.argmax_finalize(best, tokens, state, cur, MAX_POS)
+    tok = int(tokens[0])
+    kept = int(cur) == tok and state.tolist() == [4, 1] and int(best) == 0
+    gap = float(logits.max() - logits[tok]) if kept and 0 <= tok < VOCAB else math.inf
+    yield 'lm_head_argmax', gap, TOL_ARGMAX_GAP
+
+    # final residual + LN + LM head + finalize in one launch == add_layernorm, lm_head_argmax, finalize
+    h, x = inp.dev(inp.draw(1, HIDDEN)), inp.dev(inp.draw(1, HIDDEN))
+    ones = torch.ones(HIDDEN, dtype=torch.float16, device='cuda')
+    zeros = torch.zeros(HIDDEN, dtype=torch.float16, device='cuda')
+    results = {}
+    h_unfused, y_unfused = h.clone(), torch.empty_like(h)
+    ext.add_layernorm(h_unfused, x, ones, zeros, y_unfused, EPS)
+    st = _finalize_state()
+    ext.lm_head_argmax(y_unfused, tw, tsup, st[0])
+    ext.argmax_finalize(*st, MAX_POS)
+    results['unfused'] = st
+    st = _finalize_state()
+    ext.lm_head_argmax_fused(h, x, ones, zeros, EPS, tw, tsup, *st, MAX_POS)
+    results['fused'] = st
+    wq, meta = ext.lm_head_q8_table(tw)
+    st = _finalize_state()
+    ext.lm_head_argmax_q8(h, x, ones, zeros, EPS, tw, wq, meta, tsup, *st, MAX_POS)
+    results['q8'] = st
+
+    def same(a, b):  # token list, state and current token identical; both `best` words reset
+        return (torch.equal(a[1], b[1]) and torch.equal(a[2], b[2]) and torch.equal(a[3], b[3])
+                and int(a[0]) == 0 and int(b[0]) == 0)
+
+    yield 'lm_head_argmax_fused_vs_unfused', 0.0 if same(results['fused'], results['unfused']) else 1.0, EXACT
+    yield 'lm_head_argmax_q8_vs_fused', 0.0 if same(results['q8'], results['fused']) else 1.0, EXACT
+
+
+FAMILIES = (_layernorm_family, _self_attention_family, _cross_attention_family, _lm_head_family)
 
 
 @torch.inference_mode()
-def run_selftest(ext):
-    torch.manual_seed(0)
-    dev, half = 'cuda', torch.float16
+def run_selftest(ext, seed=0):
     checks = []
-
-    h = torch.randn(1, HIDDEN, device=dev, dtype=half)
-    x = torch.randn_like(h)
-    gamma, beta = torch.randn(HIDDEN, device=dev, dtype=half), torch.randn(HIDDEN, device=dev, dtype=half)
-    residual = h + x
-    ref = F.layer_norm(residual.float(), (HIDDEN,), gamma.float(), beta.float(), 1e-5)
-    y = torch.empty_like(h)
-    h0 = h.clone()
-    ext.add_layernorm(h, x, gamma, beta, y, 1e-5)
-    checks.append(_check('add_layernorm', max((y.float() - ref).abs().max(), (h - residual).abs().max()), 2e-2))
-
-    # fused residual + LN + GEMV must reproduce add_layernorm followed by the GEMV exactly
-    w = torch.randn(3840, HIDDEN, device=dev, dtype=half) * 0.02
-    b = torch.randn(3840, device=dev, dtype=half) * 0.02
-    out_fused, out_ref, h_out = (torch.empty(3840, device=dev, dtype=half), torch.empty(3840, device=dev, dtype=half),
-                                 torch.empty_like(h0))
-    ext.ln_gemv(h0, x, h_out, gamma, beta, 1e-5, w, b, out_fused)
-    ext.gemv(y, w, b, out_ref)
-    checks.append(_check('ln_gemv_vs_unfused', max((out_fused - out_ref).abs().max(), (h_out - h).abs().max()), 0))
-
-    scale = HEAD_DIM ** -0.5
-    ws = workspace(HEADS, 24)
-    for length in (1, 63, 64, 65, 200, 448):
-        max_len, pos = 448, length - 1
-        q = torch.randn(HEADS * HEAD_DIM, device=dev, dtype=half)
-        k = torch.randn(HEADS, max_len, HEAD_DIM, device=dev, dtype=half)
-        v = torch.randn_like(k)
-        k_new = torch.randn(HEADS, 1, HEAD_DIM, device=dev, dtype=half)
-        v_new = torch.randn_like(k_new)
-        k_ref, v_ref = k.clone(), v.clone()
-        k_ref[:, pos], v_ref[:, pos] = k_new[:, 0], v_new[:, 0]
-        k2, v2 = k.clone(), v.clone()
-        out = torch.empty_like(q)
-        state = torch.tensor([pos, 0], device=dev, dtype=torch.long)
-        ext.decode_attention(q, k, v, out, state, k_new, v_new, *ws, scale)
-        ref = _attention_ref(q.view(HEADS, HEAD_DIM), k_ref, v_ref, length, scale).flatten()
-        checks.append(_check(f'decode_attention_self_{length}', (out.float() - ref).abs().max(), 1e-2))
-        written = max((k[:, pos] - k_new[:, 0]).abs().max(), (v[:, pos] - v_new[:, 0]).abs().max())
-        untouched = max((k - k_ref).abs().max(), (v - v_ref).abs().max())
-        checks.append(_check(f'kv_write_{length}', max(written, untouched), 0))
-        out_f = torch.empty_like(q)
-        ext.decode_attention_fused(q, k2, v2, out_f, state, k_new, v_new, scale)
-        checks.append(_check(f'decode_attention_fused_self_{length}', (out_f.float() - ref).abs().max(), 1e-2))
-        checks.append(_check(f'kv_write_fused_{length}', max((k2 - k).abs().max(), (v2 - v).abs().max()), 0))
-
-    q = torch.randn(HEADS * HEAD_DIM, device=dev, dtype=half)
-    k = torch.randn(HEADS, 1500, HEAD_DIM, device=dev, dtype=half)
-    v = torch.randn_like(k)
-    out = torch.empty_like(q)
-    ext.decode_attention(q, k, v, out, None, None, None, *ws, scale)
-    ref = _attention_ref(q.view(HEADS, HEAD_DIM), k, v, 1500, scale).flatten()
-    checks.append(_check('decode_attention_cross', (out.float() - ref).abs().max(), 1e-2))
-    out_f = torch.empty_like(q)
-    ext.decode_attention_fused(q, k, v, out_f, None, None, None, scale)
-    checks.append(_check('decode_attention_fused_cross', (out_f.float() - ref).abs().max(), 1e-2))
-
-    hidden = torch.randn(1, HIDDEN, device=dev, dtype=half)
-    weight = torch.randn(VOCAB, HIDDEN, device=dev, dtype=half) * 0.02
-    suppress = torch.rand(VOCAB, device=dev) < 0.01
-    logits = (weight.float() @ hidden.float()[0]).masked_fill(suppress, float('-inf'))
-    best, tokens = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
-    state, cur = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
-    ext.lm_head_argmax(hidden, weight, suppress, best)
-    ext.argmax_finalize(best, tokens, state, cur, 448)
-    token = int(tokens[0])
-    # A different index is acceptable only when it ties the reference max at fp16 precision.
-    gap = float(logits.max() - logits[token]) if 0 <= token < VOCAB else float('inf')
-    bookkeeping = int(cur) == token and state.tolist() == [4, 1] and int(best) == 0
-    checks.append(_check('lm_head_argmax', gap if bookkeeping else float('inf'), 1e-3))
-
-    # fused final LN + LM head + finalize vs add_layernorm -> lm_head_argmax -> argmax_finalize
-    hres, xres = torch.randn(1, HIDDEN, device=dev, dtype=half), torch.randn(1, HIDDEN, device=dev, dtype=half)
-    g1, b0 = torch.ones(HIDDEN, device=dev, dtype=half), torch.zeros(HIDDEN, device=dev, dtype=half)
-    h1, y1 = hres.clone(), torch.empty_like(hres)
-    ext.add_layernorm(h1, xres, g1, b0, y1, 1e-5)
-    best1, tok1 = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
-    st1, cur1 = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
-    ext.lm_head_argmax(y1, weight, suppress, best1)
-    ext.argmax_finalize(best1, tok1, st1, cur1, 448)
-    best2, tok2 = torch.zeros(1, device=dev, dtype=torch.long), torch.zeros(8, device=dev, dtype=torch.long)
-    st2, cur2 = torch.tensor([3, 0], device=dev, dtype=torch.long), torch.zeros(1, device=dev, dtype=torch.long)
-    ext.lm_head_argmax_fused(hres, xres, g1, b0, 1e-5, weight, suppress, best2, tok2, st2, cur2, 448)
-    same = torch.equal(tok1, tok2) and torch.equal(st1, st2) and torch.equal(cur1, cur2) and int(best2) == 0
-    checks.append(_check('lm_head_argmax_fused_vs_unfused', 0 if same else 1, 0))
-
+    inp = _Inputs(seed)
+    for family in FAMILIES:
+        for name, err, tol in family(ext, inp):
+            checks.append({'name': name, 'max_err': float(err), 'ok': bool(err <= tol)})
+    torch.cuda.synchronize()
     return {'ok': all(c['ok'] for c in checks), 'checks': checks}
 
 
 def main():
     from .ext import load_ext
 
-    parser = argparse.ArgumentParser()
+    parser = argparse.ArgumentParser(description='run the kernel self-checks and write DIR/selftest.json')
     parser.add_argument('--out', type=Path, required=True)
     args = parser.parse_args()
     args.out.mkdir(parents=True, exist_ok=True)

@@ -35,7 +35,7 @@ extern "C" {
 #define FW_EPI_BIAS 0          /* out = fp16(acc + b)                                   */
 #define FW_EPI_BIAS_GELU 1     /* out = fp16(gelu(fp16(acc + b)))                       */
 #define FW_EPI_BIAS_RESID 2    /* out = fp16(res + fp16(acc + b))   (out may alias res) */
-#define FW_EPI_BIAS_RESID_CLAMP 3 /* as RESID, then clamp to +-(65504 - 1000)           */
+#define FW_EPI_BIAS_RESID_CLAMP 3 /* as RESID, then clamp to +-(65504 - 1000): +-64512 in fp16 */
 #define FW_EPI_BIAS_GELU_POS 4 /* out = fp16(fp16(gelu(fp16(acc + b))) + res)           */
 #define FW_EPI_SCALE_Q 5       /* columns < q_cols: fp16(fp16(acc + b) * 0.125); k/v as BIAS */
 
@@ -209,7 +209,8 @@ int fw_gemm_splitk(const void* a, int lda, const void* w, int ldw, float* part, 
 /* The end of a split-k product and the next LayerNorm in one launch (no reference counterpart): for
  * each row r, acc = part[0][r] + part[1][r], then h[r] <- the residual epilogue of fw_gemm with that
  * acc (epilogue FW_EPI_BIAS_RESID or FW_EPI_BIAS_RESID_CLAMP: fp16(acc + bias) added to h[r] in fp16,
- * clamped to +-64504 with the latter), then y[r] <- fp16(LN(h[r]) * gamma + beta) as fw_layernorm_rows.
+ * clamped to +-(65504 - 1000) with the latter, which fp16 stores as +-64512), then
+ * y[r] <- fp16(LN(h[r]) * gamma + beta) of the stored h[r], as fw_layernorm_rows.
  * part fp32 [2][rows][1280] from fw_gemm_splitk; h fp16[rows, 1280] updated in place; splits == 2. */
 int fw_layernorm_rows_residual(const float* part, int splits, const void* bias, void* h, const void* gamma,
                                const void* beta, void* y, int rows, int n, float eps, int epilogue,

@@ -2,16 +2,29 @@
 
 Restates transformers WhisperEncoder.forward (models/whisper/modeling_whisper.py:592-648) as the
 reference runs it in fp16 (custom/model.py:32-34,143-147): every op output is rounded to fp16 with
-fp32 accumulation inside the op. Rounding points (``fp16=True``):
+fp32 accumulation inside the op. Rounding points (``fp16=True``), one function per op so each can be
+checked on its own against transformers' intermediate tensors:
   conv1: fp16(conv + b) -> fp16(gelu)            (:618)
   conv2 (stride 2): same, then fp16(x + positions) (:619-623, sinusoids :55-65)
-  layer (:379-414): y = fp16(LN(x)); q = fp16(fp16(y Wq^T + bq) * head_dim^-0.5) (:309);
-    k = fp16(y Wk^T) (no bias, :279); v = fp16(y Wv^T + bv); o = fp16(softmax(q k^T) v) (SDPA, scale 1);
-    x = fp16(x + fp16(o Wo^T + bo)); y = fp16(LN(x)); u = fp16(gelu(fp16(y W1^T + b1)));
-    x = fp16(x + fp16(u W2^T + b2)); clamp to +-(65504 - 1000) (:409-411)
+  layer (:379-414):
+    ln_op      y = fp16(LN(x))
+    q_op       q = fp16(fp16(y Wq^T + bq) * head_dim^-0.5)   (q scaled after its rounding, :309)
+    k_op       k = fp16(y Wk^T)                               (no bias, :279)
+    v_op       v = fp16(y Wv^T + bv)
+    attention_core  o = fp16(softmax(q k^T) v)                (SDPA with scale 1; fp32 softmax here)
+    linear_op  fp16(o Wo^T + bo), fc1, fc2 (bias added before the single rounding)
+    gelu_op    fp16(gelu(a))                                  (exact erf)
+    residual_op x = fp16(x + r); after fc2, clamp(x, +-(65504 - 1000)) in fp16 (:409-411), which
+                rounds the bound to fp16: +-64512
   final: fp16(LN(x)) (:642)
 With ``fp16=False`` nothing is rounded and the clamp is skipped (transformers clamps only in fp16),
 which is the setting the fp32 golden vectors of a tiny transformers model pin.
+
+The attention core computes the softmax in float32 and rounds the output once. Flash-style kernels
+(torch SDPA on the CPU and on CUDA, and this build's HIP kernel) round the unnormalised
+probabilities to fp16 before the P.V product; that moves results by about one fp16 ulp and is inside
+the 2e-3 relative tolerance the parity tests use.
+
 Cross K/V: fp16(enc @ [k_0; v_0; k_1; ...]^T + [0; b_v0; 0; ...]) permuted to [layers, 2, heads, t, hd]
 (custom/model.py:53-55, 145-146).
 """
@@ -37,24 +50,70 @@ def conv1d(x, w, b, stride):
     return out + to32(b)[:, None]
 
 
-def self_attention(y, p, heads, rnd, fp16):
-    t, dm = y.shape
+def ln_op(x, ln, eps, fp16=True):
+    return rounder(fp16)(layer_norm(x, *ln, eps))
+
+
+def linear_op(a, w, b=None, fp16=True):
+    """fp16(a W^T + b): fp32 accumulation, bias added before the single rounding."""
+    out = a @ to32(w).T
+    if b is not None:
+        out = out + to32(b)
+    return rounder(fp16)(out)
+
+
+def q_op(y, p, heads, fp16=True):
+    """The query as transformers hands it to SDPA: the projection is rounded, then scaled and rounded
+    again (modeling_whisper.py:309); SDPA itself then runs with scale 1."""
+    scale = (y.shape[-1] // heads) ** -0.5
+    return rounder(fp16)(linear_op(y, p['q_w'], p['q_b'], fp16) * scale)
+
+
+def k_op(y, p, fp16=True):
+    return linear_op(y, p['k_w'], None, fp16)
+
+
+def v_op(y, p, fp16=True):
+    return linear_op(y, p['v_w'], p['v_b'], fp16)
+
+
+def attention_core(q, k, v, heads, fp16=True):
+    """Non-causal softmax(q k^T) v per head (q already scaled); q/k/v and the result are [t, d_model]."""
+    t, dm = q.shape
     hd = dm // heads
-    scale = hd ** -0.5
-    q = rnd(rnd(y @ p['q_w'].T + p['q_b']) * scale)
-    k = rnd(y @ p['k_w'].T)
-    v = rnd(y @ p['v_w'].T + p['v_b'])
-    qh = q.reshape(t, heads, hd).transpose(1, 0, 2)
-    kh = k.reshape(t, heads, hd).transpose(1, 0, 2)
-    vh = v.reshape(t, heads, hd).transpose(1, 0, 2)
+    split = lambda a: to32(a).reshape(a.shape[0], heads, hd).transpose(1, 0, 2)
+    qh, kh, vh = split(q), split(k), split(v)
     o = np.empty((heads, t, hd), np.float32)
     for h in range(heads):  # one head at a time keeps the score matrix small
         s = qh[h] @ kh[h].T
         s -= s.max(axis=1, keepdims=True)
         e = np.exp(s)
         o[h] = (e @ vh[h]) / e.sum(axis=1, keepdims=True)
-    o = rnd(o.transpose(1, 0, 2).reshape(t, dm))
-    return rnd(o @ p['o_w'].T + p['o_b'])
+    return rounder(fp16)(o.transpose(1, 0, 2).reshape(t, dm))
+
+
+def gelu_op(a, fp16=True):
+    return rounder(fp16)(gelu(a))
+
+
+def residual_op(x, r, fp16=True, clamp=False):
+    """fp16(x + r); with `clamp` (the end of an fp16 layer) the result is clamped to +-CLAMP in fp16:
+    torch.clamp on a half tensor rounds the bound to fp16 too, so the clamped value is 64512 (the
+    fp16 nearest to 64504)."""
+    rnd = rounder(fp16)
+    out = rnd(to32(x) + to32(r))
+    if clamp and fp16:
+        out = rnd(np.clip(out, -CLAMP, CLAMP))
+    return out
+
+
+def self_attention(y, p, heads, fp16=True, trace=None):
+    q, k, v = q_op(y, p, heads, fp16), k_op(y, p, fp16), v_op(y, p, fp16)
+    o = attention_core(q, k, v, heads, fp16)
+    out = linear_op(o, p['o_w'], p['o_b'], fp16)
+    if trace is not None:
+        trace.update(q=q, k=k, v=v, attn=o, attn_out=out)
+    return out
 
 
 def layer_params(params, i):
@@ -70,16 +129,19 @@ def layer_params(params, i):
                 fc2_w=g(f'{q}.fc2.weight'), fc2_b=g(f'{q}.fc2.bias'))
 
 
-def encoder_layer(x, p, heads, eps, fp16=True):
-    rnd = rounder(fp16)
-    y = rnd(layer_norm(x, *p['ln1'], eps))
-    x = rnd(x + self_attention(y, p, heads, rnd, fp16))
-    y = rnd(layer_norm(x, *p['ln2'], eps))
-    u = rnd(gelu(rnd(y @ p['fc1_w'].T + p['fc1_b'])))
-    x = rnd(x + rnd(u @ p['fc2_w'].T + p['fc2_b']))
-    if fp16:
-        x = np.clip(x, -CLAMP, CLAMP)
-    return x
+def encoder_layer(x, p, heads, eps, fp16=True, trace=None):
+    """One pre-LN encoder layer. `trace`, if a dict, receives every op's output by name
+    (ln1, q, k, v, attn, attn_out, x_attn, ln2, fc1, gelu, fc2, out)."""
+    y = ln_op(x, p['ln1'], eps, fp16)
+    x_attn = residual_op(x, self_attention(y, p, heads, fp16, trace), fp16)
+    y2 = ln_op(x_attn, p['ln2'], eps, fp16)
+    a = linear_op(y2, p['fc1_w'], p['fc1_b'], fp16)
+    u = gelu_op(a, fp16)
+    m = linear_op(u, p['fc2_w'], p['fc2_b'], fp16)
+    out = residual_op(x_attn, m, fp16, clamp=True)
+    if trace is not None:
+        trace.update(ln1=y, x_attn=x_attn, ln2=y2, fc1=a, gelu=u, fc2=m, out=out)
+    return out
 
 
 def embed_stem(params, mel, fp16=True):
@@ -87,15 +149,14 @@ def embed_stem(params, mel, fp16=True):
     rnd = rounder(fp16)
     g = lambda n: to32(params[n])
     e = 'model.encoder'
-    x = rnd(gelu(rnd(conv1d(to32(mel), g(f'{e}.conv1.weight'), g(f'{e}.conv1.bias'), 1))))
-    x = rnd(gelu(rnd(conv1d(x, g(f'{e}.conv2.weight'), g(f'{e}.conv2.bias'), 2))))
-    return rnd(x.T + g(f'{e}.embed_positions.weight')[: x.shape[1]])
+    x = gelu_op(rnd(conv1d(to32(mel), g(f'{e}.conv1.weight'), g(f'{e}.conv1.bias'), 1)), fp16)
+    x = gelu_op(rnd(conv1d(x, g(f'{e}.conv2.weight'), g(f'{e}.conv2.bias'), 2)), fp16)
+    return residual_op(x.T, g(f'{e}.embed_positions.weight')[: x.shape[1]], fp16)
 
 
 def encoder_forward(params, mel, dims, fp16=True, n_layers=None, final_ln=True, collect=None):
     """Returns the encoder output [t, d_model] (float32, fp16-valued when fp16=True).
     `collect`, if a list, receives the hidden state after the stem and after every layer."""
-    rnd = rounder(fp16)
     x = embed_stem(params, mel, fp16)
     if collect is not None:
         collect.append(x.copy())
@@ -106,19 +167,18 @@ def encoder_forward(params, mel, dims, fp16=True, n_layers=None, final_ln=True, 
             collect.append(x.copy())
     if final_ln:
         g = lambda nm: to32(params[nm])
-        x = rnd(layer_norm(x, g('model.encoder.layer_norm.weight'), g('model.encoder.layer_norm.bias'), dims.ln_eps))
+        x = ln_op(x, (g('model.encoder.layer_norm.weight'), g('model.encoder.layer_norm.bias')), dims.ln_eps, fp16)
     return x
 
 
 def cross_kv(params, enc, dims, fp16=True):
     """[layers, 2, heads, t, hd] K/V of every decoder layer's cross-attention."""
-    rnd = rounder(fp16)
     t = enc.shape[0]
     out = np.empty((dims.dec_layers, 2, dims.heads, t, dims.head_dim), np.float32)
     for i in range(dims.dec_layers):
         a = f'model.decoder.layers.{i}.encoder_attn'
-        k = rnd(enc @ to32(params[f'{a}.k_proj.weight']).T)
-        v = rnd(enc @ to32(params[f'{a}.v_proj.weight']).T + to32(params[f'{a}.v_proj.bias']))
+        k = linear_op(enc, params[f'{a}.k_proj.weight'], None, fp16)
+        v = linear_op(enc, params[f'{a}.v_proj.weight'], params[f'{a}.v_proj.bias'], fp16)
         out[i, 0] = k.reshape(t, dims.heads, dims.head_dim).transpose(1, 0, 2)
         out[i, 1] = v.reshape(t, dims.heads, dims.head_dim).transpose(1, 0, 2)
     return out

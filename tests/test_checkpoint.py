@@ -126,3 +126,33 @@ def test_decode_setup_and_detokenize(tmp_path):
     (root / 'generation_config.json').write_text(json.dumps({**gen, 'suppress_tokens': [TINY.vocab + 5]}))
     with pytest.raises(C.CheckpointError, match='outside the vocabulary'):
         C.decode_setup(root, tok, TINY)
+
+
+def test_decode_setup_fallbacks(tmp_path):
+    """As transformers' generation config (custom/model.py:45-46,57-61): lists missing from
+    generation_config.json come from config.json, a null list is empty, and without any EOS id
+    nothing stops the decode."""
+    specials = {'<|endoftext|>': 100, '<|startoftranscript|>': 101, '<|en|>': 102, '<|transcribe|>': 103,
+                '<|notimestamps|>': 104}
+    tk = special_tokenizer(TINY.vocab, specials)
+    root = write_checkpoint(tmp_path / 'ckpt', TINY, tiny_params(), tokenizer=tk, gen={'eos_token_id': 100})
+    cfg = json.loads((root / 'config.json').read_text())
+    cfg.update(suppress_tokens=[7, 9], begin_suppress_tokens=[11], eos_token_id=99)
+    (root / 'config.json').write_text(json.dumps(cfg))
+    tok = C.load_tokenizer(root)
+    setup = C.decode_setup(root, tok, TINY)
+    assert setup.suppress == (7, 9) and setup.begin_suppress == (11,) and setup.eos == (100,)
+    # null in generation_config.json wins over config.json and means empty
+    (root / 'generation_config.json').write_text(json.dumps({'suppress_tokens': None, 'begin_suppress_tokens': None}))
+    setup = C.decode_setup(root, tok, TINY)
+    assert setup.suppress == () and setup.begin_suppress == () and setup.eos == (99,)
+    # neither file names any list or EOS id
+    (root / 'generation_config.json').unlink()
+    for key in ('suppress_tokens', 'begin_suppress_tokens', 'eos_token_id'):
+        cfg.pop(key)
+    (root / 'config.json').write_text(json.dumps(cfg))
+    setup = C.decode_setup(root, tok, TINY)
+    assert setup.suppress == () and setup.begin_suppress == () and setup.eos == ()
+    # a single EOS id or a list of them
+    (root / 'generation_config.json').write_text(json.dumps({'eos_token_id': [100, 98]}))
+    assert C.decode_setup(root, tok, TINY).eos == (100, 98)

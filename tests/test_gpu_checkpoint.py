@@ -1,8 +1,11 @@
 """A local checkpoint directory (config.json, model.safetensors, generation_config.json, tokenizer.json)
-written from the seeded turbo weights must give the same greedy ids as the synthetic model, with the
-prompt and suppress ids taken from those files and the text from the tokenizer."""
+written from the seeded turbo weights must give the oracle's greedy ids for the seeded clip
+(tests/golden/e2e_turbo_seed0.json), with the prompt and suppress ids taken from those files and the
+text from the tokenizer."""
 
 import json
+
+from conftest import GOLDEN
 
 import pytest
 import torch
@@ -42,12 +45,12 @@ def test_checkpoint_model_matches_synthetic(checkpoint_dir, hip_device):
     from flash_whisper_amd.config import PROMPT_IDS
     from flash_whisper_amd.model import CustomModel
 
+    fx = json.loads((GOLDEN / 'e2e_turbo_seed0.json').read_text())
     clip = synthetic_clip(0)
-    ref = CustomModel(seed=0, selftest=False).transcribe(clip, max_new_tokens=N_TOKENS, stop_at_eos=False)
-    torch.cuda.empty_cache()
     m = CustomModel(str(checkpoint_dir), None, selftest=False)
     assert m.checkpoint == str(checkpoint_dir) and tuple(m.prompt) == PROMPT_IDS
+    assert m.setup.suppress == tuple(fx['suppress']) and m.setup.begin_suppress == tuple(fx['begin_suppress'])
     out = m.transcribe(clip, max_new_tokens=N_TOKENS, stop_at_eos=False)
-    assert out['token_ids'] == ref['token_ids']
+    assert out['token_ids'] == fx['ids'][:N_TOKENS]
     words = [f'w{i}' for i in out['token_ids'] if i < 50257]
     assert out['text'] == ' '.join(words)

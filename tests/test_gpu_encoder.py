@@ -31,8 +31,8 @@ def _gemm_ref(a, w, b, epi, res=None, q_cols=0):
     elif epi in (2, 3):
         scale = np.abs(res.astype(np.float32)) + np.abs(v)
         v = f16(res.astype(np.float32) + v)
-        if epi == 3:
-            v = np.clip(v, -64504, 64504)
+        if epi == 3:  # the clamp bound 65504 - 1000 rounds to 64512 in fp16
+            v = f16(np.clip(v, -64504, 64504))
     elif epi == 4:
         g = f16(gelu(v))
         scale = np.abs(g) + np.abs(res.astype(np.float32))
@@ -92,19 +92,26 @@ def test_gelu_epilogue_within_one_ulp(ext, hip_device):
     assert (d == 0).mean() > 0.995
 
 
+@pytest.mark.parametrize('big', [False, True])
 @pytest.mark.parametrize('epi', [2, 3])  # FW_EPI_BIAS_RESID, FW_EPI_BIAS_RESID_CLAMP
-def test_splitk_residual_layernorm_matches_fused_path(ext, hip_device, epi):
+def test_splitk_residual_layernorm_matches_fused_path(ext, hip_device, epi, big):
     """fc2 as two k halves (fw_gemm_splitk) finished by fw_layernorm_rows_residual: the partial sums add
     up to the fp32 product, and the updated residual and its LayerNorm match the one-pass GEMM with
     the same residual epilogue followed by fw_layernorm_rows (within the fp16 tolerance: only the fp32
-    summation order differs), on the encoder's fc2 shape (1500 rows: a partial last 128-row tile)."""
+    summation order differs), on the encoder's fc2 shape (1500 rows: a partial last 128-row tile).
+    With `big`, 8 columns of 100 rows carry a residual of +-64992, so residual + fc2 passes the
+    fp16 clamp bound: the clamping epilogue must store +-64512 there (the bound 65504 - 1000 in fp16,
+    as transformers' clamp of a half tensor gives) and normalise the stored values."""
     dev = hip_device
-    rng = np.random.default_rng(epi)
+    rng = np.random.default_rng(epi + 10 * big)
     m, n, k = 1500, 1280, 5120
     a = np.float16(0.5 * rng.standard_normal((m, k)))
     w = np.float16(0.02 * rng.standard_normal((n, k)))
     b = np.float16(0.02 * rng.standard_normal(n))
     res = np.float16(rng.standard_normal((m, n)))
+    rows, cols = np.arange(100) * 15, np.arange(8) * 160
+    if big:
+        res[np.ix_(rows, cols)] = np.float16(64992.0) * np.where(np.arange(8) % 2, -1, 1)
     g, be = h16(1 + 0.1 * rng.standard_normal(n), dev), h16(0.1 * rng.standard_normal(n), dev)
     ta, tw, tb = h16(a, dev), h16(w, dev), h16(b, dev)
     part = torch.full((2, m, n), float('nan'), dtype=torch.float32, device=dev)
@@ -124,6 +131,15 @@ def test_splitk_residual_layernorm_matches_fused_path(ext, hip_device, epi):
     y2 = torch.empty_like(h)
     ext.layernorm_rows(h, g, be, y2, 1e-5)
     assert torch.equal(y, y2)
+    if big:
+        sign = np.where(np.arange(8) % 2, -1.0, 1.0)
+        got, one_pass = np32(h)[np.ix_(rows, cols)], np32(h_ref)[np.ix_(rows, cols)]
+        if epi == 3:
+            expect = oenc.residual_op(res[np.ix_(rows, cols)], f16(prod[np.ix_(rows, cols)] + b[cols]), clamp=True)
+            assert np.all(expect == 64512.0 * sign)
+            assert np.array_equal(got, expect) and np.array_equal(one_pass, expect)
+        else:
+            assert np.all(np.abs(got) > 64512.0) and np.all(np.abs(one_pass) > 64512.0)
 
 
 def test_gemm_row_strided_views(ext, hip_device):
@@ -278,3 +294,49 @@ def test_encoder_layer_and_stem_vs_oracle(ext, hip_device):
     ref = oenc.encoder_layer(stem, oenc.layer_params(params, 0), 20, 1e-5)
     # the layer output is x + attn + mlp: measure against the residual's magnitude
     close_rel(np32(model.ex), ref, scale=np.abs(stem) + np.abs(ref))
+
+
+@torch.inference_mode()
+def test_encoder_product_sequence_vs_oracle(ext, hip_device):
+    """The product's own encoder launch sequence (CustomModel._encode: the stem, fused q/k/v + V^T,
+    flash attention, out projection, fc1, fc2 as two k halves finished by the clamping residual
+    LayerNorm of the next layer, the final LayerNorm, cross K/V) on the seeded turbo weights, checked
+    layer by layer: each checked layer's GPU output against the oracle's layer applied to the GPU's
+    input of that layer (2e-3 relative, against the residual's magnitude), the final LayerNorm and
+    the cross K/V likewise. Layers 0-2 cover the first residual LayerNorms, 16 and 30-31 the depth."""
+    from flash_whisper_amd import weights
+    from flash_whisper_amd.config import TURBO
+    from flash_whisper_amd.model import CustomModel
+
+    check = [0, 1, 2, 16, 30, 31]
+    model = CustomModel(selftest=False, capture=False, dims=TURBO)
+    names = [n for n, _, _ in weights.param_specs(TURBO)
+             if any(n.startswith(f'model.encoder.layers.{i}.') for i in check)
+             or n.startswith('model.encoder.layer_norm') or n.startswith('model.encoder.conv')
+             or n.startswith('model.encoder.embed_positions')
+             or (n.startswith('model.decoder.layers.3.encoder_attn.') and ('k_proj' in n or 'v_proj' in n))]
+    params = weights.host_params(TURBO, 0, names)
+    rng = np.random.default_rng(12)
+    mel = np.float16(rng.standard_normal((128, 3000)) * 0.5)
+    model.mel16.copy_(torch.from_numpy(np.ascontiguousarray(mel.T)))
+    outs = {}
+    model._encode(hook=lambda i, x: outs.__setitem__(i, x.clone()))
+    torch.cuda.synchronize()
+    assert sorted(outs) == list(range(-1, 32))
+    stem = oenc.embed_stem(params, mel.astype(np.float32))
+    close_rel(np32(outs[-1]), stem, scale=np.abs(stem) + np.abs(params['model.encoder.embed_positions.weight']))
+    for i in check:
+        x_in = np32(outs[i - 1])
+        ref = oenc.encoder_layer(x_in, oenc.layer_params(params, i), 20, 1e-5)
+        close_rel(np32(outs[i]), ref, scale=np.abs(x_in) + np.abs(ref))
+    x_last = np32(outs[31])
+    enc_ref = oenc.ln_op(x_last, (params['model.encoder.layer_norm.weight'].astype(np.float32),
+                                  params['model.encoder.layer_norm.bias'].astype(np.float32)), 1e-5)
+    close_rel(np32(model.enc_out), enc_ref)
+    # the cross K/V of the last decoder layer from the GPU's own encoder output
+    enc = np32(model.enc_out)
+    pre = 'model.decoder.layers.3.encoder_attn'
+    k = oenc.linear_op(enc, params[f'{pre}.k_proj.weight'])
+    v = oenc.linear_op(enc, params[f'{pre}.v_proj.weight'], params[f'{pre}.v_proj.bias'])
+    close_rel(np32(model.cross_kv[3, 0]).transpose(1, 0, 2).reshape(1500, 1280), k)
+    close_rel(np32(model.cross_kv[3, 1]).transpose(1, 0, 2).reshape(1500, 1280), v)

@@ -37,6 +37,53 @@ def test_selftest_and_encoder_graph(model):
     assert model.selftest['encoder_graph'] and model.selftest['encoder_graph_max_abs_diff'] == 0.0
 
 
+def test_encoder_graph_capture_failure_falls_back_to_eager(model, clip, monkeypatch):
+    """custom/model.py:149-171: when the encoder graph cannot be captured, the model records why and
+    runs the encoder eagerly, with the same ids."""
+    fx = json.loads(FIXTURE.read_text())
+    saved_graph, saved_selftest = model.graph_enc, dict(model.selftest)
+
+    class RefusedGraph:
+        def __init__(self, *args, **kwargs):
+            raise RuntimeError('graph capture refused for the test')
+
+    try:
+        monkeypatch.setattr(torch.cuda, 'CUDAGraph', RefusedGraph)
+        graph = model._capture_encoder()
+        monkeypatch.undo()
+        assert graph is None and model.selftest['encoder_graph'] is False
+        assert 'graph capture refused for the test' in model.selftest['encoder_graph_error']
+        model.graph_enc = None
+        res = model.transcribe(clip, max_new_tokens=32, stop_at_eos=False)
+        assert res['token_ids'] == fx['ids'][:32]
+    finally:
+        model.graph_enc = saved_graph
+        model.selftest.clear()
+        model.selftest.update(saved_selftest)
+
+
+def test_selftest_failure_clears_ok(model):
+    """A kernel that returns a wrong result fails its check, and the gate's ok turns false
+    (the reference gates its verdict on selftest['ok'] is True)."""
+    from flash_whisper_amd.selftest import run_selftest
+
+    class WrongLayerNorm:
+        def __init__(self, ext):
+            self._ext = ext
+
+        def __getattr__(self, name):
+            return getattr(self._ext, name)
+
+        def add_layernorm(self, h, x, gamma, beta, y, eps):
+            self._ext.add_layernorm(h, x, gamma, beta, y, eps)
+            y.add_(0.5)
+
+    res = run_selftest(WrongLayerNorm(model.ext))
+    failed = {c['name'] for c in res['checks'] if not c['ok']}
+    assert res['ok'] is False and 'add_layernorm' in failed
+    assert 'decode_attention_cross' not in failed
+
+
 def test_log_mel_vs_oracle(model, clip):
     from oracle.logmel import log_mel
 

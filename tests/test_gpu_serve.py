@@ -1,7 +1,12 @@
 """Several clips in flight on separate lanes and streams (flash_whisper_amd.serve) must produce exactly
-the token ids of one-at-a-time CustomModel.transcribe, in fixed-length and EOS-stopping modes."""
+the token ids of one-at-a-time CustomModel.transcribe, in fixed-length and EOS-stopping modes; in
+fixed-length mode the seeded clip 0 must give the oracle's ids (tests/golden/e2e_turbo_seed0.json)."""
+
+import json
 
 import pytest
+
+from conftest import GOLDEN
 
 pytestmark = pytest.mark.gpu
 
@@ -31,6 +36,9 @@ def test_lanes_match_sequential_transcribe(model, lanes, stop_at_eos):
             assert len(ref[0]) <= 13 and ref[0][-1] in model.eos
         sched = Scheduler(model, lanes=lanes)
         out = sched.transcribe_many(clips, max_new_tokens=30, stop_at_eos=stop_at_eos)
+        if not stop_at_eos:
+            fx = json.loads((GOLDEN / 'e2e_turbo_seed0.json').read_text())
+            assert out[0]['token_ids'] == fx['ids'][:30]
         assert [r['token_ids'] for r in out] == ref
         assert all(r['wall_s'] >= r['e2e_s'] > 0 for r in out)
         # the lanes stay usable one at a time
