@@ -12,6 +12,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / 'libflash_whisper.so'
 
 FW_OK, FW_EINVAL, FW_EHIP = 0, -1, -2
+NOALLOC_ATTN_SLOTS = 2048  # FW_NOALLOC_ATTN_SLOTS
 ACT_NONE, ACT_GELU = 0, 1
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESID, EPI_BIAS_RESID_CLAMP, EPI_BIAS_GELU_POS, EPI_SCALE_Q = range(6)
 
@@ -23,6 +24,7 @@ SIGNATURES = {
     'fw_lm_head_argmax': (c_int, [P, P, P, c_int, c_int, P, P]),
     'fw_argmax_finalize': (c_int, [P, P, P, P, c_int, P]),
     'fw_decode_attention': (c_int, [P, P, P, P, P, P, P, c_int, c_int, P, P, P, c_int64, c_float, P]),
+    'fw_decode_attention_noalloc': (c_int, [P, P, P, P, P, P, P, c_int, c_int, c_float, P]),
     'fw_add_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
     'fw_embed': (c_int, [P, P, P, P, c_int, c_int, P, c_int, P]),
     'fw_gemv': (c_int, [P, P, P, P, c_int, c_int, c_int, P]),

@@ -5,6 +5,9 @@
 // F.linear chain of custom/model.py:107-123: fp16 residual after every add, fp16 LayerNorm output,
 // fp16 GEMV outputs (bias added in fp32 before the single rounding), fp32 softmax with the scale
 // applied after the dot, fp16 attention output, fp16-rounded logits before the argmax.
+#include <atomic>
+#include <mutex>
+
 #include "fw_common.h"
 
 namespace fw {
@@ -1607,4 +1610,70 @@ extern "C" int fw_attn_out_gemv_batch(const float* part_m, const float* part_l, 
                                       hipStream_t stream) {
   return attn_out_gemv_impl(part_m, part_l, part_acc, ws_slots, len_state, heads, max_len, split_keys, w, bias, out,
                             n_out, nv, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// fw_decode_attention without a workspace argument, for callers that cannot allocate. The split
+// partials live in `scratch`, a device array of this library: each GPU holds its own copy until
+// the process ends. Its address on a device is looked up once (hipGetSymbolAddress, with that device
+// current) and kept; the kernels are given that address, never the host-side symbol. Every call on
+// one GPU shares the array, so calls that overlap on one GPU race. Nothing in it has to start at
+// zero: the split launch writes every (m, l) slot the combine reads (m = -inf, l = 0 for an empty
+// split), and the combine reads the value sums only of splits with l > 0.
+// ------------------------------------------------------------------------------------------
+static_assert(FW_NOALLOC_ATTN_SLOTS > 0 && kHeadDim == 64, "static workspace layout");
+static __device__ __align__(256) float scratch[FW_NOALLOC_ATTN_SLOTS * (2 + 64)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<float*> g_scratch_ptr[kMaxDevices];
+
+int noalloc_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fw_fail(FW_EHIP, "decode_attention_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  FW_REQUIRE(dev >= 0 && dev < kMaxDevices, "decode_attention_noalloc: device %d out of range", dev);
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || addr == nullptr)
+        return fw_fail(FW_EHIP, "decode_attention_noalloc: hipGetSymbolAddress on device %d: %s", dev,
+                       hipGetErrorString(e));
+      p = static_cast<float*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FW_OK;
+}
+}  // namespace
+
+extern "C" int fw_decode_attention_noalloc(const void* q, void* k, void* v, void* out, const int64_t* len_state,
+                                           const void* k_new, const void* v_new, int heads, int max_len, float scale,
+                                           hipStream_t stream) {
+  FW_REQUIRE(out, "decode_attention_noalloc: null out");
+  AttnArgs a;
+  int rc = attention_common(q, k, v, out, len_state, k_new, v_new, heads, max_len, &a);
+  if (rc != FW_OK) return rc;
+  const int nsplit = (max_len + kSplitKeys - 1) / kSplitKeys;
+  FW_REQUIRE(static_cast<int64_t>(heads) * nsplit <= FW_NOALLOC_ATTN_SLOTS,
+             "decode_attention_noalloc: heads * ceil(max_len / %d) = %lld exceeds the %d slots of the static "
+             "workspace",
+             kSplitKeys, static_cast<long long>(heads) * nsplit, FW_NOALLOC_ATTN_SLOTS);
+  float* ws = nullptr;
+  rc = noalloc_scratch(&ws);
+  if (rc != FW_OK) return rc;
+  a.scale = scale;
+  a.part_m = ws;
+  a.part_l = ws + FW_NOALLOC_ATTN_SLOTS;
+  a.part_acc = ws + 2 * FW_NOALLOC_ATTN_SLOTS;
+  rc = launch_attn_split(a, nsplit, heads, stream);
+  if (rc != FW_OK) return rc;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(heads), dim3(kHeadDim), 0, stream, a, nsplit);
+  return fw_check_launch("decode_attention_noalloc combine");
 }

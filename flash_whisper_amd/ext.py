@@ -185,8 +185,7 @@ class WhisperExt:
         else:
             self._call('fw_ln_gemv_batch', *args, nv, _stream())
 
-    def decode_attention_fused(self, q, k, v, out, len_state, k_new, v_new, scale):
-        """decode_attention in a single launch (one block per head, no workspace)."""
+    def _attn_io_checks(self, q, k, v, out, len_state, k_new, v_new):
         for t, n in ((q, 'q'), (k, 'k'), (v, 'v'), (out, 'out')):
             check_half(t, n)
         _require(k.dim() == 3 and k.size(2) == HEAD_DIM and k.shape == v.shape, 'k, v must be [heads, max_len, 64]')
@@ -200,7 +199,19 @@ class WhisperExt:
             _require(k_new.numel() == heads * HEAD_DIM and v_new.numel() == heads * HEAD_DIM,
                      'k_new, v_new must be [heads, 64]')
             _require(len_state.dtype == torch.int64 and len_state.is_cuda, 'len_state must be CUDA int64')
+        return heads, max_len
+
+    def decode_attention_fused(self, q, k, v, out, len_state, k_new, v_new, scale):
+        """decode_attention in a single launch (one block per head, no workspace)."""
+        heads, max_len = self._attn_io_checks(q, k, v, out, len_state, k_new, v_new)
         self._call('fw_decode_attention_fused', q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                   _ptr(len_state), _ptr(k_new), _ptr(v_new), heads, max_len, float(scale), _stream())
+
+    def decode_attention_noalloc(self, q, k, v, out, len_state, k_new, v_new, scale):
+        """decode_attention with its split partials in the library's static device array: no workspace,
+        no allocation (heads * ceil(max_len / 64) <= 2048; calls that overlap on one GPU race)."""
+        heads, max_len = self._attn_io_checks(q, k, v, out, len_state, k_new, v_new)
+        self._call('fw_decode_attention_noalloc', q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                    _ptr(len_state), _ptr(k_new), _ptr(v_new), heads, max_len, float(scale), _stream())
 
     def attention_split(self, q, k, v, len_state, k_new, v_new, part_m, part_l, part_acc, scale, split_keys=SPLIT_KEYS):

@@ -66,6 +66,19 @@ int fw_decode_attention(const void* q, void* k, void* v, void* out, const int64_
                         const void* k_new, const void* v_new, int heads, int max_len, float* part_m,
                         float* part_l, float* part_acc, int64_t ws_slots, float scale, hipStream_t stream);
 
+/* fw_decode_attention without the workspace arguments, for callers that cannot allocate (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc); it has no counterpart in
+ * the reference. Same kernels and the same result, bit for bit. The split partials live in a static
+ * device array of this library: FW_NOALLOC_ATTN_SLOTS (head, split) slots, 528 KiB on each GPU the
+ * library runs on, held until the process ends. heads * ceil(max_len / 64) above FW_NOALLOC_ATTN_SLOTS
+ * fails with FW_EINVAL before any launch. The array's address on a device is looked up at the first
+ * call on that device; no call allocates or frees memory. Calls on one GPU share the array: calls that
+ * overlap on one GPU (different streams) race. */
+#define FW_NOALLOC_ATTN_SLOTS 2048
+int fw_decode_attention_noalloc(const void* q, void* k, void* v, void* out, const int64_t* len_state,
+                                const void* k_new, const void* v_new, int heads, int max_len, float scale,
+                                hipStream_t stream);
+
 /* Replaces add_layernorm (whisper_kernels.cu:341-356, kernel :215-267).
  * If x != NULL: h <- fp16(h + x). Then y <- fp16(LN(h) * gamma + beta), two-pass fp32 statistics.
  * h, x, gamma, beta, y fp16[n]; n == 1280. */
