@@ -31,7 +31,7 @@ Cross K/V: fp16(enc @ [k_0; v_0; k_1; ...]^T + [0; b_v0; 0; ...]) permuted to [l
 
 import numpy as np
 
-from .common import gelu, rounder, to32
+from .common import f16, gelu, gelu_f16, rounder, to32
 from .decoder import layer_norm
 
 CLAMP = 65504.0 - 1000.0
@@ -93,6 +93,8 @@ def attention_core(q, k, v, heads, fp16=True):
 
 
 def gelu_op(a, fp16=True):
+    if fp16 and np.array_equal(f16(a), a):  # fp16-valued input: table lookup, same values
+        return gelu_f16(a)
     return rounder(fp16)(gelu(a))
 
 

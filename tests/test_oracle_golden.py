@@ -136,3 +136,12 @@ def test_conv1d_closed_form():
         ref = np.array([[np.sum(w[o] * xp[:, t * stride: t * stride + 3]) + b[o] for t in range(t_out)]
                         for o in range(2)])
         np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_gelu_lookup_equals_direct_evaluation():
+    """The oracle's fp16 GELU lookup gives exactly f16(gelu(x)) at every finite fp16 input."""
+    from oracle.common import f16, gelu, gelu_f16
+
+    every = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    every = every[np.isfinite(every)]
+    assert np.array_equal(gelu_f16(every), f16(gelu(every)))
