@@ -983,6 +983,82 @@ __device__ __forceinline__ int attn_pos(const AttnArgs& a) {
   return static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
 }
 
+// The scores, softmax and P.V of one wave's keys of a split (MAXP passes of 8 keys, keys at or past w1
+// masked): the wave's (max, exp-sum, value sum) go to wm, wl and wacc_row for split_merge_store. Lane
+// l holds key w0 + 8 p + l / 8 of pass p and chunk l % 8 of its row; fp32 throughout, the scale
+// applied after the dot.
+template <int MAXP>
+__device__ __forceinline__ void split_wave_partial(const uint4 (&kr)[MAXP], const uint4 (&vr)[MAXP], const uint4& qc,
+                                                   int w0, int w1, float scale, float* wm, float* wl,
+                                                   float* wacc_row) {
+  const int lane = threadIdx.x & 63, ks = lane >> 3, c = lane & 7;
+  float sc[MAXP];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    sc[p] = group_sum<8>(dot8(kr[p], qc, 0.f)) * scale;
+    if (w0 + p * 8 + ks >= w1) sc[p] = -INFINITY;
+    mx = fmaxf(mx, sc[p]);
+  }
+  mx = group_max<64>(mx);
+  float acc[8], psum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const float pj = __expf(sc[p] - mx);
+      psum += pj;
+      const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
+        acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
+      }
+    }
+  }
+  psum = xor_add<32>(xor_add<16>(xor_add<8>(psum)));
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    acc[t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[t])));
+  }
+  if (lane == 0) {
+    *wm = mx;
+    *wl = psum;
+  }
+  if (ks == 0) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) wacc_row[c * 8 + t] = acc[t];
+  }
+}
+
+// After a block barrier: thread d < 64 merges the NW wave partials in wave order and stores the
+// split's (m, l, acc[d]) at `slot`.
+template <int NW>
+__device__ __forceinline__ void split_merge_store(const float* wm, const float* wl, const float (*wacc)[kHeadDim],
+                                                  const AttnArgs& a, int slot) {
+  const int tid = threadIdx.x;
+  if (tid < kHeadDim) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) m = fmaxf(m, wm[w]);
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      if (wl[w] > 0.f) {
+        const float wgt = __expf(wm[w] - m);
+        l = fmaf(wl[w], wgt, l);
+        o = fmaf(wacc[w][tid], wgt, o);
+      }
+    }
+    a.part_acc[static_cast<size_t>(slot) * kHeadDim + tid] = o;
+    if (tid == 0) {
+      a.part_m[slot] = m;
+      a.part_l[slot] = l;
+    }
+  }
+}
+
 // BATCH: a batch of queries (grid.z, the prompt) takes the fresh K/V rows of the batch's earlier
 // queries straight from k_new / v_new: their cache rows are written by other blocks of the same
 // launch, so a cache row at or past the batch's first position is never trusted. The single-query
@@ -1056,64 +1132,9 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnArgs a) {
       vr[p] = reinterpret_cast<const uint4*>(a.v_new + r)[c];
     }
   }
-  float sc[MAXP];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int p = 0; p < MAXP; ++p) {
-    sc[p] = group_sum<8>(dot8(kr[p], qc, 0.f)) * a.scale;
-    if (w0 + p * 8 + ks >= w1) sc[p] = -INFINITY;
-    mx = fmaxf(mx, sc[p]);
-  }
-  mx = group_max<64>(mx);
-  float acc[8], psum = 0.f;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
-  if (mx != -INFINITY) {
-#pragma unroll
-    for (int p = 0; p < MAXP; ++p) {
-      const float pj = __expf(sc[p] - mx);
-      psum += pj;
-      const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
-        acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
-      }
-    }
-  }
-  psum = xor_add<32>(xor_add<16>(xor_add<8>(psum)));
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    acc[t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[t])));
-  }
-  if (lane == 0) {
-    wm[wave] = mx;
-    wl[wave] = psum;
-  }
-  if (ks == 0) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) wacc[wave][c * 8 + t] = acc[t];
-  }
+  split_wave_partial<MAXP>(kr, vr, qc, w0, w1, a.scale, wm + wave, wl + wave, wacc[wave]);
   __syncthreads();
-  if (tid < kHeadDim) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) m = fmaxf(m, wm[w]);
-    float l = 0.f, o = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      if (wl[w] > 0.f) {
-        const float wgt = __expf(wm[w] - m);
-        l = fmaf(wl[w], wgt, l);
-        o = fmaf(wacc[w][tid], wgt, o);
-      }
-    }
-    a.part_acc[static_cast<size_t>(slot) * kHeadDim + tid] = o;
-    if (tid == 0) {
-      a.part_m[slot] = m;
-      a.part_l[slot] = l;
-    }
-  }
+  split_merge_store<NW>(wm, wl, wacc, a, slot);
 }
 
 // Splits of up to 256 keys (the cross attention): FW_ATTN256_P passes of 8 keys per wave, 32 / P
