@@ -19,6 +19,8 @@ namespace {
 #ifndef FW_LM_HEAD_NT
 #define FW_LM_HEAD_NT 1
 #endif
+static_assert((FW_GEMV_WEIGHTS_NT == 0 || FW_GEMV_WEIGHTS_NT == 1) && (FW_LM_HEAD_NT == 0 || FW_LM_HEAD_NT == 1),
+              "FW_GEMV_WEIGHTS_NT and FW_LM_HEAD_NT are switches (0 or 1)");
 __device__ __forceinline__ uint4 ld_weights(const uint4* p) {
 #if FW_GEMV_WEIGHTS_NT
   return ld_stream(p);
@@ -533,6 +535,16 @@ void launch_gemv_batch(int nv, const _Float16* x, const LnArgs& ln, const Combin
 #ifndef FW_CMB_NW
 #define FW_CMB_NW 12  // combine + out projection: 24 rows per block
 #endif
+// Block shapes are whole blocks within the 1024-thread launch bound with at least one row group per
+// wave; any such shape computes the same rows (each row's lane split and order depend on K only).
+// The LayerNorm prologue of a shape fixes its reduction order, so the batched prompt launches reuse
+// the single-vector block sizes.
+#define FW_GEMV_SHAPE_OK(NW, U) ((NW) >= 1 && (NW) <= 16 && (U) >= 1 && (U) <= 4)
+static_assert(FW_GEMV_SHAPE_OK(FW_G5120_NW, FW_G5120_U) && FW_GEMV_SHAPE_OK(FW_G3840_NW, FW_G3840_U) &&
+                  FW_GEMV_SHAPE_OK(FW_G1280_NW, 1) && FW_GEMV_SHAPE_OK(FW_GK5120_NW, FW_GK5120_U) &&
+                  FW_GEMV_SHAPE_OK(FW_CMB_NW, 1),
+              "decode GEMV block shapes: 1..16 waves, 1..4 row groups per wave");
+#undef FW_GEMV_SHAPE_OK
 template <int MODE, int ACT>
 void dispatch_gemv_1280(const _Float16* x, const LnArgs& ln, const CombineArgs& cb, const _Float16* w,
                         const _Float16* b, _Float16* out, int n, hipStream_t s) {
@@ -573,9 +585,14 @@ void dispatch_gemv_1280_batch(int nv, const _Float16* x, const LnArgs& ln, const
 #ifndef FW_LM_U
 #define FW_LM_U 2
 #endif
+// The int8 pre-pass kernel scores one row per 16 lanes (64 rows a batch at 16 waves, so two row groups
+// per wave in the fp16 kernel's layout) and gives each pair of the 1280 y values its own thread.
+static_assert(FW_LM_U == 2, "FW_LM_U: the int8 LM head shares the fp16 head's batch of 4 rows per wave");
+static_assert(FW_LM_NW >= 10 && FW_LM_NW <= 16, "FW_LM_NW: 640..1024 threads (one per pair of y values)");
 #ifndef FW_LM_BPC
-#define FW_LM_BPC 1
+#define FW_LM_BPC 1  // fp16 LM head: blocks per CU the grid is sized for
 #endif
+static_assert(FW_LM_BPC >= 1 && FW_LM_BPC <= 4, "FW_LM_BPC: 1..4 blocks per CU");
 
 constexpr int kLmNW = FW_LM_NW, kLmU = FW_LM_U;
 constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // rows per block iteration
@@ -1142,6 +1159,8 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnArgs a) {
 #ifndef FW_ATTN256_P
 #define FW_ATTN256_P 8
 #endif
+static_assert(FW_ATTN256_P >= 2 && 32 % FW_ATTN256_P == 0,
+              "FW_ATTN256_P: whole waves of P passes over 256 keys, at most 16 waves");
 int launch_attn_split(const AttnArgs& a, int nsplit, int heads, hipStream_t s, int nq = 1) {
   const dim3 grid(nsplit, heads, nq);
   constexpr int kP256 = FW_ATTN256_P, kW256 = 32 / FW_ATTN256_P;

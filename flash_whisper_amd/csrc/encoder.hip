@@ -289,12 +289,21 @@ template <int BM>
 constexpr int dma_stages() {
   return BM == 256 ? FW_ST256 : BM == 192 ? FW_ST192 : BM == 128 ? FW_ST128 : FW_ST64;
 }
+// Ring depths: at least two stages (one read while the next lands) and a ring that fits the 160 KB of
+// LDS of a CU; the vmcnt range of the explicit waits is checked where they are instantiated.
+template <int BM>
+constexpr bool ring_fits() { return dma_stages<BM>() >= 2 && dma_stages<BM>() * (BM + kBN) * 128 <= 160 * 1024; }
+static_assert(ring_fits<256>() && ring_fits<192>() && ring_fits<128>() && ring_fits<64>(),
+              "FW_ST256 / FW_ST192 / FW_ST128 / FW_ST64: 2 or more stages within 160 KB of LDS");
+static_assert(FW_MIN_TILES256 >= 1, "FW_MIN_TILES256 must be positive");
 // Waves per block, in gemm_wave_cols columns (kBN / cols output columns each) and waves / cols rows;
 // each wave owns a (BM / rows) x (kBN / cols) tile. 192-row tiles use 2 x 4 waves of 96 x 32 and
 // 128-row tiles 4 x 2 waves of 32 x 64.
 #ifndef FW_W256
 #define FW_W256 8
 #endif
+static_assert(FW_W256 == 2 || FW_W256 == 4 || FW_W256 == 8 || FW_W256 == 16,
+              "FW_W256: 2 x (FW_W256 / 2) waves, each a whole number of 32-row MFMA tiles of the 256 rows");
 template <int BM>
 constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 || BM == 128 ? 8 : 4; }
 template <int BM>
@@ -574,6 +583,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g) {
 #ifndef FW_XCD_GROUP
 #define FW_XCD_GROUP 1
 #endif
+static_assert(FW_XCD_GROUP == 0 || FW_XCD_GROUP == 1, "FW_XCD_GROUP is a switch (0 or 1)");
 // Picks the XCD rectangle grid that divides the tile grid and moves the fewest bytes into the L2s:
 // A is fetched once per column group (xn), W once per row group (xm).
 void choose_xcd_groups(GemmArgs& g, int bm) {
@@ -660,6 +670,7 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
 #ifndef FW_USE192
 #define FW_USE192 1
 #endif
+static_assert(FW_USE192 == 0 || FW_USE192 == 1, "FW_USE192 is a switch (0 or 1)");
 int launch_gemm(const GemmArgs& g, int epi, hipStream_t s) {
   const int tiles256 = (g.n / kBN) * ((g.m + 255) / 256);
   const int tiles192 = (g.n / kBN) * ((g.m + 191) / 192);
@@ -885,6 +896,9 @@ extern "C" int fw_gemm_splitk(const void* a, int lda, const void* w, int ldw, fl
   g.k = k / splits;  // per split
   g.splits = splits;
   g.part = part;
+  // the XCD rectangles of the plain GEMMs (both k halves of a tile land on the same XCD when the tile
+  // count is a multiple of 8): 126 -> 84 MB fetched from beyond L2 for the encoder's fc2
+  choose_xcd_groups(g, 128);
   const int tiles = (n / kBN) * ((m + 127) / 128);
   hipLaunchKernelGGL((gemm_dma_kernel<128, kEpiPartial>), dim3(splits * tiles), dim3(gemm_waves<128>() * 64), 0,
                      stream, g);

@@ -14,6 +14,9 @@ namespace fw {
 #ifndef FW_SWZ_SHIFT
 #define FW_SWZ_SHIFT 1
 #endif
+// Any shift gives a permutation of a row's 8 chunks (so every shift is correct); it sets only which
+// rows share banks.
+static_assert(FW_SWZ_SHIFT >= 0 && FW_SWZ_SHIFT <= 4, "FW_SWZ_SHIFT: 0..4");
 __device__ __forceinline__ int swz_slot(int row, int chunk) { return chunk ^ ((row >> FW_SWZ_SHIFT) & 7); }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + swz_slot(row, chunk); }
 
