@@ -71,7 +71,9 @@ __device__ __forceinline__ void ln_load(const _Float16* a, const _Float16* b, co
   }
 }
 
-template <int NT>
+// kOwnSlots: the two reductions use red[0 .. NT/64) and red[NT/64 .. 2 NT/64) with one barrier each
+// (the same sums); red must then hold 2 NT/64 floats and is free again after the caller's next barrier.
+template <int NT, bool kOwnSlots = false>
 __device__ __forceinline__ void ln_finish(const LnRegs<NT>& in, bool has_b, _Float16* r_out, float eps,
                                           _Float16* y_out, float* red) {
   constexpr int kPer = LnRegs<NT>::kPer;
@@ -99,7 +101,7 @@ __device__ __forceinline__ void ln_finish(const LnRegs<NT>& in, bool has_b, _Flo
       }
     }
   }
-  const float mean = block_sum<NT>(sum, red) * (1.0f / kHidden);
+  const float mean = (kOwnSlots ? block_sum_once<NT>(sum, red) : block_sum<NT>(sum, red)) * (1.0f / kHidden);
   float sq = 0.f;
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -109,7 +111,7 @@ __device__ __forceinline__ void ln_finish(const LnRegs<NT>& in, bool has_b, _Flo
       sq += dx * dx + dy * dy;
     }
   }
-  const float var = block_sum<NT>(sq, red) * (1.0f / kHidden);
+  const float var = (kOwnSlots ? block_sum_once<NT>(sq, red + NT / kWave) : block_sum<NT>(sq, red)) * (1.0f / kHidden);
   const float inv = rsqrtf(var + eps);
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
@@ -803,7 +805,7 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_q8_kernel(const _Float16* 
   __shared__ __align__(16) _Float16 y_lds[kHidden];
   __shared__ __align__(16) int8_t yhi[kHidden];
   __shared__ __align__(16) int8_t ylo[kHidden];
-  __shared__ float red[kLmNW];
+  __shared__ float red[4 * kLmNW];  // LayerNorm sums, then max |y| and |y|^2: a slot set per round
   __shared__ float ub_lds[kQ8RowsPerBlock];
   __shared__ int cand[kQ8RowsPerBlock];
   __shared__ int ncand;
@@ -830,51 +832,57 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_q8_kernel(const _Float16* 
   LnRegs<kNT> lnr;
   if constexpr (LN) ln_load<kNT>(ln.h, ln.x, ln.gamma, ln.beta, lnr);
   if (tid == 0) ncand = 0;
-  // the first two batches are requested before the LayerNorm and y statistics, which take several
-  // block reductions; the other two are requested as soon as a register buffer frees up
+  // The first batch is requested before the LayerNorm, the second after it, the other two as soon as a
+  // register buffer frees up. About one 82 KB batch per CU in flight streams faster than more: with
+  // two requested up front the launch took 0.5 us longer, with all four 3 us longer (the table's DRAM
+  // pages are then visited by many more interleaved request streams).
   Batch ba, bb;
   load(base_of(0), ba);
-  load(base_of(1), bb);
 
   if constexpr (LN) {
-    ln_finish<kNT>(lnr, ln.x != nullptr, nullptr, ln.eps, y_lds, red);
+    ln_finish<kNT, true>(lnr, ln.x != nullptr, nullptr, ln.eps, y_lds, red);  // thread tid owns pair tid
   } else {
     for (int i = tid; i < kHidden / 8; i += kNT)
       reinterpret_cast<uint4*>(y_lds)[i] = reinterpret_cast<const uint4*>(yin)[i];
+    __syncthreads();
   }
-  __syncthreads();
-  // y statistics (same values and reduction order in every block): max |y|, |y|^2, then the
-  // quantization y_int = rint(y / t) into two int8 digits and |eta|^2 = |y - t y_int|^2.
+  load(base_of(1), bb);
+  // y statistics in one reduction round: max |y| and |y|^2. Then y_int = rint(y / t) in two int8 digits.
   constexpr int kPairs = kHidden / 2;
   const bool has_pair = tid < kPairs;
   h2v yp = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
   if (has_pair) yp = reinterpret_cast<const h2v*>(y_lds)[tid];
   const float y0 = h2f(yp.x), y1 = h2f(yp.y);
-  float amax = group_max<64>(fmaxf(fabsf(y0), fabsf(y1)));
-  if (lane == 0) red[wave] = amax;
+  const float wmax = group_max<64>(fmaxf(fabsf(y0), fabsf(y1)));
+  const float wsq = group_sum<64>(y0 * y0 + y1 * y1);
+  if (lane == 0) {
+    red[2 * kLmNW + wave] = wmax;
+    red[3 * kLmNW + wave] = wsq;
+  }
   __syncthreads();
-  amax = 0.f;
+  float amax = 0.f, ysq = 0.f;
 #pragma unroll
-  for (int i = 0; i < kLmNW; ++i) amax = fmaxf(amax, red[i]);
-  __syncthreads();
+  for (int i = 0; i < kLmNW; ++i) {
+    amax = fmaxf(amax, red[2 * kLmNW + i]);
+    ysq += red[3 * kLmNW + i];
+  }
   const float t = amax > 0.f ? amax / static_cast<float>(kQ8YMax) : 1.0f;
   const float tinv = amax > 0.f ? static_cast<float>(kQ8YMax) / amax : 0.f;
-  const float i0 = fminf(fmaxf(rintf(y0 * tinv), -kQ8YMax), kQ8YMax);
-  const float i1 = fminf(fmaxf(rintf(y1 * tinv), -kQ8YMax), kQ8YMax);
-  const float e0 = fmaf(-t, i0, y0), e1 = fmaf(-t, i1, y1);
   if (has_pair) {
-    const int n0 = static_cast<int>(i0), n1 = static_cast<int>(i1);
+    const int n0 = static_cast<int>(fminf(fmaxf(rintf(y0 * tinv), -kQ8YMax), kQ8YMax));
+    const int n1 = static_cast<int>(fminf(fmaxf(rintf(y1 * tinv), -kQ8YMax), kQ8YMax));
     const int h0 = (n0 + 64) >> 7, h1 = (n1 + 64) >> 7;  // floor division; lo digits in [-64, 63]
     yhi[2 * tid] = static_cast<int8_t>(h0);
     yhi[2 * tid + 1] = static_cast<int8_t>(h1);
     ylo[2 * tid] = static_cast<int8_t>(n0 - 128 * h0);
     ylo[2 * tid + 1] = static_cast<int8_t>(n1 - 128 * h1);
   }
-  const float ysq = block_sum<kNT>(y0 * y0 + y1 * y1, red);
-  const float esq = block_sum<kNT>(e0 * e0 + e1 * e1, red);  // its barriers also publish the digits
-  // upper bounds: fp32 sums of <= 1280 non-negative terms are within 1280 * 2^-24 < 2^-10 relative
+  __syncthreads();  // publishes the digits and y_lds
+  // Upper bounds. |y|: an fp32 sum of <= 1280 non-negative terms is within 1280 * 2^-24 < 2^-10
+  // relative. |eta|: with t and 1 / t each rounded once and y / t = y * tinv to within 3 * 2^-24 of
+  // |y / t| <= kQ8YMax (< 0.003), every |y_i - t y_int_i| <= 0.503 t (one more rounding included).
   const double ny = static_cast<double>(sqrtf(ysq)) * (1.0 + 0x1p-9);
-  const double neta = static_cast<double>(sqrtf(esq)) * (1.0 + 0x1p-9);
+  const double neta = amax > 0.f ? 0.51 * static_cast<double>(t) * sqrt(static_cast<double>(kHidden)) : 0.0;
   const double nE_per_s = 127.0 * sqrt(static_cast<double>(kHidden)) * (1.0 + 0x1p-30);
   uint4 dh[kQ8C], dl[kQ8C];
 #pragma unroll

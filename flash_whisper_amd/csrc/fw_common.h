@@ -152,6 +152,21 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return s;
 }
 
+// block_sum with the same arithmetic and one barrier: `red` is not reused before a later barrier, so the
+// caller gives every reduction round its own kThreads/64 slots.
+template <int kThreads>
+__device__ __forceinline__ float block_sum_once(float v, float* red) {
+  constexpr int kWaves = kThreads / kWave;
+  v = group_sum<kWave>(v);
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) s += red[i];
+  return s;
+}
+
 }  // namespace fw
 
 // Records a launch error (if any) and returns the C-ABI status.

@@ -13,6 +13,7 @@ from oracle.decoder import masked_argmax
 D = 1280
 GAMMA = 7.7e-5  # >= D * 2^-24 / (1 - D * 2^-24), as in the kernel
 YMAX = 127 * 128
+ETA_PER_T = 0.51  # the kernel's bound on |y_i - t y_int_i| / t
 
 
 def pack_table(w):
@@ -39,9 +40,8 @@ def candidates(q, s, e, y, live, radius_scale=1.0):
     t = np.float32(amax / YMAX) if amax > 0 else np.float32(1)
     tinv = np.float32(YMAX / amax) if amax > 0 else np.float32(0)
     yi = np.clip(np.rint(y * tinv), -YMAX, YMAX)
-    eta = y.astype(np.float64) - np.float64(t) * yi
     ny = np.sqrt((y.astype(np.float64) ** 2).sum()) * (1 + 2 ** -9)
-    neta = np.sqrt((eta ** 2).sum()) * (1 + 2 ** -9)
+    neta = ETA_PER_T * np.float64(t) * np.sqrt(D) if amax > 0 else 0.0   # closed-form bound on |y - t yi|
     a = s.astype(np.float64) * np.float64(t) * (q @ yi)            # exact integer dot, then scaled
     n_e = s.astype(np.float64) * 127 * np.sqrt(D) * (1 + 2 ** -30) + e
     r = (ny * e + (neta + GAMMA * ny) * n_e) * (1 + 2 ** -20) * radius_scale
@@ -117,3 +117,42 @@ def test_planted_mistake_is_caught():
         assert win in set(candidates(q, s, e, y, ~sup).tolist())
         missed += win not in set(candidates(q, s, e, y, ~sup, radius_scale=0.0).tolist())
     assert missed > 0
+
+
+def _quantize_like_kernel(y):
+    """t, y_int and eta = y - t y_int with the kernel's fp32 roundings (fp32 t and 1 / t, fp32 product,
+    fused y - t y_int)."""
+    y = np.asarray(y, np.float32)
+    amax = np.abs(y).max()
+    t = np.float32(amax / np.float32(YMAX))
+    tinv = np.float32(np.float32(YMAX) / amax)
+    yi = np.clip(np.rint(np.float32(y * tinv)), -YMAX, YMAX)
+    eta = np.float32(y.astype(np.float64) - np.float64(t) * yi)
+    return t, yi, eta
+
+
+def test_eta_closed_form_bound_dominates():
+    """|y_i - t y_int_i| <= 0.503 t for every element, so |eta| <= 0.51 t sqrt(1280), the bound the kernel
+    uses instead of reducing |eta|^2: fp16 inputs over many scales, values at +-max |y|, and values one
+    fp16 step either side of a half-integer multiple of t."""
+    rng = np.random.default_rng(5)
+    worst = 0.0
+    for trial in range(400):
+        scale = 10.0 ** rng.uniform(-4, 4)
+        y = np.float16(rng.standard_normal(D) * scale)
+        if trial % 4 == 1:  # heavy tails: a few large entries set max |y|
+            y[rng.integers(0, D, 3)] = np.float16(min(scale * 40, 6e4))
+        if trial % 4 == 2:  # entries near (k + 1/2) t
+            amax = float(np.abs(y.astype(np.float32)).max())
+            t = amax / YMAX
+            k = rng.integers(-YMAX, YMAX, 64)
+            y[:64] = np.float16((k + 0.5) * t)
+            y[64:128] = np.float16(np.nextafter(np.float16((k + 0.5) * t), np.float16(np.inf)))
+        if not np.isfinite(y.astype(np.float32)).all() or not np.abs(y).max() > 0:
+            continue
+        t, yi, eta = _quantize_like_kernel(y)
+        per = np.abs(eta.astype(np.float64)) / np.float64(t)
+        worst = max(worst, per.max())
+        assert per.max() <= 0.503, per.max()
+        assert np.sqrt((eta.astype(np.float64) ** 2).sum()) <= ETA_PER_T * np.float64(t) * np.sqrt(D)
+    assert worst > 0.49  # the rounding errors do reach t / 2: the check is not vacuous
