@@ -403,7 +403,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   using RS = RowSplit<K>;
   constexpr int kRowsPerBlock = NW * RS::kRPW * U;
   __shared__ __align__(16) _Float16 y_lds[MODE != kModePlain ? NV * K : 8];
-  __shared__ float red[MODE == kModeLn && NV > 1 ? 2 * NV * NW : NW];
+  __shared__ float red[MODE == kModeLn ? 2 * NV * NW : NW];
   __shared__ float wgt[MODE == kModeCombine ? kMaxCombineHeads * kMaxCombineSplits : 1];
   __shared__ float inv_den[MODE == kModeCombine ? kMaxCombineHeads : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -442,7 +442,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(const _Float16* __restric
   const uint4* xv;
   if constexpr (MODE == kModeLn) {
     if constexpr (NV == 1)
-      ln_finish<NW * 64>(lnr[0], ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
+      ln_finish<NW * 64, true>(lnr[0], ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
     else
       ln_finish_multi<NW * 64, NV>(lnr, ln.cur != nullptr || ln.x != nullptr, ln.h_out, ln.eps, y_lds, red);
     __syncthreads();
