@@ -338,7 +338,7 @@ class WhisperExt:
     def log_mel_workspace(self, n_samples, device='cuda'):
         return torch.empty(int(self.lib.fw_log_mel_ws_floats(int(n_samples))), dtype=torch.float32, device=device)
 
-    def log_mel(self, wave, filters, out, out16, ws):
+    def _log_mel_checks(self, wave, filters, out, out16, ws):
         _check(wave, 'wave', torch.float32, 'fp32')
         _check(filters, 'filters', torch.float32, 'fp32')
         _check(out, 'out', torch.float32, 'fp32')
@@ -349,7 +349,24 @@ class WhisperExt:
         if out16 is not None:
             check_half(out16, 'out16')
             _require(out16.numel() == 128 * n_frames, f'out16 must be [{n_frames}, 128]')
+
+    def log_mel(self, wave, filters, out, out16, ws):
+        """Log-mel of one clip: log_mel_prepare then log_mel_run."""
+        self._log_mel_checks(wave, filters, out, out16, ws)
         self._call('fw_log_mel', wave.data_ptr(), wave.numel(), filters.data_ptr(), out.data_ptr(), _ptr(out16),
+                   ws.data_ptr(), ws.numel(), _stream())
+
+    def log_mel_prepare(self, filters, ws):
+        """Writes the FFT twiddles and the compacted filterbank of ``filters`` to the start of ``ws``."""
+        _check(filters, 'filters', torch.float32, 'fp32')
+        _check(ws, 'ws', torch.float32, 'fp32')
+        _require(filters.shape == (201, 128), 'filters must be [201, 128]')
+        self._call('fw_log_mel_prepare', filters.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+
+    def log_mel_run(self, wave, filters, out, out16, ws):
+        """Log-mel of one clip on a workspace that log_mel_prepare filled from the same ``filters``."""
+        self._log_mel_checks(wave, filters, out, out16, ws)
+        self._call('fw_log_mel_run', wave.data_ptr(), wave.numel(), filters.data_ptr(), out.data_ptr(), _ptr(out16),
                    ws.data_ptr(), ws.numel(), _stream())
 
     # ---- encoder ---------------------------------------------------------------------------

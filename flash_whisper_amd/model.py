@@ -84,6 +84,7 @@ class CustomModel:
         self.mel32 = torch.zeros(d.n_mels, d.mel_frames, device=dev)
         self.mel16 = torch.zeros(d.mel_frames, d.n_mels, dtype=half, device=dev)  # time-major encoder input
         self.mel_ws = self.ext.log_mel_workspace(N_SAMPLES)
+        self.ext.log_mel_prepare(self.mel_filters, self.mel_ws)  # per clip only the frames + finalize run
 
     def _alloc_encoder_buffers(self):
         d, half = self.dims, torch.float16
@@ -242,7 +243,7 @@ class CustomModel:
     # ---- front end ---------------------------------------------------------------------------
     def _log_mel(self, wave):
         """HIP log-mel into self.mel32 [128, 3000] fp32 and self.mel16 [3000, 128] fp16 (custom/model.py:93-98)."""
-        self.ext.log_mel(wave, self.mel_filters, self.mel32, self.mel16, self.mel_ws)
+        self.ext.log_mel_run(wave, self.mel_filters, self.mel32, self.mel16, self.mel_ws)
         return self.mel32
 
     def _mel_diff(self):

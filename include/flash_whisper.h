@@ -191,10 +191,19 @@ int fw_lm_head_argmax_q8(const void* h, const void* x, const void* gamma, const 
  * with n_frames = n_samples / 160: periodic Hann(400), reflect-padded centred STFT (hop 160),
  * power, filters fp32[201, 128] (Slaney), log10(max(., 1e-10)), max(x, max - 8), (x + 4) / 4.
  * out16 (may be NULL) receives fp16 of the same values, time-major [n_frames, 128].
- * ws fp32[>= fw_log_mel_ws_floats(n_samples)]. */
+ * ws fp32[>= fw_log_mel_ws_floats(n_samples)], 16-byte aligned. fw_log_mel = fw_log_mel_prepare
+ * followed by fw_log_mel_run. */
 int fw_log_mel(const float* wave, int n_samples, const float* filters, float* out, void* out16, float* ws,
                int64_t ws_floats, hipStream_t stream);
 int64_t fw_log_mel_ws_floats(int n_samples);
+/* The per-filterbank part of fw_log_mel, once per workspace and filterbank: the FFT twiddle table and
+ * the compacted filterbank are written to the start of ws (no reference counterpart: the reference's
+ * filterbank is a constant tensor, custom/model.py:37-38). */
+int fw_log_mel_prepare(const float* filters, float* ws, int64_t ws_floats, hipStream_t stream);
+/* The per-clip part of fw_log_mel, on a workspace that fw_log_mel_prepare filled from the same
+ * filters (custom/model.py:93-98). */
+int fw_log_mel_run(const float* wave, int n_samples, const float* filters, float* out, void* out16, float* ws,
+                   int64_t ws_floats, hipStream_t stream);
 
 /* ---- encoder (HF WhisperEncoder.forward semantics in fp16; MFMA) ------------------------ */
 

@@ -54,6 +54,11 @@ def test_validation_errors_return_einval(built_lib):
     rc = lib.fw_gemm(dummy, 1280, dummy, 1280, None, dummy, 1280, None, 0, 1500, 1280, 1280, 2, 0, None)
     assert rc == _lib.FW_EINVAL and b'needs res' in lib.fw_last_error()
     assert lib.fw_log_mel(dummy, 100, dummy, dummy, None, dummy, 100, None) == _lib.FW_EINVAL
+    assert lib.fw_log_mel_prepare(dummy, dummy, 100, None) == _lib.FW_EINVAL  # workspace too small
+    assert b'workspace needs' in lib.fw_last_error()
+    assert lib.fw_log_mel_prepare(None, dummy, 1 << 20, None) == _lib.FW_EINVAL
+    assert lib.fw_log_mel_run(dummy, 480000, dummy, dummy, None, dummy, 100, None) == _lib.FW_EINVAL
+    assert b'workspace needs' in lib.fw_last_error()
     rc = lib.fw_encoder_qkv(dummy, dummy, None, dummy, dummy, 1500, 3, None)  # 3 * 64 is not a multiple of 128
     assert rc == _lib.FW_EINVAL and b'multiple of 128' in lib.fw_last_error()
     assert lib.fw_encoder_attention(dummy, None, dummy, 1500, 20, None) == _lib.FW_EINVAL

@@ -96,6 +96,39 @@ def test_log_mel_vs_oracle(model, clip):
         assert np.array_equal(np32(model.mel16), np32(model.mel32).T.astype(np.float16).astype(np.float32))
 
 
+def test_log_mel_prepared_run_matches_one_call(model, clip):
+    """The model's per-clip path (log_mel_run on the workspace prepared at construction) gives exactly
+    what the one-call op (prepare + run on a fresh workspace) gives."""
+    ext = model.ext
+    wave = torch.zeros(480000, device='cuda')
+    wave[:clip.size] = torch.from_numpy(clip).cuda()
+    model._log_mel(wave)
+    ref32, ref16 = torch.empty_like(model.mel32), torch.empty_like(model.mel16)
+    ext.log_mel(wave, model.mel_filters, ref32, ref16, ext.log_mel_workspace(480000))
+    assert torch.equal(model.mel32, ref32) and torch.equal(model.mel16, ref16)
+
+
+def test_log_mel_long_filter_runs(model, clip):
+    """A filterbank with runs longer than the 16 compacted weights (read from the dense filters) and
+    empty mels, against the oracle with the same filters."""
+    from oracle.logmel import log_mel
+
+    rng = np.random.default_rng(3)
+    filters = np.zeros((201, 128), np.float32)
+    for m in range(128):
+        if m % 9 == 4:
+            continue  # an all-zero mel: log10(1e-10)
+        lo = int(rng.integers(0, 150))
+        n = int(rng.integers(1, 50)) if m % 3 else int(rng.integers(17, 50))
+        filters[lo:lo + n, m] = rng.uniform(0.001, 0.01, min(n, 201 - lo))
+    wave = np.zeros(480000, np.float32)
+    wave[:clip.size] = clip
+    f_dev = torch.from_numpy(filters).cuda()
+    out = torch.empty(128, 3000, device='cuda')
+    model.ext.log_mel(torch.from_numpy(wave).cuda(), f_dev, out, None, model.ext.log_mel_workspace(480000))
+    assert np.abs(np32(out) - log_mel(wave, filters)).max() <= 1e-4
+
+
 def test_transcribe_ids_match_oracle_fixture(model, clip):
     from flash_whisper_amd.audio import sha256
 
