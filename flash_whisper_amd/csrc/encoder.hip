@@ -230,15 +230,34 @@ struct Frags {
   h8v b[kBK / 16][kTN];
 };
 
+// Byte offsets, within one ring stage (A tile, then the B tile at BM * 128 bytes), of a lane's
+// fragments for each k-step s. Rows wm + 32 i + lr and wm + lr have the same swizzle (wm and 32 i are
+// multiples of 16), so row group i (or j) is the k-step's offset plus 4096 i bytes, an immediate of
+// the LDS read: a stage's reads then cost one address add per k-step and operand.
+struct FragOffsets {
+  uint32_t a[kBK / 16], b[kBK / 16];
+};
+static_assert(FW_SWZ_SHIFT <= 2, "fragment offsets need rows r and r + 32 to share the swizzle");
+
+template <int BM>
+__device__ __forceinline__ FragOffsets frag_offsets(int wm, int wn, int lr, int lg) {
+  FragOffsets o;
+#pragma unroll
+  for (int s = 0; s < kBK / 16; ++s) {
+    o.a[s] = static_cast<uint32_t>(swz(wm + lr, 2 * s + lg) * 16);
+    o.b[s] = static_cast<uint32_t>(BM * 128 + swz(wn + lr, 2 * s + lg) * 16);
+  }
+  return o;
+}
+
 template <int kTM, int kTN>
-__device__ __forceinline__ void load_frags(const u32x4* As, const u32x4* Bs, int wm, int wn, int lr, int lg,
-                                           Frags<kTM, kTN>& f) {
+__device__ __forceinline__ void load_frags(const char* stage, const FragOffsets& o, Frags<kTM, kTN>& f) {
 #pragma unroll
   for (int s = 0; s < kBK / 16; ++s) {
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) f.a[s][i] = __builtin_bit_cast(h8v, As[swz(wm + 32 * i + lr, 2 * s + lg)]);
+    for (int i = 0; i < kTM; ++i) f.a[s][i] = *reinterpret_cast<const h8v*>(stage + o.a[s] + 4096 * i);
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) f.b[s][j] = __builtin_bit_cast(h8v, Bs[swz(wn + 32 * j + lr, 2 * s + lg)]);
+    for (int j = 0; j < kTN; ++j) f.b[s][j] = *reinterpret_cast<const h8v*>(stage + o.b[s] + 4096 * j);
   }
 }
 
@@ -347,6 +366,47 @@ __device__ __forceinline__ void dma_stage(const GemmArgs& g, int m0, int n0, int
   }
 }
 
+// Plain GEMMs: the same copies with the k offset of a stage in the scalar base. Each lane keeps the
+// byte offset of its 16-byte chunk (row * ld + swizzled chunk) for every copy it issues, so a stage
+// costs kA + kB copy instructions and no vector address arithmetic (the per-stage 64-bit address
+// updates were half the vector instructions of the main loop). The host keeps both operands below
+// 4 GiB, the range of the 32-bit offsets.
+template <int BM, int kNW>
+struct CopyOffsets {
+  static constexpr int kA = BM / 8 / kNW, kB = kBN / 8 / kNW;  // copies per wave and stage
+  uint32_t a[kA], b[kB];
+};
+
+template <int BM, int kNW>
+__device__ __forceinline__ void copy_offsets(const GemmArgs& g, int m0, int n0, int wave, int lane,
+                                             CopyOffsets<BM, kNW>& c) {
+  using C = CopyOffsets<BM, kNW>;
+  const int rsub = lane >> 3, slot = lane & 7;
+#pragma unroll
+  for (int i = 0; i < C::kA; ++i) {
+    const int row = (wave * C::kA + i) * 8 + rsub;
+    const int gm = min(m0 + row, g.m - 1);  // rows past m are computed and never stored
+    c.a[i] = static_cast<uint32_t>((static_cast<size_t>(gm) * g.lda + swz_slot(row, slot) * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < C::kB; ++i) {
+    const int row = (wave * C::kB + i) * 8 + rsub;
+    c.b[i] = static_cast<uint32_t>((static_cast<size_t>(n0 + row) * g.ldw + swz_slot(row, slot) * 8) * 2);
+  }
+}
+
+template <int BM, int kNW>
+__device__ __forceinline__ void dma_stage_s(const GemmArgs& g, const CopyOffsets<BM, kNW>& c, int kt, int wave,
+                                            uint32_t lds_stage) {
+  using C = CopyOffsets<BM, kNW>;
+  const char* ab = reinterpret_cast<const char*>(g.a) + static_cast<size_t>(kt) * (kBK * 2);
+  const char* wb = reinterpret_cast<const char*>(g.w) + static_cast<size_t>(kt) * (kBK * 2);
+#pragma unroll
+  for (int i = 0; i < C::kA; ++i) dma16_s(c.a[i], ab, lds_stage + (wave * C::kA + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < C::kB; ++i) dma16_s(c.b[i], wb, lds_stage + BM * 128 + (wave * C::kB + i) * 1024);
+}
+
 // v columns of the q/k/v projection -> vt[head * 64 + d][vt_pos(t)]; rows in [m, vt_pad) get zeros so
 // the padding keys of the last attention tile hold finite values. The tile is transposed through LDS
 // (the operand ring is free once every wave has left the main loop): each lane puts its 4-row runs
@@ -407,10 +467,12 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
     g.a += static_cast<size_t>(split) * g.k;
     g.w += static_cast<size_t>(split) * g.k;
   }
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave is uniform: the copies' LDS targets and the offsets that depend on it stay scalar
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = (wave / kNWN) * kWM, wn = (wave % kNWN) * (kBN / kNWN);
   const int lr = lane & 31, lg = lane >> 5;
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
+  const char* lds_bytes = reinterpret_cast<const char*>(lds);
 
   f16v acc[kTM][kTN];
 #pragma unroll
@@ -420,24 +482,34 @@ __global__ void __launch_bounds__(gemm_waves<BM>() * 64) gemm_dma_kernel(GemmArg
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  CopyOffsets<BM, kNW> co;
+  if constexpr (!CONV) copy_offsets<BM, kNW>(g, m0, n0, wave, lane, co);
+  const FragOffsets fo = frag_offsets<BM>(wm, wn, lr, lg);
+  auto issue = [&](int kt, int ring_slot) {  // stage kt's copies into ring slot ring_slot
+    const uint32_t dst = lds0 + ring_slot * kStageBytes;
+    if constexpr (CONV)
+      dma_stage<BM, true>(g, m0, n0, kt * kBK, wave, lane, dst);
+    else
+      dma_stage_s<BM, kNW>(g, co, kt, wave, dst);
+  };
   const int kt_n = g.k / kBK;
 #pragma unroll
   for (int s = 0; s < kDmaStages; ++s)
-    if (s < kt_n) dma_stage<BM, CONV>(g, m0, n0, s * kBK, wave, lane, lds0 + s * kStageBytes);
-  auto slot = [&](int kt) { return lds + (kt % kDmaStages) * (kStageBytes / 16); };
+    if (s < kt_n) issue(s, s);
   Frags<kTM, kTN> fa, fb;
   // this thread's copies of stage kt have landed once at most the later issued stages remain
   wait_stages_ahead<kPerStage, kDmaStages - 1>(min(kDmaStages - 1, kt_n - 1));
   barrier_only();
-  load_frags<kTM, kTN>(slot(0), slot(0) + BM * 8, wm, wn, lr, lg, fa);
+  load_frags<kTM, kTN>(lds_bytes, fo, fa);
+  int cur = 0;  // ring slot of stage kt
   // stage kt with a stage kt + 1 after it
-  auto step = [&](int kt, const Frags<kTM, kTN>& cur, Frags<kTM, kTN>& nxt) {
+  auto step = [&](int kt, const Frags<kTM, kTN>& frags_kt, Frags<kTM, kTN>& nxt) {
     wait_stages_ahead<kPerStage, kDmaStages - 1>(min(kDmaStages - 2, kt_n - 2 - kt));
     lds_barrier();  // own fragment reads of stage kt done; stage kt + 1 visible; slot kt free
-    if (kt + kDmaStages < kt_n)
-      dma_stage<BM, CONV>(g, m0, n0, (kt + kDmaStages) * kBK, wave, lane, lds0 + (kt % kDmaStages) * kStageBytes);
-    load_frags<kTM, kTN>(slot(kt + 1), slot(kt + 1) + BM * 8, wm, wn, lr, lg, nxt);
-    mma_frags<kTM, kTN, kT>(cur, acc);
+    if (kt + kDmaStages < kt_n) issue(kt + kDmaStages, cur);
+    cur = cur + 1 == kDmaStages ? 0 : cur + 1;
+    load_frags<kTM, kTN>(lds_bytes + cur * kStageBytes, fo, nxt);
+    mma_frags<kTM, kTN, kT>(frags_kt, acc);
   };
   int kt = 0;
   for (; kt + 2 < kt_n; kt += 2) {
@@ -603,6 +675,14 @@ void choose_xcd_groups(GemmArgs& g, int bm) {
   }
 }
 
+// The plain GEMMs address each operand as a scalar base plus a 32-bit per-lane byte offset
+// (dma_stage_s): the rows a block reads must lie within 4 GiB of the operand's start.
+bool copy_offsets_fit(const GemmArgs& g) {
+  constexpr size_t kLimit = static_cast<size_t>(1) << 32;
+  return (static_cast<size_t>(g.m - 1) * g.lda + kBK) * 2 < kLimit &&
+         (static_cast<size_t>(g.n - 1) * g.ldw + kBK) * 2 < kLimit;
+}
+
 template <int BM>
 int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
   const int tiles = (g.n / kBN) * ((g.m + BM - 1) / BM);
@@ -642,6 +722,7 @@ int launch_gemm_bm(GemmArgs g, int epi, hipStream_t s) {
     return fw_check_launch("conv1d");
   }
   }
+  if (!copy_offsets_fit(g)) return fw_fail(FW_EINVAL, "gemm: each operand must span less than 4 GiB");
   switch (epi) {
 #define FW_GEMM_CASE(E) \
   case E:               \
@@ -899,6 +980,7 @@ extern "C" int fw_gemm_splitk(const void* a, int lda, const void* w, int ldw, fl
   // the XCD rectangles of the plain GEMMs (both k halves of a tile land on the same XCD when the tile
   // count is a multiple of 8): 126 -> 84 MB fetched from beyond L2 for the encoder's fc2
   choose_xcd_groups(g, 128);
+  if (!copy_offsets_fit(g)) return fw_fail(FW_EINVAL, "gemm_splitk: each operand must span less than 4 GiB");
   const int tiles = (n / kBN) * ((m + 127) / 128);
   hipLaunchKernelGGL((gemm_dma_kernel<128, kEpiPartial>), dim3(splits * tiles), dim3(gemm_waves<128>() * 64), 0,
                      stream, g);

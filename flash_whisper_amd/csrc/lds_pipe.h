@@ -30,6 +30,13 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * 8 + swz_sl
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory", "m0");
 }
+// The same copy from a wave-uniform base (scalar registers) plus a 32-bit per-lane byte offset. A
+// loop that walks the base (one k stage after another) then needs no per-copy address arithmetic in
+// the vector unit: the offsets stay in registers and only the scalar base moves.
+__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 template <int N>
