@@ -47,6 +47,36 @@ __device__ __forceinline__ void ea_dma(const _Float16* kbase, int ld, const _Flo
   }
 }
 
+// The same copies for a tile whose 64 keys all lie below seq (every tile but a partial last one): the
+// tile's first key only moves the scalar bases, and each lane keeps the byte offsets of its four chunks
+// (rows of 64 keys or head dims times the row pitch, plus the swizzled chunk), so a stage costs no
+// vector address arithmetic. The host keeps 64 rows of either operand within the 32-bit offsets.
+struct EaCopyOffsets {
+  uint32_t k[2], v[2];
+};
+
+__device__ __forceinline__ EaCopyOffsets ea_offsets(int ld, int seq_pad, int wave, int lane) {
+  const int rsub = lane >> 3, slot = lane & 7;
+  EaCopyOffsets o;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = (2 * wave + i) * 8 + rsub;  // key row of the K tile, head dim of the V^T tile
+    o.k[i] = static_cast<uint32_t>((row * ld + swz_slot(row, slot) * 8) * 2);
+    o.v[i] = static_cast<uint32_t>((row * seq_pad + swz_slot(row, slot) * 8) * 2);
+  }
+  return o;
+}
+
+__device__ __forceinline__ void ea_dma_full(const _Float16* kbase, int ld, const _Float16* vtbase, int kv0,
+                                            const EaCopyOffsets& o, int wave, uint32_t stage) {
+  const _Float16* kb = kbase + static_cast<size_t>(kv0) * ld;
+  const _Float16* vb = vtbase + kv0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) dma16_s(o.k[i], kb, stage + (2 * wave + i) * 1024);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) dma16_s(o.v[i], vb, stage + kEaTileBytes + (2 * wave + i) * 1024);
+}
+
 // Scores are kept in log2 units (x log2 e). The running max m used for p = exp2(s - m) is only moved
 // when some lane of the wave sees a score more than kEaSlack above it, so p stays in [0, 2^kEaSlack]
 // (exact in fp16's range) and the O/l rescale runs on few tiles instead of every tile.
@@ -135,7 +165,7 @@ __global__ void __launch_bounds__(kEaWaves * 64) encoder_attention_kernel(const 
   const int bid = blockIdx.x, full = (nblk / 8) * 8;
   const int job = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
   const int head = job / qblocks, qb = job % qblocks;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wq = wave & (kEaQGroups - 1), half = wave / kEaQGroups;  // query group, key half (both wave-uniform)
   const int lr = lane & 31, lg = lane >> 5;
   const int ld = 3 * heads * kHeadDim, seq_pad = vt_pad(seq);
@@ -155,10 +185,14 @@ __global__ void __launch_bounds__(kEaWaves * 64) encoder_attention_kernel(const 
   // Stage p holds tiles 2p (half 0) and 2p + 1 (half 1). A half whose tile is past the end copies the
   // last tile again, so every thread issues the same number of copies per stage (the vmcnt waits
   // count this thread's own copies).
+  const EaCopyOffsets co = ea_offsets(ld, seq_pad, wq, lane);
   auto issue = [&](int p) {
     const int t = min(2 * p + half, nt - 1);
-    ea_dma(kbase, ld, vtbase, seq_pad, seq, t * kEaKV, wq, lane,
-           lds0 + (p % kEaStages) * kPairBytes + half * 2 * kEaTileBytes);
+    const uint32_t stage = lds0 + (p % kEaStages) * kPairBytes + half * 2 * kEaTileBytes;
+    if ((t + 1) * kEaKV <= seq)  // wave-uniform; both forms issue the same four copies
+      ea_dma_full(kbase, ld, vtbase, t * kEaKV, co, wq, stage);
+    else
+      ea_dma(kbase, ld, vtbase, seq_pad, seq, t * kEaKV, wq, lane, stage);
   };
 #pragma unroll
   for (int k = 0; k < kEaStages - 1; ++k)
@@ -264,6 +298,9 @@ extern "C" int fw_encoder_attention(const void* qkv, const void* vt, void* out, 
                                     hipStream_t stream) {
   if (!qkv || !vt || !out) return fw_fail(FW_EINVAL, "encoder_attention: null pointer");
   if (seq <= 0 || heads <= 0) return fw_fail(FW_EINVAL, "encoder_attention: seq and heads must be positive");
+  // 64 rows of K (pitch 3 heads 64) or of V^T (pitch vt_pad(seq)) within the copies' 32-bit byte offsets
+  if (64LL * 3 * heads * kHeadDim * 2 >= (1LL << 32) || 64LL * vt_pad(seq) * 2 >= (1LL << 32))
+    return fw_fail(FW_EINVAL, "encoder_attention: seq or heads too large");
   if (!aligned(qkv, 16) || !aligned(vt, 16) || !aligned(out, 8))
     return fw_fail(FW_EINVAL, "encoder_attention: qkv and vt must be 16-byte aligned, out 8-byte aligned");
   const int blocks = (seq + kEaQ - 1) / kEaQ * heads;
