@@ -57,7 +57,22 @@ SIGNATURES = {
     'fw_cross_kv': (c_int, [P, c_int, P, P, P, c_int, c_int, P]),
     'fw_synth_normal_f16': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float, P]),
     'fw_synth_normal_f16_host': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float]),
+    'fw_decoder_step_workspace_bytes': (ctypes.c_size_t, [c_int]),
+    'fw_decoder_step_max_layers': (c_int, []),
+    'fw_decoder_step_layers': (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, P, P, c_int64, c_int64,
+                                       P]),
 }
+
+DEC_LAYER_TENSORS = ('ln1_gamma', 'ln1_beta', 'qkv_w', 'qkv_b', 'out_w', 'out_b', 'ln2_gamma', 'ln2_beta',
+                     'cross_q_w', 'cross_q_b', 'cross_out_w', 'cross_out_b', 'ln3_gamma', 'ln3_beta', 'fc1_w',
+                     'fc1_b', 'fc2_w', 'fc2_b')
+
+
+class DecLayer(ctypes.Structure):
+    """struct fw_dec_layer: one decoder layer's device pointers for fw_decoder_step_layers."""
+    _fields_ = ([(n, c_void_p) for n in DEC_LAYER_TENSORS] + [(f'ln{i}_eps', c_float) for i in (1, 2, 3)]
+                + [(n, c_void_p) for n in ('self_k', 'self_v', 'cross_k', 'cross_v')])
+
 
 _lib = None
 _lock = threading.Lock()

@@ -8,231 +8,11 @@
 #include <atomic>
 #include <mutex>
 
+#include "decode_dev.h"
 #include "fw_common.h"
 
 namespace fw {
 namespace {
-
-#ifndef FW_GEMV_WEIGHTS_NT
-#define FW_GEMV_WEIGHTS_NT 0  // decoder weights may stay resident in the 256 MB MALL
-#endif
-#ifndef FW_LM_HEAD_NT
-#define FW_LM_HEAD_NT 1
-#endif
-static_assert((FW_GEMV_WEIGHTS_NT == 0 || FW_GEMV_WEIGHTS_NT == 1) && (FW_LM_HEAD_NT == 0 || FW_LM_HEAD_NT == 1),
-              "FW_GEMV_WEIGHTS_NT and FW_LM_HEAD_NT are switches (0 or 1)");
-__device__ __forceinline__ uint4 ld_weights(const uint4* p) {
-#if FW_GEMV_WEIGHTS_NT
-  return ld_stream(p);
-#else
-  return *p;
-#endif
-}
-__device__ __forceinline__ uint4 ld_lm_head(const uint4* p) {
-#if FW_LM_HEAD_NT
-  return ld_stream(p);
-#else
-  return *p;
-#endif
-}
-
-// ------------------------------------------------------------------------------------------
-// Residual + LayerNorm prologue shared by add_layernorm, the fused LN+GEMV and the LM head.
-// Produces y = fp16(LN(r) * gamma + beta) for the 1280-wide hidden vector in `y_out` (LDS or
-// global), where r = fp16(a + b) (b may be null) and a, b are either (h, x) or the embedding rows
-// (embed[cur], pos_embed[pos]). Block 0 stores r to r_out when r_out is non-null.
-// ------------------------------------------------------------------------------------------
-// The inputs are loaded into registers by ln_load and consumed by ln_finish, so a kernel can issue
-// its other global loads (the weight rows) in between: vector-memory counters retire in order, and
-// inputs requested after the weights could not be used before the weights had arrived.
-template <int NT>
-struct LnRegs {
-  static constexpr int kPairs = kHidden / 2;
-  static constexpr int kPer = (kPairs + NT - 1) / NT;
-  h2v a[kPer], b[kPer], g[kPer], be[kPer];
-};
-
-template <int NT>
-__device__ __forceinline__ void ln_load(const _Float16* a, const _Float16* b, const _Float16* gamma,
-                                        const _Float16* beta, LnRegs<NT>& in) {
-  const h2v* a2 = reinterpret_cast<const h2v*>(a);
-  const h2v* b2 = reinterpret_cast<const h2v*>(b);
-  const h2v* g2 = reinterpret_cast<const h2v*>(gamma);
-  const h2v* be2 = reinterpret_cast<const h2v*>(beta);
-  const h2v zero = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
-#pragma unroll
-  for (int i = 0; i < LnRegs<NT>::kPer; ++i) {
-    const int idx = threadIdx.x + i * NT;
-    const bool ok = idx < LnRegs<NT>::kPairs;
-    in.a[i] = ok ? a2[idx] : zero;
-    in.b[i] = (ok && b2) ? b2[idx] : zero;
-    in.g[i] = ok ? g2[idx] : zero;
-    in.be[i] = ok ? be2[idx] : zero;
-  }
-}
-
-// kOwnSlots: the two reductions use red[0 .. NT/64) and red[NT/64 .. 2 NT/64) with one barrier each
-// (the same sums); red must then hold 2 NT/64 floats and is free again after the caller's next barrier.
-template <int NT, bool kOwnSlots = false>
-__device__ __forceinline__ void ln_finish(const LnRegs<NT>& in, bool has_b, _Float16* r_out, float eps,
-                                          _Float16* y_out, float* red) {
-  constexpr int kPer = LnRegs<NT>::kPer;
-  h2v* r2 = reinterpret_cast<h2v*>(r_out);
-  h2v* y2 = reinterpret_cast<h2v*>(y_out);
-  float2 r[kPer];
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int idx = threadIdx.x + i * NT;
-    r[i] = make_float2(0.f, 0.f);
-    if (idx < LnRegs<NT>::kPairs) {
-      float rx = h2f(in.a[i].x), ry = h2f(in.a[i].y);
-      if (has_b) {
-        rx = round_h(rx + h2f(in.b[i].x));
-        ry = round_h(ry + h2f(in.b[i].y));
-      }
-      r[i] = make_float2(rx, ry);
-      sum += rx + ry;
-      if (r2 && blockIdx.x == 0) {
-        h2v o;
-        o.x = f2h(rx);
-        o.y = f2h(ry);
-        r2[idx] = o;
-      }
-    }
-  }
-  const float mean = (kOwnSlots ? block_sum_once<NT>(sum, red) : block_sum<NT>(sum, red)) * (1.0f / kHidden);
-  float sq = 0.f;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int idx = threadIdx.x + i * NT;
-    if (idx < LnRegs<NT>::kPairs) {
-      const float dx = r[i].x - mean, dy = r[i].y - mean;
-      sq += dx * dx + dy * dy;
-    }
-  }
-  const float var = (kOwnSlots ? block_sum_once<NT>(sq, red + NT / kWave) : block_sum<NT>(sq, red)) * (1.0f / kHidden);
-  const float inv = rsqrtf(var + eps);
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int idx = threadIdx.x + i * NT;
-    if (idx < LnRegs<NT>::kPairs) {
-      h2v o;
-      o.x = f2h((r[i].x - mean) * inv * h2f(in.g[i].x) + h2f(in.be[i].x));
-      o.y = f2h((r[i].y - mean) * inv * h2f(in.g[i].y) + h2f(in.be[i].y));
-      y2[idx] = o;
-    }
-  }
-}
-
-// ln_finish for NV vectors at once: the vectors' sums share each reduction round (two barriers in all
-// instead of four per vector). Every value is reduced in the order block_sum uses (the wave butterfly,
-// then the wave partials in wave order), so each vector's result is that of ln_finish on it alone.
-// red holds 2 * NV * (NT / 64) floats.
-template <int NT, int NV>
-__device__ __forceinline__ void ln_finish_multi(const LnRegs<NT> (&in)[NV], bool has_b, _Float16* r_out, float eps,
-                                                _Float16* y_out, float* red) {
-  constexpr int kPer = LnRegs<NT>::kPer, kWaves = NT / kWave;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  float2 r[NV][kPer];
-  float part[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    h2v* r2 = r_out ? reinterpret_cast<h2v*>(r_out + v * kHidden) : nullptr;
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      r[v][i] = make_float2(0.f, 0.f);
-      if (idx < LnRegs<NT>::kPairs) {
-        float rx = h2f(in[v].a[i].x), ry = h2f(in[v].a[i].y);
-        if (has_b) {
-          rx = round_h(rx + h2f(in[v].b[i].x));
-          ry = round_h(ry + h2f(in[v].b[i].y));
-        }
-        r[v][i] = make_float2(rx, ry);
-        sum += rx + ry;
-        if (r2 && blockIdx.x == 0) {
-          h2v o;
-          o.x = f2h(rx);
-          o.y = f2h(ry);
-          r2[idx] = o;
-        }
-      }
-    }
-    part[v] = group_sum<kWave>(sum);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) red[v * kWaves + wave] = part[v];
-  }
-  __syncthreads();
-  float mean[NV];
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) s += red[v * kWaves + w];
-    mean[v] = s * (1.0f / kHidden);
-  }
-  float* red2 = red + NV * kWaves;
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float sq = 0.f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < LnRegs<NT>::kPairs) {
-        const float dx = r[v][i].x - mean[v], dy = r[v][i].y - mean[v];
-        sq += dx * dx + dy * dy;
-      }
-    }
-    part[v] = group_sum<kWave>(sq);
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) red2[v * kWaves + wave] = part[v];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int v = 0; v < NV; ++v) {
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) s += red2[v * kWaves + w];
-    const float inv = rsqrtf(s * (1.0f / kHidden) + eps);
-    h2v* y2 = reinterpret_cast<h2v*>(y_out + v * kHidden);
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int idx = threadIdx.x + i * NT;
-      if (idx < LnRegs<NT>::kPairs) {
-        h2v o;
-        o.x = f2h((r[v][i].x - mean[v]) * inv * h2f(in[v].g[i].x) + h2f(in[v].be[i].x));
-        o.y = f2h((r[v][i].y - mean[v]) * inv * h2f(in[v].g[i].y) + h2f(in[v].be[i].y));
-        y2[idx] = o;
-      }
-    }
-  }
-}
-
-template <int NT>
-__device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b, _Float16* r_out,
-                                            const _Float16* gamma, const _Float16* beta, float eps,
-                                            _Float16* y_out, float* red) {
-  LnRegs<NT> in;
-  ln_load<NT>(a, b, gamma, beta, in);
-  ln_finish<NT>(in, b != nullptr, r_out, eps, y_out, red);
-}
-
-// Token and position embedding rows of vector v of a batch: token cur[v] at position state[0] + v.
-__device__ __forceinline__ void embed_rows(const int64_t* cur, const int64_t* state, const _Float16* embed,
-                                           const _Float16* pos_embed, int vocab, int max_pos, const _Float16** a,
-                                           const _Float16** b, int v = 0) {
-  int64_t tok = cur[v], pos = state[0] + v;
-  tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
-  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
-  *a = embed + tok * kHidden;
-  *b = pos_embed + pos * kHidden;
-}
 
 // ------------------------------------------------------------------------------------------
 // add_layernorm (reference semantics: h updated in place, y written to global memory).
@@ -257,140 +37,6 @@ __global__ void __launch_bounds__(256) embed_kernel(const int64_t* cur, const in
 // arithmetic so every lane keeps U * kC 16-byte loads in flight. Blocks own contiguous row ranges.
 // With LN, the 1280-wide input is the LayerNorm of the residual, computed per block into LDS.
 // ------------------------------------------------------------------------------------------
-template <int K>
-struct RowSplit {
-  static constexpr int kChunksRow = K / 8;
-  static constexpr int kLPR = (K == kHidden) ? 32 : 64;
-  static constexpr int kC = kChunksRow / kLPR;
-  static constexpr int kRPW = kWave / kLPR;
-  static_assert(kChunksRow % kLPR == 0, "row must split evenly over the lanes");
-};
-
-struct LnArgs {
-  const _Float16* h;
-  const _Float16* x;
-  _Float16* h_out;
-  const _Float16* gamma;
-  const _Float16* beta;
-  float eps;
-  const int64_t* cur;
-  const int64_t* state;
-  const _Float16* embed;
-  const _Float16* pos_embed;
-  int vocab;
-  int max_pos;
-};
-
-// Split-K attention partials consumed by the GEMV that follows the attention (the out projection):
-// the combine of the reference's decode_attention_combine_kernel (whisper_kernels.cu:191-213) runs
-// as that GEMV's prologue, so the attention output never makes a round trip through a separate
-// launch. `len_state` (self attention) limits the combine to the splits that held keys.
-struct CombineArgs {
-  const float* part_m;
-  const float* part_l;
-  const float* part_acc;
-  const int64_t* len_state;
-  int max_len;
-  int split_keys;
-  int nsplit;
-  int heads;
-  int pos_offset;  // vector v of a batch attends at position len_state[0] + v
-
-  // The partials of vector v of a batch (laid out vector-major, heads * nsplit slots each).
-  __device__ CombineArgs vec(int v) const {
-    CombineArgs c = *this;
-    const size_t slots = static_cast<size_t>(heads) * nsplit;
-    c.part_m += v * slots;
-    c.part_l += v * slots;
-    c.part_acc += v * slots * kHeadDim;
-    c.pos_offset = v;
-    return c;
-  }
-};
-
-constexpr int kMaxCombineSplits = 8;   // splits per head the combine prologue merges
-constexpr int kMaxCombineHeads = 32;
-
-__device__ __forceinline__ int active_splits(const int64_t* len_state, int max_len, int split_keys, int nsplit,
-                                             int pos_offset = 0) {
-  if (!len_state) return nsplit;
-  int64_t p = len_state[0] + pos_offset;
-  p = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
-  return static_cast<int>((p + split_keys) / split_keys);  // ceil((p + 1) / split_keys)
-}
-
-// x[h * 64 + d] = fp16(sum_s acc[h, s, d] e^(m_s - M) / sum_s l_s e^(m_s - M)), splits with l = 0 skipped
-// (the arithmetic of the combine launch). combine_load requests every partial a thread needs;
-// combine_finish merges them once they have landed.
-template <int NT>
-struct CombineRegs {
-  static constexpr int kPer = (kHidden + NT - 1) / NT;
-  float pm[kMaxCombineSplits], pl[kMaxCombineSplits];
-  float pa[kPer][kMaxCombineSplits];
-  int active;
-};
-
-template <int NT>
-__device__ __forceinline__ void combine_load(const CombineArgs& c, CombineRegs<NT>& r) {
-  constexpr int S = kMaxCombineSplits;
-  r.active = active_splits(c.len_state, c.max_len, c.split_keys, c.nsplit, c.pos_offset);
-  const int h0 = threadIdx.x;  // threads below `heads` also own one head's weights
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const bool ok = h0 < c.heads && s < r.active;
-    r.pm[s] = ok ? c.part_m[h0 * c.nsplit + s] : -INFINITY;
-    r.pl[s] = ok ? c.part_l[h0 * c.nsplit + s] : 0.f;
-  }
-#pragma unroll
-  for (int i = 0; i < CombineRegs<NT>::kPer; ++i) {
-    const int j = threadIdx.x + i * NT;
-    const int h = j / kHeadDim, d = j % kHeadDim;
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-      r.pa[i][s] = (j < c.heads * kHeadDim && s < r.active)
-                       ? c.part_acc[(static_cast<size_t>(h) * c.nsplit + s) * kHeadDim + d] : 0.f;
-  }
-}
-
-template <int NT>
-__device__ __forceinline__ void combine_finish(const CombineArgs& c, const CombineRegs<NT>& r, _Float16* x,
-                                               float* wgt, float* den_lds) {
-  constexpr int S = kMaxCombineSplits;
-  static_assert(NT >= kMaxCombineHeads, "one thread per head computes the split weights");
-  if (threadIdx.x < c.heads) {
-    const int h = threadIdx.x;
-    float m = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < S; ++s) m = fmaxf(m, r.pm[s]);
-    float den = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const float w = r.pl[s] > 0.f ? __expf(r.pm[s] - m) : 0.f;
-      wgt[h * S + s] = w;
-      den = fmaf(r.pl[s], w, den);
-    }
-    den_lds[h] = den;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < CombineRegs<NT>::kPer; ++i) {
-    const int j = threadIdx.x + i * NT;
-    if (j < c.heads * kHeadDim) {
-      const int h = j / kHeadDim;
-      float num = 0.f;
-#pragma unroll
-      for (int s = 0; s < S; ++s)
-        if (wgt[h * S + s] != 0.f) num = fmaf(r.pa[i][s], wgt[h * S + s], num);
-      x[j] = f2h(num / den_lds[h]);
-    }
-  }
-}
-
-constexpr int kModePlain = 0, kModeLn = 1, kModeCombine = 2;
-
-// Stands in for a missing bias: a load from it replaces a branch around the bias load (a branch
-// whose join would wait for every load issued before it).
-__device__ _Float16 g_zero_half = static_cast<_Float16>(0.f);
 
 // NV input vectors (a batch of decoder positions, NV <= kMaxBatch) share every weight row load: vector
 // v reads x / h / h_out at offset v * K and writes out + v * n; its LN or combine prologue is that of
@@ -599,23 +245,6 @@ static_assert(FW_LM_BPC >= 1 && FW_LM_BPC <= 4, "FW_LM_BPC: 1..4 blocks per CU")
 constexpr int kLmNW = FW_LM_NW, kLmU = FW_LM_U;
 constexpr int kLmRowsIter = kLmNW * 2 * kLmU;  // rows per block iteration
 
-struct FinArgs {
-  int64_t* tokens;
-  int64_t* state;
-  int64_t* cur;
-  int max_pos;
-};
-
-__device__ __forceinline__ void finalize_token(unsigned long long* best, const FinArgs& f) {
-  const unsigned long long b = *best;
-  *best = 0ull;
-  const int64_t tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
-  const int64_t n = f.state[1];
-  if (n < f.max_pos) f.tokens[n] = tok;
-  f.state[1] = n < f.max_pos ? n + 1 : n;
-  f.state[0] = f.state[0] + 1 < f.max_pos ? f.state[0] + 1 : f.max_pos - 1;
-  *f.cur = tok;
-}
 
 template <bool LN>
 __global__ void __launch_bounds__(kLmNW * 64) lm_head_kernel(const _Float16* __restrict__ yin, LnArgs ln,
@@ -973,116 +602,6 @@ int lm_head_q8_grid(int vocab) {
   return (batches + 3) / 4;
 }
 
-// ------------------------------------------------------------------------------------------
-// Split-K single-query attention (flash-decoding; reference decode_attention_split_kernel,
-// whisper_kernels.cu:102-189). Block (split, head) covers split_keys keys. A key row is 64 fp16 =
-// 8 lanes x 16 bytes, so one wave scores 8 keys per pass and a 256-thread block 32 keys. Scores,
-// max and exp-sum stay in fp32; the block writes its (m, l, acc[64]) partial and a second launch
-// merges them (reference decode_attention_combine_kernel, :191-213). Self mode reads
-// len = state[0] + 1 from device memory and the block owning row pos writes k_new/v_new into the
-// cache while using the new row directly.
-// ------------------------------------------------------------------------------------------
-struct AttnArgs {
-  const _Float16* q;
-  _Float16* k;
-  _Float16* v;
-  const _Float16* k_new;
-  const _Float16* v_new;
-  const int64_t* len_state;
-  int max_len;
-  int split_keys;
-  float scale;
-  float* part_m;
-  float* part_l;
-  float* part_acc;
-  _Float16* out;
-  // batches of queries (split kernel, grid.z): query z is q + z * q_stride at position len_state[0] + z,
-  // and its fresh K/V row is k_new / v_new + z * kv_stride
-  int q_stride;
-  int kv_stride;
-};
-
-__device__ __forceinline__ int attn_pos(const AttnArgs& a) {
-  if (!a.len_state) return -1;
-  const int64_t p = a.len_state[0];
-  return static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
-}
-
-// The scores, softmax and P.V of one wave's keys of a split (MAXP passes of 8 keys, keys at or past w1
-// masked): the wave's (max, exp-sum, value sum) go to wm, wl and wacc_row for split_merge_store. Lane
-// l holds key w0 + 8 p + l / 8 of pass p and chunk l % 8 of its row; fp32 throughout, the scale
-// applied after the dot.
-template <int MAXP>
-__device__ __forceinline__ void split_wave_partial(const uint4 (&kr)[MAXP], const uint4 (&vr)[MAXP], const uint4& qc,
-                                                   int w0, int w1, float scale, float* wm, float* wl,
-                                                   float* wacc_row) {
-  const int lane = threadIdx.x & 63, ks = lane >> 3, c = lane & 7;
-  float sc[MAXP];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int p = 0; p < MAXP; ++p) {
-    sc[p] = group_sum<8>(dot8(kr[p], qc, 0.f)) * scale;
-    if (w0 + p * 8 + ks >= w1) sc[p] = -INFINITY;
-    mx = fmaxf(mx, sc[p]);
-  }
-  mx = group_max<64>(mx);
-  float acc[8], psum = 0.f;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) acc[t] = 0.f;
-  if (mx != -INFINITY) {
-#pragma unroll
-    for (int p = 0; p < MAXP; ++p) {
-      const float pj = __expf(sc[p] - mx);
-      psum += pj;
-      const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
-        acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
-      }
-    }
-  }
-  psum = xor_add<32>(xor_add<16>(xor_add<8>(psum)));
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    acc[t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[t])));
-  }
-  if (lane == 0) {
-    *wm = mx;
-    *wl = psum;
-  }
-  if (ks == 0) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) wacc_row[c * 8 + t] = acc[t];
-  }
-}
-
-// After a block barrier: thread d < 64 merges the NW wave partials in wave order and stores the
-// split's (m, l, acc[d]) at `slot`.
-template <int NW>
-__device__ __forceinline__ void split_merge_store(const float* wm, const float* wl, const float (*wacc)[kHeadDim],
-                                                  const AttnArgs& a, int slot) {
-  const int tid = threadIdx.x;
-  if (tid < kHeadDim) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) m = fmaxf(m, wm[w]);
-    float l = 0.f, o = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      if (wl[w] > 0.f) {
-        const float wgt = __expf(wm[w] - m);
-        l = fmaf(wl[w], wgt, l);
-        o = fmaf(wacc[w][tid], wgt, o);
-      }
-    }
-    a.part_acc[static_cast<size_t>(slot) * kHeadDim + tid] = o;
-    if (tid == 0) {
-      a.part_m[slot] = m;
-      a.part_l[slot] = l;
-    }
-  }
-}
 
 // BATCH: a batch of queries (grid.z, the prompt) takes the fresh K/V rows of the batch's earlier
 // queries straight from k_new / v_new: their cache rows are written by other blocks of the same

@@ -1,0 +1,867 @@
+// The decoder layers of one token (reference custom/model.py:107-121) as one persistent launch.
+//
+// The 34-launch step pays a kernel boundary between every pair of dependent operations: the end of
+// a kernel writes its XCD's L2 back, the next kernel is dispatched and its blocks read the vector the
+// previous one wrote from the MALL. Here one block per CU runs every operation of every layer in
+// turn, and each operation hands its output vector to the next with tagged stores instead: every
+// 8-byte word carries 4 bytes of payload (two fp16, or one fp32) and a 4-byte tag, written with one
+// agent-scope store and read with agent-scope loads that repeat until the tag is the launch's (the
+// low-latency protocol of ring collectives). A word's payload and tag arrive together, so no fence,
+// flag or barrier sits between producer and consumer; a consumer waits one store-to-load trip.
+//
+// Per layer the operations ("phases") are those of the 34-launch step, with its arithmetic:
+//   1 residual + LN1 + q/k/v GEMV          5 cross-attention splits (256 keys)
+//   2 self-attention splits (64 keys)      6 combine + cross-out GEMV
+//   3 combine + out GEMV                   7 residual + LN3 + fc1 + GELU
+//   4 residual + LN2 + cross-q GEMV        8 fc2 GEMV
+// Each phase runs on a run of blocks that did not work in the previous phase, so its workers have
+// requested their weight rows (or K/V rows) before its input arrives. The residual stream lives in
+// every block's LDS; a block adds the vectors it missed, in order, before its next LayerNorm. Every
+// row's dot, the LayerNorm reductions (512-thread blocks, as the LN+GEMV launches), the split
+// attention (4-wave items) and the combine are the device functions of the separate launches, so the
+// outputs are bit-identical to the 34-launch step.
+//
+// Every wait is bounded: past a time limit a block flags an error in the control words and carries
+// on with what it has, so the launch always drains. All blocks must be resident at once: one block
+// per CU, and nothing else running on the device while the step runs.
+#include "decode_dev.h"
+
+namespace fw {
+namespace {
+
+constexpr int kStepWaves = 8;
+constexpr int kStepThreads = kStepWaves * kWave;  // the LN+GEMV launches' block size: same LN reduction order
+constexpr int kStepHeads = 20;
+constexpr int kStepFfn = 4 * kHidden;
+constexpr int kSelfSplitKeys = 64, kCrossSplitKeys = 256;
+constexpr int kStepMaxLayers = 8;
+constexpr int kPartWords = kHeadDim + 2;  // acc[64], m, l of one split
+constexpr int kPartRegion = kStepHeads * kMaxCombineSplits * kPartWords;
+// Tagged-word regions of one layer (8-byte words; a vector of fp16 takes one word per pair)
+constexpr int kQkvWords = 3 * kHidden / 2, kVecWords = kHidden / 2, kFfnWords = kStepFfn / 2;
+constexpr int kOffQkv = 0;
+constexpr int kOffSelfVec = kOffQkv + kQkvWords;     // self-attention output (640 words)
+constexpr int kOffAttnOut = kOffSelfVec + kVecWords;
+constexpr int kOffCrossQ = kOffAttnOut + kVecWords;
+constexpr int kOffCrossPart = kOffCrossQ + kVecWords;
+constexpr int kOffCrossVec = kOffCrossPart + kPartRegion;  // cross-attention output (640 words)
+constexpr int kOffCrossOut = kOffCrossVec + kVecWords;
+constexpr int kOffFfn = kOffCrossOut + kVecWords;
+constexpr int kOffMlpOut = kOffFfn + kFfnWords;
+constexpr int kLayerWords = kOffMlpOut + kVecWords;
+constexpr int kCtlBytes = 256;  // control words ahead of the regions: [0] epoch, [1] arrivals, [2] error
+// Worker counts of the phases that need few blocks (pairs of rows / items are spread over them).
+constexpr int kVecWorkers = 80;    // 640 row pairs: one pair per wave
+constexpr int kCrossWorkers = 60;  // 20 heads x 6 splits of the cross attention, two items per block
+static_assert(kStepHeads * kHeadDim == kHidden, "20 heads of 64");
+static_assert(kStepThreads == 512, "the LayerNorm reduction order of the 8-wave LN+GEMV launches");
+
+struct StepLayer {
+  const _Float16 *ln1_g, *ln1_b, *qkv_w, *qkv_b, *out_w, *out_b;
+  const _Float16 *ln2_g, *ln2_b, *cq_w, *cq_b, *co_w, *co_b;
+  const _Float16 *ln3_g, *ln3_b, *fc1_w, *fc1_b, *fc2_w, *fc2_b;
+  float eps1, eps2, eps3;
+  _Float16 *self_k, *self_v;
+  const _Float16 *cross_k, *cross_v;
+};
+
+struct StepArgs {
+  StepLayer layer[kStepMaxLayers];
+  int n_layers;
+  const int64_t* cur;
+  const int64_t* state;
+  const _Float16* embed;
+  const _Float16* pos_embed;
+  int vocab, max_pos, enc_len;
+  float scale;
+  _Float16* h_out;  // residual stream before the last fc2 output is added
+  _Float16* x_out;  // last fc2 output
+  unsigned char* ws;
+  long long spin_limit;  // wall-clock ticks (100 MHz) a wait may take before it flags an error
+};
+
+struct Ll {
+  unsigned* ctl;
+  unsigned tag;
+  long long limit;
+};
+
+__device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_store(uint64_t* p, unsigned tag, unsigned v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Payloads of the words buf[idx[k]] (idx[k] < 0: not wanted) once each carries the launch's tag. All
+// words are requested at once and only the missing ones again. With kPlain the first read goes through
+// the L2 (blocks of one XCD that read the same words then share one fetch); a word that comes back
+// stale (an old tag: the L2 may hold a line from before its last write) is polled again with
+// agent-scope loads, which always reach the coherent copy. Bounded: a wait that outlives the time
+// limit, or that sees another block's error flag, stops and returns what it read.
+template <int N, bool kPlain = false>
+__device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N], unsigned (&val)[N], const Ll& c) {
+  uint64_t w[N];
+  const uint64_t want = static_cast<uint64_t>(c.tag) << 32;
+#pragma unroll
+  for (int k = 0; k < N; ++k) w[k] = idx[k] >= 0 ? (kPlain ? buf[idx[k]] : ll_load(buf + idx[k])) : want;
+  static_assert(N <= 64, "one pending bit per word");
+  unsigned long long pending = 0;
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+    pending |= static_cast<unsigned long long>(static_cast<unsigned>(w[k] >> 32) != c.tag) << k;
+  if (pending) {
+    const long long t0 = wall_clock64();
+    for (int it = 1; pending; ++it) {
+      if (!kPlain || it > 1) __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int k = 0; k < N; ++k)
+        if (pending >> k & 1ull) w[k] = ll_load(buf + idx[k]);
+      pending = 0;
+#pragma unroll
+      for (int k = 0; k < N; ++k)
+        pending |= static_cast<unsigned long long>(static_cast<unsigned>(w[k] >> 32) != c.tag) << k;
+      if (pending && (it & 15) == 0) {
+        if (__hip_atomic_load(c.ctl + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+        if (wall_clock64() - t0 > c.limit) {
+          __hip_atomic_store(c.ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) val[k] = static_cast<unsigned>(w[k]);
+}
+
+// Wave 0 waits until each of the n <= 64 * kMaxSentinels sentinel words buf[i * stride + off] carries
+// the tag (all requested at once), then the block passes a barrier. A consumer polls one word per
+// producer this way before it reads the whole region, so blocks that wait long keep few requests in
+// the memory system.
+constexpr int kMaxSentinels = 5;
+__device__ __forceinline__ void ll_sentinels(const uint64_t* buf, int n, int stride, int off, const Ll& c) {
+  if (threadIdx.x < kWave) {
+    int idx[kMaxSentinels];
+#pragma unroll
+    for (int k = 0; k < kMaxSentinels; ++k) {
+      const int i = static_cast<int>(threadIdx.x) + k * kWave;
+      idx[k] = i < n ? i * stride + off : -1;
+    }
+    unsigned v[kMaxSentinels];
+    ll_wait<kMaxSentinels>(buf, idx, v, c);
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ unsigned half_bits(_Float16 x) { return __builtin_bit_cast(unsigned short, x); }
+
+// ---------------------------------------------------------------------------------------------
+// GEMV rows. A wave owns row pairs: for K = 1280 rows 2q and 2q + 1 side by side (32 lanes each, as
+// gemv_kernel), for K = 5120 one after the other (64 lanes each). Lane 0 stores the pair's word.
+// Rows are requested by gv_load before the phase's input arrives and scored by gv_finish.
+// ---------------------------------------------------------------------------------------------
+constexpr int kMaxPasses = 3;  // row pairs per wave requested ahead (the U of Gv)
+
+template <int K, int U>
+struct Gv {
+  static_assert(U >= 1 && U <= kMaxPasses, "the output staging holds kMaxPasses words per wave");
+  using RS = RowSplit<K>;
+  static constexpr int kRowsPerPair = K == kHidden ? 1 : 2;  // rows per pair held by one lane
+  uint4 w[U][kRowsPerPair][RS::kC];
+  _Float16 b[U][kRowsPerPair];
+  int q[U];  // pair index, or -1
+};
+
+template <int K, int U>
+__device__ __forceinline__ void gv_load(Gv<K, U>& g, const _Float16* __restrict__ w, const _Float16* __restrict__ bias,
+                                        int npairs, int q0, int qstride) {
+  using RS = RowSplit<K>;
+  const int lane = threadIdx.x & 63, sub = lane % RS::kLPR, rsel = lane / RS::kLPR;
+  const uint4* w4 = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int q = q0 + u * qstride;
+    g.q[u] = q < npairs ? q : -1;
+    const int qc = q < npairs ? q : npairs - 1;
+#pragma unroll
+    for (int r = 0; r < Gv<K, U>::kRowsPerPair; ++r) {
+      const int row = K == kHidden ? 2 * qc + rsel : 2 * qc + r;
+      g.b[u][r] = *(bias ? bias + row : &g_zero_half);
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) g.w[u][r][c] = ld_weights(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub + RS::kLPR * c);
+    }
+  }
+}
+
+// Scores the pairs requested by gv_load, then stores the block's words: wave w's word of pass u is
+// word base + u * qs + w, so each pass gives a run of 8 consecutive words, staged in LDS and written by
+// 8 lanes of wave 0 with one store (one coalesced write per line instead of one per wave). All waves
+// of the block call it (it has a barrier).
+template <int K, int U, int ACT>
+__device__ __forceinline__ void gv_finish(const Gv<K, U>& g, const _Float16* x_lds, unsigned* stage, uint64_t* out,
+                                          unsigned tag, _Float16* plain_out, int base, int qs, int npairs) {
+  using RS = RowSplit<K>;
+  const int lane = threadIdx.x & 63, sub = lane % RS::kLPR, wave = threadIdx.x >> 6;
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(x_lds)[sub + RS::kLPR * c];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (g.q[u] < 0) continue;  // wave-uniform
+    unsigned bits[Gv<K, U>::kRowsPerPair];
+#pragma unroll
+    for (int r = 0; r < Gv<K, U>::kRowsPerPair; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) acc = dot8(g.w[u][r][c], xr[c], acc);
+      acc = group_sum<RS::kLPR>(acc);
+      float y = acc + h2f(g.b[u][r]);
+      if constexpr (ACT == FW_ACT_GELU) y = gelu_erf(round_h(y));
+      // y is rounded to fp32 first, as gemv_kernel does (its store pins y the same way): without the
+      // pin the compiler may fold the GELU's last product into the fp16 conversion (one rounding
+      // instead of two), which differs in rare elements
+      asm volatile("" : "+v"(y));
+      bits[r] = half_bits(f2h(y));
+    }
+    unsigned lo, hi;
+    if constexpr (K == kHidden) {
+      lo = bits[0];
+      hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(bits[0]), 32));
+    } else {
+      lo = bits[0];
+      hi = bits[1];
+    }
+    if (lane == 0) stage[u * kStepWaves + wave] = lo | (hi << 16);
+  }
+  __syncthreads();
+  if (threadIdx.x < U * kStepWaves) {
+    const int u = threadIdx.x / kStepWaves, q = base + u * qs + static_cast<int>(threadIdx.x) % kStepWaves;
+    if (q < npairs) {
+      const unsigned word = stage[threadIdx.x];
+      ll_store(out + q, tag, word);
+      if (plain_out) reinterpret_cast<unsigned*>(plain_out)[q] = word;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// The residual stream is the token + position embedding plus, per layer, the out, cross-out and fc2
+// outputs ("contributions" 0, then 1 + 3 l + {0, 1, 2}). A block keeps the count it has added; one
+// that works in a LayerNorm phase first adds, in order, every contribution it has not.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ const uint64_t* contribution(uint64_t* regions, int i) {
+  const int l = (i - 1) / 3, k = (i - 1) % 3;
+  return regions + static_cast<size_t>(l) * kLayerWords + (k == 0 ? kOffAttnOut : (k == 1 ? kOffCrossOut : kOffMlpOut));
+}
+
+__device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, int upto, uint64_t* regions,
+                                               const StepArgs& a, const Ll& c) {
+  h2v* h2 = reinterpret_cast<h2v*>(h_res);
+  const int tid = threadIdx.x;
+  for (; applied < upto; ++applied) {  // block-uniform
+    if (applied == 0) {
+      const _Float16 *ea, *eb;
+      embed_rows(a.cur, a.state, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
+      const h2v* a2 = reinterpret_cast<const h2v*>(ea);
+      const h2v* b2 = reinterpret_cast<const h2v*>(eb);
+      for (int i = tid; i < kHidden / 2; i += kStepThreads) {
+        const h2v p = a2[i], q = b2[i];
+        h2v o;
+        o.x = f2h(h2f(p.x) + h2f(q.x));
+        o.y = f2h(h2f(p.y) + h2f(q.y));
+        h2[i] = o;
+      }
+    } else {
+      const uint64_t* x = contribution(regions, applied);
+      ll_sentinels(x, kVecWords / kStepWaves, kStepWaves, kStepWaves - 1, c);
+      const int idx[2] = {tid < kVecWords ? tid : -1, tid + kStepThreads < kVecWords ? tid + kStepThreads : -1};
+      unsigned v[2];
+      ll_wait<2, true>(x, idx, v, c);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        if (idx[k] < 0) continue;
+        const h2v hp = h2[idx[k]];
+        const h2v xp = __builtin_bit_cast(h2v, v[k]);
+        h2v o;
+        o.x = f2h(h2f(hp.x) + h2f(xp.x));
+        o.y = f2h(h2f(hp.y) + h2f(xp.y));
+        h2[idx[k]] = o;
+      }
+    }
+  }
+}
+
+// y = LN(h_res) with gamma / beta, the arithmetic of ln_finish<512, true> on the (already rounded)
+// residual: ln_params requests gamma and beta (before the phase's input is awaited), resid_layernorm
+// takes the residual pairs each thread owns (the ones it wrote itself) and finishes the LayerNorm.
+__device__ __forceinline__ void ln_params(LnRegs<kStepThreads>& in, const _Float16* gamma, const _Float16* beta) {
+  const h2v* g2 = reinterpret_cast<const h2v*>(gamma);
+  const h2v* be2 = reinterpret_cast<const h2v*>(beta);
+  const h2v zero = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
+#pragma unroll
+  for (int i = 0; i < LnRegs<kStepThreads>::kPer; ++i) {
+    const int idx = static_cast<int>(threadIdx.x) + i * kStepThreads;
+    const bool ok = idx < LnRegs<kStepThreads>::kPairs;
+    in.a[i] = in.b[i] = zero;
+    in.g[i] = ok ? g2[idx] : zero;
+    in.be[i] = ok ? be2[idx] : zero;
+  }
+}
+
+__device__ __forceinline__ void resid_layernorm(LnRegs<kStepThreads>& in, const _Float16* h_res, float eps,
+                                                _Float16* y, float* red) {
+  const h2v* h2 = reinterpret_cast<const h2v*>(h_res);
+#pragma unroll
+  for (int i = 0; i < LnRegs<kStepThreads>::kPer; ++i) {
+    const int idx = static_cast<int>(threadIdx.x) + i * kStepThreads;
+    if (idx < LnRegs<kStepThreads>::kPairs) in.a[i] = h2[idx];
+  }
+  ln_finish<kStepThreads, true>(in, false, nullptr, eps, y, red);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Split attention items: item i of a phase is (head i / nsplit, split i % nsplit); a block runs two
+// at once, waves 0-3 and 4-7, each exactly as attn_split_kernel<MAXP, false, 4> runs one block.
+// ---------------------------------------------------------------------------------------------
+struct AttnLds {
+  float wm[2][4], wl[2][4];
+  float wacc[2][4][kHeadDim];
+  uint4 q[2][3][8];  // q, fresh k, fresh v of the item's head (8 chunks of 8 fp16 each)
+};
+
+// One head's attention output from its split partials (LDS: part[s * kPartWords + d], d < 64 the value
+// sums, then m and l), with combine_finish's arithmetic over kMaxCombineSplits slots (splits past ns
+// empty): thread 0 the split weights, then thread d < 64 element d. The 64 fp16 results go to the
+// head's 32 words of `out` as one coalesced store. All threads of the block call it (barriers).
+__device__ __forceinline__ void head_combine(const float* part, int ns, int head, float* wgt, float* den_lds,
+                                             uint64_t* out, unsigned tag) {
+  constexpr int S = kMaxCombineSplits;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    float pm[S], pl[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      pm[s] = s < ns ? part[s * kPartWords + kHeadDim] : -INFINITY;
+      pl[s] = s < ns ? part[s * kPartWords + kHeadDim + 1] : 0.f;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < S; ++s) m = fmaxf(m, pm[s]);
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float w = pl[s] > 0.f ? __expf(pm[s] - m) : 0.f;
+      wgt[s] = w;
+      den = fmaf(pl[s], w, den);
+    }
+    den_lds[0] = den;
+  }
+  __syncthreads();
+  if (tid < kHeadDim) {
+    float num = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float pa = s < ns ? part[s * kPartWords + tid] : 0.f;
+      if (wgt[s] != 0.f) num = fmaf(pa, wgt[s], num);
+    }
+    const unsigned lo = half_bits(f2h(num / den_lds[0]));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_ds_swizzle(static_cast<int>(lo), 0x041F));  // lane ^ 1
+    if ((tid & 1) == 0) ll_store(out + head * 32 + tid / 2, tag, lo | (hi << 16));
+  }
+  __syncthreads();  // part, wgt and den are free again
+}
+
+// The q (and fresh k, v) words of one head: threads t < 96 fetch word t % 32 of part t / 32 (q, k, v;
+// parts with want[p] false are skipped) into q_lds[p][...].
+__device__ __forceinline__ void fetch_head_vectors(const uint64_t* qsrc, int head, bool want_kv, uint4 (*q_lds)[8],
+                                                   const Ll& c) {
+  const int tid = threadIdx.x, part_sel = tid >> 5, word = tid & 31;
+  int idx[1] = {-1};
+  if (part_sel == 0 || (want_kv && part_sel < 3)) idx[0] = part_sel * kVecWords + head * 32 + word;
+  unsigned v[1];
+  ll_wait<1>(qsrc, idx, v, c);
+  if (idx[0] >= 0) reinterpret_cast<unsigned*>(&q_lds[part_sel][0])[word] = v[0];
+}
+
+// Self attention of one head in one block, every split of 64 keys (reference split kernel arithmetic,
+// attn_split_kernel<2, false>: waves 0-3 take splits 0, 2, 4, 6, waves 4-7 splits 1, 3, 5, 7), the
+// split partials kept in LDS and combined in the block: no partial leaves the CU. The head's K/V rows
+// are requested before its query is awaited; the fresh K/V row (position pos) is written to the cache
+// and used in place of the cached one.
+__device__ __forceinline__ void self_attn_head(const Ll& c, int head, int ns, _Float16* kc, _Float16* vc,
+                                               int max_len, int pos, const uint64_t* qkv, uint64_t* out, float scale,
+                                               AttnLds& s, float* part, float* wgt, float* den) {
+  constexpr int MAXP = 2, kRounds = kMaxCombineSplits / 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
+  const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
+  const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
+  uint4 kr[kRounds][MAXP], vr[kRounds][MAXP];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    const int split = half + 2 * r, begin = split * kSelfSplitKeys;
+    const int w0 = begin + hw * MAXP * 8;
+    const int wend = min(min(w0 + MAXP * 8, begin + kSelfSplitKeys), max_len);
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const int j = w0 + p * 8 + ks;
+      kr[r][p] = vr[r][p] = make_uint4(0, 0, 0, 0);
+      if (split < ns && j < wend) {
+        kr[r][p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+        vr[r][p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      }
+    }
+  }
+  fetch_head_vectors(qkv, head, true, s.q[0], c);
+  __syncthreads();
+  if (tid < 16) {  // the fresh row into the cache, for the steps that follow
+    if (tid < 8)
+      reinterpret_cast<uint4*>(kc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid] = s.q[0][1][tid];
+    else
+      reinterpret_cast<uint4*>(vc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = s.q[0][2][tid - 8];
+  }
+  const uint4 qc = s.q[0][0][cc];
+#pragma unroll
+  for (int r = 0; r < kRounds; ++r) {
+    if (2 * r >= ns) break;  // block-uniform
+    const int split = half + 2 * r, begin = split * kSelfSplitKeys;
+    const bool act = split < ns;
+    const int w0 = begin + hw * MAXP * 8;
+    const int wend = min(min(w0 + MAXP * 8, begin + kSelfSplitKeys), max_len);
+    const int n = min(kSelfSplitKeys, pos + 1 - begin);
+    if (act) {
+#pragma unroll
+      for (int p = 0; p < MAXP; ++p) {
+        if (w0 + p * 8 + ks == pos) {  // the new row replaces the (stale) cached one
+          kr[r][p] = s.q[0][1][cc];
+          vr[r][p] = s.q[0][2][cc];
+        }
+      }
+      split_wave_partial<MAXP>(kr[r], vr[r], qc, w0, min(wend, begin + n), scale, &s.wm[half][hw], &s.wl[half][hw],
+                               s.wacc[half][hw]);
+    }
+    __syncthreads();
+    if (act && t4 < kHeadDim) {
+      float m, l, o;
+      split_merge<4>(s.wm[half], s.wl[half], s.wacc[half], t4, m, l, o);
+      part[split * kPartWords + t4] = o;
+      if (t4 == 0) {
+        part[split * kPartWords + kHeadDim] = m;
+        part[split * kPartWords + kHeadDim + 1] = l;
+      }
+    }
+    __syncthreads();
+  }
+  head_combine(part, ns, head, wgt, den, out, c.tag);
+}
+
+// Cross-attention split items: item i is (head i / nsplit, split i % nsplit); a block runs two at once,
+// waves 0-3 and 4-7, each exactly as attn_split_kernel<8, false, 4> runs one block, and stores its
+// partial (66 words, one coalesced store). The block that ran a head's last split then collects the
+// head's partials and combines them.
+__device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int workers, int nitems, int nsplit,
+                                                 const _Float16* kc, const _Float16* vc, int max_len,
+                                                 const uint64_t* qsrc, uint64_t* part_g, uint64_t* out, float scale,
+                                                 AttnLds& s, float* part, float* wgt, float* den) {
+  constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
+  const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
+  for (int base = 2 * rank; base < nitems; base += 2 * workers) {  // block-uniform
+    const int item = base + half;
+    const bool act = item < nitems;
+    const int head = act ? item / nsplit : 0, split = act ? item % nsplit : 0;
+    const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
+    const int begin = split * kKeys;
+    const int w0 = begin + hw * MAXP * 8;
+    const int wend = min(min(w0 + MAXP * 8, begin + kKeys), max_len);
+    const int n = min(kKeys, max_len - begin);
+    uint4 kr[MAXP], vr[MAXP];
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const int j = w0 + p * 8 + ks;
+      kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
+      if (act && j < wend) {
+        kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+        vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      }
+    }
+    {  // the head's query: 32 words per half
+      const int word = t4;
+      int idx[1] = {act && word < 32 ? head * 32 + word : -1};
+      unsigned v[1];
+      ll_wait<1>(qsrc, idx, v, c);
+      if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[half][0][0])[word] = v[0];
+    }
+    __syncthreads();
+    if (act && n > 0)
+      split_wave_partial<MAXP>(kr, vr, s.q[half][0][cc], w0, min(wend, begin + n), scale, &s.wm[half][hw],
+                               &s.wl[half][hw], s.wacc[half][hw]);
+    __syncthreads();
+    if (act && t4 < kPartWords) {
+      float m = -INFINITY, l = 0.f, o = 0.f;
+      if (n > 0) split_merge<4>(s.wm[half], s.wl[half], s.wacc[half], t4 < kHeadDim ? t4 : 0, m, l, o);
+      const float val = t4 < kHeadDim ? o : (t4 == kHeadDim ? m : l);
+      ll_store(part_g + static_cast<size_t>(split * kStepHeads + head) * kPartWords + t4, c.tag, __float_as_uint(val));
+    }
+    __syncthreads();  // s is reused below
+    // heads whose last split this block ran: collect their partials and combine
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int it = base + hf;
+      if (it >= nitems || it % nsplit != nsplit - 1) continue;  // block-uniform
+      const int h = it / nsplit;
+      int idx[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int t = tid + k * kStepThreads;
+        idx[k] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + h) * kPartWords + t % kPartWords : -1;
+      }
+      unsigned v[2];
+      ll_wait<2>(part_g, idx, v, c);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(v[k]);
+      __syncthreads();
+      head_combine(part, nsplit, h, wgt, den, out, c.tag);
+    }
+  }
+}
+
+// An attention output vector (640 words: 20 heads of 32, each head written by one store) into x_lds:
+// one sentinel per head, then every word.
+__device__ __forceinline__ void fetch_attn_vector(const uint64_t* src, _Float16* x_lds, const Ll& c) {
+  ll_sentinels(src, kStepHeads, 32, 31, c);
+  const int tid = threadIdx.x;
+  const int idx[2] = {tid < kVecWords ? tid : -1, tid + kStepThreads < kVecWords ? tid + kStepThreads : -1};
+  unsigned v[2];
+  ll_wait<2, true>(src, idx, v, c);
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    if (idx[k] >= 0) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
+}
+
+// ---------------------------------------------------------------------------------------------
+// The kernel
+// ---------------------------------------------------------------------------------------------
+struct Sched {
+  int start;  // first block of the current phase's run
+  int G;
+  __device__ int rank() const { return (static_cast<int>(blockIdx.x) - start + G) % G; }
+  __device__ void next(int used) { start = (start + used) % G; }
+};
+
+__global__ void __launch_bounds__(kStepThreads) decoder_layers_kernel(StepArgs a) {
+  __shared__ __align__(16) _Float16 h_res[kHidden];
+  __shared__ __align__(16) _Float16 x_lds[kStepFfn];
+  __shared__ float red[4 * kStepWaves];
+  __shared__ float wgt[kMaxCombineHeads * kMaxCombineSplits];
+  __shared__ float den[kMaxCombineHeads];
+  __shared__ AttnLds att;
+  __shared__ float part_lds[kMaxCombineSplits * kPartWords];
+  __shared__ unsigned epoch_lds;
+  __shared__ unsigned stage[kMaxPasses * kStepWaves];  // a GEMV phase's output words before their coalesced store
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int G = gridDim.x;
+  unsigned* ctl = reinterpret_cast<unsigned*>(a.ws);
+  uint64_t* regions = reinterpret_cast<uint64_t*>(a.ws + kCtlBytes);
+
+  // The launch's tag: the epoch every block reads before it arrives; the last block to arrive moves
+  // the epoch on for the next launch, when no block of this one can still be reading it.
+  if (tid == 0) epoch_lds = __hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const unsigned epoch = epoch_lds;
+  unsigned arrived = 0;
+  if (tid == 0) arrived = atomicAdd(ctl + 1, 1u);
+  const Ll c{ctl, epoch + 1u, a.spin_limit};
+
+  const int64_t pos_raw = a.state[0];
+  const int pos = static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw));
+  const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
+  const int ns_cross = (a.enc_len + kCrossSplitKeys - 1) / kCrossSplitKeys;
+
+  // worker counts: the phases with many rows use every block the previous phase did not
+  // Runs of blocks per phase, taken in turn around the grid: consecutive phases use disjoint blocks, the
+  // LN3 + fc1 phase also avoids the cross-attention blocks (which finish late), and the runs of one
+  // layer add up to three times the grid, so every layer repeats the pattern. At 256 CUs: LN1+q/k/v
+  // 176 blocks, self attention 20 (of a run of 176), out 80, LN2+cross-q 80, cross attention 60,
+  // cross-out 80, LN3+fc1 116, fc2 80.
+  const int w_vec = min(kVecWorkers, max(1, G * 5 / 16));
+  const int w_cross = min(kCrossWorkers, max(1, G * 15 / 64));
+  const int w_qkv = max(1, G - w_vec);
+  const int w_fc1 = max(1, G - w_vec - w_cross);
+  Sched sc{0, G};
+  int applied = 0;  // residual contributions added to h_res
+
+  for (int l = 0; l < a.n_layers; ++l) {
+    const StepLayer& L = a.layer[l];
+    uint64_t* R = regions + static_cast<size_t>(l) * kLayerWords;
+
+    // 1: residual + LN1 + q/k/v (1920 pairs)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = w_qkv;
+      constexpr int U = 2;
+      const int npairs = kQkvWords;
+      if (rank < W) {
+        Gv<kHidden, U> g;
+        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+        const int qs = W * kStepWaves;
+        gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
+        LnRegs<kStepThreads> lnr;
+        ln_params(lnr, L.ln1_g, L.ln1_b);
+        resid_catch_up(h_res, applied, 1 + 3 * l, regions, a, c);
+        resid_layernorm(lnr, h_res, L.eps1, x_lds, red);
+        __syncthreads();
+        for (;;) {
+          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffQkv, c.tag, nullptr, base, qs, npairs);
+          base += U * qs;
+          if (base >= npairs) break;
+          __syncthreads();
+          gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
+        }
+      }
+      sc.next(W);
+    }
+    // 2: self attention, one block per head (its splits combined in the block)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = kStepHeads;
+      if (rank < W)
+        self_attn_head(c, rank, ns_self, L.self_k, L.self_v, a.max_pos, pos, R + kOffQkv, R + kOffSelfVec, a.scale,
+                       att, part_lds, wgt, den);
+      sc.next(w_qkv);
+    }
+    // 3: out projection (640 pairs)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = w_vec;
+      constexpr int U = 1;
+      const int npairs = kVecWords;
+      if (rank < W) {
+        Gv<kHidden, U> g;
+        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+        const int qs = W * kStepWaves;
+        gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
+        fetch_attn_vector(R + kOffSelfVec, x_lds, c);
+        __syncthreads();
+        for (;;) {
+          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffAttnOut, c.tag, nullptr, base, qs, npairs);
+          base += U * qs;
+          if (base >= npairs) break;
+          __syncthreads();
+          gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
+        }
+      }
+      sc.next(W);
+    }
+    // 4: residual + LN2 + cross q (640 pairs)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = w_vec;
+      constexpr int U = 1;
+      const int npairs = kVecWords;
+      if (rank < W) {
+        Gv<kHidden, U> g;
+        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+        const int qs = W * kStepWaves;
+        gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
+        LnRegs<kStepThreads> lnr;
+        ln_params(lnr, L.ln2_g, L.ln2_b);
+        resid_catch_up(h_res, applied, 2 + 3 * l, regions, a, c);
+        resid_layernorm(lnr, h_res, L.eps2, x_lds, red);
+        __syncthreads();
+        for (;;) {
+          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossQ, c.tag, nullptr, base, qs, npairs);
+          base += U * qs;
+          if (base >= npairs) break;
+          __syncthreads();
+          gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
+        }
+      }
+      sc.next(W);
+    }
+    // 5: cross-attention splits, each head combined by the block that ran its last split
+    {
+      __syncthreads();
+      const int nitems = kStepHeads * ns_cross;
+      const int W = min(w_cross, (nitems + 1) / 2);
+      const int rank = sc.rank();
+      if (rank < W)
+        cross_attn_items(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
+                         R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den);
+      sc.next(w_cross);
+    }
+    // 6: cross-out projection (640 pairs)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = w_vec;
+      constexpr int U = 1;
+      const int npairs = kVecWords;
+      if (rank < W) {
+        Gv<kHidden, U> g;
+        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+        const int qs = W * kStepWaves;
+        gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
+        fetch_attn_vector(R + kOffCrossVec, x_lds, c);
+        __syncthreads();
+        for (;;) {
+          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossOut, c.tag, nullptr, base, qs, npairs);
+          base += U * qs;
+          if (base >= npairs) break;
+          __syncthreads();
+          gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
+        }
+      }
+      sc.next(W);
+    }
+    // 7: residual + LN3 + fc1 + GELU (2560 pairs)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = w_fc1;
+      constexpr int U = 3;
+      const int npairs = kFfnWords;
+      if (rank < W) {
+        Gv<kHidden, U> g;
+        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+        const int qs = W * kStepWaves;
+        gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
+        LnRegs<kStepThreads> lnr;
+        ln_params(lnr, L.ln3_g, L.ln3_b);
+        resid_catch_up(h_res, applied, 3 + 3 * l, regions, a, c);
+        resid_layernorm(lnr, h_res, L.eps3, x_lds, red);
+        __syncthreads();
+        for (;;) {
+          gv_finish<kHidden, U, FW_ACT_GELU>(g, x_lds, stage, R + kOffFfn, c.tag, nullptr, base, qs, npairs);
+          base += U * qs;
+          if (base >= npairs) break;
+          __syncthreads();
+          gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
+        }
+      }
+      sc.next(W);
+    }
+    // 8: fc2 (640 pairs of 5120-wide rows)
+    {
+      __syncthreads();
+      const int rank = sc.rank(), W = w_vec;
+      constexpr int U = 1;
+      const int npairs = kVecWords;
+      const bool last = l + 1 == a.n_layers;
+      if (rank < W) {
+        Gv<kStepFfn, U> g;
+        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+        const int qs = W * kStepWaves;
+        gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
+        // the fc1 output, 2560 words, into LDS
+        constexpr int kPer = kFfnWords / kStepThreads;
+        static_assert(kFfnWords % kStepThreads == 0, "whole words per thread");
+        int idx[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads;
+        unsigned v[kPer];
+        ll_sentinels(R + kOffFfn, kFfnWords / kStepWaves, kStepWaves, kStepWaves - 1, c);
+        ll_wait<kPer, true>(R + kOffFfn, idx, v, c);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
+        __syncthreads();
+        for (;;) {
+          gv_finish<kStepFfn, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffMlpOut, c.tag, last ? a.x_out : nullptr, base, qs, npairs);
+          base += U * qs;
+          if (base >= npairs) break;
+          __syncthreads();
+          gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
+        }
+      }
+      sc.next(W);
+    }
+  }
+
+  // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
+  if (blockIdx.x == 0) {
+    __syncthreads();
+    resid_catch_up(h_res, applied, 3 * a.n_layers, regions, a, c);  // the last fc2 output stays out
+    __syncthreads();
+    for (int i = tid; i < kHidden / 2; i += kStepThreads)
+      reinterpret_cast<unsigned*>(a.h_out)[i] = reinterpret_cast<const unsigned*>(h_res)[i];
+  }
+  if (tid == 0 && arrived == static_cast<unsigned>(G) - 1u) {
+    __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctl, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+}  // namespace
+}  // namespace fw
+
+using namespace fw;
+
+extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
+  if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
+  return kCtlBytes + static_cast<size_t>(n_layers) * kLayerWords * sizeof(uint64_t);
+}
+
+extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }
+
+extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, const int64_t* cur,
+                                      const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                                      int max_pos, int enc_len, float scale, void* h_out, void* x_out,
+                                      void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
+  if (!layers || !cur || !state || !embed || !pos_embed || !h_out || !x_out || !workspace)
+    return fw_fail(FW_EINVAL, "decoder_step_layers: null pointer");
+  if (n_layers < 1 || n_layers > kStepMaxLayers)
+    return fw_fail(FW_EINVAL, "decoder_step_layers: n_layers must be in [1, %d]", kStepMaxLayers);
+  if (vocab < 1 || max_pos < 1 || max_pos > kMaxCombineSplits * kSelfSplitKeys)
+    return fw_fail(FW_EINVAL, "decoder_step_layers: max_pos must be in [1, %d]", kMaxCombineSplits * kSelfSplitKeys);
+  if (enc_len < 1 || enc_len > kMaxCombineSplits * kCrossSplitKeys)
+    return fw_fail(FW_EINVAL, "decoder_step_layers: enc_len must be in [1, %d]", kMaxCombineSplits * kCrossSplitKeys);
+  if (ws_bytes < static_cast<int64_t>(fw_decoder_step_workspace_bytes(n_layers)))
+    return fw_fail(FW_EINVAL, "decoder_step_layers: workspace too small (%lld < %zu bytes)",
+                   static_cast<long long>(ws_bytes), fw_decoder_step_workspace_bytes(n_layers));
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) || (reinterpret_cast<uintptr_t>(h_out) & 3u) ||
+      (reinterpret_cast<uintptr_t>(x_out) & 3u))
+    return fw_fail(FW_EINVAL, "decoder_step_layers: workspace must be 256-byte and h_out / x_out 4-byte aligned");
+  if (spin_limit < 0) return fw_fail(FW_EINVAL, "decoder_step_layers: spin_limit must be >= 0");
+  StepArgs a{};
+  for (int l = 0; l < n_layers; ++l) {
+    const fw_dec_layer& s = layers[l];
+    const void* must[] = {s.ln1_gamma, s.ln1_beta, s.qkv_w, s.out_w, s.ln2_gamma, s.ln2_beta, s.cross_q_w,
+                          s.cross_out_w, s.ln3_gamma, s.ln3_beta, s.fc1_w, s.fc2_w, s.self_k, s.self_v,
+                          s.cross_k, s.cross_v};
+    for (const void* p : must)
+      if (!p) return fw_fail(FW_EINVAL, "decoder_step_layers: layer %d has a null tensor", l);
+    const void* mats[] = {s.qkv_w, s.out_w, s.cross_q_w, s.cross_out_w, s.fc1_w, s.fc2_w,
+                          s.self_k, s.self_v, s.cross_k, s.cross_v};
+    for (const void* p : mats)
+      if (reinterpret_cast<uintptr_t>(p) & 15u)
+        return fw_fail(FW_EINVAL, "decoder_step_layers: layer %d: weights and caches must be 16-byte aligned", l);
+    StepLayer& d = a.layer[l];
+    auto h = [](const void* p) { return static_cast<const _Float16*>(p); };
+    d.ln1_g = h(s.ln1_gamma); d.ln1_b = h(s.ln1_beta); d.qkv_w = h(s.qkv_w); d.qkv_b = h(s.qkv_b);
+    d.out_w = h(s.out_w); d.out_b = h(s.out_b);
+    d.ln2_g = h(s.ln2_gamma); d.ln2_b = h(s.ln2_beta); d.cq_w = h(s.cross_q_w); d.cq_b = h(s.cross_q_b);
+    d.co_w = h(s.cross_out_w); d.co_b = h(s.cross_out_b);
+    d.ln3_g = h(s.ln3_gamma); d.ln3_b = h(s.ln3_beta); d.fc1_w = h(s.fc1_w); d.fc1_b = h(s.fc1_b);
+    d.fc2_w = h(s.fc2_w); d.fc2_b = h(s.fc2_b);
+    d.eps1 = s.ln1_eps; d.eps2 = s.ln2_eps; d.eps3 = s.ln3_eps;
+    d.self_k = static_cast<_Float16*>(s.self_k); d.self_v = static_cast<_Float16*>(s.self_v);
+    d.cross_k = h(s.cross_k); d.cross_v = h(s.cross_v);
+  }
+  a.n_layers = n_layers;
+  a.cur = cur;
+  a.state = state;
+  a.embed = static_cast<const _Float16*>(embed);
+  a.pos_embed = static_cast<const _Float16*>(pos_embed);
+  a.vocab = vocab;
+  a.max_pos = max_pos;
+  a.enc_len = enc_len;
+  a.scale = scale;
+  a.h_out = static_cast<_Float16*>(h_out);
+  a.x_out = static_cast<_Float16*>(x_out);
+  a.ws = static_cast<unsigned char*>(workspace);
+  a.spin_limit = spin_limit;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 2)
+    return fw_fail(FW_EHIP, "decoder_step_layers: cannot read the device's CU count");
+  hipLaunchKernelGGL(decoder_layers_kernel, dim3(cus), dim3(kStepThreads), 0, stream, a);
+  return fw_check_launch("decoder_step_layers");
+}

@@ -13,6 +13,7 @@ compiler's per-kernel register, LDS and spill report, like the reference's ``mai
 """
 
 import argparse
+import ctypes
 import sys
 
 import torch
@@ -273,6 +274,73 @@ class WhisperExt:
             self._call('fw_attn_out_gemv', *args, _stream())
         else:
             self._call('fw_attn_out_gemv_batch', *args, nv, _stream())
+
+    # ---- the decoder layers of one token in one launch --------------------------------------
+    def decoder_step_workspace(self, n_layers):
+        """Zero-filled workspace of fw_decoder_step_layers for n_layers (one per decoding stream)."""
+        nbytes = self.lib.fw_decoder_step_workspace_bytes(int(n_layers))
+        _require(nbytes > 0, f'decoder_step: n_layers must be in [1, {self.lib.fw_decoder_step_max_layers()}]')
+        return torch.zeros(nbytes, dtype=torch.uint8, device='cuda')
+
+    def decoder_layer_table(self, layers):
+        """The fw_dec_layer array for decoder_step_layers. `layers`: one dict per layer with the tensors
+        named in _lib.DEC_LAYER_TENSORS (biases may be None), ln{1,2,3}_eps, and self_k / self_v
+        ([heads, max_pos, 64]), cross_k / cross_v ([heads, enc_len, 64]). The table holds raw pointers:
+        the tensors must outlive it."""
+        table = (_lib.DecLayer * len(layers))()
+        shapes = {'qkv_w': (3 * HIDDEN, HIDDEN), 'out_w': (HIDDEN, HIDDEN), 'cross_q_w': (HIDDEN, HIDDEN),
+                  'cross_out_w': (HIDDEN, HIDDEN), 'fc1_w': (4 * HIDDEN, HIDDEN), 'fc2_w': (HIDDEN, 4 * HIDDEN)}
+        rows = {'qkv_b': 3 * HIDDEN, 'fc1_b': 4 * HIDDEN}
+        for i, lay in enumerate(layers):
+            for name in _lib.DEC_LAYER_TENSORS:
+                t = lay.get(name)
+                if t is None:
+                    _require(name.endswith('_b'), f'layer {i}: {name} is required')
+                    continue
+                check_half(t, f'layer {i} {name}')
+                if name in shapes:
+                    _require(tuple(t.shape) == shapes[name], f'layer {i}: {name} must be {list(shapes[name])}')
+                else:
+                    _require(t.numel() == rows.get(name, HIDDEN), f'layer {i}: {name} has the wrong size')
+                setattr(table[i], name, t.data_ptr())
+            for n in ('self_k', 'self_v', 'cross_k', 'cross_v'):
+                t = lay[n]
+                check_half(t, f'layer {i} {n}')
+                _require(t.dim() == 3 and t.size(0) * HEAD_DIM == HIDDEN and t.size(2) == HEAD_DIM,
+                         f'layer {i}: {n} must be [heads, len, 64]')
+                setattr(table[i], n, t.data_ptr())
+            _require(lay['self_k'].shape == lay['self_v'].shape and lay['cross_k'].shape == lay['cross_v'].shape,
+                     f'layer {i}: K and V shapes differ')
+            for j in (1, 2, 3):
+                setattr(table[i], f'ln{j}_eps', float(lay[f'ln{j}_eps']))
+        return table
+
+    def decoder_step_layers(self, table, cur, state, embed, pos_embed, max_pos, enc_len, scale, h_out, x_out, ws,
+                            spin_limit=2_000_000):
+        """Every decoder layer of one token in one launch (fw_decoder_step_layers): from the embedding of
+        cur[0] at state[0] to the residual h_out and the last fc2 output x_out, K/V rows written at
+        state[0]. Nothing else may run on the device meanwhile. A wait past spin_limit ticks (100 MHz)
+        sets the workspace's error word; read it with decoder_step_error."""
+        for t, n in ((embed, 'embed'), (pos_embed, 'pos_embed'), (h_out, 'h_out'), (x_out, 'x_out')):
+            check_half(t, n)
+        _require(embed.dim() == 2 and embed.size(1) == HIDDEN and pos_embed.dim() == 2 and pos_embed.size(1) == HIDDEN
+                 and pos_embed.size(0) >= max_pos, 'embed / pos_embed must be [rows, 1280]')
+        _require(h_out.numel() == HIDDEN and x_out.numel() == HIDDEN, 'h_out, x_out must be [1280]')
+        for t, n in ((cur, 'cur'), (state, 'state')):
+            _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
+        _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')
+        self._call('fw_decoder_step_layers', ctypes.addressof(table), len(table), cur.data_ptr(), state.data_ptr(),
+                   embed.data_ptr(), pos_embed.data_ptr(), embed.size(0), int(max_pos), int(enc_len), float(scale),
+                   h_out.data_ptr(), x_out.data_ptr(), ws.data_ptr(), ws.numel(), int(spin_limit), _stream())
+
+    @staticmethod
+    def decoder_step_error(ws, clear=True):
+        """The workspace's error word (nonzero: a wait of the step timed out); synchronises."""
+        word = ws[8:12].view(torch.int32)
+        err = int(word.item())
+        if err and clear:
+            word.zero_()
+        return err
 
     def lm_head_argmax_fused(self, h, x, gamma, beta, eps, w, suppress, best, tokens, state, cur, max_pos):
         """Final residual + LN + lm_head_argmax + argmax_finalize (finalize skipped when tokens, state and

@@ -34,7 +34,7 @@ SELF_SPLIT, CROSS_SPLIT = 64, 256  # keys per split block of the decoder's self 
 class CustomModel:
     @torch.inference_mode()
     def __init__(self, model_id=SYNTHETIC, cache_dir=None, *, seed=0, dims=TURBO, setup=None, selftest=True,
-                 capture=True, lm_q8=True):
+                 capture=True, lm_q8=True, persistent_step=True):
         if not torch.cuda.is_available():
             raise RuntimeError('CustomModel requires a HIP device')
         self._weights, self.tokenizer, self.checkpoint = None, None, None
@@ -59,6 +59,8 @@ class CustomModel:
         self.eos = set(self.setup.eos)
         self.record_events = False   # time every chunk replay with HIP events (bench.py)
         self.use_lm_q8 = lm_q8       # LM head with the int8 pre-pass (same token as the fp16 head)
+        # the decoder layers of a step as one persistent launch (same outputs as the 34-launch step)
+        self.persistent_step = persistent_step
         self.chunk_events = []
 
         self._specs = W.spec_map(dims)
@@ -118,6 +120,11 @@ class CustomModel:
         self.tokens = torch.zeros(d.max_pos, dtype=torch.long, device='cuda')
         self.tokens_host = torch.zeros(d.max_pos, dtype=torch.long, pin_memory=True)
         self.best = torch.zeros(1, dtype=torch.long, device='cuda')
+        # the persistent step's workspace, layer table and outputs (residual, last fc2 output)
+        self.step_ws = self.ext.decoder_step_workspace(d.dec_layers)
+        self.h_fin = torch.zeros(dm, dtype=half, device='cuda')
+        self.x_fin = torch.zeros(dm, dtype=half, device='cuda')
+        self.step_table = self.ext.decoder_layer_table([self._layer_tensors(i) for i in range(d.dec_layers)])
         # split-K attention partials (the fused step, the reference-granularity step and the batched
         # prompt, whose n queries take n times the splits of one)
         n = len(self.prompt) if self.batch_prompt else 1
@@ -141,6 +148,7 @@ class CustomModel:
         lane.__dict__.update(self.__dict__)
         lane.selftest = dict(self.selftest)
         lane.chunk_events, lane.record_events = [], False
+        lane.persistent_step = False  # lanes run concurrently; the persistent step needs the whole device
         lane._alloc_frontend_buffers()
         lane._alloc_encoder_buffers()
         lane._alloc_decoder_buffers()
@@ -324,13 +332,31 @@ class CustomModel:
             torch.cuda.synchronize()
 
     # ---- decoder -----------------------------------------------------------------------------
+    def _layer_tensors(self, i):
+        lay = self.layers[i]
+        t = {'qkv_w': lay.qkv_w, 'qkv_b': lay.qkv_b}
+        for j, ln in enumerate((lay.ln1, lay.ln2, lay.ln3), 1):
+            t[f'ln{j}_gamma'], t[f'ln{j}_beta'], t[f'ln{j}_eps'] = ln
+        for name, (w, b) in (('out', lay.out), ('cross_q', lay.cross_q), ('cross_out', lay.cross_out),
+                             ('fc1', lay.fc1), ('fc2', lay.fc2)):
+            t[f'{name}_w'], t[f'{name}_b'] = w, b
+        t['self_k'], t['self_v'] = self.self_kv[i, 0], self.self_kv[i, 1]
+        t['cross_k'], t['cross_v'] = self.cross_kv[i, 0], self.cross_kv[i, 1]
+        return t
+
     def _step(self, lm_head=True):
-        """One decoder token, entirely on the device (custom/model.py:107-123) in 34 launches:
-        per layer [LN1+QKV] [self-attn split-K + KV write] [combine + out] [LN2+cross-q]
-        [cross-attn split-K] [combine + cross-out] [LN3+fc1+GELU] [fc2], then
-        [final LN + LM head + argmax] [finalize]. Without `lm_head` (prompt tokens whose prediction
-        is discarded) the step ends after the layers and only advances the position."""
+        """One decoder token, entirely on the device (custom/model.py:107-123): the decoder layers as one
+        persistent launch (``persistent_step``), or in 32 launches, per layer [LN1+QKV] [self-attn
+        split-K + KV write] [combine + out] [LN2+cross-q] [cross-attn split-K] [combine + cross-out]
+        [LN3+fc1+GELU] [fc2]; then [final LN + LM head + argmax] [finalize]. The two forms give
+        bit-identical outputs. Without `lm_head` (prompt tokens whose prediction is discarded) the step
+        ends after the layers and only advances the position."""
         ext, d, dm = self.ext, self.dims, self.dims.d_model
+        if self.persistent_step and lm_head:
+            ext.decoder_step_layers(self.step_table, self.cur, self.state, self.embed, self.pos_embed, self.max_pos,
+                                    self.enc_len, self.scale, self.h_fin, self.x_fin, self.step_ws)
+            self._lm_head(self.h_fin, self.x_fin)
+            return
         ws = self.workspace
         q, k_new, v_new = self.qkv[:dm], self.qkv[dm:2 * dm], self.qkv[2 * dm:]
         a, b = 0, 1
@@ -464,6 +490,11 @@ class CustomModel:
                 self._step(lm_head)
 
     # ---- per-clip ------------------------------------------------------------------------------
+    def _check_step_error(self):
+        if self.persistent_step and self.ext.decoder_step_error(self.step_ws):
+            raise RuntimeError('decoder step: a hand-off wait timed out (another kernel on the device, or '
+                               'fewer resident blocks than CUs); the tokens of this call are not valid')
+
     def _check_audio(self, audio, max_new_tokens):
         """custom/model.py:175-178; returns the token budget."""
         if not isinstance(audio, np.ndarray) or audio.dtype != np.float32 or audio.ndim != 1:
@@ -582,6 +613,7 @@ class CustomModel:
                     break
         ttlt = time.perf_counter() - start
         decode_s = ttlt - mel_s - encoder_s  # from the end of the encoder on the GPU timeline
+        self._check_step_error()
         detok_start = time.perf_counter()
         text = C.detokenize(self.tokenizer, token_ids)
         return {

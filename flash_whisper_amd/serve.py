@@ -33,7 +33,9 @@ class Scheduler:
     def __init__(self, model, lanes=2):
         if lanes < 1:
             raise ValueError('lanes must be >= 1')
-        self.lanes = [model] + [model.new_lane() for _ in range(lanes - 1)]
+        # One lane may be the model itself. Several lanes run concurrently, so each is a new lane with the
+        # 32-launch decoder step: the persistent step needs every CU to itself.
+        self.lanes = [model] if lanes == 1 else [model.new_lane() for _ in range(lanes)]
         self.streams = [torch.cuda.Stream() for _ in self.lanes]
         self.host_tokens = [torch.zeros(model.max_pos, dtype=torch.long, pin_memory=True) for _ in self.lanes]
 

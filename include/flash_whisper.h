@@ -160,6 +160,44 @@ int fw_attn_out_gemv_batch(const float* part_m, const float* part_l, const float
                            const int64_t* len_state, int heads, int max_len, int split_keys, const void* w,
                            const void* bias, void* out, int n_out, int nv, hipStream_t stream);
 
+/* One decoder layer's tensors for fw_decoder_step_layers (fp16; weights in torch Linear layout).
+ * qkv_w [3 * 1280, 1280] packed [q; k; v] with bias [b_q; 0; b_v] (custom/model.py:81-91); out_w,
+ * cross_q_w, cross_out_w [1280, 1280]; fc1_w [5120, 1280]; fc2_w [1280, 5120]; null biases read as 0.
+ * self_k / self_v [20, max_pos, 64] (this layer's KV cache), cross_k / cross_v [20, enc_len, 64]. */
+typedef struct fw_dec_layer {
+  const void *ln1_gamma, *ln1_beta, *qkv_w, *qkv_b, *out_w, *out_b;
+  const void *ln2_gamma, *ln2_beta, *cross_q_w, *cross_q_b, *cross_out_w, *cross_out_b;
+  const void *ln3_gamma, *ln3_beta, *fc1_w, *fc1_b, *fc2_w, *fc2_b;
+  float ln1_eps, ln2_eps, ln3_eps;
+  void *self_k, *self_v;
+  const void *cross_k, *cross_v;
+} fw_dec_layer;
+
+/* Bytes of the workspace fw_decoder_step_layers needs for n_layers (0 if n_layers is out of range). The
+ * caller allocates it once, zero-filled, 256-byte aligned, and passes the same workspace to every call
+ * of one decoding stream; it holds control words (an epoch, an arrival count, an error flag: uint32 at
+ * byte offsets 0, 4, 8) and the tagged hand-off vectors. */
+size_t fw_decoder_step_workspace_bytes(int n_layers);
+int fw_decoder_step_max_layers(void);
+
+/* The decoder layers of one token in ONE launch: replaces the per-layer op chain of the reference step
+ * (custom/model.py:107-121: add_layernorm, the q/k/v, out, cross-q, cross-out, fc1, fc2 F.linear
+ * calls and the two decode_attention calls per layer, whisper_kernels.cu:215-267,102-213) with the
+ * arithmetic of fw_ln_gemv / fw_attention_split / fw_attn_out_gemv / fw_gemv, outputs bit-identical.
+ * Starts from the embedding of token cur[0] at position state[0] (as fw_ln_gemv's embedding mode),
+ * writes each layer's new K/V row at state[0], and leaves the final residual stream split as the LM
+ * head takes it: h_out (residual before the last fc2 output) and x_out (that output), fp16[1280] each.
+ * d_model 1280, 20 heads, FFN 5120; max_pos <= 512, enc_len <= 2048, n_layers <= 8; scale is the
+ * attention scale (1/8). One block per CU, all resident at once: nothing else may run on the device
+ * concurrently (no second call in flight on another stream). Every internal wait is bounded by
+ * spin_limit ticks of the 100 MHz wall clock; a wait that runs out sets the workspace's error word
+ * (byte offset 8) to nonzero, the launch then completes with undefined outputs, and the caller must
+ * check the word and clear it. */
+int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, const int64_t* cur, const int64_t* state,
+                           const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len, float scale,
+                           void* h_out, void* x_out, void* workspace, int64_t ws_bytes, int64_t spin_limit,
+                           hipStream_t stream);
+
 /* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
  * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by
  * fw_argmax_finalize. best must be zero on entry and is left zero. With tokens, state and cur all

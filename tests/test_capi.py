@@ -71,6 +71,33 @@ def test_validation_errors_return_einval(built_lib):
     assert lib.fw_encoder_vt_elems(1500, 20) == 20 * 64 * 1536 and lib.fw_encoder_vt_elems(0, 20) == 0
 
 
+def test_decoder_step_entry_points_validate(built_lib):
+    """fw_decoder_step_layers checks its arguments before any HIP call; the workspace size covers the
+    control words and every layer's hand-off regions."""
+    from flash_whisper_amd import _lib
+
+    lib = built_lib
+    assert lib.fw_decoder_step_max_layers() == 8
+    one = lib.fw_decoder_step_workspace_bytes(1)
+    assert one > 256 and lib.fw_decoder_step_workspace_bytes(4) == 256 + 4 * (one - 256)
+    assert lib.fw_decoder_step_workspace_bytes(0) == 0 and lib.fw_decoder_step_workspace_bytes(9) == 0
+    assert ctypes.sizeof(_lib.DecLayer) == 18 * 8 + 3 * 4 + 4 + 4 * 8  # C layout: pad before the caches
+    table = (_lib.DecLayer * 4)()
+    d = ctypes.c_void_p(256)
+    args = [d, d, d, d, 51866, 448, 1500, 0.125, d, d, d, lib.fw_decoder_step_workspace_bytes(4), 1000, None]
+    assert lib.fw_decoder_step_layers(table, 4, *args) == _lib.FW_EINVAL
+    assert b'null tensor' in lib.fw_last_error()  # the layer table is empty
+    assert lib.fw_decoder_step_layers(table, 9, *args) == _lib.FW_EINVAL
+    assert b'n_layers' in lib.fw_last_error()
+    bad = list(args)
+    bad[5] = 513  # max_pos beyond 8 splits of 64 keys
+    assert lib.fw_decoder_step_layers(table, 4, *bad) == _lib.FW_EINVAL and b'max_pos' in lib.fw_last_error()
+    bad = list(args)
+    bad[11] = 100  # workspace too small
+    assert lib.fw_decoder_step_layers(table, 4, *bad) == _lib.FW_EINVAL and b'too small' in lib.fw_last_error()
+    assert lib.fw_decoder_step_layers(None, 4, *args) == _lib.FW_EINVAL
+
+
 def test_status_becomes_runtime_error(built_lib):
     from flash_whisper_amd import _lib
 
