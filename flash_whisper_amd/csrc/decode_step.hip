@@ -273,10 +273,9 @@ __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, in
       }
     } else {
       const uint64_t* x = contribution(regions, applied);
-      ll_sentinels(x, kVecWords / kStepWaves, kStepWaves, kStepWaves - 1, c);
       const int idx[2] = {tid < kVecWords ? tid : -1, tid + kStepThreads < kVecWords ? tid + kStepThreads : -1};
       unsigned v[2];
-      ll_wait<2, true>(x, idx, v, c);
+      ll_wait<2>(x, idx, v, c);
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
         if (idx[k] < 0) continue;
@@ -529,11 +528,10 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
 // An attention output vector (640 words: 20 heads of 32, each head written by one store) into x_lds:
 // one sentinel per head, then every word.
 __device__ __forceinline__ void fetch_attn_vector(const uint64_t* src, _Float16* x_lds, const Ll& c) {
-  ll_sentinels(src, kStepHeads, 32, 31, c);
   const int tid = threadIdx.x;
   const int idx[2] = {tid < kVecWords ? tid : -1, tid + kStepThreads < kVecWords ? tid + kStepThreads : -1};
   unsigned v[2];
-  ll_wait<2, true>(src, idx, v, c);
+  ll_wait<2>(src, idx, v, c);
 #pragma unroll
   for (int k = 0; k < 2; ++k)
     if (idx[k] >= 0) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
@@ -758,8 +756,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_layers_kernel(StepArgs a
 #pragma unroll
         for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads;
         unsigned v[kPer];
-        ll_sentinels(R + kOffFfn, kFfnWords / kStepWaves, kStepWaves, kStepWaves - 1, c);
-        ll_wait<kPer, true>(R + kOffFfn, idx, v, c);
+        ll_wait<kPer>(R + kOffFfn, idx, v, c);
 #pragma unroll
         for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
         __syncthreads();
