@@ -61,6 +61,8 @@ SIGNATURES = {
     'fw_decoder_step_max_layers': (c_int, []),
     'fw_decoder_step_layers': (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, P, P, c_int64, c_int64,
                                        P]),
+    'fw_final_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
+    'fw_decoder_step': (c_int, [P, c_int, P, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64, P]),
 }
 
 DEC_LAYER_TENSORS = ('ln1_gamma', 'ln1_beta', 'qkv_w', 'qkv_b', 'out_w', 'out_b', 'ln2_gamma', 'ln2_beta',
@@ -72,6 +74,12 @@ class DecLayer(ctypes.Structure):
     """struct fw_dec_layer: one decoder layer's device pointers for fw_decoder_step_layers."""
     _fields_ = ([(n, c_void_p) for n in DEC_LAYER_TENSORS] + [(f'ln{i}_eps', c_float) for i in (1, 2, 3)]
                 + [(n, c_void_p) for n in ('self_k', 'self_v', 'cross_k', 'cross_v')])
+
+
+class DecHead(ctypes.Structure):
+    """struct fw_dec_head: the LM head of fw_decoder_step."""
+    _fields_ = [('ln_gamma', c_void_p), ('ln_beta', c_void_p), ('ln_eps', c_float), ('w', c_void_p), ('wq', c_void_p),
+                ('meta', c_void_p), ('suppress', c_void_p), ('tokens', c_void_p), ('y_out', c_void_p)]
 
 
 _lib = None

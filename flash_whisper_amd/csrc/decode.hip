@@ -24,6 +24,16 @@ __global__ void __launch_bounds__(256) add_layernorm_kernel(_Float16* h, const _
   ln_prologue<256>(h, x, x ? h : nullptr, gamma, beta, eps, y, red);
 }
 
+// The final LayerNorm of the LM-head kernels on its own (their 1024-thread reduction order).
+__global__ void __launch_bounds__(1024) final_layernorm_kernel(const _Float16* h, const _Float16* x,
+                                                               const _Float16* gamma, const _Float16* beta,
+                                                               _Float16* y, float eps) {
+  __shared__ float red[2 * 1024 / kWave];
+  LnRegs<1024> in;
+  ln_load<1024>(h, x, gamma, beta, in);
+  ln_finish<1024, true>(in, x != nullptr, nullptr, eps, y, red);
+}
+
 __global__ void __launch_bounds__(256) embed_kernel(const int64_t* cur, const int64_t* state, const _Float16* embed,
                                                     const _Float16* pos_embed, int vocab, int max_pos, _Float16* h) {
   const _Float16 *a, *b;
@@ -361,37 +371,8 @@ __global__ void argmax_finalize_kernel(unsigned long long* best, FinArgs fin) { 
 // is equal (y = 0) all rows are candidates and the block reads its fp16 rows as lm_head_kernel does.
 // ------------------------------------------------------------------------------------------
 constexpr int kQ8RowsPerBlock = kLmRowsIter * 4;  // 4 batches of 64 rows, dealt round-robin
-constexpr int kQ8Chunks = kHidden / 16;           // 16-byte int8 chunks per row (80)
-constexpr int kQ8Lpr = 16;                        // lanes per row in the int8 pass
-constexpr int kQ8C = kQ8Chunks / kQ8Lpr;          // chunks per lane (5)
-constexpr int kQ8YMax = 127 * 128;                // |y_int| bound: digits hi in [-127, 127], lo in [-64, 63]
-constexpr float kQ8Gamma = 7.7e-5f;               // >= 1280 * 2^-24 / (1 - 1280 * 2^-24)
 static_assert(kLmNW * 64 / kQ8Lpr == kLmRowsIter, "one int8 row per 16 lanes per batch");
 static_assert(kLmNW * 64 >= kHidden / 2, "the y statistics and digits take one thread per pair of y values");
-
-__device__ __forceinline__ int xor_add_i16(int v) {
-  // integer butterfly over 16 lanes (partners 8, 4, 2, 1), exact
-  v += __builtin_bit_cast(int, xor_lane<8>(__builtin_bit_cast(float, v)));
-  v += __builtin_bit_cast(int, xor_lane<4>(__builtin_bit_cast(float, v)));
-  v += __builtin_bit_cast(int, xor_lane<2>(__builtin_bit_cast(float, v)));
-  v += __builtin_bit_cast(int, xor_lane<1>(__builtin_bit_cast(float, v)));
-  return v;
-}
-
-__device__ __forceinline__ int dot16_i8(const uint4& a, const uint4& b, int acc) {
-  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.x), static_cast<int>(b.x), acc, false);
-  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.y), static_cast<int>(b.y), acc, false);
-  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.z), static_cast<int>(b.z), acc, false);
-  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.w), static_cast<int>(b.w), acc, false);
-  return acc;
-}
-
-// Smallest X that can still tie or beat a row whose fp32 logit is at least T once both are rounded to
-// fp16 (round to nearest even; logits at or beyond 65520 round to +-inf and tie there).
-__device__ __forceinline__ float q8_threshold(float t) {
-  if (!(t > -65504.0f)) return -INFINITY;  // also NaN: keep every row
-  return fminf(t - (fabsf(t) * 0x1p-9f + 0x1p-23f), 65504.0f);
-}
 
 __global__ void __launch_bounds__(256) lm_q8_pack_kernel(const _Float16* __restrict__ w, int vocab,
                                                          int8_t* __restrict__ wq, float2* __restrict__ meta) {
@@ -993,6 +974,16 @@ extern "C" int fw_add_layernorm(void* h, const void* x, const void* gamma, const
                      static_cast<const _Float16*>(x), static_cast<const _Float16*>(gamma),
                      static_cast<const _Float16*>(beta), static_cast<_Float16*>(y), eps);
   return fw_check_launch("add_layernorm");
+}
+
+extern "C" int fw_final_layernorm(const void* h, const void* x, const void* gamma, const void* beta, void* y, int n,
+                                  float eps, hipStream_t stream) {
+  FW_REQUIRE(h && gamma && beta && y, "final_layernorm: null pointer");
+  FW_REQUIRE(n == kHidden, "hidden size must be %d", kHidden);
+  hipLaunchKernelGGL(final_layernorm_kernel, dim3(1), dim3(1024), 0, stream, static_cast<const _Float16*>(h),
+                     static_cast<const _Float16*>(x), static_cast<const _Float16*>(gamma),
+                     static_cast<const _Float16*>(beta), static_cast<_Float16*>(y), eps);
+  return fw_check_launch("final_layernorm");
 }
 
 extern "C" int fw_embed(const int64_t* cur, const int64_t* state, const void* embed, const void* pos_embed, int vocab,

@@ -372,15 +372,20 @@ struct FinArgs {
   int max_pos;
 };
 
+// The finalize with the packed maximum b and the state words already read: n = state[1] (tokens so
+// far), p = state[0] (position).
+__device__ __forceinline__ void finalize_known(unsigned long long b, int64_t n, int64_t p, const FinArgs& f) {
+  const int64_t tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
+  if (n < f.max_pos) f.tokens[n] = tok;
+  f.state[1] = n < f.max_pos ? n + 1 : n;
+  f.state[0] = p + 1 < f.max_pos ? p + 1 : f.max_pos - 1;
+  *f.cur = tok;
+}
+
 __device__ __forceinline__ void finalize_token(unsigned long long* best, const FinArgs& f) {
   const unsigned long long b = *best;
   *best = 0ull;
-  const int64_t tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
-  const int64_t n = f.state[1];
-  if (n < f.max_pos) f.tokens[n] = tok;
-  f.state[1] = n < f.max_pos ? n + 1 : n;
-  f.state[0] = f.state[0] + 1 < f.max_pos ? f.state[0] + 1 : f.max_pos - 1;
-  *f.cur = tok;
+  finalize_known(b, f.state[1], f.state[0], f);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -501,6 +506,39 @@ __device__ __forceinline__ void split_merge_store(const float* wm, const float* 
       a.part_l[slot] = l;
     }
   }
+}
+
+// ------------------------------------------------------------------------------------------
+// The int8 pre-pass of the LM head (the soundness argument is at lm_head_q8_kernel in decode.hip).
+// ------------------------------------------------------------------------------------------
+constexpr int kQ8Chunks = kHidden / 16;           // 16-byte int8 chunks per row (80)
+constexpr int kQ8Lpr = 16;                        // lanes per row in the int8 pass
+constexpr int kQ8C = kQ8Chunks / kQ8Lpr;          // chunks per lane (5)
+constexpr int kQ8YMax = 127 * 128;                // |y_int| bound: digits hi in [-127, 127], lo in [-64, 63]
+constexpr float kQ8Gamma = 7.7e-5f;               // >= 1280 * 2^-24 / (1 - 1280 * 2^-24)
+
+__device__ __forceinline__ int xor_add_i16(int v) {
+  // integer butterfly over 16 lanes (partners 8, 4, 2, 1), exact
+  v += __builtin_bit_cast(int, xor_lane<8>(__builtin_bit_cast(float, v)));
+  v += __builtin_bit_cast(int, xor_lane<4>(__builtin_bit_cast(float, v)));
+  v += __builtin_bit_cast(int, xor_lane<2>(__builtin_bit_cast(float, v)));
+  v += __builtin_bit_cast(int, xor_lane<1>(__builtin_bit_cast(float, v)));
+  return v;
+}
+
+__device__ __forceinline__ int dot16_i8(const uint4& a, const uint4& b, int acc) {
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.x), static_cast<int>(b.x), acc, false);
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.y), static_cast<int>(b.y), acc, false);
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.z), static_cast<int>(b.z), acc, false);
+  acc = __builtin_amdgcn_sdot4(static_cast<int>(a.w), static_cast<int>(b.w), acc, false);
+  return acc;
+}
+
+// Smallest X that can still tie or beat a row whose fp32 logit is at least T once both are rounded to
+// fp16 (round to nearest even; logits at or beyond 65520 round to +-inf and tie there).
+__device__ __forceinline__ float q8_threshold(float t) {
+  if (!(t > -65504.0f)) return -INFINITY;  // also NaN: keep every row
+  return fminf(t - (fabsf(t) * 0x1p-9f + 0x1p-23f), 65504.0f);
 }
 
 }  // namespace

@@ -65,11 +65,23 @@ struct StepLayer {
   const _Float16 *cross_k, *cross_v;
 };
 
+struct StepHead {
+  const _Float16* gamma;
+  const _Float16* beta;
+  float eps;
+  const _Float16* w;
+  const int8_t* wq;
+  const float2* meta;
+  const uint8_t* suppress;
+  int64_t* tokens;
+  _Float16* y_out;  // optional: the final LayerNorm output, written by block 0
+};
+
 struct StepArgs {
   StepLayer layer[kStepMaxLayers];
   int n_layers;
-  const int64_t* cur;
-  const int64_t* state;
+  int64_t* cur;
+  int64_t* state;
   const _Float16* embed;
   const _Float16* pos_embed;
   int vocab, max_pos, enc_len;
@@ -78,6 +90,8 @@ struct StepArgs {
   _Float16* x_out;  // last fc2 output
   unsigned char* ws;
   long long spin_limit;  // wall-clock ticks (100 MHz) a wait may take before it flags an error
+  int has_head;          // run the final LN + LM head + argmax + finalize as the last phase
+  StepHead head;
 };
 
 struct Ll {
@@ -132,25 +146,6 @@ __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N]
   }
 #pragma unroll
   for (int k = 0; k < N; ++k) val[k] = static_cast<unsigned>(w[k]);
-}
-
-// Wave 0 waits until each of the n <= 64 * kMaxSentinels sentinel words buf[i * stride + off] carries
-// the tag (all requested at once), then the block passes a barrier. A consumer polls one word per
-// producer this way before it reads the whole region, so blocks that wait long keep few requests in
-// the memory system.
-constexpr int kMaxSentinels = 5;
-__device__ __forceinline__ void ll_sentinels(const uint64_t* buf, int n, int stride, int off, const Ll& c) {
-  if (threadIdx.x < kWave) {
-    int idx[kMaxSentinels];
-#pragma unroll
-    for (int k = 0; k < kMaxSentinels; ++k) {
-      const int i = static_cast<int>(threadIdx.x) + k * kWave;
-      idx[k] = i < n ? i * stride + off : -1;
-    }
-    unsigned v[kMaxSentinels];
-    ll_wait<kMaxSentinels>(buf, idx, v, c);
-  }
-  __syncthreads();
 }
 
 __device__ __forceinline__ unsigned half_bits(_Float16 x) { return __builtin_bit_cast(unsigned short, x); }
@@ -254,17 +249,20 @@ __device__ __forceinline__ const uint64_t* contribution(uint64_t* regions, int i
   return regions + static_cast<size_t>(l) * kLayerWords + (k == 0 ? kOffAttnOut : (k == 1 ? kOffCrossOut : kOffMlpOut));
 }
 
+// Adds the contributions applied .. upto - 1 to h_res, in order; run by kThreads threads (the block, or
+// one wave), t the thread's index among them.
+template <int kThreads = kStepThreads>
 __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, int upto, uint64_t* regions,
-                                               const StepArgs& a, const Ll& c) {
+                                               const StepArgs& a, const Ll& c, int t = threadIdx.x) {
+  constexpr int kPer = (kVecWords + kThreads - 1) / kThreads;
   h2v* h2 = reinterpret_cast<h2v*>(h_res);
-  const int tid = threadIdx.x;
-  for (; applied < upto; ++applied) {  // block-uniform
+  for (; applied < upto; ++applied) {  // uniform over the threads
     if (applied == 0) {
       const _Float16 *ea, *eb;
       embed_rows(a.cur, a.state, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
       const h2v* a2 = reinterpret_cast<const h2v*>(ea);
       const h2v* b2 = reinterpret_cast<const h2v*>(eb);
-      for (int i = tid; i < kHidden / 2; i += kStepThreads) {
+      for (int i = t; i < kHidden / 2; i += kThreads) {
         const h2v p = a2[i], q = b2[i];
         h2v o;
         o.x = f2h(h2f(p.x) + h2f(q.x));
@@ -273,11 +271,13 @@ __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, in
       }
     } else {
       const uint64_t* x = contribution(regions, applied);
-      const int idx[2] = {tid < kVecWords ? tid : -1, tid + kStepThreads < kVecWords ? tid + kStepThreads : -1};
-      unsigned v[2];
-      ll_wait<2>(x, idx, v, c);
+      int idx[kPer];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
+      for (int k = 0; k < kPer; ++k) idx[k] = t + k * kThreads < kVecWords ? t + k * kThreads : -1;
+      unsigned v[kPer];
+      ll_wait<kPer>(x, idx, v, c);
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
         if (idx[k] < 0) continue;
         const h2v hp = h2[idx[k]];
         const h2v xp = __builtin_bit_cast(h2v, v[k]);
@@ -538,6 +538,299 @@ __device__ __forceinline__ void fetch_attn_vector(const uint64_t* src, _Float16*
 }
 
 // ---------------------------------------------------------------------------------------------
+// Final LayerNorm + LM head with the int8 pre-pass + argmax + finalize (the arithmetic of
+// lm_head_q8_kernel<true> and argmax_finalize_kernel in decode.hip). Every block scores 28-row
+// batches k * G + b of the int8 table (the candidate rule holds for any partition of the rows into
+// blocks), rescores its candidates on the fp16 table with lm_head_kernel's lane split and order, and
+// hands its packed maximum to block 0 as two tagged words; block 0 takes the maximum and finalizes.
+// ---------------------------------------------------------------------------------------------
+constexpr int kLmRowWaves = kStepWaves - 1;                    // waves 0-6 score rows, wave 7 awaits the
+constexpr int kLmBatchRows = kLmRowWaves * (kWave / kQ8Lpr);  // last fc2 output; 28 rows a batch, 4 a wave
+constexpr int kLmMaxBatches = 8;                              // per block: ceil(vocab / G) <= 8 * 28
+// Batches in flight per wave. Two measured best: requested deeper (4, 6) or earlier than the block's
+// arrival here, the table loads slow the last fc2 and the stream itself down.
+constexpr int kLmBufs = 2;
+constexpr int kMaxGrid = 1024;                                // blocks whose maxima the hand-off region holds
+static_assert(kLmMaxBatches * kLmBatchRows <= 256, "candidate list");
+
+
+struct alignas(16) LmLds {  // yhi / ylo are read as 16-byte chunks
+  int8_t yhi[kHidden], ylo[kHidden];
+  h2v gamma[kHidden / 2], beta[kHidden / 2];  // the final LayerNorm's, read at the start of the launch
+  float ub[kLmMaxBatches * kLmBatchRows];
+  int cand[kLmMaxBatches * kLmBatchRows];
+  int ncand;
+  unsigned long long best[kStepWaves * 2];
+};
+
+// y = LN(h_res) with the reduction order of ln_finish<1024, true> (the LM-head kernel's 1024-thread
+// block): thread t stands for threads t and t + 512 of that block, whose partial sums go through the
+// same wave butterflies and are added over the 16 wave slots in order. h_res is already rounded.
+__device__ __forceinline__ void ln_final(const _Float16* h_res, const h2v* g2, const h2v* b2, float eps, _Float16* y,
+                                         float* red) {
+  constexpr int NT = 1024, kVirt = NT / kStepThreads, kWaves = NT / kWave;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const h2v* h2 = reinterpret_cast<const h2v*>(h_res);
+  float2 r[kVirt];
+  h2v g[kVirt], be[kVirt];
+  float part[kVirt];
+#pragma unroll
+  for (int k = 0; k < kVirt; ++k) {
+    const int vt = tid + k * kStepThreads;
+    r[k] = make_float2(0.f, 0.f);
+    g[k] = be[k] = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
+    float sum = 0.f;
+    if (vt < kHidden / 2) {
+      const h2v a = h2[vt];
+      const float rx = h2f(a.x), ry = h2f(a.y);
+      r[k] = make_float2(rx, ry);
+      sum += rx + ry;
+      g[k] = g2[vt];
+      be[k] = b2[vt];
+    }
+    part[k] = group_sum<kWave>(sum);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < kVirt; ++k) red[wave + k * kStepWaves] = part[k];
+  }
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) s += red[i];
+  const float mean = s * (1.0f / kHidden);
+#pragma unroll
+  for (int k = 0; k < kVirt; ++k) {
+    const int vt = tid + k * kStepThreads;
+    float sq = 0.f;
+    if (vt < kHidden / 2) {
+      const float dx = r[k].x - mean, dy = r[k].y - mean;
+      sq += dx * dx + dy * dy;
+    }
+    part[k] = group_sum<kWave>(sq);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < kVirt; ++k) red[kWaves + wave + k * kStepWaves] = part[k];
+  }
+  __syncthreads();
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) s2 += red[kWaves + i];
+  const float var = s2 * (1.0f / kHidden);
+  const float inv = rsqrtf(var + eps);
+  h2v* y2 = reinterpret_cast<h2v*>(y);
+#pragma unroll
+  for (int k = 0; k < kVirt; ++k) {
+    const int vt = tid + k * kStepThreads;
+    if (vt < kHidden / 2) {
+      h2v o;
+      o.x = f2h((r[k].x - mean) * inv * h2f(g[k].x) + h2f(be[k].x));
+      o.y = f2h((r[k].y - mean) * inv * h2f(g[k].y) + h2f(be[k].y));
+      y2[vt] = o;
+    }
+  }
+}
+
+__device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead& H, const Ll& c, _Float16* h_res,
+                                              int& applied, uint64_t* regions, uint64_t* maxima, _Float16* y_lds,
+                                              float* red, LmLds& s, int64_t pos_raw, int64_t n_tok) {
+  constexpr int NT = 1024, kWaves = NT / kWave;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, b = blockIdx.x, vocab = a.vocab;
+  const int sub = lane & (kQ8Lpr - 1), rsel = lane / kQ8Lpr;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // branches on it are wave-uniform
+  // the block's rows: an even, contiguous share [r0, r1) of the table, in batches of kLmBatchRows
+  const int r0 = static_cast<int>(static_cast<int64_t>(b) * vocab / G);
+  const int r1 = static_cast<int>(static_cast<int64_t>(b + 1) * vocab / G);
+  const int nb = (r1 - r0 + kLmBatchRows - 1) / kLmBatchRows;  // <= kLmMaxBatches
+  auto base_of = [&](int k) { return r0 + k * kLmBatchRows; };
+  const uint4* wq4 = reinterpret_cast<const uint4*>(H.wq);
+  struct Batch {
+    uint4 w[kQ8C];
+    float2 m;
+    uint32_t sp;
+  };
+  auto load = [&](int k, Batch& bt) {  // rows past r1 load row r1 - 1 and are dropped when scored
+    const size_t row = min(base_of(k) + wave * 4 + rsel, r1 - 1);
+#pragma unroll
+    for (int cc = 0; cc < kQ8C; ++cc) bt.w[cc] = ld_lm_head(wq4 + row * kQ8Chunks + sub + kQ8Lpr * cc);
+    bt.m = H.meta[row];
+    bt.sp = H.suppress[row];
+  };
+  if (tid == 0) s.ncand = 0;
+  // Waves 0-6 request their first batches as soon as the block gets here (its layer work is done, the
+  // last fc2 output may be microseconds away); wave 7 alone awaits the missing residual contributions,
+  // so its polls do not queue behind the table loads (a wave's loads return in order).
+  Batch bt[kLmBufs];
+  if (wv < kLmRowWaves) {
+#pragma unroll
+    for (int k = 0; k < kLmBufs; ++k)
+      if (k < nb) load(k, bt[k]);
+  } else {
+    resid_catch_up<kWave>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, lane);
+  }
+  applied = 3 * a.n_layers + 1;
+  __syncthreads();
+  ln_final(h_res, s.gamma, s.beta, H.eps, y_lds, red);
+  __syncthreads();
+  if (H.y_out && b == 0)
+    for (int i = tid; i < kHidden / 2; i += kStepThreads)
+      reinterpret_cast<unsigned*>(H.y_out)[i] = reinterpret_cast<const unsigned*>(y_lds)[i];
+  // y statistics (max |y| and |y|^2, each thread standing for threads t and t + 512 of the 1024-thread
+  // block), then y_int = rint(y / t) in two int8 digits
+  float wmax[2], wsq[2];
+  h2v yp[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int vt = tid + k * kStepThreads;
+    yp[k] = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
+    if (vt < kHidden / 2) yp[k] = reinterpret_cast<const h2v*>(y_lds)[vt];
+    const float y0 = h2f(yp[k].x), y1 = h2f(yp[k].y);
+    wmax[k] = group_max<64>(fmaxf(fabsf(y0), fabsf(y1)));
+    wsq[k] = group_sum<64>(y0 * y0 + y1 * y1);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      red[2 * kWaves + wave + k * kStepWaves] = wmax[k];
+      red[3 * kWaves + wave + k * kStepWaves] = wsq[k];
+    }
+  }
+  __syncthreads();
+  float amax = 0.f, ysq = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    amax = fmaxf(amax, red[2 * kWaves + i]);
+    ysq += red[3 * kWaves + i];
+  }
+  const float t = amax > 0.f ? amax / static_cast<float>(kQ8YMax) : 1.0f;
+  const float tinv = amax > 0.f ? static_cast<float>(kQ8YMax) / amax : 0.f;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int vt = tid + k * kStepThreads;
+    if (vt < kHidden / 2) {
+      const float y0 = h2f(yp[k].x), y1 = h2f(yp[k].y);
+      const int n0 = static_cast<int>(fminf(fmaxf(rintf(y0 * tinv), -kQ8YMax), kQ8YMax));
+      const int n1 = static_cast<int>(fminf(fmaxf(rintf(y1 * tinv), -kQ8YMax), kQ8YMax));
+      const int h0 = (n0 + 64) >> 7, h1 = (n1 + 64) >> 7;  // floor division; lo digits in [-64, 63]
+      s.yhi[2 * vt] = static_cast<int8_t>(h0);
+      s.yhi[2 * vt + 1] = static_cast<int8_t>(h1);
+      s.ylo[2 * vt] = static_cast<int8_t>(n0 - 128 * h0);
+      s.ylo[2 * vt + 1] = static_cast<int8_t>(n1 - 128 * h1);
+    }
+  }
+  __syncthreads();
+  const double ny = static_cast<double>(sqrtf(ysq)) * (1.0 + 0x1p-9);
+  const double neta = amax > 0.f ? 0.51 * static_cast<double>(t) * sqrt(static_cast<double>(kHidden)) : 0.0;
+  const double nE_per_s = 127.0 * sqrt(static_cast<double>(kHidden)) * (1.0 + 0x1p-30);
+  float lb_max = -INFINITY;
+  auto score = [&](int k, const Batch& bt) {
+    const int slot_row = wave * 4 + rsel;
+    const int row = base_of(k) + slot_row;
+    int ah = 0, al = 0;
+#pragma unroll
+    for (int cc = 0; cc < kQ8C; ++cc) {
+      const uint4 dh = reinterpret_cast<const uint4*>(s.yhi)[sub + kQ8Lpr * cc];
+      const uint4 dl = reinterpret_cast<const uint4*>(s.ylo)[sub + kQ8Lpr * cc];
+      ah = dot16_i8(bt.w[cc], dh, ah);
+      al = dot16_i8(bt.w[cc], dl, al);
+    }
+    ah = xor_add_i16(ah);
+    al = xor_add_i16(al);
+    const double av = static_cast<double>(bt.m.x) * static_cast<double>(t) * static_cast<double>(128ll * ah + al);
+    const double nE = static_cast<double>(bt.m.x) * nE_per_s + static_cast<double>(bt.m.y);
+    const double rv = (ny * static_cast<double>(bt.m.y) + (neta + static_cast<double>(kQ8Gamma) * ny) * nE) *
+                      (1.0 + 0x1p-20);
+    const bool live = row < r1 && !bt.sp;
+    const float ub = live ? __double2float_ru(av + rv) : -INFINITY;
+    const float lb = live ? __double2float_rd(av - rv) : -INFINITY;
+    lb_max = fmaxf(lb_max, lb);
+    if (sub == 0) s.ub[k * kLmBatchRows + slot_row] = ub;
+  };
+  if (wv < kLmRowWaves) {
+#pragma unroll
+    for (int k = 0; k < kLmMaxBatches; ++k) {  // batch k in buffer k % kLmBufs, refilled once scored
+      if (k < nb) {
+        score(k, bt[k % kLmBufs]);
+        if (k + kLmBufs < nb) load(k + kLmBufs, bt[k % kLmBufs]);
+      }
+    }
+  }
+  lb_max = group_max<64>(lb_max);
+  if (lane == 0) red[wave] = lb_max;
+  __syncthreads();  // also publishes s.ub
+  float tb = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kStepWaves; ++i) tb = fmaxf(tb, red[i]);
+  const float thr = q8_threshold(tb);
+  for (int i = tid; i < nb * kLmBatchRows; i += kStepThreads) {
+    const int row = base_of(i / kLmBatchRows) + i % kLmBatchRows;
+    const float ub = s.ub[i];
+    if (row < r1 && ub != -INFINITY && !(ub < thr)) s.cand[atomicAdd(&s.ncand, 1)] = row;
+  }
+  __syncthreads();
+  // exact logits of the candidates: the lane split and order of lm_head_kernel
+  using RS = RowSplit<kHidden>;
+  const int sub32 = lane & 31, rsel32 = lane >> 5;
+  const uint4* w4 = reinterpret_cast<const uint4*>(H.w);
+  uint4 xr[RS::kC];
+#pragma unroll
+  for (int cc = 0; cc < RS::kC; ++cc) xr[cc] = reinterpret_cast<const uint4*>(y_lds)[sub32 + 32 * cc];
+  const int nc = s.ncand;
+  unsigned long long mine = 0;
+  for (int i0c = wave * 2; i0c < nc; i0c += kStepWaves * 2) {
+    const int i = i0c + rsel32;
+    const int row = s.cand[i < nc ? i : i0c];
+    uint4 wr[RS::kC];
+#pragma unroll
+    for (int cc = 0; cc < RS::kC; ++cc)
+      wr[cc] = ld_lm_head(w4 + static_cast<size_t>(row) * RS::kChunksRow + sub32 + 32 * cc);
+    float acc = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < RS::kC; ++cc) acc = dot8(wr[cc], xr[cc], acc);
+    acc = group_sum<32>(acc);
+    const unsigned long long sc = pack_score(round_h(acc), row);
+    if (i < nc && sc > mine) mine = sc;
+  }
+  if (sub32 == 0) s.best[wave * 2 + rsel32] = mine;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long m = 0;
+#pragma unroll
+    for (int i = 0; i < kStepWaves * 2; ++i) m = s.best[i] > m ? s.best[i] : m;
+    ll_store(maxima + 2 * b, c.tag, static_cast<unsigned>(m));
+    ll_store(maxima + 2 * b + 1, c.tag, static_cast<unsigned>(m >> 32));
+  }
+  if (b != 0) return;  // block-uniform
+  // block 0: the maximum over the blocks (thread i takes block i's two words), then the finalize of
+  // argmax_finalize_kernel with the state words read at the start of the launch (no other block writes
+  // them)
+  unsigned long long m = 0;
+  for (int i = tid; i < G; i += kStepThreads) {
+    const int idx[2] = {2 * i, 2 * i + 1};
+    unsigned v[2];
+    ll_wait<2>(maxima, idx, v, c);
+    const unsigned long long x = (static_cast<unsigned long long>(v[1]) << 32) | v[0];
+    m = x > m ? x : m;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned lo = __shfl_xor(static_cast<unsigned>(m), o), hi = __shfl_xor(static_cast<unsigned>(m >> 32), o);
+    const unsigned long long x = (static_cast<unsigned long long>(hi) << 32) | lo;
+    m = x > m ? x : m;
+  }
+  if (lane == 0) s.best[wave] = m;
+  __syncthreads();
+  if (tid == 0) {
+#pragma unroll
+    for (int i = 0; i < kStepWaves; ++i) m = s.best[i] > m ? s.best[i] : m;
+    const FinArgs fin{H.tokens, a.state, a.cur, a.max_pos};
+    finalize_known(m, n_tok, pos_raw, fin);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // The kernel
 // ---------------------------------------------------------------------------------------------
 struct Sched {
@@ -550,7 +843,8 @@ struct Sched {
 __global__ void __launch_bounds__(kStepThreads) decoder_layers_kernel(StepArgs a) {
   __shared__ __align__(16) _Float16 h_res[kHidden];
   __shared__ __align__(16) _Float16 x_lds[kStepFfn];
-  __shared__ float red[4 * kStepWaves];
+  __shared__ float red[8 * kStepWaves];  // LayerNorm sums (16 slots each for the LM head's 1024-thread order)
+  __shared__ __align__(16) LmLds lm;
   __shared__ float wgt[kMaxCombineHeads * kMaxCombineSplits];
   __shared__ float den[kMaxCombineHeads];
   __shared__ AttnLds att;
@@ -572,6 +866,12 @@ __global__ void __launch_bounds__(kStepThreads) decoder_layers_kernel(StepArgs a
   const Ll c{ctl, epoch + 1u, a.spin_limit};
 
   const int64_t pos_raw = a.state[0];
+  const int64_t n_tok = a.has_head && blockIdx.x == 0 ? a.state[1] : 0;  // for block 0's finalize
+  if (a.has_head)
+    for (int i = tid; i < kHidden / 2; i += kStepThreads) {
+      lm.gamma[i] = reinterpret_cast<const h2v*>(a.head.gamma)[i];
+      lm.beta[i] = reinterpret_cast<const h2v*>(a.head.beta)[i];
+    }
   const int pos = static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw));
   const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
   const int ns_cross = (a.enc_len + kCrossSplitKeys - 1) / kCrossSplitKeys;
@@ -772,8 +1072,12 @@ __global__ void __launch_bounds__(kStepThreads) decoder_layers_kernel(StepArgs a
     }
   }
 
-  // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
-  if (blockIdx.x == 0) {
+  if (a.has_head) {
+    __syncthreads();
+    lm_head_phase(a, a.head, c, h_res, applied, regions, regions + static_cast<size_t>(a.n_layers) * kLayerWords,
+                  x_lds, red, lm, pos_raw, n_tok);
+  } else if (blockIdx.x == 0) {
+    // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
     __syncthreads();
     resid_catch_up(h_res, applied, 3 * a.n_layers, regions, a, c);  // the last fc2 output stays out
     __syncthreads();
@@ -793,30 +1097,39 @@ using namespace fw;
 
 extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
-  return kCtlBytes + static_cast<size_t>(n_layers) * kLayerWords * sizeof(uint64_t);
+  // control words, each layer's hand-off regions, then the LM head's per-block maxima
+  return kCtlBytes + (static_cast<size_t>(n_layers) * kLayerWords + 2 * kMaxGrid) * sizeof(uint64_t);
 }
 
 extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }
 
-extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, const int64_t* cur,
-                                      const int64_t* state, const void* embed, const void* pos_embed, int vocab,
-                                      int max_pos, int enc_len, float scale, void* h_out, void* x_out,
-                                      void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
-  if (!layers || !cur || !state || !embed || !pos_embed || !h_out || !x_out || !workspace)
-    return fw_fail(FW_EINVAL, "decoder_step_layers: null pointer");
+static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int n_layers, const fw_dec_head* head,
+                               int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                               int max_pos, int enc_len, float scale, void* h_out, void* x_out, void* workspace,
+                               int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
+  if (!layers || !cur || !state || !embed || !pos_embed || !workspace || (!head && (!h_out || !x_out)))
+    return fw_fail(FW_EINVAL, "%s: null pointer", name);
   if (n_layers < 1 || n_layers > kStepMaxLayers)
-    return fw_fail(FW_EINVAL, "decoder_step_layers: n_layers must be in [1, %d]", kStepMaxLayers);
+    return fw_fail(FW_EINVAL, "%s: n_layers must be in [1, %d]", name, kStepMaxLayers);
   if (vocab < 1 || max_pos < 1 || max_pos > kMaxCombineSplits * kSelfSplitKeys)
-    return fw_fail(FW_EINVAL, "decoder_step_layers: max_pos must be in [1, %d]", kMaxCombineSplits * kSelfSplitKeys);
+    return fw_fail(FW_EINVAL, "%s: max_pos must be in [1, %d]", name, kMaxCombineSplits * kSelfSplitKeys);
   if (enc_len < 1 || enc_len > kMaxCombineSplits * kCrossSplitKeys)
-    return fw_fail(FW_EINVAL, "decoder_step_layers: enc_len must be in [1, %d]", kMaxCombineSplits * kCrossSplitKeys);
+    return fw_fail(FW_EINVAL, "%s: enc_len must be in [1, %d]", name, kMaxCombineSplits * kCrossSplitKeys);
   if (ws_bytes < static_cast<int64_t>(fw_decoder_step_workspace_bytes(n_layers)))
-    return fw_fail(FW_EINVAL, "decoder_step_layers: workspace too small (%lld < %zu bytes)",
-                   static_cast<long long>(ws_bytes), fw_decoder_step_workspace_bytes(n_layers));
+    return fw_fail(FW_EINVAL, "%s: workspace too small (%lld < %zu bytes)", name, static_cast<long long>(ws_bytes),
+                   fw_decoder_step_workspace_bytes(n_layers));
   if ((reinterpret_cast<uintptr_t>(workspace) & 255u) || (reinterpret_cast<uintptr_t>(h_out) & 3u) ||
       (reinterpret_cast<uintptr_t>(x_out) & 3u))
-    return fw_fail(FW_EINVAL, "decoder_step_layers: workspace must be 256-byte and h_out / x_out 4-byte aligned");
-  if (spin_limit < 0) return fw_fail(FW_EINVAL, "decoder_step_layers: spin_limit must be >= 0");
+    return fw_fail(FW_EINVAL, "%s: workspace must be 256-byte and h_out / x_out 4-byte aligned", name);
+  if (spin_limit < 0) return fw_fail(FW_EINVAL, "%s: spin_limit must be >= 0", name);
+  if (head) {
+    const fw_dec_head& hd = *head;
+    if (!hd.ln_gamma || !hd.ln_beta || !hd.w || !hd.wq || !hd.meta || !hd.suppress || !hd.tokens)
+      return fw_fail(FW_EINVAL, "%s: null LM-head tensor", name);
+    if ((reinterpret_cast<uintptr_t>(hd.w) & 15u) || (reinterpret_cast<uintptr_t>(hd.wq) & 15u) ||
+        (reinterpret_cast<uintptr_t>(hd.meta) & 7u) || (reinterpret_cast<uintptr_t>(hd.y_out) & 3u))
+      return fw_fail(FW_EINVAL, "%s: w and wq must be 16-byte aligned, meta 8-byte and y_out 4-byte aligned", name);
+  }
   StepArgs a{};
   for (int l = 0; l < n_layers; ++l) {
     const fw_dec_layer& s = layers[l];
@@ -824,12 +1137,12 @@ extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, 
                           s.cross_out_w, s.ln3_gamma, s.ln3_beta, s.fc1_w, s.fc2_w, s.self_k, s.self_v,
                           s.cross_k, s.cross_v};
     for (const void* p : must)
-      if (!p) return fw_fail(FW_EINVAL, "decoder_step_layers: layer %d has a null tensor", l);
+      if (!p) return fw_fail(FW_EINVAL, "%s: layer %d has a null tensor", name, l);
     const void* mats[] = {s.qkv_w, s.out_w, s.cross_q_w, s.cross_out_w, s.fc1_w, s.fc2_w,
                           s.self_k, s.self_v, s.cross_k, s.cross_v};
     for (const void* p : mats)
       if (reinterpret_cast<uintptr_t>(p) & 15u)
-        return fw_fail(FW_EINVAL, "decoder_step_layers: layer %d: weights and caches must be 16-byte aligned", l);
+        return fw_fail(FW_EINVAL, "%s: layer %d: weights and caches must be 16-byte aligned", name, l);
     StepLayer& d = a.layer[l];
     auto h = [](const void* p) { return static_cast<const _Float16*>(p); };
     d.ln1_g = h(s.ln1_gamma); d.ln1_b = h(s.ln1_beta); d.qkv_w = h(s.qkv_w); d.qkv_b = h(s.qkv_b);
@@ -841,6 +1154,22 @@ extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, 
     d.eps1 = s.ln1_eps; d.eps2 = s.ln2_eps; d.eps3 = s.ln3_eps;
     d.self_k = static_cast<_Float16*>(s.self_k); d.self_v = static_cast<_Float16*>(s.self_v);
     d.cross_k = h(s.cross_k); d.cross_v = h(s.cross_v);
+  }
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 2)
+    return fw_fail(FW_EHIP, "%s: cannot read the device's CU count", name);
+  const int grid = cus < kMaxGrid ? cus : kMaxGrid;
+  if (head) {
+    const fw_dec_head& hd = *head;
+    if ((vocab + grid - 1) / grid > kLmMaxBatches * kLmBatchRows)
+      return fw_fail(FW_EINVAL, "%s: vocab %d exceeds %d rows for each of %d blocks", name, vocab,
+                     kLmMaxBatches * kLmBatchRows, grid);
+    a.has_head = 1;
+    a.head = StepHead{static_cast<const _Float16*>(hd.ln_gamma), static_cast<const _Float16*>(hd.ln_beta), hd.ln_eps,
+                      static_cast<const _Float16*>(hd.w), static_cast<const int8_t*>(hd.wq),
+                      reinterpret_cast<const float2*>(hd.meta), hd.suppress, hd.tokens,
+                      static_cast<_Float16*>(hd.y_out)};
   }
   a.n_layers = n_layers;
   a.cur = cur;
@@ -855,10 +1184,24 @@ extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, 
   a.x_out = static_cast<_Float16*>(x_out);
   a.ws = static_cast<unsigned char*>(workspace);
   a.spin_limit = spin_limit;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus < 2)
-    return fw_fail(FW_EHIP, "decoder_step_layers: cannot read the device's CU count");
-  hipLaunchKernelGGL(decoder_layers_kernel, dim3(cus), dim3(kStepThreads), 0, stream, a);
-  return fw_check_launch("decoder_step_layers");
+  hipLaunchKernelGGL(decoder_layers_kernel, dim3(grid), dim3(kStepThreads), 0, stream, a);
+  return fw_check_launch(name);
+}
+
+extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, const int64_t* cur,
+                                      const int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                                      int max_pos, int enc_len, float scale, void* h_out, void* x_out,
+                                      void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
+  return decoder_step_launch("decoder_step_layers", layers, n_layers, nullptr, const_cast<int64_t*>(cur),
+                             const_cast<int64_t*>(state), embed, pos_embed, vocab, max_pos, enc_len, scale, h_out,
+                             x_out, workspace, ws_bytes, spin_limit, stream);
+}
+
+extern "C" int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, int64_t* cur,
+                               int64_t* state, const void* embed, const void* pos_embed, int vocab, int max_pos,
+                               int enc_len, float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit,
+                               hipStream_t stream) {
+  if (!head) return fw_fail(FW_EINVAL, "decoder_step: null LM head");
+  return decoder_step_launch("decoder_step", layers, n_layers, head, cur, state, embed, pos_embed, vocab, max_pos,
+                             enc_len, scale, nullptr, nullptr, workspace, ws_bytes, spin_limit, stream);
 }

@@ -333,6 +333,47 @@ class WhisperExt:
                    embed.data_ptr(), pos_embed.data_ptr(), embed.size(0), int(max_pos), int(enc_len), float(scale),
                    h_out.data_ptr(), x_out.data_ptr(), ws.data_ptr(), ws.numel(), int(spin_limit), _stream())
 
+    def final_layernorm(self, h, x, gamma, beta, y, eps):
+        """The LM-head kernels' final LayerNorm (their reduction order): y = LN(fp16(h + x))."""
+        for t, n in ((h, 'h'), (gamma, 'gamma'), (beta, 'beta'), (y, 'y')):
+            check_half(t, n)
+        if x is not None:
+            check_half(x, 'x')
+        _require(h.numel() == HIDDEN and y.numel() == HIDDEN, f'hidden size must be {HIDDEN}')
+        self._call('fw_final_layernorm', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(),
+                   HIDDEN, float(eps), _stream())
+
+    def decoder_head(self, gamma, beta, eps, w, wq, meta, suppress, tokens, y_out=None):
+        """The fw_dec_head of decoder_step (raw pointers: the tensors must outlive it)."""
+        for t, n in ((gamma, 'gamma'), (beta, 'beta'), (w, 'w')):
+            check_half(t, n)
+        _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
+        _check(wq, 'wq', torch.int8, 'int8')
+        _check(meta, 'meta', torch.float32, 'fp32')
+        _require(tuple(wq.shape) == tuple(w.shape) and tuple(meta.shape) == (w.size(0), 2),
+                 'wq must match w and meta be [vocab, 2]')
+        _require(suppress.dtype == torch.bool and suppress.is_cuda and suppress.is_contiguous()
+                 and suppress.numel() == w.size(0), 'suppress must be bool [vocab]')
+        _check(tokens, 'tokens', torch.int64, 'int64')
+        if y_out is not None:
+            check_half(y_out, 'y_out')
+            _require(y_out.numel() == HIDDEN, f'y_out must be [{HIDDEN}]')
+        return _lib.DecHead(gamma.data_ptr(), beta.data_ptr(), float(eps), w.data_ptr(), wq.data_ptr(), meta.data_ptr(),
+                            suppress.data_ptr(), tokens.data_ptr(), _ptr(y_out))
+
+    def decoder_step(self, table, head, cur, state, embed, pos_embed, max_pos, enc_len, scale, ws, vocab,
+                     spin_limit=2_000_000):
+        """A whole decoder step in one launch (fw_decoder_step): the layers of decoder_step_layers, then the
+        final LN, the int8-pre-pass LM head, the argmax and the finalize (tokens, state and cur advance)."""
+        check_half(embed, 'embed')
+        check_half(pos_embed, 'pos_embed')
+        for t, n in ((cur, 'cur'), (state, 'state')):
+            _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
+        _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')
+        self._call('fw_decoder_step', ctypes.addressof(table), len(table), ctypes.addressof(head), cur.data_ptr(),
+                   state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(), int(vocab), int(max_pos), int(enc_len),
+                   float(scale), ws.data_ptr(), ws.numel(), int(spin_limit), _stream())
+
     @staticmethod
     def decoder_step_error(ws, clear=True):
         """The workspace's error word (nonzero: a wait of the step timed out); synchronises."""

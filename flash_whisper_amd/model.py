@@ -34,7 +34,7 @@ SELF_SPLIT, CROSS_SPLIT = 64, 256  # keys per split block of the decoder's self 
 class CustomModel:
     @torch.inference_mode()
     def __init__(self, model_id=SYNTHETIC, cache_dir=None, *, seed=0, dims=TURBO, setup=None, selftest=True,
-                 capture=True, lm_q8=True, persistent_step=True):
+                 capture=True, lm_q8=True, persistent_step=True, persistent_head=True):
         if not torch.cuda.is_available():
             raise RuntimeError('CustomModel requires a HIP device')
         self._weights, self.tokenizer, self.checkpoint = None, None, None
@@ -59,8 +59,10 @@ class CustomModel:
         self.eos = set(self.setup.eos)
         self.record_events = False   # time every chunk replay with HIP events (bench.py)
         self.use_lm_q8 = lm_q8       # LM head with the int8 pre-pass (same token as the fp16 head)
-        # the decoder layers of a step as one persistent launch (same outputs as the 34-launch step)
+        # the decoder step as one persistent launch, layers and LM head (same outputs as the 34-launch step);
+        # persistent_head=False keeps the LM head and finalize as launches of their own
         self.persistent_step = persistent_step
+        self.persistent_head = persistent_head
         self.chunk_events = []
 
         self._specs = W.spec_map(dims)
@@ -125,6 +127,7 @@ class CustomModel:
         self.h_fin = torch.zeros(dm, dtype=half, device='cuda')
         self.x_fin = torch.zeros(dm, dtype=half, device='cuda')
         self.step_table = self.ext.decoder_layer_table([self._layer_tensors(i) for i in range(d.dec_layers)])
+        self._make_step_head()
         # split-K attention partials (the fused step, the reference-granularity step and the batched
         # prompt, whose n queries take n times the splits of one)
         n = len(self.prompt) if self.batch_prompt else 1
@@ -344,6 +347,12 @@ class CustomModel:
         t['cross_k'], t['cross_v'] = self.cross_kv[i, 0], self.cross_kv[i, 1]
         return t
 
+    def _make_step_head(self, y_out=None):
+        """The LM head of the one-launch step; y_out (fp16 [d_model]) receives the final LayerNorm output."""
+        g, be, eps = self.final_ln
+        self.step_head = self.ext.decoder_head(g, be, eps, self.lm_head, self.lm_q8, self.lm_meta, self.suppress,
+                                               self.tokens, y_out)
+
     def _step(self, lm_head=True):
         """One decoder token, entirely on the device (custom/model.py:107-123): the decoder layers as one
         persistent launch (``persistent_step``), or in 32 launches, per layer [LN1+QKV] [self-attn
@@ -353,6 +362,10 @@ class CustomModel:
         ends after the layers and only advances the position."""
         ext, d, dm = self.ext, self.dims, self.dims.d_model
         if self.persistent_step and lm_head:
+            if self.persistent_head and self.use_lm_q8:
+                ext.decoder_step(self.step_table, self.step_head, self.cur, self.state, self.embed, self.pos_embed,
+                                 self.max_pos, self.enc_len, self.scale, self.step_ws, self.dims.vocab)
+                return
             ext.decoder_step_layers(self.step_table, self.cur, self.state, self.embed, self.pos_embed, self.max_pos,
                                     self.enc_len, self.scale, self.h_fin, self.x_fin, self.step_ws)
             self._lm_head(self.h_fin, self.x_fin)

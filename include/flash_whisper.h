@@ -107,6 +107,13 @@ int fw_ln_gemv(const void* h, const void* x, void* h_out, const void* gamma, con
                int max_pos, const void* w, const void* bias, void* out, int n_out, int k_in, int act,
                hipStream_t stream);
 
+/* The LM head's final LayerNorm alone: y <- fp16(LN(fp16(h + x)) * gamma + beta) (x may be NULL) with
+ * the reduction order of the 1024-thread LM-head kernels (fw_lm_head_argmax_fused, fw_lm_head_argmax_q8),
+ * so y is the vector those kernels score, bit for bit. Replaces the final add_layernorm of
+ * custom/model.py:121 at that order. n == 1280. */
+int fw_final_layernorm(const void* h, const void* x, const void* gamma, const void* beta, void* y, int n, float eps,
+                       hipStream_t stream);
+
 /* Decode attention in one launch (same contract as fw_decode_attention, no workspace): one
  * 1024-thread block per head covers all keys and merges its 16 wave partials on chip. */
 int fw_decode_attention_fused(const void* q, void* k, void* v, void* out, const int64_t* len_state,
@@ -197,6 +204,30 @@ int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, const int64
                            const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len, float scale,
                            void* h_out, void* x_out, void* workspace, int64_t ws_bytes, int64_t spin_limit,
                            hipStream_t stream);
+
+/* The LM head of fw_decoder_step: final LayerNorm (gamma, beta, eps), the tied fp16 table w [vocab, 1280]
+ * with its int8 copy wq [vocab, 1280] and meta fp32 [vocab, 2] (fw_lm_head_q8_pack), the suppress mask
+ * u8 [vocab], the token list the finalize appends to (int64 [max_pos]), and optionally y_out fp16[1280]
+ * (NULL: not written) for the final LayerNorm output the LM head scores. */
+typedef struct fw_dec_head {
+  const void *ln_gamma, *ln_beta;
+  float ln_eps;
+  const void *w, *wq;
+  const float* meta;
+  const uint8_t* suppress;
+  int64_t* tokens;
+  void* y_out;
+} fw_dec_head;
+
+/* One whole decoder step in ONE launch: fw_decoder_step_layers followed by the final LayerNorm, the LM
+ * head with the int8 pre-pass, the argmax and the finalize (replaces custom/model.py:107-123, i.e. the
+ * per-layer ops above plus lm_head_argmax and argmax_finalize, whisper_kernels.cu:278-298). The token
+ * is that of fw_lm_head_argmax_q8 + fw_argmax_finalize, bit for bit: tokens[state[1]] <- token,
+ * state advances, cur <- token. Same workspace, limits and residency rules as fw_decoder_step_layers;
+ * vocab <= 224 * (the device's CU count). */
+int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, int64_t* cur, int64_t* state,
+                    const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len, float scale,
+                    void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream);
 
 /* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
  * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by

@@ -72,14 +72,16 @@ def test_validation_errors_return_einval(built_lib):
 
 
 def test_decoder_step_entry_points_validate(built_lib):
-    """fw_decoder_step_layers checks its arguments before any HIP call; the workspace size covers the
-    control words and every layer's hand-off regions."""
+    """fw_decoder_step_layers and fw_decoder_step check their arguments before any HIP call; the workspace
+    size covers the control words, every layer's hand-off regions and the LM head's per-block maxima."""
     from flash_whisper_amd import _lib
 
     lib = built_lib
     assert lib.fw_decoder_step_max_layers() == 8
-    one = lib.fw_decoder_step_workspace_bytes(1)
-    assert one > 256 and lib.fw_decoder_step_workspace_bytes(4) == 256 + 4 * (one - 256)
+    one, two = lib.fw_decoder_step_workspace_bytes(1), lib.fw_decoder_step_workspace_bytes(2)
+    layer = two - one
+    assert layer > 0 and one == 256 + layer + 2 * 1024 * 8  # two 8-byte words per block, up to 1024 blocks
+    assert lib.fw_decoder_step_workspace_bytes(4) == one + 3 * layer
     assert lib.fw_decoder_step_workspace_bytes(0) == 0 and lib.fw_decoder_step_workspace_bytes(9) == 0
     assert ctypes.sizeof(_lib.DecLayer) == 18 * 8 + 3 * 4 + 4 + 4 * 8  # C layout: pad before the caches
     table = (_lib.DecLayer * 4)()
@@ -96,6 +98,17 @@ def test_decoder_step_entry_points_validate(built_lib):
     bad[11] = 100  # workspace too small
     assert lib.fw_decoder_step_layers(table, 4, *bad) == _lib.FW_EINVAL and b'too small' in lib.fw_last_error()
     assert lib.fw_decoder_step_layers(None, 4, *args) == _lib.FW_EINVAL
+    # the whole step: the LM head is required and checked like the layers
+    step = [d, d, d, d, 51866, 448, 1500, 0.125, d, lib.fw_decoder_step_workspace_bytes(4), 1000, None]
+    assert lib.fw_decoder_step(table, 4, None, *step) == _lib.FW_EINVAL and b'null LM head' in lib.fw_last_error()
+    assert ctypes.sizeof(_lib.DecHead) == 2 * 8 + 8 + 6 * 8  # the float is padded to the next pointer
+    head = _lib.DecHead(256, 256, 1e-5, 256, 256, 256, None, 256, None)
+    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), *step) == _lib.FW_EINVAL
+    assert b'null LM-head tensor' in lib.fw_last_error()  # no suppress mask
+    head.suppress = 256
+    head.wq = 264
+    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), *step) == _lib.FW_EINVAL
+    assert b'16-byte aligned' in lib.fw_last_error()
 
 
 def test_status_becomes_runtime_error(built_lib):

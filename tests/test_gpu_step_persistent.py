@@ -1,8 +1,10 @@
-"""The decoder layers of a step as one persistent launch (fw_decoder_step_layers) against the 32-launch
-step of the same layers: K/V cache, residual, last fc2 output, token, state and current token
-bit-identical after every step, at positions across the self-attention split boundaries and up to the
-end of the cache; the error word after a flagged wait. The 224-id oracle fixture runs through the
-persistent step in tests/test_gpu_model.py (it is the model's default)."""
+"""The decoder step as one persistent launch against the 34-launch step of the same weights: the layers
+alone (fw_decoder_step_layers: K/V cache, residual, last fc2 output) and the whole step with the final
+LayerNorm, int8-pre-pass LM head, argmax and finalize (fw_decoder_step: K/V cache, final LayerNorm
+output, token list, state, current token), bit-identical after every step, at positions across the
+self-attention split boundaries and up to the end of the cache; the error word after a flagged wait.
+The 224-id oracle fixture runs through the one-launch step in tests/test_gpu_model.py (it is the
+model's default)."""
 
 import pytest
 import torch
@@ -20,9 +22,19 @@ def model(hip_device):
     return m
 
 
+def _start(model, pos, cur, kv0):
+    model.self_kv.copy_(kv0)
+    model.state.copy_(torch.tensor([pos, 0], device='cuda'))
+    model.cur.fill_(cur)
+    model.tokens.zero_()
+    model.best.zero_()
+
+
 def _run(model, persistent, pos, cur, kv0, steps):
-    """`steps` steps from position pos with cache kv0; per step the tensors both step forms produce."""
+    """`steps` steps from position pos with cache kv0, the persistent form without its LM head; per step
+    the tensors both step forms produce."""
     model.persistent_step = persistent
+    model.persistent_head = False
     model.self_kv.copy_(kv0)
     model.state.copy_(torch.tensor([pos, 0], device='cuda'))
     model.cur.fill_(cur)
@@ -34,6 +46,25 @@ def _run(model, persistent, pos, cur, kv0, steps):
         model._step()
         h, x = (model.h_fin, model.x_fin) if persistent else (model.h[b], model.pending)
         out.append([t.clone() for t in (model.self_kv, h, x, model.tokens, model.state, model.cur)])
+    torch.cuda.synchronize()
+    model.persistent_head = True
+    return out
+
+
+def _run_full(model, persistent, pos, cur, kv0, steps, y):
+    """`steps` whole steps (LM head included); per step the cache, the final LayerNorm output (written
+    by the one-launch step into y, recomputed for the launch chain with the LM-head kernels' final
+    LayerNorm), tokens, state and current token."""
+    model.persistent_step = persistent
+    _start(model, pos, cur, kv0)
+    b = (model.dims.dec_layers - 1) % 2
+    g, be, eps = model.final_ln
+    out = []
+    for _ in range(steps):
+        model._step()
+        if not persistent:
+            model.ext.final_layernorm(model.h[b], model.pending, g, be, y, eps)
+        out.append([t.clone() for t in (model.self_kv, y, model.tokens, model.state, model.cur)])
     torch.cuda.synchronize()
     return out
 
@@ -54,6 +85,33 @@ def test_persistent_step_matches_launch_chain(model, pos):
     for s, (a, b) in enumerate(zip(got, ref)):
         for name, ta, tb in zip(names, a, b):
             assert torch.equal(ta, tb), f'step {s} (position {pos + s}): {name} differs'
+
+
+@torch.inference_mode()
+@pytest.mark.parametrize('pos', [0, 60, 126, 250, 443])
+def test_one_launch_step_matches_launch_chain(model, pos):
+    """The whole step in one launch: the LM head's int8 pre-pass, fp16 rescoring, block maxima and
+    finalize inside the persistent kernel pick the chain's token at every step; from the last start
+    position the steps reach the cache's last row, where the finalize holds the position."""
+    g = torch.Generator(device='cuda').manual_seed(1000 + pos)
+    kv0 = (torch.randn(model.self_kv.shape, generator=g, device='cuda') * 0.7).half()
+    steps = 6
+    y = torch.zeros(model.dims.d_model, dtype=torch.float16, device='cuda')
+    names = ('self_kv', 'final LN', 'tokens', 'state', 'cur')
+    try:
+        model._make_step_head(y)
+        got = _run_full(model, True, pos, 1234, kv0, steps, y)
+        ref = _run_full(model, False, pos, 1234, kv0, steps, y)
+    finally:
+        model.persistent_step = True
+        model._make_step_head()
+    assert model.ext.decoder_step_error(model.step_ws) == 0
+    for s, (a, b) in enumerate(zip(got, ref)):
+        for name, ta, tb in zip(names, a, b):
+            assert torch.equal(ta, tb), f'step {s} (position {pos + s}): {name} differs'
+    assert int(got[-1][3][1]) == steps and int(got[-1][3][0]) == min(pos + steps, model.max_pos - 1)
+    toks = got[-1][2][:steps]
+    assert int(toks.min()) >= 0 and int(toks.max()) < model.dims.vocab
 
 
 @torch.inference_mode()
