@@ -11,11 +11,16 @@ replay inside the timed transcribes), the rate of the step's algorithmic bytes (
 the path, fp16 LM head included: the decoder weights, cross K/V, self K/V rows and the tied embedding),
 the 30 s-clip E2E ms and TTFT.
 
-``roofline`` covers the step's LM-head kernel (final LN + int8 pre-pass over the tied embedding +
-exact fp16 logits of the candidate rows + argmax), timed standalone: a hipGraph of launches over
-rotating copies of its table (more than the 256 MB MALL), between HIP events on the graph's stream.
-Its ``achieved`` counts the bytes it reads; ``achieved_s8d`` counts the bytes of the fp16 LM head it
-replaces (the argmax it returns is that of the fp16 table), so ``frac_s8d`` can exceed 1.
+``roofline`` covers the dominant kernel, the one-launch decoder step (``decoder_step_kernel``: the 4
+decoder layers, final LN, int8 pre-pass LM head, argmax and finalize in one persistent launch, one
+launch per token): ``achieved`` is the step's algorithmic bytes (fp16 LM head, as the unit is
+defined) over its average launch duration, HIP events around every 8-launch graph replay on the
+stream the graph runs on; ``achieved_read`` counts the bytes the step must read with the int8 table
+instead. ``traffic`` is the kernel's calibrated PMC fetch + write bytes per launch from
+profiles/decoder_step_kernel_traffic.md. ``lm_head`` times the LM-head kernel alone (final LN +
+int8 pre-pass + exact fp16 candidates + argmax, h ~ N(0, 1)) over rotating copies of its table (more
+than the 256 MB MALL) in a hipGraph between HIP events on the graph's stream; with
+``--fp16-lm-head`` the step is not one launch and ``roofline`` is that LM-head kernel's.
 
 ``configs`` times the path's per-config units standalone, each over rotating buffers of more than
 300 MB so every call streams from HBM: the log-mel front end, split-K self attention at L in
@@ -41,6 +46,9 @@ MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 LM_KERNEL = {False: 'lm_head_kernel<true> (final LN + LM head GEMV + argmax)',
              True: 'lm_head_q8_kernel<true> (final LN + int8 pre-pass over the LM head + exact fp16 candidates + argmax)'}
 LM_TRAFFIC = {False: 'profiles/lm_head_kernel_traffic.md', True: 'profiles/lm_head_q8_kernel_traffic.md'}
+STEP_KERNEL = ('decoder_step_kernel (one persistent launch per token: 4 decoder layers, final LN, int8 pre-pass '
+               'LM head with exact fp16 candidates, argmax, finalize)')
+STEP_TRAFFIC = 'profiles/decoder_step_kernel_traffic.md'
 ROTATE_BYTES = 300 << 20  # more than the 256 MB MALL
 LOG_MEL_BYTES = 3_558_912          # 480000 fp32 in, 128 x 3000 fp32 out, the 201 x 128 filterbank
 CROSS_MLP_BYTES = 33_925_120       # cross K/V 7.68 MB + fc1, fc2 26.2 MB + vectors
@@ -71,7 +79,7 @@ def encoder_flops(dims):
 
 
 def measured_traffic(path):
-    """HBM bytes per LM-head launch from the committed, copy-calibrated rocprofv3 PMC summary
+    """HBM bytes per launch of a kernel from its committed, copy-calibrated rocprofv3 PMC summary
     (FETCH_SIZE and WRITE_SIZE passes), or None when that summary is absent."""
     import pathlib
     import re
@@ -149,7 +157,9 @@ def time_lm_head(model, reps, q8):
         tables = [model.lm_head] + [model.lm_head.clone() for _ in range(copies - 1)]
     best = torch.zeros(1, dtype=torch.long, device='cuda')
     g, b, eps = model.final_ln
-    h, x = model.h[0], model.pending
+    gen = torch.Generator(device='cuda').manual_seed(4)
+    h = torch.randn(d.d_model, generator=gen, device='cuda').half()  # the LM-head unit's input, N(0, 1)
+    x = torch.zeros_like(h)
 
     def launch(i):
         if q8:
@@ -467,16 +477,27 @@ def main():
         'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
         'encoder_tflops': round(enc_tflops, 1), 'encoder_mfma_frac': round(enc_tflops / MFMA_FP16_PEAK_TFLOPS, 4),
         'n_tokens': rows[-1]['n_tokens'],
-        'roofline': {'kernel': LM_KERNEL[q8], 'bound': 'hbm', 'achieved': round(lm_gbps, 1),
-                     'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(lm_gbps / HBM_PEAK_GBPS, 4),
-                     'traffic': measured_traffic(LM_TRAFFIC[q8]), 'traffic_source': LM_TRAFFIC[q8],
-                     'us_per_launch': round(lm_us, 2), 'bytes_per_launch': lm_bytes,
-                     'bytes_s8d': lm_bytes_s8d, 'achieved_s8d': round(lm_gbps_s8d, 1),
-                     'frac_s8d': round(lm_gbps_s8d / HBM_PEAK_GBPS, 4),
-                     'fp16_head': {'kernel': LM_KERNEL[False], 'us_per_launch': round(lm16_us, 2),
-                                   'achieved': round(lm16_gbps, 1), 'frac': round(lm16_gbps / HBM_PEAK_GBPS, 4),
-                                   'traffic': measured_traffic(LM_TRAFFIC[False])}},
     }
+    lm_head = {'kernel': LM_KERNEL[q8], 'bound': 'hbm', 'achieved': round(lm_gbps, 1),
+               'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(lm_gbps / HBM_PEAK_GBPS, 4),
+               'traffic': measured_traffic(LM_TRAFFIC[q8]), 'traffic_source': LM_TRAFFIC[q8],
+               'us_per_launch': round(lm_us, 2), 'bytes_per_launch': lm_bytes,
+               'bytes_s8d': lm_bytes_s8d, 'achieved_s8d': round(lm_gbps_s8d, 1),
+               'frac_s8d': round(lm_gbps_s8d / HBM_PEAK_GBPS, 4),
+               'fp16_head': {'kernel': LM_KERNEL[False], 'us_per_launch': round(lm16_us, 2),
+                             'achieved': round(lm16_gbps, 1), 'frac': round(lm16_gbps / HBM_PEAK_GBPS, 4),
+                             'traffic': measured_traffic(LM_TRAFFIC[False])}}
+    if model.persistent_step and model.persistent_head and q8:
+        read_gbps = read_bytes / (med_step * 1e-6) / 1e9
+        out['roofline'] = {'kernel': STEP_KERNEL, 'bound': 'hbm', 'achieved': round(step_gbps, 1),
+                           'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(step_gbps / HBM_PEAK_GBPS, 4),
+                           'traffic': measured_traffic(STEP_TRAFFIC), 'traffic_source': STEP_TRAFFIC,
+                           'us_per_launch': round(med_step, 2), 'bytes_per_launch': round(step_bytes),
+                           'bytes_read': round(read_bytes), 'achieved_read': round(read_gbps, 1),
+                           'frac_read': round(read_gbps / HBM_PEAK_GBPS, 4)}
+        out['lm_head'] = lm_head
+    else:
+        out['roofline'] = lm_head
     if configs is not None:
         out['configs'] = configs
     if serve is not None:

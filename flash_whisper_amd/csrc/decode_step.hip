@@ -840,7 +840,7 @@ struct Sched {
   __device__ void next(int used) { start = (start + used) % G; }
 };
 
-__global__ void __launch_bounds__(kStepThreads) decoder_layers_kernel(StepArgs a) {
+__global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs a) {
   __shared__ __align__(16) _Float16 h_res[kHidden];
   __shared__ __align__(16) _Float16 x_lds[kStepFfn];
   __shared__ float red[8 * kStepWaves];  // LayerNorm sums (16 slots each for the LM head's 1024-thread order)
@@ -1184,7 +1184,7 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
   a.x_out = static_cast<_Float16*>(x_out);
   a.ws = static_cast<unsigned char*>(workspace);
   a.spin_limit = spin_limit;
-  hipLaunchKernelGGL(decoder_layers_kernel, dim3(grid), dim3(kStepThreads), 0, stream, a);
+  hipLaunchKernelGGL(decoder_step_kernel, dim3(grid), dim3(kStepThreads), 0, stream, a);
   return fw_check_launch(name);
 }
 
