@@ -62,7 +62,7 @@ SIGNATURES = {
     'fw_decoder_step_layers': (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, P, P, c_int64, c_int64,
                                        P]),
     'fw_final_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
-    'fw_decoder_step': (c_int, [P, c_int, P, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64, P]),
+    'fw_decoder_step': (c_int, [P, c_int, P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64, P]),
 }
 
 DEC_LAYER_TENSORS = ('ln1_gamma', 'ln1_beta', 'qkv_w', 'qkv_b', 'out_w', 'out_b', 'ln2_gamma', 'ln2_beta',

@@ -220,14 +220,19 @@ __device__ __forceinline__ void ln_prologue(const _Float16* a, const _Float16* b
 }
 
 // Token and position embedding rows of vector v of a batch: token cur[v] at position state[0] + v.
-__device__ __forceinline__ void embed_rows(const int64_t* cur, const int64_t* state, const _Float16* embed,
-                                           const _Float16* pos_embed, int vocab, int max_pos, const _Float16** a,
-                                           const _Float16** b, int v = 0) {
-  int64_t tok = cur[v], pos = state[0] + v;
+// The token and position embedding rows of token tok at position pos (both clamped into range).
+__device__ __forceinline__ void embed_rows_of(int64_t tok, int64_t pos, const _Float16* embed, const _Float16* pos_embed,
+                                              int vocab, int max_pos, const _Float16** a, const _Float16** b) {
   tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);
   pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
   *a = embed + tok * kHidden;
   *b = pos_embed + pos * kHidden;
+}
+
+__device__ __forceinline__ void embed_rows(const int64_t* cur, const int64_t* state, const _Float16* embed,
+                                           const _Float16* pos_embed, int vocab, int max_pos, const _Float16** a,
+                                           const _Float16** b, int v = 0) {
+  embed_rows_of(cur[v], state[0] + v, embed, pos_embed, vocab, max_pos, a, b);
 }
 
 template <int K>
@@ -373,13 +378,20 @@ struct FinArgs {
 };
 
 // The finalize with the packed maximum b and the state words already read: n = state[1] (tokens so
-// far), p = state[0] (position).
-__device__ __forceinline__ void finalize_known(unsigned long long b, int64_t n, int64_t p, const FinArgs& f) {
-  const int64_t tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
-  if (n < f.max_pos) f.tokens[n] = tok;
-  f.state[1] = n < f.max_pos ? n + 1 : n;
-  f.state[0] = p + 1 < f.max_pos ? p + 1 : f.max_pos - 1;
-  *f.cur = tok;
+// far), p = state[0] (position). Returns the token and the new state words it wrote.
+struct FinOut {
+  int64_t tok, n, pos;
+};
+__device__ __forceinline__ FinOut finalize_known(unsigned long long b, int64_t n, int64_t p, const FinArgs& f) {
+  FinOut o;
+  o.tok = static_cast<int64_t>(0xFFFFFFFFu - static_cast<unsigned int>(b & 0xFFFFFFFFull));
+  if (n < f.max_pos) f.tokens[n] = o.tok;
+  o.n = n < f.max_pos ? n + 1 : n;
+  o.pos = p + 1 < f.max_pos ? p + 1 : f.max_pos - 1;
+  f.state[1] = o.n;
+  f.state[0] = o.pos;
+  *f.cur = o.tok;
+  return o;
 }
 
 __device__ __forceinline__ void finalize_token(unsigned long long* best, const FinArgs& f) {

@@ -35,6 +35,7 @@ constexpr int kStepHeads = 20;
 constexpr int kStepFfn = 4 * kHidden;
 constexpr int kSelfSplitKeys = 64, kCrossSplitKeys = 256;
 constexpr int kStepMaxLayers = 8;
+constexpr int kStepMaxSteps = 1024;  // tokens one launch may decode
 constexpr int kPartWords = kHeadDim + 2;  // acc[64], m, l of one split
 constexpr int kPartRegion = kStepHeads * kMaxCombineSplits * kPartWords;
 // Tagged-word regions of one layer (8-byte words; a vector of fp16 takes one word per pair)
@@ -91,7 +92,14 @@ struct StepArgs {
   unsigned char* ws;
   long long spin_limit;  // wall-clock ticks (100 MHz) a wait may take before it flags an error
   int has_head;          // run the final LN + LM head + argmax + finalize as the last phase
+  int n_steps;           // tokens decoded by the launch (1 without the LM head)
   StepHead head;
+};
+
+// The token a step embeds and the state word that gives its position: read from memory by the first
+// step of a launch, then from the words the previous step's finalizing block broadcast.
+struct StepPos {
+  int64_t tok, pos_raw;
 };
 
 struct Ll {
@@ -253,13 +261,14 @@ __device__ __forceinline__ const uint64_t* contribution(uint64_t* regions, int i
 // one wave), t the thread's index among them.
 template <int kThreads = kStepThreads>
 __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, int upto, uint64_t* regions,
-                                               const StepArgs& a, const Ll& c, int t = threadIdx.x) {
+                                               const StepArgs& a, const Ll& c, const StepPos& sp,
+                                               int t = threadIdx.x) {
   constexpr int kPer = (kVecWords + kThreads - 1) / kThreads;
   h2v* h2 = reinterpret_cast<h2v*>(h_res);
   for (; applied < upto; ++applied) {  // uniform over the threads
     if (applied == 0) {
       const _Float16 *ea, *eb;
-      embed_rows(a.cur, a.state, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
+      embed_rows_of(sp.tok, sp.pos_raw, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
       const h2v* a2 = reinterpret_cast<const h2v*>(ea);
       const h2v* b2 = reinterpret_cast<const h2v*>(eb);
       for (int i = t; i < kHidden / 2; i += kThreads) {
@@ -404,7 +413,9 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int ns, _F
     for (int p = 0; p < MAXP; ++p) {
       const int j = w0 + p * 8 + ks;
       kr[r][p] = vr[r][p] = make_uint4(0, 0, 0, 0);
-      if (split < ns && j < wend) {
+      // rows past the position are never read: a later step of the same launch writes them, and an
+      // earlier read could leave a stale copy in this CU's caches
+      if (split < ns && j < wend && j <= pos) {
         kr[r][p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
         vr[r][p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
       }
@@ -561,6 +572,7 @@ struct alignas(16) LmLds {  // yhi / ylo are read as 16-byte chunks
   int cand[kLmMaxBatches * kLmBatchRows];
   int ncand;
   unsigned long long best[kStepWaves * 2];
+  unsigned long long fin[kStepWaves];  // the finalizing block's wave maxima
 };
 
 // y = LN(h_res) with the reduction order of ln_finish<1024, true> (the LM-head kernel's 1024-thread
@@ -632,9 +644,14 @@ __device__ __forceinline__ void ln_final(const _Float16* h_res, const h2v* g2, c
   }
 }
 
+// The block that takes the maximum over the blocks and finalizes: the last one, which the first
+// phase of the next step does not use.
+__device__ __forceinline__ int fin_block() { return gridDim.x - 1; }
+
 __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead& H, const Ll& c, _Float16* h_res,
-                                              int& applied, uint64_t* regions, uint64_t* maxima, _Float16* y_lds,
-                                              float* red, LmLds& s, int64_t pos_raw, int64_t n_tok) {
+                                              int& applied, uint64_t* regions, uint64_t* maxima, uint64_t* bcast,
+                                              _Float16* y_lds, float* red, LmLds& s, const StepPos& sp,
+                                              int64_t n_tok) {
   constexpr int NT = 1024, kWaves = NT / kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x, b = blockIdx.x, vocab = a.vocab;
@@ -668,7 +685,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     for (int k = 0; k < kLmBufs; ++k)
       if (k < nb) load(k, bt[k]);
   } else {
-    resid_catch_up<kWave>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, lane);
+    resid_catch_up<kWave>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp, lane);
   }
   applied = 3 * a.n_layers + 1;
   __syncthreads();
@@ -802,10 +819,10 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     ll_store(maxima + 2 * b, c.tag, static_cast<unsigned>(m));
     ll_store(maxima + 2 * b + 1, c.tag, static_cast<unsigned>(m >> 32));
   }
-  if (b != 0) return;  // block-uniform
-  // block 0: the maximum over the blocks (thread i takes block i's two words), then the finalize of
-  // argmax_finalize_kernel with the state words read at the start of the launch (no other block writes
-  // them)
+  if (b != fin_block()) return;  // block-uniform
+  // the maximum over the blocks (thread i takes block i's two words), then the finalize of
+  // argmax_finalize_kernel with the step's state words (only this block writes them), broadcast to
+  // every block for the next step as three tagged words: token, position, tokens so far
   unsigned long long m = 0;
   for (int i = tid; i < G; i += kStepThreads) {
     const int idx[2] = {2 * i, 2 * i + 1};
@@ -820,13 +837,16 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     const unsigned long long x = (static_cast<unsigned long long>(hi) << 32) | lo;
     m = x > m ? x : m;
   }
-  if (lane == 0) s.best[wave] = m;
+  if (lane == 0) s.fin[wave] = m;
   __syncthreads();
   if (tid == 0) {
 #pragma unroll
-    for (int i = 0; i < kStepWaves; ++i) m = s.best[i] > m ? s.best[i] : m;
+    for (int i = 0; i < kStepWaves; ++i) m = s.fin[i] > m ? s.fin[i] : m;
     const FinArgs fin{H.tokens, a.state, a.cur, a.max_pos};
-    finalize_known(m, n_tok, pos_raw, fin);
+    const FinOut o = finalize_known(m, n_tok, sp.pos_raw, fin);
+    ll_store(bcast + 0, c.tag, static_cast<unsigned>(o.tok));
+    ll_store(bcast + 1, c.tag, static_cast<unsigned>(o.pos));
+    ll_store(bcast + 2, c.tag, static_cast<unsigned>(o.n));
   }
 }
 
@@ -840,7 +860,17 @@ struct Sched {
   __device__ void next(int used) { start = (start + used) % G; }
 };
 
-__global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs a) {
+// The kernel's arguments, re-read from the kernel-argument segment wherever this is called: the
+// pointer is opaque to the compiler, so it cannot hoist argument loads out of the step loop and keep
+// them in registers across a whole step (scalar loads of the segment are cheap; the registers are not).
+__device__ __forceinline__ const StepArgs& step_args() {
+  auto p = __builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *(const StepArgs*)p;  // the constant-segment pointer as a generic one (an address-space cast)
+}
+
+__global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs args) {
+  const StepArgs& a = args;
   __shared__ __align__(16) _Float16 h_res[kHidden];
   __shared__ __align__(16) _Float16 x_lds[kStepFfn];
   __shared__ float red[8 * kStepWaves];  // LayerNorm sums (16 slots each for the LM head's 1024-thread order)
@@ -850,243 +880,265 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs a) 
   __shared__ AttnLds att;
   __shared__ float part_lds[kMaxCombineSplits * kPartWords];
   __shared__ unsigned epoch_lds;
+  __shared__ unsigned bcast_lds[3];
   __shared__ unsigned stage[kMaxPasses * kStepWaves];  // a GEMV phase's output words before their coalesced store
   const int tid = threadIdx.x, wave = tid >> 6;
   const int G = gridDim.x;
   unsigned* ctl = reinterpret_cast<unsigned*>(a.ws);
   uint64_t* regions = reinterpret_cast<uint64_t*>(a.ws + kCtlBytes);
 
-  // The launch's tag: the epoch every block reads before it arrives; the last block to arrive moves
-  // the epoch on for the next launch, when no block of this one can still be reading it.
+  // The launch's tags: the epoch every block reads before it arrives; step st of the launch tags its
+  // words epoch + 1 + st. The last block to arrive moves the epoch on by the launch's steps, when no
+  // block of this one can still be reading it.
   if (tid == 0) epoch_lds = __hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   const unsigned epoch = epoch_lds;
   unsigned arrived = 0;
   if (tid == 0) arrived = atomicAdd(ctl + 1, 1u);
-  const Ll c{ctl, epoch + 1u, a.spin_limit};
+  uint64_t* maxima = regions + static_cast<size_t>(a.n_layers) * kLayerWords;
+  uint64_t* bcast = maxima + 2 * kMaxGrid;
 
-  const int64_t pos_raw = a.state[0];
-  const int64_t n_tok = a.has_head && blockIdx.x == 0 ? a.state[1] : 0;  // for block 0's finalize
   if (a.has_head)
     for (int i = tid; i < kHidden / 2; i += kStepThreads) {
       lm.gamma[i] = reinterpret_cast<const h2v*>(a.head.gamma)[i];
       lm.beta[i] = reinterpret_cast<const h2v*>(a.head.beta)[i];
     }
-  const int pos = static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_pos ? a.max_pos - 1 : pos_raw));
-  const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
+  StepPos sp{a.cur[0], a.state[0]};
+  int64_t n_tok = a.has_head && blockIdx.x == fin_block() ? a.state[1] : 0;  // for the finalize
   const int ns_cross = (a.enc_len + kCrossSplitKeys - 1) / kCrossSplitKeys;
 
   // worker counts: the phases with many rows use every block the previous phase did not
-  // Runs of blocks per phase, taken in turn around the grid: consecutive phases use disjoint blocks, the
-  // LN3 + fc1 phase also avoids the cross-attention blocks (which finish late), and the runs of one
-  // layer add up to three times the grid, so every layer repeats the pattern. At 256 CUs: LN1+q/k/v
+  // Runs of blocks per phase, taken in turn around the grid: consecutive phases use disjoint blocks and
+  // the LN3 + fc1 phase also avoids the cross-attention blocks (which finish late). At 256 CUs: LN1+q/k/v
   // 176 blocks, self attention 20 (of a run of 176), out 80, LN2+cross-q 80, cross attention 60,
-  // cross-out 80, LN3+fc1 116, fc2 80.
+  // cross-out 80, LN3+fc1 116, fc2 80. Every step starts the runs at block 0, so a layer's phase
+  // runs on the same blocks in every step: the self-attention block of a head reads back the cache
+  // rows it wrote itself (through its own CU's caches) in the steps before.
   const int w_vec = min(kVecWorkers, max(1, G * 5 / 16));
   const int w_cross = min(kCrossWorkers, max(1, G * 15 / 64));
   const int w_qkv = max(1, G - w_vec);
   const int w_fc1 = max(1, G - w_vec - w_cross);
-  Sched sc{0, G};
-  int applied = 0;  // residual contributions added to h_res
 
-  for (int l = 0; l < a.n_layers; ++l) {
-    const StepLayer& L = a.layer[l];
-    uint64_t* R = regions + static_cast<size_t>(l) * kLayerWords;
-
-    // 1: residual + LN1 + q/k/v (1920 pairs)
-    {
+  for (int st = 0; st < args.n_steps; ++st) {
+    const StepArgs& a = step_args();
+    const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit};
+    if (st > 0) {  // the previous step's token, position and token count
       __syncthreads();
-      const int rank = sc.rank(), W = w_qkv;
-      constexpr int U = 2;
-      const int npairs = kQkvWords;
-      if (rank < W) {
-        Gv<kHidden, U> g;
-        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
-        const int qs = W * kStepWaves;
-        gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
-        LnRegs<kStepThreads> lnr;
-        ln_params(lnr, L.ln1_g, L.ln1_b);
-        resid_catch_up(h_res, applied, 1 + 3 * l, regions, a, c);
-        resid_layernorm(lnr, h_res, L.eps1, x_lds, red);
+      if (tid < 3) {
+        const int idx[1] = {tid};
+        unsigned v[1];
+        const Ll prev{ctl, c.tag - 1u, a.spin_limit};
+        ll_wait<1>(bcast, idx, v, prev);
+        bcast_lds[tid] = v[0];
+      }
+      __syncthreads();
+      sp.tok = __builtin_amdgcn_readfirstlane(bcast_lds[0]);  // uniform: scalar registers
+      sp.pos_raw = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[1]));
+      n_tok = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[2]));
+    }
+    const int pos = static_cast<int>(sp.pos_raw < 0 ? 0 : (sp.pos_raw >= a.max_pos ? a.max_pos - 1 : sp.pos_raw));
+    const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
+    Sched sc{0, G};
+    int applied = 0;  // residual contributions added to h_res
+
+    for (int l = 0; l < a.n_layers; ++l) {
+      const StepLayer& L = a.layer[l];
+      uint64_t* R = regions + static_cast<size_t>(l) * kLayerWords;
+
+      // 1: residual + LN1 + q/k/v (1920 pairs)
+      {
         __syncthreads();
-        for (;;) {
-          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffQkv, c.tag, nullptr, base, qs, npairs);
-          base += U * qs;
-          if (base >= npairs) break;
-          __syncthreads();
+        const int rank = sc.rank(), W = w_qkv;
+        constexpr int U = 2;
+        const int npairs = kQkvWords;
+        if (rank < W) {
+          Gv<kHidden, U> g;
+          int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+          const int qs = W * kStepWaves;
           gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
-        }
-      }
-      sc.next(W);
-    }
-    // 2: self attention, one block per head (its splits combined in the block)
-    {
-      __syncthreads();
-      const int rank = sc.rank(), W = kStepHeads;
-      if (rank < W)
-        self_attn_head(c, rank, ns_self, L.self_k, L.self_v, a.max_pos, pos, R + kOffQkv, R + kOffSelfVec, a.scale,
-                       att, part_lds, wgt, den);
-      sc.next(w_qkv);
-    }
-    // 3: out projection (640 pairs)
-    {
-      __syncthreads();
-      const int rank = sc.rank(), W = w_vec;
-      constexpr int U = 1;
-      const int npairs = kVecWords;
-      if (rank < W) {
-        Gv<kHidden, U> g;
-        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
-        const int qs = W * kStepWaves;
-        gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
-        fetch_attn_vector(R + kOffSelfVec, x_lds, c);
-        __syncthreads();
-        for (;;) {
-          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffAttnOut, c.tag, nullptr, base, qs, npairs);
-          base += U * qs;
-          if (base >= npairs) break;
+          LnRegs<kStepThreads> lnr;
+          ln_params(lnr, L.ln1_g, L.ln1_b);
+          resid_catch_up(h_res, applied, 1 + 3 * l, regions, a, c, sp);
+          resid_layernorm(lnr, h_res, L.eps1, x_lds, red);
           __syncthreads();
+          for (;;) {
+            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffQkv, c.tag, nullptr, base, qs, npairs);
+            base += U * qs;
+            if (base >= npairs) break;
+            __syncthreads();
+            gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
+          }
+        }
+        sc.next(W);
+      }
+      // 2: self attention, one block per head (its splits combined in the block)
+      {
+        __syncthreads();
+        const int rank = sc.rank(), W = kStepHeads;
+        if (rank < W)
+          self_attn_head(c, rank, ns_self, L.self_k, L.self_v, a.max_pos, pos, R + kOffQkv, R + kOffSelfVec, a.scale,
+                         att, part_lds, wgt, den);
+        sc.next(w_qkv);
+      }
+      // 3: out projection (640 pairs)
+      {
+        __syncthreads();
+        const int rank = sc.rank(), W = w_vec;
+        constexpr int U = 1;
+        const int npairs = kVecWords;
+        if (rank < W) {
+          Gv<kHidden, U> g;
+          int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+          const int qs = W * kStepWaves;
           gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
-        }
-      }
-      sc.next(W);
-    }
-    // 4: residual + LN2 + cross q (640 pairs)
-    {
-      __syncthreads();
-      const int rank = sc.rank(), W = w_vec;
-      constexpr int U = 1;
-      const int npairs = kVecWords;
-      if (rank < W) {
-        Gv<kHidden, U> g;
-        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
-        const int qs = W * kStepWaves;
-        gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
-        LnRegs<kStepThreads> lnr;
-        ln_params(lnr, L.ln2_g, L.ln2_b);
-        resid_catch_up(h_res, applied, 2 + 3 * l, regions, a, c);
-        resid_layernorm(lnr, h_res, L.eps2, x_lds, red);
-        __syncthreads();
-        for (;;) {
-          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossQ, c.tag, nullptr, base, qs, npairs);
-          base += U * qs;
-          if (base >= npairs) break;
+          fetch_attn_vector(R + kOffSelfVec, x_lds, c);
           __syncthreads();
+          for (;;) {
+            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffAttnOut, c.tag, nullptr, base, qs, npairs);
+            base += U * qs;
+            if (base >= npairs) break;
+            __syncthreads();
+            gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
+          }
+        }
+        sc.next(W);
+      }
+      // 4: residual + LN2 + cross q (640 pairs)
+      {
+        __syncthreads();
+        const int rank = sc.rank(), W = w_vec;
+        constexpr int U = 1;
+        const int npairs = kVecWords;
+        if (rank < W) {
+          Gv<kHidden, U> g;
+          int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+          const int qs = W * kStepWaves;
           gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
-        }
-      }
-      sc.next(W);
-    }
-    // 5: cross-attention splits, each head combined by the block that ran its last split
-    {
-      __syncthreads();
-      const int nitems = kStepHeads * ns_cross;
-      const int W = min(w_cross, (nitems + 1) / 2);
-      const int rank = sc.rank();
-      if (rank < W)
-        cross_attn_items(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
-                         R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den);
-      sc.next(w_cross);
-    }
-    // 6: cross-out projection (640 pairs)
-    {
-      __syncthreads();
-      const int rank = sc.rank(), W = w_vec;
-      constexpr int U = 1;
-      const int npairs = kVecWords;
-      if (rank < W) {
-        Gv<kHidden, U> g;
-        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
-        const int qs = W * kStepWaves;
-        gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
-        fetch_attn_vector(R + kOffCrossVec, x_lds, c);
-        __syncthreads();
-        for (;;) {
-          gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossOut, c.tag, nullptr, base, qs, npairs);
-          base += U * qs;
-          if (base >= npairs) break;
+          LnRegs<kStepThreads> lnr;
+          ln_params(lnr, L.ln2_g, L.ln2_b);
+          resid_catch_up(h_res, applied, 2 + 3 * l, regions, a, c, sp);
+          resid_layernorm(lnr, h_res, L.eps2, x_lds, red);
           __syncthreads();
+          for (;;) {
+            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossQ, c.tag, nullptr, base, qs, npairs);
+            base += U * qs;
+            if (base >= npairs) break;
+            __syncthreads();
+            gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
+          }
+        }
+        sc.next(W);
+      }
+      // 5: cross-attention splits, each head combined by the block that ran its last split
+      {
+        __syncthreads();
+        const int nitems = kStepHeads * ns_cross;
+        const int W = min(w_cross, (nitems + 1) / 2);
+        const int rank = sc.rank();
+        if (rank < W)
+          cross_attn_items(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
+                           R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den);
+        sc.next(w_cross);
+      }
+      // 6: cross-out projection (640 pairs)
+      {
+        __syncthreads();
+        const int rank = sc.rank(), W = w_vec;
+        constexpr int U = 1;
+        const int npairs = kVecWords;
+        if (rank < W) {
+          Gv<kHidden, U> g;
+          int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+          const int qs = W * kStepWaves;
           gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
-        }
-      }
-      sc.next(W);
-    }
-    // 7: residual + LN3 + fc1 + GELU (2560 pairs)
-    {
-      __syncthreads();
-      const int rank = sc.rank(), W = w_fc1;
-      constexpr int U = 3;
-      const int npairs = kFfnWords;
-      if (rank < W) {
-        Gv<kHidden, U> g;
-        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
-        const int qs = W * kStepWaves;
-        gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
-        LnRegs<kStepThreads> lnr;
-        ln_params(lnr, L.ln3_g, L.ln3_b);
-        resid_catch_up(h_res, applied, 3 + 3 * l, regions, a, c);
-        resid_layernorm(lnr, h_res, L.eps3, x_lds, red);
-        __syncthreads();
-        for (;;) {
-          gv_finish<kHidden, U, FW_ACT_GELU>(g, x_lds, stage, R + kOffFfn, c.tag, nullptr, base, qs, npairs);
-          base += U * qs;
-          if (base >= npairs) break;
+          fetch_attn_vector(R + kOffCrossVec, x_lds, c);
           __syncthreads();
+          for (;;) {
+            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossOut, c.tag, nullptr, base, qs, npairs);
+            base += U * qs;
+            if (base >= npairs) break;
+            __syncthreads();
+            gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
+          }
+        }
+        sc.next(W);
+      }
+      // 7: residual + LN3 + fc1 + GELU (2560 pairs)
+      {
+        __syncthreads();
+        const int rank = sc.rank(), W = w_fc1;
+        constexpr int U = 3;
+        const int npairs = kFfnWords;
+        if (rank < W) {
+          Gv<kHidden, U> g;
+          int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+          const int qs = W * kStepWaves;
           gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
-        }
-      }
-      sc.next(W);
-    }
-    // 8: fc2 (640 pairs of 5120-wide rows)
-    {
-      __syncthreads();
-      const int rank = sc.rank(), W = w_vec;
-      constexpr int U = 1;
-      const int npairs = kVecWords;
-      const bool last = l + 1 == a.n_layers;
-      if (rank < W) {
-        Gv<kStepFfn, U> g;
-        int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
-        const int qs = W * kStepWaves;
-        gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
-        // the fc1 output, 2560 words, into LDS
-        constexpr int kPer = kFfnWords / kStepThreads;
-        static_assert(kFfnWords % kStepThreads == 0, "whole words per thread");
-        int idx[kPer];
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads;
-        unsigned v[kPer];
-        ll_wait<kPer>(R + kOffFfn, idx, v, c);
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
-        __syncthreads();
-        for (;;) {
-          gv_finish<kStepFfn, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffMlpOut, c.tag, last ? a.x_out : nullptr, base, qs, npairs);
-          base += U * qs;
-          if (base >= npairs) break;
+          LnRegs<kStepThreads> lnr;
+          ln_params(lnr, L.ln3_g, L.ln3_b);
+          resid_catch_up(h_res, applied, 3 + 3 * l, regions, a, c, sp);
+          resid_layernorm(lnr, h_res, L.eps3, x_lds, red);
           __syncthreads();
-          gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
+          for (;;) {
+            gv_finish<kHidden, U, FW_ACT_GELU>(g, x_lds, stage, R + kOffFfn, c.tag, nullptr, base, qs, npairs);
+            base += U * qs;
+            if (base >= npairs) break;
+            __syncthreads();
+            gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
+          }
         }
+        sc.next(W);
       }
-      sc.next(W);
+      // 8: fc2 (640 pairs of 5120-wide rows)
+      {
+        __syncthreads();
+        const int rank = sc.rank(), W = w_vec;
+        constexpr int U = 1;
+        const int npairs = kVecWords;
+        const bool last = l + 1 == a.n_layers;
+        if (rank < W) {
+          Gv<kStepFfn, U> g;
+          int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
+          const int qs = W * kStepWaves;
+          gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
+          // the fc1 output, 2560 words, into LDS
+          constexpr int kPer = kFfnWords / kStepThreads;
+          static_assert(kFfnWords % kStepThreads == 0, "whole words per thread");
+          int idx[kPer];
+  #pragma unroll
+          for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads;
+          unsigned v[kPer];
+          ll_wait<kPer>(R + kOffFfn, idx, v, c);
+  #pragma unroll
+          for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
+          __syncthreads();
+          for (;;) {
+            gv_finish<kStepFfn, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffMlpOut, c.tag, last ? a.x_out : nullptr, base, qs, npairs);
+            base += U * qs;
+            if (base >= npairs) break;
+            __syncthreads();
+            gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
+          }
+        }
+        sc.next(W);
+      }
     }
-  }
 
-  if (a.has_head) {
-    __syncthreads();
-    lm_head_phase(a, a.head, c, h_res, applied, regions, regions + static_cast<size_t>(a.n_layers) * kLayerWords,
-                  x_lds, red, lm, pos_raw, n_tok);
-  } else if (blockIdx.x == 0) {
-    // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
-    __syncthreads();
-    resid_catch_up(h_res, applied, 3 * a.n_layers, regions, a, c);  // the last fc2 output stays out
-    __syncthreads();
-    for (int i = tid; i < kHidden / 2; i += kStepThreads)
-      reinterpret_cast<unsigned*>(a.h_out)[i] = reinterpret_cast<const unsigned*>(h_res)[i];
+    if (a.has_head) {
+      __syncthreads();
+      lm_head_phase(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok);
+    } else if (blockIdx.x == 0) {
+      // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
+      __syncthreads();
+      resid_catch_up(h_res, applied, 3 * a.n_layers, regions, a, c, sp);  // the last fc2 output stays out
+      __syncthreads();
+      for (int i = tid; i < kHidden / 2; i += kStepThreads)
+        reinterpret_cast<unsigned*>(a.h_out)[i] = reinterpret_cast<const unsigned*>(h_res)[i];
+    }
   }
   if (tid == 0 && arrived == static_cast<unsigned>(G) - 1u) {
     __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(ctl, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctl, epoch + static_cast<unsigned>(a.n_steps), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1097,20 +1149,23 @@ using namespace fw;
 
 extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
-  // control words, each layer's hand-off regions, then the LM head's per-block maxima
-  return kCtlBytes + (static_cast<size_t>(n_layers) * kLayerWords + 2 * kMaxGrid) * sizeof(uint64_t);
+  // control words, each layer's hand-off regions, the LM head's per-block maxima, then the words the
+  // finalizing block broadcasts to the next step (three, in eight)
+  return kCtlBytes + (static_cast<size_t>(n_layers) * kLayerWords + 2 * kMaxGrid + 8) * sizeof(uint64_t);
 }
 
 extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }
 
 static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int n_layers, const fw_dec_head* head,
-                               int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                               int n_steps, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
                                int max_pos, int enc_len, float scale, void* h_out, void* x_out, void* workspace,
                                int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
   if (!layers || !cur || !state || !embed || !pos_embed || !workspace || (!head && (!h_out || !x_out)))
     return fw_fail(FW_EINVAL, "%s: null pointer", name);
   if (n_layers < 1 || n_layers > kStepMaxLayers)
     return fw_fail(FW_EINVAL, "%s: n_layers must be in [1, %d]", name, kStepMaxLayers);
+  if (n_steps < 1 || n_steps > kStepMaxSteps || (!head && n_steps != 1))
+    return fw_fail(FW_EINVAL, "%s: n_steps must be in [1, %d] (1 without the LM head)", name, kStepMaxSteps);
   if (vocab < 1 || max_pos < 1 || max_pos > kMaxCombineSplits * kSelfSplitKeys)
     return fw_fail(FW_EINVAL, "%s: max_pos must be in [1, %d]", name, kMaxCombineSplits * kSelfSplitKeys);
   if (enc_len < 1 || enc_len > kMaxCombineSplits * kCrossSplitKeys)
@@ -1172,6 +1227,7 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
                       static_cast<_Float16*>(hd.y_out)};
   }
   a.n_layers = n_layers;
+  a.n_steps = n_steps;
   a.cur = cur;
   a.state = state;
   a.embed = static_cast<const _Float16*>(embed);
@@ -1192,16 +1248,16 @@ extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, 
                                       const int64_t* state, const void* embed, const void* pos_embed, int vocab,
                                       int max_pos, int enc_len, float scale, void* h_out, void* x_out,
                                       void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
-  return decoder_step_launch("decoder_step_layers", layers, n_layers, nullptr, const_cast<int64_t*>(cur),
+  return decoder_step_launch("decoder_step_layers", layers, n_layers, nullptr, 1, const_cast<int64_t*>(cur),
                              const_cast<int64_t*>(state), embed, pos_embed, vocab, max_pos, enc_len, scale, h_out,
                              x_out, workspace, ws_bytes, spin_limit, stream);
 }
 
-extern "C" int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, int64_t* cur,
-                               int64_t* state, const void* embed, const void* pos_embed, int vocab, int max_pos,
-                               int enc_len, float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit,
-                               hipStream_t stream) {
+extern "C" int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, int n_steps,
+                               int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                               int max_pos, int enc_len, float scale, void* workspace, int64_t ws_bytes,
+                               int64_t spin_limit, hipStream_t stream) {
   if (!head) return fw_fail(FW_EINVAL, "decoder_step: null LM head");
-  return decoder_step_launch("decoder_step", layers, n_layers, head, cur, state, embed, pos_embed, vocab, max_pos,
-                             enc_len, scale, nullptr, nullptr, workspace, ws_bytes, spin_limit, stream);
+  return decoder_step_launch("decoder_step", layers, n_layers, head, n_steps, cur, state, embed, pos_embed, vocab,
+                             max_pos, enc_len, scale, nullptr, nullptr, workspace, ws_bytes, spin_limit, stream);
 }

@@ -362,16 +362,17 @@ class WhisperExt:
                             suppress.data_ptr(), tokens.data_ptr(), _ptr(y_out))
 
     def decoder_step(self, table, head, cur, state, embed, pos_embed, max_pos, enc_len, scale, ws, vocab,
-                     spin_limit=2_000_000):
-        """A whole decoder step in one launch (fw_decoder_step): the layers of decoder_step_layers, then the
-        final LN, the int8-pre-pass LM head, the argmax and the finalize (tokens, state and cur advance)."""
+                     spin_limit=2_000_000, n_steps=1):
+        """n_steps whole decoder steps in one launch (fw_decoder_step): each runs the layers of
+        decoder_step_layers, then the final LN, the int8-pre-pass LM head, the argmax and the finalize
+        (tokens, state and cur advance after every step)."""
         check_half(embed, 'embed')
         check_half(pos_embed, 'pos_embed')
         for t, n in ((cur, 'cur'), (state, 'state')):
             _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
         _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')
-        self._call('fw_decoder_step', ctypes.addressof(table), len(table), ctypes.addressof(head), cur.data_ptr(),
-                   state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(), int(vocab), int(max_pos), int(enc_len),
+        self._call('fw_decoder_step', ctypes.addressof(table), len(table), ctypes.addressof(head), int(n_steps),
+                   cur.data_ptr(), state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(), int(vocab), int(max_pos), int(enc_len),
                    float(scale), ws.data_ptr(), ws.numel(), int(spin_limit), _stream())
 
     @staticmethod

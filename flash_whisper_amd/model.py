@@ -63,6 +63,7 @@ class CustomModel:
         # persistent_head=False keeps the LM head and finalize as launches of their own
         self.persistent_step = persistent_step
         self.persistent_head = persistent_head
+        self.multi_step = True  # one launch for all steps of a graph chunk (else one launch per step)
         self.chunk_events = []
 
         self._specs = W.spec_map(dims)
@@ -353,18 +354,35 @@ class CustomModel:
         self.step_head = self.ext.decoder_head(g, be, eps, self.lm_head, self.lm_q8, self.lm_meta, self.suppress,
                                                self.tokens, y_out)
 
+    def _one_launch(self):
+        """Whether whole steps run as one persistent launch (layers and the int8 LM head)."""
+        return self.persistent_step and self.persistent_head and self.use_lm_q8
+
+    def _steps(self, n):
+        """n decoder tokens (custom/model.py:107-123, n times): one persistent launch for all of them when
+        whole steps run in one launch, else n calls of _step."""
+        if self._one_launch():
+            per = n if self.multi_step else 1
+            for _ in range(n // per):
+                self.ext.decoder_step(self.step_table, self.step_head, self.cur, self.state, self.embed,
+                                      self.pos_embed, self.max_pos, self.enc_len, self.scale, self.step_ws,
+                                      self.dims.vocab, n_steps=per)
+            return
+        for _ in range(n):
+            self._step()
+
     def _step(self, lm_head=True):
-        """One decoder token, entirely on the device (custom/model.py:107-123): the decoder layers as one
-        persistent launch (``persistent_step``), or in 32 launches, per layer [LN1+QKV] [self-attn
-        split-K + KV write] [combine + out] [LN2+cross-q] [cross-attn split-K] [combine + cross-out]
-        [LN3+fc1+GELU] [fc2]; then [final LN + LM head + argmax] [finalize]. The two forms give
+        """One decoder token, entirely on the device (custom/model.py:107-123): the whole step as one
+        persistent launch (``persistent_step`` with ``persistent_head``), the decoder layers as one launch
+        and the LM head as its own (``persistent_head`` off), or in 34 launches, per layer [LN1+QKV]
+        [self-attn split-K + KV write] [combine + out] [LN2+cross-q] [cross-attn split-K] [combine +
+        cross-out] [LN3+fc1+GELU] [fc2]; then [final LN + LM head + argmax] [finalize]. The forms give
         bit-identical outputs. Without `lm_head` (prompt tokens whose prediction is discarded) the step
         ends after the layers and only advances the position."""
         ext, d, dm = self.ext, self.dims, self.dims.d_model
         if self.persistent_step and lm_head:
-            if self.persistent_head and self.use_lm_q8:
-                ext.decoder_step(self.step_table, self.step_head, self.cur, self.state, self.embed, self.pos_embed,
-                                 self.max_pos, self.enc_len, self.scale, self.step_ws, self.dims.vocab)
+            if self._one_launch():
+                self._steps(1)
                 return
             ext.decoder_step_layers(self.step_table, self.cur, self.state, self.embed, self.pos_embed, self.max_pos,
                                     self.enc_len, self.scale, self.h_fin, self.x_fin, self.step_ws)
@@ -483,12 +501,11 @@ class CustomModel:
         torch.cuda.current_stream().wait_stream(side)
         graphs = []
         prompt_fn = self._prefill if self.batch_prompt else (lambda: self._step(lm_head=False))
-        for steps, fn in ((1, self._step), (CHUNK, self._step), (1, prompt_fn)):
+        for fn in (self._step, lambda: self._steps(CHUNK), prompt_fn):
             self.state.zero_()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                for _ in range(steps):
-                    fn()
+                fn()
             graphs.append(graph)
         torch.cuda.synchronize()
         self.self_kv.zero_()
@@ -498,6 +515,8 @@ class CustomModel:
     def _replay(self, graph, steps, lm_head=True):
         if graph is not None:
             graph.replay()
+        elif lm_head:
+            self._steps(steps)
         else:
             for _ in range(steps):
                 self._step(lm_head)

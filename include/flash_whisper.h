@@ -219,15 +219,17 @@ typedef struct fw_dec_head {
   void* y_out;
 } fw_dec_head;
 
-/* One whole decoder step in ONE launch: fw_decoder_step_layers followed by the final LayerNorm, the LM
- * head with the int8 pre-pass, the argmax and the finalize (replaces custom/model.py:107-123, i.e. the
- * per-layer ops above plus lm_head_argmax and argmax_finalize, whisper_kernels.cu:278-298). The token
- * is that of fw_lm_head_argmax_q8 + fw_argmax_finalize, bit for bit: tokens[state[1]] <- token,
- * state advances, cur <- token. Same workspace, limits and residency rules as fw_decoder_step_layers;
- * vocab <= 224 * (the device's CU count). */
-int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, int64_t* cur, int64_t* state,
-                    const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len, float scale,
-                    void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream);
+/* n_steps whole decoder steps in ONE launch: each is fw_decoder_step_layers followed by the final
+ * LayerNorm, the LM head with the int8 pre-pass, the argmax and the finalize (replaces n_steps calls of
+ * custom/model.py:107-123, i.e. the per-layer ops above plus lm_head_argmax and argmax_finalize,
+ * whisper_kernels.cu:278-298, as the 8-step graph of custom/model.py:125-141 replays them). Every
+ * token is that of fw_lm_head_argmax_q8 + fw_argmax_finalize, bit for bit: tokens[state[1]] <- token,
+ * state advances, cur <- token, after every step; a step takes the previous step's token and state
+ * from words the finalizing block broadcasts. Same workspace, limits and residency rules as
+ * fw_decoder_step_layers; 1 <= n_steps <= 1024; vocab <= 224 * (the device's CU count). */
+int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, int n_steps, int64_t* cur,
+                    int64_t* state, const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len,
+                    float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream);
 
 /* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
  * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by

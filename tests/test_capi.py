@@ -80,7 +80,8 @@ def test_decoder_step_entry_points_validate(built_lib):
     assert lib.fw_decoder_step_max_layers() == 8
     one, two = lib.fw_decoder_step_workspace_bytes(1), lib.fw_decoder_step_workspace_bytes(2)
     layer = two - one
-    assert layer > 0 and one == 256 + layer + 2 * 1024 * 8  # two 8-byte words per block, up to 1024 blocks
+    # two 8-byte words per block (up to 1024 blocks), then eight for the finalizing block's broadcast
+    assert layer > 0 and one == 256 + layer + 2 * 1024 * 8 + 8 * 8
     assert lib.fw_decoder_step_workspace_bytes(4) == one + 3 * layer
     assert lib.fw_decoder_step_workspace_bytes(0) == 0 and lib.fw_decoder_step_workspace_bytes(9) == 0
     assert ctypes.sizeof(_lib.DecLayer) == 18 * 8 + 3 * 4 + 4 + 4 * 8  # C layout: pad before the caches
@@ -100,15 +101,19 @@ def test_decoder_step_entry_points_validate(built_lib):
     assert lib.fw_decoder_step_layers(None, 4, *args) == _lib.FW_EINVAL
     # the whole step: the LM head is required and checked like the layers
     step = [d, d, d, d, 51866, 448, 1500, 0.125, d, lib.fw_decoder_step_workspace_bytes(4), 1000, None]
-    assert lib.fw_decoder_step(table, 4, None, *step) == _lib.FW_EINVAL and b'null LM head' in lib.fw_last_error()
+    assert lib.fw_decoder_step(table, 4, None, 1, *step) == _lib.FW_EINVAL and b'null LM head' in lib.fw_last_error()
     assert ctypes.sizeof(_lib.DecHead) == 2 * 8 + 8 + 6 * 8  # the float is padded to the next pointer
     head = _lib.DecHead(256, 256, 1e-5, 256, 256, 256, None, 256, None)
-    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), *step) == _lib.FW_EINVAL
+    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), 8, *step) == _lib.FW_EINVAL
     assert b'null LM-head tensor' in lib.fw_last_error()  # no suppress mask
     head.suppress = 256
     head.wq = 264
-    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), *step) == _lib.FW_EINVAL
+    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), 8, *step) == _lib.FW_EINVAL
     assert b'16-byte aligned' in lib.fw_last_error()
+    head.wq = 256
+    for n in (0, 1025):
+        assert lib.fw_decoder_step(table, 4, ctypes.byref(head), n, *step) == _lib.FW_EINVAL
+        assert b'n_steps' in lib.fw_last_error()
 
 
 def test_status_becomes_runtime_error(built_lib):

@@ -115,6 +115,34 @@ def test_one_launch_step_matches_launch_chain(model, pos):
 
 
 @torch.inference_mode()
+@pytest.mark.parametrize('pos,steps', [(0, 8), (120, 8), (437, 12)])
+def test_multi_step_launch_matches_launch_chain(model, pos, steps):
+    """Several steps in one launch (each step takes the previous one's token and position from the
+    finalizing block's broadcast, and the self-attention blocks read back cache rows written earlier in
+    the same launch) against as many 34-launch steps: cache, final LayerNorm output of the last step,
+    tokens, state and current token bit-identical; from position 437 the steps run into the cache's
+    last row and stay there."""
+    g = torch.Generator(device='cuda').manual_seed(2000 + pos)
+    kv0 = (torch.randn(model.self_kv.shape, generator=g, device='cuda') * 0.7).half()
+    y = torch.zeros(model.dims.d_model, dtype=torch.float16, device='cuda')
+    try:
+        model._make_step_head(y)
+        ref = _run_full(model, False, pos, 4321, kv0, steps, y)[-1]
+        model.persistent_step = True
+        _start(model, pos, 4321, kv0)
+        model._steps(steps)
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (model.self_kv, y, model.tokens, model.state, model.cur)]
+    finally:
+        model.persistent_step = True
+        model._make_step_head()
+    assert model.ext.decoder_step_error(model.step_ws) == 0
+    for name, ta, tb in zip(('self_kv', 'final LN', 'tokens', 'state', 'cur'), got, ref):
+        assert torch.equal(ta, tb), f'{steps} steps from position {pos}: {name} differs'
+    assert int(got[3][1]) == steps
+
+
+@torch.inference_mode()
 def test_persistent_step_repeats_exactly(model):
     """Two runs of the same steps (the epoch moves on every launch) give the same bits."""
     g = torch.Generator(device='cuda').manual_seed(7)
