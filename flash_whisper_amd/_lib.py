@@ -61,6 +61,8 @@ SIGNATURES = {
     'fw_decoder_step_max_layers': (c_int, []),
     'fw_decoder_step_layers': (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, P, P, c_int64, c_int64,
                                        P]),
+    'fw_host_alloc_coherent': (c_void_p, [ctypes.c_size_t]),
+    'fw_host_free': (None, [P]),
     'fw_final_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
     'fw_decoder_step': (c_int, [P, c_int, P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64, P]),
 }
@@ -79,7 +81,8 @@ class DecLayer(ctypes.Structure):
 class DecHead(ctypes.Structure):
     """struct fw_dec_head: the LM head of fw_decoder_step."""
     _fields_ = [('ln_gamma', c_void_p), ('ln_beta', c_void_p), ('ln_eps', c_float), ('w', c_void_p), ('wq', c_void_p),
-                ('meta', c_void_p), ('suppress', c_void_p), ('tokens', c_void_p), ('y_out', c_void_p)]
+                ('meta', c_void_p), ('suppress', c_void_p), ('tokens', c_void_p), ('y_out', c_void_p),
+                ('host_tokens', c_void_p), ('n_eos', c_int), ('eos', c_int64 * 4)]
 
 
 _lib = None

@@ -36,6 +36,7 @@ constexpr int kStepFfn = 4 * kHidden;
 constexpr int kSelfSplitKeys = 64, kCrossSplitKeys = 256;
 constexpr int kStepMaxLayers = 8;
 constexpr int kStepMaxSteps = 1024;  // tokens one launch may decode
+constexpr int kStepMaxEos = 4;       // end-of-text ids a launch stops at
 constexpr int kPartWords = kHeadDim + 2;  // acc[64], m, l of one split
 constexpr int kPartRegion = kStepHeads * kMaxCombineSplits * kPartWords;
 // Tagged-word regions of one layer (8-byte words; a vector of fp16 takes one word per pair)
@@ -75,7 +76,10 @@ struct StepHead {
   const float2* meta;
   const uint8_t* suppress;
   int64_t* tokens;
-  _Float16* y_out;  // optional: the final LayerNorm output, written by block 0
+  _Float16* y_out;        // optional: the final LayerNorm output, written by block 0
+  int64_t* host_tokens;   // optional: host memory that receives every token as it is decoded
+  int n_eos;              // the launch ends after a step whose token is one of eos[0 .. n_eos)
+  int64_t eos[kStepMaxEos];
 };
 
 struct StepArgs {
@@ -844,9 +848,16 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     for (int i = 0; i < kStepWaves; ++i) m = s.fin[i] > m ? s.fin[i] : m;
     const FinArgs fin{H.tokens, a.state, a.cur, a.max_pos};
     const FinOut o = finalize_known(m, n_tok, sp.pos_raw, fin);
+    bool stop = false;
+    for (int i = 0; i < H.n_eos; ++i) stop = stop || o.tok == H.eos[i];
     ll_store(bcast + 0, c.tag, static_cast<unsigned>(o.tok));
     ll_store(bcast + 1, c.tag, static_cast<unsigned>(o.pos));
     ll_store(bcast + 2, c.tag, static_cast<unsigned>(o.n));
+    ll_store(bcast + 3, c.tag, stop ? 1u : 0u);
+    // the token to the host as well (the host polls for it; the token is the whole message, so no
+    // ordering with other stores is needed)
+    if (H.host_tokens && n_tok < a.max_pos)
+      __hip_atomic_store(H.host_tokens + n_tok, o.tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -880,7 +891,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   __shared__ AttnLds att;
   __shared__ float part_lds[kMaxCombineSplits * kPartWords];
   __shared__ unsigned epoch_lds;
-  __shared__ unsigned bcast_lds[3];
+  __shared__ unsigned bcast_lds[4];
   __shared__ unsigned stage[kMaxPasses * kStepWaves];  // a GEMV phase's output words before their coalesced store
   const int tid = threadIdx.x, wave = tid >> 6;
   const int G = gridDim.x;
@@ -922,9 +933,9 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   for (int st = 0; st < args.n_steps; ++st) {
     const StepArgs& a = step_args();
     const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit};
-    if (st > 0) {  // the previous step's token, position and token count
+    if (st > 0) {  // the previous step's token, position, token count and stop flag
       __syncthreads();
-      if (tid < 3) {
+      if (tid < 4) {
         const int idx[1] = {tid};
         unsigned v[1];
         const Ll prev{ctl, c.tag - 1u, a.spin_limit};
@@ -935,6 +946,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       sp.tok = __builtin_amdgcn_readfirstlane(bcast_lds[0]);  // uniform: scalar registers
       sp.pos_raw = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[1]));
       n_tok = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[2]));
+      if (__builtin_amdgcn_readfirstlane(bcast_lds[3])) break;  // an end-of-text token: every block stops
     }
     const int pos = static_cast<int>(sp.pos_raw < 0 ? 0 : (sp.pos_raw >= a.max_pos ? a.max_pos - 1 : sp.pos_raw));
     const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
@@ -1147,10 +1159,23 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
 
 using namespace fw;
 
+extern "C" void* fw_host_alloc_coherent(size_t bytes) {
+  void* p = nullptr;
+  if (bytes == 0 || hipHostMalloc(&p, bytes, hipHostMallocCoherent) != hipSuccess) {
+    fw_fail(FW_EHIP, "host_alloc_coherent: hipHostMalloc of %zu bytes failed", bytes);
+    return nullptr;
+  }
+  return p;
+}
+
+extern "C" void fw_host_free(void* p) {
+  if (p) (void)hipHostFree(p);
+}
+
 extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
   // control words, each layer's hand-off regions, the LM head's per-block maxima, then the words the
-  // finalizing block broadcasts to the next step (three, in eight)
+  // finalizing block broadcasts to the next step (four, in eight)
   return kCtlBytes + (static_cast<size_t>(n_layers) * kLayerWords + 2 * kMaxGrid + 8) * sizeof(uint64_t);
 }
 
@@ -1182,8 +1207,12 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
     if (!hd.ln_gamma || !hd.ln_beta || !hd.w || !hd.wq || !hd.meta || !hd.suppress || !hd.tokens)
       return fw_fail(FW_EINVAL, "%s: null LM-head tensor", name);
     if ((reinterpret_cast<uintptr_t>(hd.w) & 15u) || (reinterpret_cast<uintptr_t>(hd.wq) & 15u) ||
-        (reinterpret_cast<uintptr_t>(hd.meta) & 7u) || (reinterpret_cast<uintptr_t>(hd.y_out) & 3u))
-      return fw_fail(FW_EINVAL, "%s: w and wq must be 16-byte aligned, meta 8-byte and y_out 4-byte aligned", name);
+        (reinterpret_cast<uintptr_t>(hd.meta) & 7u) || (reinterpret_cast<uintptr_t>(hd.y_out) & 3u) ||
+        (reinterpret_cast<uintptr_t>(hd.host_tokens) & 7u))
+      return fw_fail(FW_EINVAL, "%s: w and wq must be 16-byte aligned, meta and host_tokens 8-byte and y_out 4-byte aligned",
+                     name);
+    if (hd.n_eos < 0 || hd.n_eos > kStepMaxEos)
+      return fw_fail(FW_EINVAL, "%s: n_eos must be in [0, %d]", name, kStepMaxEos);
   }
   StepArgs a{};
   for (int l = 0; l < n_layers; ++l) {
@@ -1224,7 +1253,8 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
     a.head = StepHead{static_cast<const _Float16*>(hd.ln_gamma), static_cast<const _Float16*>(hd.ln_beta), hd.ln_eps,
                       static_cast<const _Float16*>(hd.w), static_cast<const int8_t*>(hd.wq),
                       reinterpret_cast<const float2*>(hd.meta), hd.suppress, hd.tokens,
-                      static_cast<_Float16*>(hd.y_out)};
+                      static_cast<_Float16*>(hd.y_out), hd.host_tokens, hd.n_eos, {}};
+    for (int i = 0; i < hd.n_eos; ++i) a.head.eos[i] = hd.eos[i];
   }
   a.n_layers = n_layers;
   a.n_steps = n_steps;

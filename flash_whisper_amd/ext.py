@@ -59,6 +59,26 @@ def _check(t, name, dtype, what):
              f'{name} must be contiguous CUDA {what}')
 
 
+class HostTokens:
+    """n int64 of pinned host memory that device stores reach while a kernel runs (fw_host_alloc_coherent):
+    the one-launch decode stores each token here as it is decoded and the host polls `array`."""
+
+    def __init__(self, lib, n):
+        import numpy as np
+
+        self._lib = lib
+        self.address = lib.fw_host_alloc_coherent(8 * n)
+        if not self.address:
+            raise RuntimeError(f'host_alloc_coherent: {lib.fw_last_error().decode(errors="replace")}')
+        self.array = np.ctypeslib.as_array((ctypes.c_int64 * n).from_address(self.address))
+
+    def __del__(self):
+        if getattr(self, 'address', None):
+            self.array = None
+            self._lib.fw_host_free(self.address)
+            self.address = None
+
+
 class WhisperExt:
     """The op set of the reference extension plus the fused/encoder/front-end ops of this build."""
 
@@ -343,8 +363,13 @@ class WhisperExt:
         self._call('fw_final_layernorm', h.data_ptr(), _ptr(x), gamma.data_ptr(), beta.data_ptr(), y.data_ptr(),
                    HIDDEN, float(eps), _stream())
 
-    def decoder_head(self, gamma, beta, eps, w, wq, meta, suppress, tokens, y_out=None):
-        """The fw_dec_head of decoder_step (raw pointers: the tensors must outlive it)."""
+    def host_tokens(self, n):
+        """HostTokens: n int64 of device-coherent pinned host memory (fw_dec_head.host_tokens)."""
+        return HostTokens(self.lib, n)
+
+    def decoder_head(self, gamma, beta, eps, w, wq, meta, suppress, tokens, y_out=None, host_tokens=None, eos=()):
+        """The fw_dec_head of decoder_step (raw pointers: the tensors and host_tokens must outlive it).
+        eos: up to 4 end-of-text ids at which a launch stops (set_eos changes them later)."""
         for t, n in ((gamma, 'gamma'), (beta, 'beta'), (w, 'w')):
             check_half(t, n)
         _require(w.dim() == 2 and w.size(1) == HIDDEN, f'hidden size must be {HIDDEN}')
@@ -358,8 +383,20 @@ class WhisperExt:
         if y_out is not None:
             check_half(y_out, 'y_out')
             _require(y_out.numel() == HIDDEN, f'y_out must be [{HIDDEN}]')
-        return _lib.DecHead(gamma.data_ptr(), beta.data_ptr(), float(eps), w.data_ptr(), wq.data_ptr(), meta.data_ptr(),
-                            suppress.data_ptr(), tokens.data_ptr(), _ptr(y_out))
+        head = _lib.DecHead(gamma.data_ptr(), beta.data_ptr(), float(eps), w.data_ptr(), wq.data_ptr(), meta.data_ptr(),
+                            suppress.data_ptr(), tokens.data_ptr(), _ptr(y_out),
+                            host_tokens.address if host_tokens is not None else None)
+        self.set_eos(head, eos)
+        return head
+
+    @staticmethod
+    def set_eos(head, eos):
+        """The end-of-text ids a decoder_step launch stops at (at most 4)."""
+        eos = [int(e) for e in eos]
+        _require(len(eos) <= 4, 'at most 4 end-of-text ids')
+        head.n_eos = len(eos)
+        for i, e in enumerate(eos):
+            head.eos[i] = e
 
     def decoder_step(self, table, head, cur, state, embed, pos_embed, max_pos, enc_len, scale, ws, vocab,
                      spin_limit=2_000_000, n_steps=1):

@@ -64,6 +64,10 @@ class CustomModel:
         self.persistent_step = persistent_step
         self.persistent_head = persistent_head
         self.multi_step = True  # one launch for all steps of a graph chunk (else one launch per step)
+        # the whole decode after the prompt as one launch, its tokens polled from host memory as they come
+        # (else chunks of CHUNK steps replayed as graphs, their tokens copied after each chunk)
+        self.stream_decode = True
+        self.decode_events = []
         self.chunk_events = []
 
         self._specs = W.spec_map(dims)
@@ -125,6 +129,7 @@ class CustomModel:
         self.best = torch.zeros(1, dtype=torch.long, device='cuda')
         # the persistent step's workspace, layer table and outputs (residual, last fc2 output)
         self.step_ws = self.ext.decoder_step_workspace(d.dec_layers)
+        self.stream_host = self.ext.host_tokens(d.max_pos)  # tokens of the one-launch decode, as they come
         self.h_fin = torch.zeros(dm, dtype=half, device='cuda')
         self.x_fin = torch.zeros(dm, dtype=half, device='cuda')
         self.step_table = self.ext.decoder_layer_table([self._layer_tensors(i) for i in range(d.dec_layers)])
@@ -352,11 +357,44 @@ class CustomModel:
         """The LM head of the one-launch step; y_out (fp16 [d_model]) receives the final LayerNorm output."""
         g, be, eps = self.final_ln
         self.step_head = self.ext.decoder_head(g, be, eps, self.lm_head, self.lm_q8, self.lm_meta, self.suppress,
-                                               self.tokens, y_out)
+                                               self.tokens, y_out, self.stream_host)
 
     def _one_launch(self):
         """Whether whole steps run as one persistent launch (layers and the int8 LM head)."""
         return self.persistent_step and self.persistent_head and self.use_lm_q8
+
+    def _streams(self, stop_at_eos):
+        """Whether transcribe decodes in one launch with its tokens streamed to the host."""
+        return self._one_launch() and self.stream_decode and (not stop_at_eos or len(self.eos) <= 4)
+
+    def _decode_stream(self, token_ids, max_new, stop_at_eos):
+        """custom/model.py:208-215 as one launch: every token after the first, up to max_new in all or
+        the first end-of-text id (included), decoded by one fw_decoder_step launch that stops at an
+        end-of-text id itself. Each token is stored into coherent host memory as it is decoded; the host
+        polls for it, so nothing waits for a chunk boundary. The ids are those of the chunked loop."""
+        n = max_new - len(token_ids)
+        if n <= 0 or (stop_at_eos and token_ids[-1] in self.eos):
+            return token_ids
+        host = self.stream_host.array
+        host[:] = -1  # nothing of this launch has arrived (the device is idle: transcribe synchronised)
+        self.ext.set_eos(self.step_head, sorted(self.eos) if stop_at_eos else ())
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        if self.record_events:
+            ev[0].record()
+        self._steps(n)
+        if self.record_events:
+            ev[1].record()
+            self.decode_events.append((ev[0], ev[1], n))
+        i, deadline = len(token_ids), time.perf_counter() + 60.0
+        while len(token_ids) < max_new and not (stop_at_eos and token_ids[-1] in self.eos):
+            v = int(host[i])
+            if v < 0:
+                if time.perf_counter() > deadline:
+                    raise RuntimeError('decoder step: no token from the device for 60 s')
+                continue
+            token_ids.append(v)
+            i += 1
+        return token_ids
 
     def _steps(self, n):
         """n decoder tokens (custom/model.py:107-123, n times): one persistent launch for all of them when
@@ -617,10 +655,12 @@ class CustomModel:
         stage[2].record()
 
         # The reference replays a chunk, then reads its tokens before replaying the next
-        # (custom/model.py:208-215). Here the next chunk is already queued while the host reads the
-        # previous one (an asynchronous copy of its token slice into pinned memory, then an event), so
-        # the GPU never waits for the host. The ids are the same: a chunk queued past an EOS only
-        # decodes tokens that are never read, and no chunk is queued past the token budget.
+        # (custom/model.py:208-215). With the one-launch step the whole decode is one launch that
+        # stops at EOS itself and stores each token into host memory as it goes (_decode_stream).
+        # Otherwise the next chunk is already queued while the host reads the previous one (an
+        # asynchronous copy of its token slice into pinned memory, then an event), so the GPU never
+        # waits for the host. The ids are the same: a chunk queued past an EOS only decodes tokens that
+        # are never read, and no chunk is queued past the token budget.
         self._enqueue_prompt()
         host = self.tokens_host
         self._publish(0, 1).synchronize()
@@ -628,8 +668,11 @@ class CustomModel:
         ttft = time.perf_counter() - start
         mel_s = enqueue_s + stage[0].elapsed_time(stage[1]) * 1e-3
         encoder_s = stage[1].elapsed_time(stage[2]) * 1e-3
-        self.chunk_events = []
-        n_chunks = -(-(max_new - 1) // CHUNK)
+        self.chunk_events, self.decode_events = [], []
+        stream = self._streams(stop_at_eos)
+        n_chunks = 0 if stream else -(-(max_new - 1) // CHUNK)
+        if stream:
+            token_ids = self._decode_stream(token_ids, max_new, stop_at_eos)
         done = stop_at_eos and token_ids[0] in self.eos
         queued = [] if done else [self._queue_chunk(i) for i in range(min(2, n_chunks))]
         for i in range(n_chunks):

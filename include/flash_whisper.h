@@ -207,8 +207,12 @@ int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, const int64
 
 /* The LM head of fw_decoder_step: final LayerNorm (gamma, beta, eps), the tied fp16 table w [vocab, 1280]
  * with its int8 copy wq [vocab, 1280] and meta fp32 [vocab, 2] (fw_lm_head_q8_pack), the suppress mask
- * u8 [vocab], the token list the finalize appends to (int64 [max_pos]), and optionally y_out fp16[1280]
- * (NULL: not written) for the final LayerNorm output the LM head scores. */
+ * u8 [vocab], the token list the finalize appends to (int64 [max_pos]), optionally y_out fp16[1280]
+ * (NULL: not written) for the final LayerNorm output the LM head scores, optionally host_tokens (NULL:
+ * not written): host memory, int64 [max_pos], coherent with the device (hipHostMallocCoherent), into
+ * which every token is also stored at its index as soon as it is decoded, so a host can poll for it
+ * while the launch runs; and the end-of-text ids: the launch ends after the first step whose token is
+ * one of eos[0 .. n_eos), n_eos <= 4. */
 typedef struct fw_dec_head {
   const void *ln_gamma, *ln_beta;
   float ln_eps;
@@ -217,7 +221,16 @@ typedef struct fw_dec_head {
   const uint8_t* suppress;
   int64_t* tokens;
   void* y_out;
+  int64_t* host_tokens;
+  int n_eos;
+  int64_t eos[4];
 } fw_dec_head;
+
+/* Host memory for fw_dec_head.host_tokens: `bytes` of pinned host memory that device stores reach
+ * while a kernel runs (hipHostMalloc with hipHostMallocCoherent); NULL on failure. No counterpart in the
+ * reference (it copies each chunk's tokens after the chunk, custom/model.py:208-215). */
+void* fw_host_alloc_coherent(size_t bytes);
+void fw_host_free(void* p);
 
 /* n_steps whole decoder steps in ONE launch: each is fw_decoder_step_layers followed by the final
  * LayerNorm, the LM head with the int8 pre-pass, the argmax and the finalize (replaces n_steps calls of

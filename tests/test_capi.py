@@ -102,7 +102,8 @@ def test_decoder_step_entry_points_validate(built_lib):
     # the whole step: the LM head is required and checked like the layers
     step = [d, d, d, d, 51866, 448, 1500, 0.125, d, lib.fw_decoder_step_workspace_bytes(4), 1000, None]
     assert lib.fw_decoder_step(table, 4, None, 1, *step) == _lib.FW_EINVAL and b'null LM head' in lib.fw_last_error()
-    assert ctypes.sizeof(_lib.DecHead) == 2 * 8 + 8 + 6 * 8  # the float is padded to the next pointer
+    # the float and the int are padded to the next 8-byte field; four int64 end-of-text ids
+    assert ctypes.sizeof(_lib.DecHead) == 2 * 8 + 8 + 7 * 8 + 8 + 4 * 8
     head = _lib.DecHead(256, 256, 1e-5, 256, 256, 256, None, 256, None)
     assert lib.fw_decoder_step(table, 4, ctypes.byref(head), 8, *step) == _lib.FW_EINVAL
     assert b'null LM-head tensor' in lib.fw_last_error()  # no suppress mask
@@ -111,6 +112,10 @@ def test_decoder_step_entry_points_validate(built_lib):
     assert lib.fw_decoder_step(table, 4, ctypes.byref(head), 8, *step) == _lib.FW_EINVAL
     assert b'16-byte aligned' in lib.fw_last_error()
     head.wq = 256
+    head.n_eos = 5
+    assert lib.fw_decoder_step(table, 4, ctypes.byref(head), 8, *step) == _lib.FW_EINVAL
+    assert b'n_eos' in lib.fw_last_error()
+    head.n_eos = 1
     for n in (0, 1025):
         assert lib.fw_decoder_step(table, 4, ctypes.byref(head), n, *step) == _lib.FW_EINVAL
         assert b'n_steps' in lib.fw_last_error()

@@ -178,3 +178,29 @@ def test_flagged_error_ends_waits_and_is_reported(model):
         for ta, tb in zip(x, y):
             assert torch.equal(ta, tb)
 
+
+
+@torch.inference_mode()
+def test_streamed_decode_matches_chunked_decode(model):
+    """transcribe's whole decode as one launch, its tokens polled from host memory as they are stored,
+    gives the ids of the chunked decode (8-step launches, tokens copied after each chunk): 224 fixed
+    tokens, and with an end-of-text id the launch stops itself at its first occurrence."""
+    from flash_whisper_amd.audio import synthetic_clip
+
+    clip = synthetic_clip(0)
+    saved = model.eos
+    try:
+        model.stream_decode = False
+        ref = model.transcribe(clip, max_new_tokens=224, stop_at_eos=False)['token_ids']
+        model.stream_decode = True
+        got = model.transcribe(clip, max_new_tokens=224, stop_at_eos=False)['token_ids']
+        assert got == ref
+        model.eos = {ref[30], ref[50]}  # the launch stops at the first of them
+        first = min(ref.index(ref[30]), ref.index(ref[50]))
+        got = model.transcribe(clip)['token_ids']
+        assert got == ref[:first + 1]
+        assert int(model.state[1]) == first + 1  # the device stopped there too
+    finally:
+        model.eos = saved
+        model.stream_decode = True
+    assert model.ext.decoder_step_error(model.step_ws) == 0
