@@ -78,16 +78,16 @@ def encoder_flops(dims):
     return stem + dims.enc_layers * layer + 2 * t * (dims.dec_layers * 2 * d) * d
 
 
-def measured_traffic(path):
-    """HBM bytes per launch of a kernel from its committed, copy-calibrated rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE passes), or None when that summary is absent."""
+def measured_traffic(path, per='launch'):
+    """HBM bytes per launch (or per step) of a kernel from its committed, copy-calibrated rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE passes), or None when that summary is absent."""
     import pathlib
     import re
 
     f = pathlib.Path(__file__).resolve().parent / path
     if not f.exists():
         return None
-    m = re.search(r'^traffic_bytes_per_launch:\s*(\d+)', f.read_text(), re.M)
+    m = re.search(rf'^traffic_bytes_per_{per}:\s*(\d+)', f.read_text(), re.M)
     return int(m.group(1)) if m else None
 
 
@@ -498,7 +498,8 @@ def main():
         read_gbps = read_bytes / (med_step * 1e-6) / 1e9
         out['roofline'] = {'kernel': STEP_KERNEL, 'bound': 'hbm', 'achieved': round(step_gbps, 1),
                            'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(step_gbps / HBM_PEAK_GBPS, 4),
-                           'traffic': measured_traffic(STEP_TRAFFIC), 'traffic_source': STEP_TRAFFIC,
+                           'traffic': measured_traffic(STEP_TRAFFIC, 'step'), 'traffic_per': 'step',
+                           'traffic_source': STEP_TRAFFIC,
                            'us_per_step': round(med_step, 2), 'bytes_per_step': round(step_bytes),
                            'bytes_read': round(read_bytes), 'achieved_read': round(read_gbps, 1),
                            'frac_read': round(read_gbps / HBM_PEAK_GBPS, 4)}
