@@ -471,7 +471,7 @@ def main():
         'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'fp16',
         'data': 'synthetic: seeded 30 s clip (3 tones + noise), seeded random-init N(0, 0.02) fp16 weights',
         'config': {'workload': f'whisper-large-v3-turbo batch 1: 30 s clip -> log-mel -> 32-layer encoder -> '
-                               f'{args.tokens} greedy tokens (8-step decoder hipGraph)',
+                               f'{args.tokens} greedy tokens (prompt pass and decode each one persistent launch)',
                    'clip_s': 30, 'tokens': args.tokens, 'batch': 1},
         'decode_step_us': round(med_step, 2),
         # the step's algorithmic bytes (fp16 LM head) over its time; 214 MB of them (decoder weights,

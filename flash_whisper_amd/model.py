@@ -376,8 +376,7 @@ class CustomModel:
         n = max_new - len(token_ids)
         if n <= 0 or (stop_at_eos and token_ids[-1] in self.eos):
             return token_ids
-        host = self.stream_host.array
-        host[:] = -1  # nothing of this launch has arrived (the device is idle: transcribe synchronised)
+        self.stream_host.array[len(token_ids):] = -1  # nothing of this launch has arrived yet
         self.ext.set_eos(self.step_head, sorted(self.eos) if stop_at_eos else ())
         ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
         if self.record_events:
@@ -386,16 +385,23 @@ class CustomModel:
         if self.record_events:
             ev[1].record()
             self.decode_events.append((ev[0], ev[1], n))
-        i, deadline = len(token_ids), time.perf_counter() + 60.0
         while len(token_ids) < max_new and not (stop_at_eos and token_ids[-1] in self.eos):
-            v = int(host[i])
-            if v < 0:
-                if time.perf_counter() > deadline:
-                    raise RuntimeError('decoder step: no token from the device for 60 s')
-                continue
-            token_ids.append(v)
-            i += 1
+            token_ids.append(self._poll_host_token(len(token_ids)))
         return token_ids
+
+    def _prompt_to_host(self):
+        """Whether the prompt pass ends in a one-launch step, which stores the first token into host memory."""
+        return self._one_launch() and (not self.batch_prompt or (self.persistent_prompt and len(self.prompt) == 4))
+
+    def _poll_host_token(self, i, timeout_s=60.0):
+        """Token i of the one-launch decode, polled from coherent host memory (-1 until it is stored)."""
+        host, deadline = self.stream_host.array, time.perf_counter() + timeout_s
+        while True:
+            v = int(host[i])
+            if v >= 0:
+                return v
+            if time.perf_counter() > deadline:
+                raise RuntimeError(f'decoder step: token {i} did not arrive from the device in {timeout_s:.0f} s')
 
     def _steps(self, n):
         """n decoder tokens (custom/model.py:107-123, n times): one persistent launch for all of them when
@@ -667,15 +673,19 @@ class CustomModel:
         # asynchronous copy of its token slice into pinned memory, then an event), so the GPU never
         # waits for the host. The ids are the same: a chunk queued past an EOS only decodes tokens that
         # are never read, and no chunk is queued past the token budget.
-        self._enqueue_prompt()
-        host = self.tokens_host
-        self._publish(0, 1).synchronize()
-        token_ids = [int(host[0])]
+        stream = self._streams(stop_at_eos)
+        if stream and self._prompt_to_host():  # the prompt pass stores the first token into host memory
+            self.stream_host.array[:] = -1
+            self._enqueue_prompt()
+            token_ids = [self._poll_host_token(0)]
+        else:
+            self._enqueue_prompt()
+            self._publish(0, 1).synchronize()
+            token_ids = [int(self.tokens_host[0])]
         ttft = time.perf_counter() - start
         mel_s = enqueue_s + stage[0].elapsed_time(stage[1]) * 1e-3
         encoder_s = stage[1].elapsed_time(stage[2]) * 1e-3
         self.chunk_events, self.decode_events = [], []
-        stream = self._streams(stop_at_eos)
         n_chunks = 0 if stream else -(-(max_new - 1) // CHUNK)
         if stream:
             token_ids = self._decode_stream(token_ids, max_new, stop_at_eos)
@@ -688,7 +698,7 @@ class CustomModel:
             if i + 2 < n_chunks:
                 queued.append(self._queue_chunk(i + 2))
             n0 = 1 + i * CHUNK
-            for token in host[n0:n0 + CHUNK].tolist():
+            for token in self.tokens_host[n0:n0 + CHUNK].tolist():
                 token_ids.append(token)
                 if (stop_at_eos and token in self.eos) or len(token_ids) >= max_new:
                     break
