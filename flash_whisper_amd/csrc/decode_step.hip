@@ -24,6 +24,7 @@
 // Every wait is bounded: past a time limit a block flags an error in the control words and carries
 // on with what it has, so the launch always drains. All blocks must be resident at once: one block
 // per CU, and nothing else running on the device while the step runs.
+#include <algorithm>
 #include <type_traits>
 
 #include "decode_dev.h"
@@ -902,20 +903,32 @@ __device__ __forceinline__ void ln_final(const _Float16* h_res, const h2v* g2, c
 // phase of the next step does not use.
 __device__ __forceinline__ int fin_block() { return gridDim.x - 1; }
 
+// LM-head rows of blocks 0 .. b - 1: the table split in proportion to block weights, kLmWeight for
+// most blocks and kLmLateWeight for the n_late blocks from late0 on (taken round the grid).
+constexpr int kLmWeight = 7, kLmLateWeight = 6;
+__host__ __device__ inline int lm_rows_before(int b, int vocab, int G, int late0, int n_late) {
+  const int wrap = late0 + n_late - G;  // late blocks past the end of the grid, counted from block 0
+  const int late = (wrap > 0 ? min(b, wrap) : 0) + max(0, min(b, min(G, late0 + n_late)) - late0);
+  const int64_t weight = static_cast<int64_t>(kLmWeight) * b - (kLmWeight - kLmLateWeight) * late;
+  const int64_t total = static_cast<int64_t>(kLmWeight) * G - (kLmWeight - kLmLateWeight) * n_late;
+  return static_cast<int>(static_cast<int64_t>(vocab) * weight / total);
+}
+
 // With NV vectors (the prompt pass) the LM head scores the last one, at position pos_raw + NV - 1.
 template <int NV = 1>
 __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead& H, const Ll& c, _Float16* h_res,
                                               int& applied, uint64_t* regions, uint64_t* maxima, uint64_t* bcast,
                                               _Float16* y_lds, float* red, LmLds& s, const StepPos& sp,
-                                              int64_t n_tok) {
+                                              int64_t n_tok, int late0, int n_late) {
   constexpr int NT = 1024, kWaves = NT / kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x, b = blockIdx.x, vocab = a.vocab;
   const int sub = lane & (kQ8Lpr - 1), rsel = lane / kQ8Lpr;
   const int wv = __builtin_amdgcn_readfirstlane(wave);  // branches on it are wave-uniform
-  // the block's rows: an even, contiguous share [r0, r1) of the table, in batches of kLmBatchRows
-  const int r0 = static_cast<int>(static_cast<int64_t>(b) * vocab / G);
-  const int r1 = static_cast<int>(static_cast<int64_t>(b + 1) * vocab / G);
+  // the block's rows: a contiguous share [r0, r1) of the table, in batches of kLmBatchRows; the blocks
+  // that ran the last fc2 start last and take kLmLateWeight / kLmWeight of the others' share
+  const int r0 = lm_rows_before(b, vocab, G, late0, n_late);
+  const int r1 = lm_rows_before(b + 1, vocab, G, late0, n_late);
   const int nb = (r1 - r0 + kLmBatchRows - 1) / kLmBatchRows;  // <= kLmMaxBatches
   auto base_of = [&](int k) { return r0 + k * kLmBatchRows; };
   const uint4* wq4 = reinterpret_cast<const uint4*>(H.wq);
@@ -1411,7 +1424,9 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
 
     if (a.has_head) {
       __syncthreads();
-      lm_head_phase<NV>(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok);
+      // the last fc2's run: the w_vec blocks before the schedule's current start
+      lm_head_phase<NV>(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok,
+                        (sc.start - w_vec + G) % G, w_vec);
     } else if (NV == 1 && blockIdx.x == 0) {
       // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
       __syncthreads();
@@ -1521,9 +1536,14 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
   const int grid = cus < kMaxGrid ? cus : kMaxGrid;
   if (head) {
     const fw_dec_head& hd = *head;
-    if ((vocab + grid - 1) / grid > kLmMaxBatches * kLmBatchRows)
-      return fw_fail(FW_EINVAL, "%s: vocab %d exceeds %d rows for each of %d blocks", name, vocab,
-                     kLmMaxBatches * kLmBatchRows, grid);
+    // the largest share: a block of weight kLmWeight next to min(80, 5 G / 16) late blocks
+    const int n_late = grid * 5 / 16 < kVecWorkers ? (grid * 5 / 16 > 1 ? grid * 5 / 16 : 1) : kVecWorkers;
+    int most = 0;
+    for (int b = 0; b < grid; ++b)
+      most = std::max(most, lm_rows_before(b + 1, vocab, grid, 0, n_late) - lm_rows_before(b, vocab, grid, 0, n_late));
+    if (most + 1 > kLmMaxBatches * kLmBatchRows)  // + 1: the rounding of another placement of the late run
+      return fw_fail(FW_EINVAL, "%s: vocab %d gives a block %d rows of the LM head (at most %d) on %d blocks", name,
+                     vocab, most, kLmMaxBatches * kLmBatchRows, grid);
     a.has_head = 1;
     a.head = StepHead{static_cast<const _Float16*>(hd.ln_gamma), static_cast<const _Float16*>(hd.ln_beta), hd.ln_eps,
                       static_cast<const _Float16*>(hd.w), static_cast<const int8_t*>(hd.wq),
