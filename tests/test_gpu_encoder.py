@@ -72,7 +72,7 @@ def _f16_order(v):
 
 
 def test_gelu_epilogue_within_one_ulp(ext, hip_device):
-    """The GELU epilogue (erfc by a Chebyshev fit) against an exact GELU, 0.5 x erfc(-x / sqrt 2) in
+    """The GELU epilogue (erfc by a fitted exponent polynomial) against an exact GELU, 0.5 x erfc(-x / sqrt 2) in
     float64, on 16384 fp16 inputs spanning both tails, passed through the GEMM unchanged (identity
     weights): every output within one fp16 ulp, and nearly all of them equal."""
     from scipy.special import erfc
