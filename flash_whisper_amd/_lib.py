@@ -45,6 +45,7 @@ SIGNATURES = {
     'fw_log_mel_ws_floats': (c_int64, [c_int]),
     'fw_log_mel_prepare': (c_int, [P, P, c_int64, P]),
     'fw_log_mel_run': (c_int, [P, c_int, P, P, P, P, c_int64, P]),
+    'fw_wave_upload': (c_int, [P, c_int64, P, P, c_int64, c_int64, P]),
     'fw_gemm': (c_int, [P, c_int, P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     'fw_conv1d': (c_int, [P, c_int, c_int, c_int, P, P, P, c_int, P, c_int, P]),
     'fw_layernorm_rows': (c_int, [P, P, P, P, c_int, c_int, c_float, P]),

@@ -12,6 +12,8 @@
 // real-input split; then the power, the compacted filterbank (the same terms in the same order as the
 // dense product, whose other terms are zero), log10 and one block maximum. Finalize reduces the block
 // maxima, clamps, rescales and writes the fp16 time-major copy the encoder's conv stem reads.
+#include <algorithm>
+#include <cstring>
 #include "fw_common.h"
 
 namespace fw {
@@ -302,6 +304,27 @@ extern "C" int fw_log_mel_run(const float* wave, int n_samples, const float* fil
   hipLaunchKernelGGL(fw::logmel_finalize_kernel, dim3(tiles), dim3(256), 0, stream, out,
                      static_cast<_Float16*>(out16), n_frames, maxima, blocks);
   return fw_check_launch("log_mel finalize");
+}
+
+// The waveform's trip to the device (custom/model.py:103-104 pads it with zeros on the device and
+// copies the samples from pageable memory): the samples are staged into pinned host memory one chunk
+// at a time and each chunk's host -> device copy is queued as soon as it is staged, so the DMA of
+// chunk i runs while the host stages chunk i + 1; the padding is cleared on the device.
+extern "C" int fw_wave_upload(const float* audio, int64_t n, float* staging, float* dev, int64_t n_total,
+                              int64_t chunk, hipStream_t stream) {
+  if (!audio || !staging || !dev) return fw_fail(FW_EINVAL, "wave_upload: null pointer");
+  if (n < 1 || n > n_total || chunk < 1) return fw_fail(FW_EINVAL, "wave_upload: need 0 < n <= n_total and chunk > 0");
+  for (int64_t i = 0; i < n; i += chunk) {
+    const int64_t m = std::min(chunk, n - i);
+    std::memcpy(staging + i, audio + i, static_cast<size_t>(m) * sizeof(float));
+    if (hipMemcpyAsync(dev + i, staging + i, static_cast<size_t>(m) * sizeof(float), hipMemcpyHostToDevice, stream) !=
+        hipSuccess)
+      return fw_fail(FW_EHIP, "wave_upload: hipMemcpyAsync failed");
+  }
+  if (n < n_total &&
+      hipMemsetAsync(dev + n, 0, static_cast<size_t>(n_total - n) * sizeof(float), stream) != hipSuccess)
+    return fw_fail(FW_EHIP, "wave_upload: hipMemsetAsync failed");
+  return FW_OK;
 }
 
 extern "C" int fw_log_mel(const float* wave, int n_samples, const float* filters, float* out, void* out16, float* ws,

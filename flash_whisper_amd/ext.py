@@ -16,6 +16,7 @@ import argparse
 import ctypes
 import sys
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -24,6 +25,7 @@ from .config import SPLIT_KEYS
 
 HIDDEN, HEAD_DIM = 1280, 64
 MAX_BATCH = 4  # decoder positions per batched launch (the prompt)
+WAVE_CHUNK = 240000  # samples per staged chunk of the waveform upload (half of 30 s: smaller chunks measured slower)
 
 
 def _stream():
@@ -516,6 +518,19 @@ class WhisperExt:
         self._log_mel_checks(wave, filters, out, out16, ws)
         self._call('fw_log_mel', wave.data_ptr(), wave.numel(), filters.data_ptr(), out.data_ptr(), _ptr(out16),
                    ws.data_ptr(), ws.numel(), _stream())
+
+    def wave_upload(self, audio, staging, wave, chunk=WAVE_CHUNK):
+        """audio (1-D float32 NumPy array) -> wave[:audio.size], zeros after it, through the pinned
+        ``staging`` tensor in chunks whose copies start as each is staged (custom/model.py:103-104)."""
+        _require(isinstance(audio, np.ndarray) and audio.dtype == np.float32 and audio.ndim == 1,
+                 'audio must be a one-dimensional float32 NumPy array')
+        _check(wave, 'wave', torch.float32, 'fp32')
+        _require(staging.dtype == torch.float32 and staging.is_pinned() and staging.is_contiguous(),
+                 'staging must be a contiguous pinned fp32 host tensor')
+        _require(0 < audio.size <= min(staging.numel(), wave.numel()), 'audio must fit staging and wave')
+        audio = np.ascontiguousarray(audio)
+        self._call('fw_wave_upload', audio.ctypes.data, audio.size, staging.data_ptr(), wave.data_ptr(), wave.numel(),
+                   int(chunk), _stream())
 
     def log_mel_prepare(self, filters, ws):
         """Writes the FFT twiddles and the compacted filterbank of ``filters`` to the start of ``ws``."""

@@ -589,10 +589,7 @@ class CustomModel:
     # scheduler can drive several lanes at once; transcribe() synchronises between them for its timings.
     def _enqueue_mel(self, audio):
         """Zero-padded waveform through the pinned staging buffer, then the HIP log-mel."""
-        host = self.wave_host.numpy()
-        host[:audio.size] = audio
-        host[audio.size:] = 0.0
-        self.wave.copy_(self.wave_host, non_blocking=True)
+        self.ext.wave_upload(audio, self.wave_host, self.wave)
         self._log_mel(self.wave)
 
     def _enqueue_encoder(self):

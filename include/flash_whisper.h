@@ -292,6 +292,12 @@ int fw_lm_head_argmax_q8(const void* h, const void* x, const void* gamma, const 
 int fw_log_mel(const float* wave, int n_samples, const float* filters, float* out, void* out16, float* ws,
                int64_t ws_floats, hipStream_t stream);
 int64_t fw_log_mel_ws_floats(int n_samples);
+/* audio fp32[n] in host memory (pageable) -> dev fp32[n_total], the samples followed by zeros
+ * (custom/model.py:103-104). The samples pass through staging, pinned host memory of at least n
+ * floats, in chunks of `chunk` samples, each chunk's copy queued on stream as soon as it is staged.
+ * Returns once every copy is queued; the caller must not write staging again before they complete. */
+int fw_wave_upload(const float* audio, int64_t n, float* staging, float* dev, int64_t n_total, int64_t chunk,
+                   hipStream_t stream);
 /* The per-filterbank part of fw_log_mel, once per workspace and filterbank: the FFT twiddle table and
  * the compacted filterbank are written to the start of ws (no reference counterpart: the reference's
  * filterbank is a constant tensor, custom/model.py:37-38). */

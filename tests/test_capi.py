@@ -57,6 +57,10 @@ def test_validation_errors_return_einval(built_lib):
     assert lib.fw_log_mel_prepare(dummy, dummy, 100, None) == _lib.FW_EINVAL  # workspace too small
     assert b'workspace needs' in lib.fw_last_error()
     assert lib.fw_log_mel_prepare(None, dummy, 1 << 20, None) == _lib.FW_EINVAL
+    assert lib.fw_wave_upload(None, 10, dummy, dummy, 10, 4, None) == _lib.FW_EINVAL
+    assert lib.fw_wave_upload(dummy, 11, dummy, dummy, 10, 4, None) == _lib.FW_EINVAL  # more samples than room
+    assert lib.fw_wave_upload(dummy, 0, dummy, dummy, 10, 4, None) == _lib.FW_EINVAL
+    assert lib.fw_wave_upload(dummy, 10, dummy, dummy, 10, 0, None) == _lib.FW_EINVAL
     assert lib.fw_log_mel_run(dummy, 480000, dummy, dummy, None, dummy, 100, None) == _lib.FW_EINVAL
     assert b'workspace needs' in lib.fw_last_error()
     rc = lib.fw_encoder_qkv(dummy, dummy, None, dummy, dummy, 1500, 3, None)  # 3 * 64 is not a multiple of 128

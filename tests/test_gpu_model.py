@@ -96,6 +96,18 @@ def test_log_mel_vs_oracle(model, clip):
         assert np.array_equal(np32(model.mel16), np32(model.mel32).T.astype(np.float16).astype(np.float32))
 
 
+@pytest.mark.parametrize('n, chunk', [(480000, 240000), (480000, 7777), (100001, 240000), (1, 3)])
+def test_wave_upload_stages_samples_then_zeros(model, n, chunk):
+    """fw_wave_upload: the samples (in whole and partial chunks) followed by device-cleared zeros,
+    over a wave buffer that held other values, equal the padded waveform bit for bit."""
+    audio = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    wave = torch.full((480000,), 7.0, device='cuda')
+    model.ext.wave_upload(audio, model.wave_host, wave, chunk)
+    ref = np.zeros(480000, np.float32)
+    ref[:n] = audio
+    assert np.array_equal(wave.cpu().numpy(), ref)
+
+
 def test_log_mel_prepared_run_matches_one_call(model, clip):
     """The model's per-clip path (log_mel_run on the workspace prepared at construction) gives exactly
     what the one-call op (prepare + run on a fresh workspace) gives."""
