@@ -481,6 +481,50 @@ __device__ __forceinline__ void head_combine(const float* part, int ns, int head
   __syncthreads();  // part, wgt and den are free again
 }
 
+// head_combine for NV vectors at once (the prompt pass): vector v's partials at part[v S kPartWords ..],
+// S = kMaxCombineSplits; 128 threads per vector run head_combine's arithmetic for it, so each vector's
+// output is what head_combine gives.
+template <int NV>
+__device__ __forceinline__ void head_combine_nv(const float* part, int ns, int head, float* wgt, float* den_lds,
+                                                uint64_t* out, unsigned tag) {
+  constexpr int S = kMaxCombineSplits;
+  static_assert(NV * 128 <= kStepThreads && NV <= kMaxCombineHeads, "one 128-thread group per vector");
+  const int tid = threadIdx.x, v = tid >> 7, t = tid & 127;
+  const float* vp = part + v * S * kPartWords;
+  if (v < NV && t == 0) {
+    float pm[S], pl[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      pm[s] = s < ns ? vp[s * kPartWords + kHeadDim] : -INFINITY;
+      pl[s] = s < ns ? vp[s * kPartWords + kHeadDim + 1] : 0.f;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < S; ++s) m = fmaxf(m, pm[s]);
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float w = pl[s] > 0.f ? __expf(pm[s] - m) : 0.f;
+      wgt[v * S + s] = w;
+      den = fmaf(pl[s], w, den);
+    }
+    den_lds[v] = den;
+  }
+  __syncthreads();
+  if (v < NV && t < kHeadDim) {  // one whole wave per vector: the lane ^ 1 swizzle pairs stay inside it
+    float num = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const float pa = s < ns ? vp[s * kPartWords + t] : 0.f;
+      if (wgt[v * S + s] != 0.f) num = fmaf(pa, wgt[v * S + s], num);
+    }
+    const unsigned lo = half_bits(f2h(num / den_lds[v]));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_ds_swizzle(static_cast<int>(lo), 0x041F));  // lane ^ 1
+    if ((t & 1) == 0) ll_store(out + v * kVecWords + head * 32 + t / 2, tag, lo | (hi << 16));
+  }
+  __syncthreads();  // part, wgt and den are free again
+}
+
 // The q (and fresh k, v) words of one head: threads t < 96 fetch word t % 32 of part t / 32 (q, k, v;
 // parts with want[p] false are skipped) into q_lds[p][...].
 __device__ __forceinline__ void fetch_head_vectors(const uint64_t* qsrc, int head, bool want_kv, uint4 (*q_lds)[8],
@@ -699,6 +743,8 @@ __device__ __forceinline__ void cross_attn_items_nv(const Ll& c, int rank, int w
                                                     float scale, AttnNvLds<NV>& s, float* part, float* wgt,
                                                     float* den) {
   constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
+  static_assert(sizeof(AttnNvLds<NV>) >= NV * kMaxCombineSplits * kPartWords * sizeof(float),
+                "the combine's partials fit the operand space");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
   const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
   for (int base = 2 * rank; base < nitems; base += 2 * workers) {  // block-uniform
@@ -752,22 +798,25 @@ __device__ __forceinline__ void cross_attn_items_nv(const Ll& c, int rank, int w
       const int it = base + hf;
       if (it >= nitems || it % nsplit != nsplit - 1) continue;  // block-uniform
       const int h = it / nsplit;
-      for (int v = 0; v < NV; ++v) {
-        const uint64_t* vpart = part_g + static_cast<size_t>(v) * kPartRegion;
-        int idx[2];
+      // every vector's partials of the head in one wait, into the operand space of s (free here)
+      constexpr int kPer = (NV * kMaxCombineSplits * kPartWords + kStepThreads - 1) / kStepThreads;
+      float* pall = reinterpret_cast<float*>(&s);
+      const int per_v = nsplit * kPartWords;
+      int idx[kPer], dst[kPer];
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          const int t = tid + k * kStepThreads;
-          idx[k] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + h) * kPartWords + t % kPartWords : -1;
-        }
-        unsigned pv[2];
-        ll_wait<2>(vpart, idx, pv, c);
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-          if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(pv[k]);
-        __syncthreads();
-        head_combine(part, nsplit, h, wgt, den, out + v * kVecWords, c.tag);
+      for (int k = 0; k < kPer; ++k) {
+        const int t = tid + k * kStepThreads, v = t / per_v, r = t - v * per_v;
+        const bool ok = v < NV;
+        idx[k] = ok ? v * kPartRegion + ((r / kPartWords) * kStepHeads + h) * kPartWords + r % kPartWords : -1;
+        dst[k] = ok ? v * kMaxCombineSplits * kPartWords + r : -1;
       }
+      unsigned pv[kPer];
+      ll_wait<kPer>(part_g, idx, pv, c);
+#pragma unroll
+      for (int k = 0; k < kPer; ++k)
+        if (dst[k] >= 0) pall[dst[k]] = __uint_as_float(pv[k]);
+      __syncthreads();
+      head_combine_nv<NV>(pall, nsplit, h, wgt, den, out, c.tag);
     }
   }
 }
