@@ -726,6 +726,70 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
   }
 }
 
+// split_wave_partial for NV queries on the same K/V registers, their steps interleaved so the
+// cross-lane reductions of the NV queries overlap. Each query's arithmetic is split_wave_partial's:
+// a query whose keys are all masked gets p = 0 for every key (split_wave_partial skips them), so its
+// sums are the same zeros.
+template <int MAXP, int NV>
+__device__ __forceinline__ void split_wave_partial_nv(const uint4 (&kr)[MAXP], const uint4 (&vr)[MAXP],
+                                                      const uint4* const (&q)[NV], int w0, int w1, float scale,
+                                                      float* const (&wm)[NV], float* const (&wl)[NV],
+                                                      float* const (&wacc_row)[NV]) {
+  const int lane = threadIdx.x & 63, ks = lane >> 3, c = lane & 7;
+  float sc[NV][MAXP], mx[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const uint4 qc = *q[v];
+    mx[v] = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      sc[v][p] = group_sum<8>(dot8(kr[p], qc, 0.f)) * scale;
+      if (w0 + p * 8 + ks >= w1) sc[v][p] = -INFINITY;
+      mx[v] = fmaxf(mx[v], sc[v][p]);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) mx[v] = group_max<64>(mx[v]);
+  float acc[NV][8], psum[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    psum[v] = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[v][t] = 0.f;
+  }
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const float pj = mx[v] != -INFINITY ? __expf(sc[v][p] - mx[v]) : 0.f;
+      psum[v] += pj;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[v][2 * t] = fmaf(pj, h2f(v2[t].x), acc[v][2 * t]);
+        acc[v][2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[v][2 * t + 1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    psum[v] = xor_add<32>(xor_add<16>(xor_add<8>(psum[v])));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[v][t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[v][t])));
+  }
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    if (lane == 0) {
+      *wm[v] = mx[v];
+      *wl[v] = psum[v];
+    }
+    if (ks == 0) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wacc_row[v][c * 8 + t] = acc[v][t];
+    }
+  }
+}
+
 // Cross attention for NV query vectors (the prompt pass): item i is (head i / nsplit, split i % nsplit)
 // as for one vector; its K/V rows are loaded once and every vector's query runs on them, each with
 // attn_split_kernel's arithmetic. Vector v's partials and output lie in regions of their own.
@@ -774,10 +838,18 @@ __device__ __forceinline__ void cross_attn_items_nv(const Ll& c, int rank, int w
     }
     __syncthreads();
     if (act && n > 0) {
+      const uint4* q[NV];
+      float* wm[NV];
+      float* wl[NV];
+      float* wa[NV];
 #pragma unroll
-      for (int v = 0; v < NV; ++v)
-        split_wave_partial<MAXP>(kr, vr, s.q[half][v][cc], w0, min(wend, begin + n), scale, &s.wm[v][half][hw],
-                                 &s.wl[v][half][hw], s.wacc[v][half][hw]);
+      for (int v = 0; v < NV; ++v) {
+        q[v] = &s.q[half][v][cc];
+        wm[v] = &s.wm[v][half][hw];
+        wl[v] = &s.wl[v][half][hw];
+        wa[v] = s.wacc[v][half][hw];
+      }
+      split_wave_partial_nv<MAXP, NV>(kr, vr, q, w0, min(wend, begin + n), scale, wm, wl, wa);
     }
     __syncthreads();
     if (act) {
