@@ -81,6 +81,7 @@ class CustomModel:
         self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
         self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
         self.graph_one = self.graph_chunk = self.graph_prompt = self.graph_enc = None
+        self.prompt_graph_one_launch = False
         if capture:
             self.graph_one, self.graph_chunk, self.graph_prompt = self._capture()
             self.graph_enc = self._capture_encoder()
@@ -355,10 +356,14 @@ class CustomModel:
         return t
 
     def _make_step_head(self, y_out=None):
-        """The LM head of the one-launch step; y_out (fp16 [d_model]) receives the final LayerNorm output."""
+        """The LM head of the one-launch step; y_out (fp16 [d_model]) receives the final LayerNorm output.
+        The one-launch prompt pass has a head of its own that reads the first step's suppress mask
+        (suppress plus begin-suppress ids) directly, so no mask is copied around it."""
         g, be, eps = self.final_ln
         self.step_head = self.ext.decoder_head(g, be, eps, self.lm_head, self.lm_q8, self.lm_meta, self.suppress,
                                                self.tokens, y_out, self.stream_host)
+        self.prompt_head = self.ext.decoder_head(g, be, eps, self.lm_head, self.lm_q8, self.lm_meta, self.first_mask,
+                                                 self.tokens, y_out, self.stream_host)
 
     def _one_launch(self):
         """Whether whole steps run as one persistent launch (layers and the int8 LM head)."""
@@ -389,9 +394,13 @@ class CustomModel:
             token_ids.append(self._poll_host_token(len(token_ids)))
         return token_ids
 
+    def _prompt_one_launch(self):
+        """Whether the batched prompt pass runs as one persistent launch (fw_decoder_prompt)."""
+        return self.batch_prompt and self._one_launch() and self.persistent_prompt and len(self.prompt) == 4
+
     def _prompt_to_host(self):
         """Whether the prompt pass ends in a one-launch step, which stores the first token into host memory."""
-        return self._one_launch() and (not self.batch_prompt or (self.persistent_prompt and len(self.prompt) == 4))
+        return self._one_launch() and (not self.batch_prompt or self._prompt_one_launch())
 
     def _poll_host_token(self, i, timeout_s=60.0):
         """Token i of the one-launch decode, polled from coherent host memory (-1 until it is stored)."""
@@ -468,8 +477,8 @@ class CustomModel:
         argmax on the last position. K/V cache rows, state and the first token are those of n
         sequential steps (each position's arithmetic is that of a single step)."""
         ext, d, dm, n = self.ext, self.dims, self.dims.d_model, len(self.prompt)
-        if self._one_launch() and self.persistent_prompt and n == 4:
-            ext.decoder_prompt(self.step_table, self.step_head, self.prompt_ids, self.cur, self.state, self.embed,
+        if self._prompt_one_launch():
+            ext.decoder_prompt(self.step_table, self.prompt_head, self.prompt_ids, self.cur, self.state, self.embed,
                                self.pos_embed, self.max_pos, self.enc_len, self.scale, self.step_ws, d.vocab)
             return
         ws = self.workspace
@@ -550,6 +559,7 @@ class CustomModel:
                 self._prefill()
         torch.cuda.current_stream().wait_stream(side)
         graphs = []
+        self.prompt_graph_one_launch = self._prompt_one_launch()  # the mask handling its replays need
         prompt_fn = self._prefill if self.batch_prompt else (lambda: self._step(lm_head=False))
         for fn in (self._step, lambda: self._steps(CHUNK), prompt_fn):
             self.state.zero_()
@@ -598,20 +608,26 @@ class CustomModel:
         else:
             self._encode()
 
-    def _enqueue_prompt(self, batched=None):
+    def _enqueue_prompt(self, batched=None, reset_state=True):
         """The prompt steps (custom/model.py:196-207): afterwards tokens[0] is the first generated token.
         The reference runs full steps and discards the predictions made inside the prompt; here the
         whole prompt runs as one batched pass (``_prefill``), or, for prompts that do not batch (or
         ``batched=False``), the tokens before the last run as steps without the LM head. Both leave the
-        same K/V cache rows, state and first token."""
-        self.state.zero_()
+        same K/V cache rows, state and first token. ``reset_state=False``: the caller has already zeroed
+        the state (transcribe does so before the log-mel, off the path to the first token)."""
+        if reset_state:
+            self.state.zero_()
         if self.batch_prompt and batched is not False:
-            self.suppress.copy_(self.first_mask)
-            if self.graph_prompt is not None:
-                self.graph_prompt.replay()
+            graph = self.graph_prompt
+            own_mask = self.prompt_graph_one_launch if graph is not None else self._prompt_one_launch()
+            if not own_mask:  # the batched launches' LM head reads the decode mask
+                self.suppress.copy_(self.first_mask)
+            if graph is not None:
+                graph.replay()
             else:
                 self._prefill()
-            self.suppress.copy_(self.base_mask)
+            if not own_mask:
+                self.suppress.copy_(self.base_mask)
             return
         last = len(self.prompt) - 1
         for i, token in enumerate(self.prompt):
@@ -658,6 +674,7 @@ class CustomModel:
         stage = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         stage[0].record()
         enqueue_s = time.perf_counter() - start
+        self.state.zero_()  # for the prompt pass; runs while the host stages the waveform
         self._enqueue_mel(audio)
         stage[1].record()
         self._enqueue_encoder()
@@ -673,10 +690,10 @@ class CustomModel:
         stream = self._streams(stop_at_eos)
         if stream and self._prompt_to_host():  # the prompt pass stores the first token into host memory
             self.stream_host.array[:] = -1
-            self._enqueue_prompt()
+            self._enqueue_prompt(reset_state=False)
             token_ids = [self._poll_host_token(0)]
         else:
-            self._enqueue_prompt()
+            self._enqueue_prompt(reset_state=False)
             self._publish(0, 1).synchronize()
             token_ids = [int(self.tokens_host[0])]
         ttft = time.perf_counter() - start

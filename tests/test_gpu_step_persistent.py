@@ -215,17 +215,31 @@ def test_prompt_pass_in_one_launch_matches_batched_launches(model, pos):
     the cache, from a filled cache and up to its last row."""
     g = torch.Generator(device='cuda').manual_seed(3000 + pos)
     kv0 = (torch.randn(model.self_kv.shape, generator=g, device='cuda') * 0.7).half()
-    out = []
+    first = model.first_mask.clone()
+
+    def run():
+        out = []
+        try:
+            for persistent in (False, True):
+                model.persistent_prompt = persistent
+                _start(model, pos, 4321, kv0)
+                if not persistent:  # the batched launches read the decode mask, set to the first step's
+                    model.suppress.copy_(model.first_mask)
+                model._prefill()
+                model.suppress.copy_(model.base_mask)
+                torch.cuda.synchronize()
+                out.append([t.clone() for t in (model.self_kv, model.tokens, model.state, model.cur)])
+        finally:
+            model.persistent_prompt = True
+        assert model.ext.decoder_step_error(model.step_ws) == 0
+        for name, ta, tb in zip(('self_kv', 'tokens', 'state', 'cur'), out[1], out[0]):
+            assert torch.equal(ta, tb), f'prompt at position {pos}: {name} differs'
+        assert out[1][2].tolist() == [min(pos + 4, model.max_pos - 1), 1]
+        return int(out[1][3])
+
     try:
-        for persistent in (False, True):
-            model.persistent_prompt = persistent
-            _start(model, pos, 4321, kv0)
-            model._prefill()
-            torch.cuda.synchronize()
-            out.append([t.clone() for t in (model.self_kv, model.tokens, model.state, model.cur)])
+        tok = run()
+        model.first_mask[tok] = True  # the one-launch pass reads the first step's mask itself
+        assert run() != tok
     finally:
-        model.persistent_prompt = True
-    assert model.ext.decoder_step_error(model.step_ws) == 0
-    for name, ta, tb in zip(('self_kv', 'tokens', 'state', 'cur'), out[1], out[0]):
-        assert torch.equal(ta, tb), f'prompt at position {pos}: {name} differs'
-    assert out[1][2].tolist() == [min(pos + 4, model.max_pos - 1), 1]
+        model.first_mask.copy_(first)
