@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. This package restates the reference algorithm on the CPU (numpy) so the
 HIP kernels can be checked against it. Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
-``cpu_baseline`` leg may import it, and only as the checker or as the timed CPU baseline. The product
+``cpu_baseline`` leg may import it, and only to compare against or as the timed CPU baseline. The product
 (``flash_whisper_amd``, ``custom``) never imports it and has no CPU fallback.
 
 Modules and what pins each function (checks live in tests/test_oracle_*.py):
