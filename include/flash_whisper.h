@@ -231,8 +231,10 @@ typedef struct fw_dec_head {
  * self attention of position state[0] + z seeing the fresh K/V rows of positions state[0] .. state[0] + z,
  * all 4 K/V rows written to the caches), then the LM head, argmax and finalize on the last position
  * (replaces custom/model.py:196-207: 4 steps whose first 3 predictions are discarded). Leaves the
- * cache rows, state, cur and tokens of those 4 steps, bit for bit. n_prompt == 4; same workspace,
- * limits and residency rules as fw_decoder_step. */
+ * cache rows, state, cur and tokens of those 4 steps, bit for bit. The LM head applies head->suppress
+ * as it is: for the first generated token pass the first step's mask (suppress plus begin-suppress ids,
+ * custom/model.py:60-61,202). n_prompt == 4; same workspace, limits and residency rules as
+ * fw_decoder_step. */
 int fw_decoder_prompt(const fw_dec_layer* layers, int n_layers, const fw_dec_head* head, const int64_t* prompt,
                       int n_prompt, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
                       int max_pos, int enc_len, float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit,
