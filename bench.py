@@ -484,6 +484,8 @@ def main():
         'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
         'encoder_tflops': round(enc_tflops, 1), 'encoder_mfma_frac': round(enc_tflops / MFMA_FP16_PEAK_TFLOPS, 4),
         'n_tokens': rows[-1]['n_tokens'],
+        # int8 LM-head rows each block of the step kernel keeps in LDS for the whole launch
+        'decode_step_lm_resident_rows': int(model.ext.lib.fw_decoder_step_resident_rows()),
     }
     lm_head = {'kernel': LM_KERNEL[q8], 'bound': 'hbm', 'achieved': round(lm_gbps, 1),
                'peak': HBM_PEAK_GBPS, 'unit': 'GB/s', 'frac': round(lm_gbps / HBM_PEAK_GBPS, 4),

@@ -1,15 +1,18 @@
 """ctypes binding of the C ABI in include/flash_whisper.h (libflash_whisper.so, built in-tree).
 
 Loading never compiles: if the library is missing this raises, so no code path can silently run
-without the HIP kernels. Build it with ``python -m flash_whisper_amd.build``.
+without the HIP kernels. Build it with ``python -m flash_whisper_amd.build``. The environment variable
+FW_LIBRARY selects another build of the same sources, e.g. the phase-timeline profiling build
+``libflash_whisper_timeline.so`` (``flash_whisper_amd.step_timeline``).
 """
 
 import ctypes
+import os
 import threading
 from ctypes import c_float, c_int, c_int64, c_uint64, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / 'libflash_whisper.so'
+LIB_PATH = Path(os.environ.get('FW_LIBRARY') or Path(__file__).resolve().parent / 'libflash_whisper.so').resolve()
 
 FW_OK, FW_EINVAL, FW_EHIP = 0, -1, -2
 NOALLOC_ATTN_SLOTS = 2048  # FW_NOALLOC_ATTN_SLOTS
@@ -68,6 +71,9 @@ SIGNATURES = {
     'fw_host_free': (None, [P]),
     'fw_final_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
     'fw_decoder_step': (c_int, [P, c_int, P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64, P]),
+    'fw_decoder_step_resident_rows': (c_int, []),
+    'fw_decoder_step_timeline': (c_int, [P, c_int64, c_int]),
+    'fw_decoder_step_timeline_slots': (c_int, []),
 }
 
 DEC_LAYER_TENSORS = ('ln1_gamma', 'ln1_beta', 'qkv_w', 'qkv_b', 'out_w', 'out_b', 'ln2_gamma', 'ln2_beta',

@@ -2,7 +2,9 @@
 
 ``python -m flash_whisper_amd.build`` compiles every ``csrc/*.hip`` for gfx950 with hipcc (in
 parallel, one object per source) and links them. The library exports the entry points declared in
-``include/flash_whisper.h``. This replaces the reference's JIT extension build (custom/ext.py:13-18),
+``include/flash_whisper.h``. It also links the profiling build ``libflash_whisper_timeline.so``: the
+same objects with the decoder step compiled with FW_STEP_TIMELINE=1, which records the phase timeline
+that ``python -m flash_whisper_amd.step_timeline`` reads (selected with FW_LIBRARY; never the default). This replaces the reference's JIT extension build (custom/ext.py:13-18),
 which ran nvcc through torch.utils.cpp_extension; here the build is ahead-of-time and in-tree so the
 built library travels with the source tree.
 """
@@ -19,6 +21,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / 'csrc'
 BUILD_DIR = Path(os.environ.get('FW_BUILD_DIR', PKG / '_build'))
 LIB = PKG / 'libflash_whisper.so'
+TIMELINE_LIB = PKG / 'libflash_whisper_timeline.so'
+TIMELINE_SRC = 'decode_step.hip'  # the one source the profiling build compiles differently
 ARCH = os.environ.get('FW_OFFLOAD_ARCH', 'gfx950')
 HIPCC = os.environ.get('HIPCC', shutil.which('hipcc') or '/opt/rocm/bin/hipcc')
 
@@ -40,9 +44,9 @@ def sources():
     return sorted(CSRC.glob('*.hip'))
 
 
-def _compile(src, verbose):
-    obj = BUILD_DIR / (src.stem + '.o')
-    cmd = [HIPCC, *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), '-c', str(src), '-o', str(obj)]
+def _compile(src, verbose, defines=(), suffix=''):
+    obj = BUILD_DIR / (src.stem + suffix + '.o')
+    cmd = [HIPCC, *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), *defines, '-c', str(src), '-o', str(obj)]
     if verbose:
         print(' '.join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,21 +61,30 @@ def _compile(src, verbose):
     return obj
 
 
-def build(verbose=False, jobs=None):
-    """Compiles all sources and links the shared library. Always rebuilds. Returns the library path."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
-    with ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
-    tmp = LIB.with_suffix('.so.tmp')
+def _link(objs, lib, verbose):
+    tmp = lib.with_suffix('.so.tmp')
     cmd = [HIPCC, f'--offload-arch={ARCH}', '-shared', '-fPIC', '-o', str(tmp), *map(str, objs), '-lpthread']
     if verbose:
         print(' '.join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f'link failed:\n{proc.stdout}{proc.stderr}')
-    os.replace(tmp, LIB)  # atomic: a process that already mapped the old file keeps it
+    os.replace(tmp, lib)  # atomic: a process that already mapped the old file keeps it
+
+
+def build(verbose=False, jobs=None):
+    """Compiles all sources and links the shared library and its phase-timeline profiling build. Always
+    rebuilds. Returns the product library's path."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    tl_src = next(s for s in srcs if s.name == TIMELINE_SRC)
+    jobs = jobs or min(len(srcs) + 1, max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as pool:
+        tl_obj = pool.submit(_compile, tl_src, verbose, ('-DFW_STEP_TIMELINE=1',), '_timeline')
+        objs = list(pool.map(lambda s: _compile(s, verbose), srcs))
+        tl_obj = tl_obj.result()
+    _link(objs, LIB, verbose)
+    _link([tl_obj if o.stem == tl_src.stem else o for o in objs], TIMELINE_LIB, verbose)
     return LIB
 
 

@@ -619,12 +619,10 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnArgs a) {
   uint4 kr[MAXP], vr[MAXP];
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
-    const int j = w0 + p * 8 + ks;
-    kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
-    if (j < wend) {
-      kr[p] = reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim)[c];
-      vr[p] = reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
-    }
+    // keys past wend load row wend - 1 (no load under a lane mask); split_wave_partial masks them
+    const int j = min(w0 + p * 8 + ks, wend - 1);
+    kr[p] = reinterpret_cast<const uint4*>(kh + static_cast<size_t>(j) * kHeadDim)[c];
+    vr[p] = reinterpret_cast<const uint4*>(vh + static_cast<size_t>(j) * kHeadDim)[c];
   }
   const int pos0 = a.len_state ? static_cast<int>(pos_raw < 0 ? 0 : (pos_raw >= a.max_len ? a.max_len - 1 : pos_raw))
                                : -1;

@@ -438,7 +438,9 @@ __device__ __forceinline__ int attn_pos(const AttnArgs& a) {
 // The scores, softmax and P.V of one wave's keys of a split (MAXP passes of 8 keys, keys at or past w1
 // masked): the wave's (max, exp-sum, value sum) go to wm, wl and wacc_row for split_merge_store. Lane
 // l holds key w0 + 8 p + l / 8 of pass p and chunk l % 8 of its row; fp32 throughout, the scale
-// applied after the dot.
+// applied after the dot. A masked key's K and V registers may hold any row (callers load a clamped
+// row rather than branch around the load, which would wait for every earlier load at the join): its
+// score is -inf and its V is taken as zero, so it adds exactly what a zero row adds.
 template <int MAXP>
 __device__ __forceinline__ void split_wave_partial(const uint4 (&kr)[MAXP], const uint4 (&vr)[MAXP], const uint4& qc,
                                                    int w0, int w1, float scale, float* wm, float* wl,
@@ -462,10 +464,11 @@ __device__ __forceinline__ void split_wave_partial(const uint4 (&kr)[MAXP], cons
       const float pj = __expf(sc[p] - mx);
       psum += pj;
       const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+      const bool live = w0 + p * 8 + ks < w1;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
-        acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
+        acc[2 * t] = fmaf(pj, live ? h2f(v2[t].x) : 0.f, acc[2 * t]);
+        acc[2 * t + 1] = fmaf(pj, live ? h2f(v2[t].y) : 0.f, acc[2 * t + 1]);
       }
     }
   }

@@ -102,6 +102,7 @@ struct StepArgs {
   int has_head;          // run the final LN + LM head + argmax + finalize as the last phase
   int n_steps;           // tokens decoded by the launch (1 without the LM head)
   const int64_t* prompt;  // the prompt pass: the tokens of the launch's kPromptLen positions
+  int lm_res_rows;        // LM-head rows per block resident in the launch's dynamic LDS
   StepHead head;
 };
 
@@ -166,6 +167,68 @@ __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N]
 }
 
 __device__ __forceinline__ unsigned half_bits(_Float16 x) { return __builtin_bit_cast(unsigned short, x); }
+
+// ---------------------------------------------------------------------------------------------
+// Phase timeline (built only with FW_STEP_TIMELINE=1, a profiling build of the library): thread 0 of
+// every block notes the 100 MHz wall clock at fixed points of each step in LDS (a global store would
+// add its completion to the next wait on the vector-memory counter), and waves 1-2 copy the step's
+// slots to a buffer set with fw_decoder_step_timeline once the step is done: slot s of block b in step
+// st at [(st * G + b) * kTlSlots + s]. Slot 0 is the step's start, layer l < kTlLayers phase p (1..8)
+// has slots tl_phase(l, p) + {0 entered and its loads issued, 1 input in (after the prologue), 2 output
+// stored, 3 the cross attention's combine stored, the self attention's split rounds done, or a
+// LayerNorm phase's residual contributions added (thread 0's share)}, the LM
+// head the slots from kTlLm on (TlLm), layer 0's self attention a few more from kTlSa on (TlSa). In the
+// product build every mark is empty.
+// ---------------------------------------------------------------------------------------------
+#ifndef FW_STEP_TIMELINE
+#define FW_STEP_TIMELINE 0
+#endif
+constexpr int kTlLayers = 4, kTlSlots = 160, kTlLm = 1 + kTlLayers * 8 * 4;
+enum TlLm { kTlArrive = 0, kTlY, kTlDigits, kTlRegScored, kTlResScored, kTlScored, kTlCand, kTlMaxStored,
+            kTlFinGathered, kTlFinStored };
+constexpr int kTlSa = kTlLm + 12;
+enum TlSa { kTlSaRow = 0, kTlSaPartial, kTlSaMerged, kTlSaWeights };
+static_assert(kTlSa + kTlSaWeights < kTlSlots, "timeline slots");
+__host__ __device__ constexpr int tl_phase(int l, int p) { return 1 + (l * 8 + (p - 1)) * 4; }
+#if FW_STEP_TIMELINE
+__device__ long long* g_step_tl;  // [steps][G][kTlSlots], or null
+__device__ int g_step_tl_steps;   // steps the buffer holds
+__shared__ long long tl_lds[kTlSlots];
+#endif
+struct Tl {
+#if FW_STEP_TIMELINE
+  long long* p;  // the step's slots of this block in the buffer, or null
+  __device__ void mark(int s) const {
+    if (p && threadIdx.x == 0) tl_lds[s] = wall_clock64();
+  }
+  __device__ void phase(int l, int ph, int k) const {
+    if (l < kTlLayers) mark(tl_phase(l, ph) + k);
+  }
+  // After a barrier that ends the step: waves 1-2 copy the slots out and clear them (wave 0 may be
+  // polling the next step's words, and its loads would wait behind these stores).
+  __device__ void flush() const {
+    const int t = threadIdx.x - kWave;
+    if (p && t >= 0 && t < kTlSlots) {
+      p[t] = tl_lds[t];
+      tl_lds[t] = 0;
+    }
+  }
+  __device__ static Tl at(int st) {
+    return {g_step_tl && st < g_step_tl_steps
+                ? g_step_tl + (static_cast<size_t>(st) * gridDim.x + blockIdx.x) * kTlSlots
+                : nullptr};
+  }
+  __device__ static void clear() {
+    if (threadIdx.x < kTlSlots) tl_lds[threadIdx.x] = 0;
+  }
+#else
+  __device__ void mark(int) const {}
+  __device__ void phase(int, int, int) const {}
+  __device__ void flush() const {}
+  __device__ static Tl at(int) { return {}; }
+  __device__ static void clear() {}
+#endif
+};
 
 // ---------------------------------------------------------------------------------------------
 // GEMV rows. A wave owns row pairs: for K = 1280 rows 2q and 2q + 1 side by side (32 lanes each, as
@@ -319,18 +382,32 @@ __device__ __forceinline__ const uint64_t* contribution(uint64_t* regions, int i
          NV * (k == 0 ? kOffAttnOut : (k == 1 ? kOffCrossOut : kOffMlpOut));
 }
 
+// Phases without a LayerNorm (out, cross-out, fc2) add the residual contributions published before
+// their input while they wait for it (the same adds in the same order), so fewer are left for the
+// block's next LayerNorm, and the blocks that ran the last fc2 reach the LM head with only that output
+// to add.
+#ifndef FW_EAGER_CATCH_UP
+#define FW_EAGER_CATCH_UP 1
+#endif
+#ifndef FW_CATCH_GROUP
+#define FW_CATCH_GROUP 1  // residual contributions awaited together by a 512-thread catch-up (4 measured 3.6 us a step slower)
+#endif
+static_assert(FW_CATCH_GROUP >= 1 && FW_CATCH_GROUP <= 8, "FW_CATCH_GROUP");
 // Adds the contributions applied .. upto - 1 to h_res, in order; run by kThreads threads (the block, or
 // one wave), t the thread's index among them. With NV vectors per phase, h_res holds NV residual
 // streams and vectors V0 .. NV - 1 are brought up to date (vector v embeds prompt token v at position
-// pos_raw + v).
+// pos_raw + v). Up to kGroup pending contributions are awaited with one wait (one memory round trip for
+// all of them), then added one after another.
 template <int kThreads = kStepThreads, int NV = 1, int V0 = 0>
 __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, int upto, uint64_t* regions,
                                                const StepArgs& a, const Ll& c, const StepPos& sp,
                                                int t = threadIdx.x) {
   constexpr int kWords = (NV - V0) * kVecWords;  // the vectors' pairs, vector-major from V0
   constexpr int kPer = (kWords + kThreads - 1) / kThreads;
+  constexpr int kGroup = kThreads >= kStepThreads && NV == 1 ? FW_CATCH_GROUP : 1;  // bounded by the registers it takes
+  static_assert(kGroup * kPer <= 64, "one pending bit per word");
   h2v* h2 = reinterpret_cast<h2v*>(h_res) + V0 * kVecWords;
-  for (; applied < upto; ++applied) {  // uniform over the threads
+  while (applied < upto) {  // uniform over the threads
     if (applied == 0) {
       if constexpr (NV == 1) {
         const _Float16 *ea, *eb;
@@ -356,23 +433,34 @@ __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, in
           h2[w] = o;
         }
       }
+      ++applied;
     } else {
-      const uint64_t* x = contribution<NV>(regions, applied) + V0 * kVecWords;
-      int idx[kPer];
+      const int ng = min(upto - applied, kGroup);  // contributions awaited together
+      int idx[kGroup * kPer];
 #pragma unroll
-      for (int k = 0; k < kPer; ++k) idx[k] = t + k * kThreads < kWords ? t + k * kThreads : -1;
-      unsigned v[kPer];
-      ll_wait<kPer>(x, idx, v, c);
+      for (int g = 0; g < kGroup; ++g) {
+        const int off = g < ng ? static_cast<int>(contribution<NV>(regions, applied + g) - regions) + V0 * kVecWords : 0;
 #pragma unroll
-      for (int k = 0; k < kPer; ++k) {
-        if (idx[k] < 0) continue;
-        const h2v hp = h2[idx[k]];
-        const h2v xp = __builtin_bit_cast(h2v, v[k]);
-        h2v o;
-        o.x = f2h(h2f(hp.x) + h2f(xp.x));
-        o.y = f2h(h2f(hp.y) + h2f(xp.y));
-        h2[idx[k]] = o;
+        for (int k = 0; k < kPer; ++k)
+          idx[g * kPer + k] = g < ng && t + k * kThreads < kWords ? off + t + k * kThreads : -1;
       }
+      unsigned v[kGroup * kPer];
+      ll_wait<kGroup * kPer>(regions, idx, v, c);
+#pragma unroll
+      for (int g = 0; g < kGroup; ++g) {  // in order: every add rounds to fp16
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          if (idx[g * kPer + k] < 0) continue;
+          const int w = t + k * kThreads;
+          const h2v hp = h2[w];
+          const h2v xp = __builtin_bit_cast(h2v, v[g * kPer + k]);
+          h2v o;
+          o.x = f2h(h2f(hp.x) + h2f(xp.x));
+          o.y = f2h(h2f(hp.y) + h2f(xp.y));
+          h2[w] = o;
+        }
+      }
+      applied += ng;
     }
   }
 }
@@ -548,7 +636,8 @@ __device__ __forceinline__ void fetch_head_vectors(const uint64_t* qsrc, int hea
 template <int NV = 1>
 __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int ns, _Float16* kc, _Float16* vc,
                                                int max_len, int pos0, const uint64_t* qkv, uint64_t* out, float scale,
-                                               AttnLds& s, float* part, float* wgt, float* den, uint4 (*kvf)[2][8]) {
+                                               AttnLds& s, float* part, float* wgt, float* den, uint4 (*kvf)[2][8],
+                                               const Tl& tl, int tl_slot) {
   constexpr int MAXP = 2, kRounds = kMaxCombineSplits / 2;
   const int pos = NV == 1 ? pos0 : min(pos0 + z, max_len - 1);  // as the batched split kernel clamps it
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
@@ -562,14 +651,14 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
     const int wend = min(min(w0 + MAXP * 8, begin + kSelfSplitKeys), max_len);
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
-      const int j = w0 + p * 8 + ks;
-      kr[r][p] = vr[r][p] = make_uint4(0, 0, 0, 0);
-      // rows past the position are never read: a later step of the same launch writes them, and an
-      // earlier read could leave a stale copy in this CU's caches
-      if (split < ns && j < wend && j <= pos) {
-        kr[r][p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-        vr[r][p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-      }
+      // Rows past the position are never read: a later step of the same launch writes them, and an
+      // earlier read could leave a stale copy in this CU's caches. A key that is not the split's (past
+      // the position or wend, or in a split past ns) loads row min(j, wend - 1, pos) instead and is
+      // masked in split_wave_partial: no load sits under a lane mask (the join after one waits for
+      // every earlier load).
+      const int j = max(0, min(min(w0 + p * 8 + ks, wend - 1), pos));
+      kr[r][p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      vr[r][p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
     }
   }
   if constexpr (NV == 1) {
@@ -590,6 +679,7 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
     if (idx[0] >= 0) *dst = v[0];
   }
   __syncthreads();
+  tl.mark(tl_slot + 1);
   if (tid < 16) {  // the fresh row into the cache, for the steps that follow
     if constexpr (NV == 1) {
       if (tid < 8)
@@ -604,6 +694,8 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
     }
   }
   const uint4 qc = s.q[0][0][cc];
+  const bool tl0 = tl_slot == tl_phase(0, 2);
+  if (tl0) tl.mark(kTlSa + kTlSaRow);
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     if (2 * r >= ns) break;  // block-uniform
@@ -632,6 +724,7 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
       split_wave_partial<MAXP>(kr[r], vr[r], qc, w0, min(wend, begin + n), scale, &s.wm[half][hw], &s.wl[half][hw],
                                s.wacc[half][hw]);
     }
+    if (tl0 && r == 0) tl.mark(kTlSa + kTlSaPartial);
     __syncthreads();
     if (act && t4 < kHeadDim) {
       float m, l, o;
@@ -643,7 +736,9 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
       }
     }
     __syncthreads();
+    if (tl0 && r == 0) tl.mark(kTlSa + kTlSaMerged);
   }
+  tl.mark(tl_slot + 3);
   head_combine(part, ns, head, wgt, den, NV == 1 ? out : out + z * kVecWords, c.tag);
 }
 
@@ -656,7 +751,8 @@ template <int NV = 1>
 __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int workers, int nitems, int nsplit,
                                                  const _Float16* kc, const _Float16* vc, int max_len,
                                                  const uint64_t* qsrc, uint64_t* part_g, uint64_t* out, float scale,
-                                                 AttnLds& s, float* part, float* wgt, float* den) {
+                                                 AttnLds& s, float* part, float* wgt, float* den, const Tl& tl,
+                                                 int tl_slot) {
   constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
   const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
@@ -674,12 +770,10 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
     uint4 kr[MAXP], vr[MAXP];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
-      const int j = w0 + p * 8 + ks;
-      kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
-      if (act && j < wend) {
-        kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-        vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-      }
+      // keys past wend (and an idle half's) load row wend - 1 and are masked: no load under a lane mask
+      const int j = max(0, min(w0 + p * 8 + ks, wend - 1));
+      kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
     }
     {  // the head's query: 32 words per half
       const int word = t4;
@@ -689,6 +783,7 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
       if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[half][0][0])[word] = v[0];
     }
     __syncthreads();
+    if (base == 2 * rank) tl.mark(tl_slot + 1);
     if (act && n > 0)
       split_wave_partial<MAXP>(kr, vr, s.q[half][0][cc], w0, min(wend, begin + n), scale, &s.wm[half][hw],
                                &s.wl[half][hw], s.wacc[half][hw]);
@@ -702,6 +797,7 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
                c.tag, __float_as_uint(val));
     }
     __syncthreads();  // s is reused below
+    tl.mark(tl_slot + 2);
     // heads whose last split this block ran: collect their partials and combine
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -722,6 +818,7 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
         if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(v[k]);
       __syncthreads();
       head_combine(part, nsplit, h, wgt, den, out + iv * kVecWords, c.tag);
+      tl.mark(tl_slot + 3);
     }
   }
 }
@@ -760,14 +857,15 @@ __device__ __forceinline__ void split_wave_partial_nv(const uint4 (&kr)[MAXP], c
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
     const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+    const bool live = w0 + p * 8 + ks < w1;  // a masked key's V counts as zero, as in split_wave_partial
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const float pj = mx[v] != -INFINITY ? __expf(sc[v][p] - mx[v]) : 0.f;
       psum[v] += pj;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        acc[v][2 * t] = fmaf(pj, h2f(v2[t].x), acc[v][2 * t]);
-        acc[v][2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[v][2 * t + 1]);
+        acc[v][2 * t] = fmaf(pj, live ? h2f(v2[t].x) : 0.f, acc[v][2 * t]);
+        acc[v][2 * t + 1] = fmaf(pj, live ? h2f(v2[t].y) : 0.f, acc[v][2 * t + 1]);
       }
     }
   }
@@ -823,12 +921,10 @@ __device__ __forceinline__ void cross_attn_items_nv(const Ll& c, int rank, int w
     uint4 kr[MAXP], vr[MAXP];
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
-      const int j = w0 + p * 8 + ks;
-      kr[p] = vr[p] = make_uint4(0, 0, 0, 0);
-      if (act && j < wend) {
-        kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-        vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-      }
+      // keys past wend (and an idle half's) load row wend - 1 and are masked: no load under a lane mask
+      const int j = max(0, min(w0 + p * 8 + ks, wend - 1));
+      kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
     }
     {  // the head's queries: 32 words per vector and half
       int idx[1] = {act && t4 < 32 * NV ? (t4 >> 5) * kVecWords + head * 32 + (t4 & 31) : -1};
@@ -926,19 +1022,53 @@ __device__ __forceinline__ void fetch_attn_vectors(const uint64_t* src, _Float16
 
 // ---------------------------------------------------------------------------------------------
 // Final LayerNorm + LM head with the int8 pre-pass + argmax + finalize (the arithmetic of
-// lm_head_q8_kernel<true> and argmax_finalize_kernel in decode.hip). Every block scores 28-row
-// batches k * G + b of the int8 table (the candidate rule holds for any partition of the rows into
-// blocks), rescores its candidates on the fp16 table with lm_head_kernel's lane split and order, and
-// hands its packed maximum to block 0 as two tagged words; block 0 takes the maximum and finalizes.
+// lm_head_q8_kernel<true> and argmax_finalize_kernel in decode.hip). Every block scores a contiguous
+// share of the int8 table (the candidate rule holds for any partition of the rows into blocks), part of
+// it held in LDS, rescores its candidates on the fp16 table with lm_head_kernel's lane split and order,
+// and hands its packed maximum to the last block as two tagged words; that block takes the maximum,
+// finalizes and broadcasts the token, position and count to every block for the next step. (Every
+// block gathering the maxima itself, with no broadcast, measured 2.6 us slower a step: 256 blocks
+// polling 512 words each load the memory system while the last blocks still score.)
 // ---------------------------------------------------------------------------------------------
 constexpr int kLmRowWaves = kStepWaves - 1;                    // waves 0-6 score rows, wave 7 awaits the
 constexpr int kLmBatchRows = kLmRowWaves * (kWave / kQ8Lpr);  // last fc2 output; 28 rows a batch, 4 a wave
 constexpr int kLmMaxBatches = 8;                              // per block: ceil(vocab / G) <= 8 * 28
-// Batches in flight per wave. Two measured best: requested deeper (4, 6) or earlier than the block's
-// arrival here, the table loads slow the last fc2 and the stream itself down.
-constexpr int kLmBufs = 2;
+// Batches in flight per wave, requested when the block arrives and refilled as they are scored. Two
+// measured best: requested deeper (4, 6) or earlier than the block's arrival here, the table loads slow
+// the last fc2 and the stream itself down (4 with the resident rows too: 105.0 against 103.1 us a step).
+#ifndef FW_LM_BUFS
+#define FW_LM_BUFS 2
+#endif
+constexpr int kLmBufs = FW_LM_BUFS;
+static_assert(kLmBufs >= 1 && kLmBufs <= kLmMaxBatches, "FW_LM_BUFS");
 constexpr int kMaxGrid = 1024;                                // blocks whose maxima the hand-off region holds
 static_assert(kLmMaxBatches * kLmBatchRows <= 256, "candidate list");
+// Rows of its share each block keeps in LDS for the whole launch (the last ones of the share): they are
+// read from HBM once per launch instead of once per step. The rest of the share streams each step. They
+// live in the launch's dynamic LDS, which sits above every static array (a 130 KB static array placed
+// first would push the others past the 64 KB reach of the LDS instructions' offset field), laid out as
+// n rows of 1280 int8, then n (scale, bound) pairs, then n suppress flags.
+#ifndef FW_LM_RES_ROWS
+#define FW_LM_RES_ROWS 104
+#endif
+constexpr int kLmResRows = FW_LM_RES_ROWS;
+constexpr int kLmResRowBytes = kHidden + sizeof(float2) + 1;
+static_assert(kLmResRows >= 0 && kLmResRows % 4 == 0 && kLmResRows <= kLmMaxBatches * kLmBatchRows,
+              "FW_LM_RES_ROWS: whole groups of 4 rows, at most a share");
+struct LmResView {
+  const uint4* q;
+  const float2* meta;
+  const uint8_t* sup;
+  int rows;  // rows the LDS holds (0: none)
+};
+__host__ __device__ inline size_t lm_res_bytes(int rows) {
+  return (static_cast<size_t>(rows) * kLmResRowBytes + 15) / 16 * 16;
+}
+extern __shared__ __align__(16) uint4 lm_res_lds[];  // the launch's dynamic LDS
+__device__ __forceinline__ LmResView lm_res_view(int rows) {
+  const float2* meta = reinterpret_cast<const float2*>(lm_res_lds + rows * kQ8Chunks);
+  return {lm_res_lds, meta, reinterpret_cast<const uint8_t*>(meta + rows), rows};
+}
 
 
 struct alignas(16) LmLds {  // yhi / ylo are read as 16-byte chunks
@@ -1035,22 +1165,53 @@ __host__ __device__ inline int lm_rows_before(int b, int vocab, int G, int late0
   return static_cast<int>(static_cast<int64_t>(vocab) * weight / total);
 }
 
-// With NV vectors (the prompt pass) the LM head scores the last one, at position pos_raw + NV - 1.
+// Blocks per phase run: the phases with many rows use every block the previous phase did not. At 256
+// CUs: LN1+q/k/v 176 blocks, self attention 20 (of a run of 176), out 80, LN2+cross-q 80, cross
+// attention 60, cross-out 80, LN3+fc1 116, fc2 80.
+struct StepWorkers {
+  int qkv, vec, cross, fc1;
+};
+__device__ __forceinline__ StepWorkers step_workers(int G) {
+  const int vec = min(kVecWorkers, max(1, G * 5 / 16));
+  const int cross = min(kCrossWorkers, max(1, G * 15 / 64));
+  return {max(1, G - vec), vec, cross, max(1, G - vec - cross)};
+}
+
+// The block's share [r0, r1) of the LM-head table: the blocks that ran the last fc2 start last and take
+// kLmLateWeight / kLmWeight of the others' share. The schedule's runs start at block 0 each step and
+// advance by the same worker counts in every layer, so the share is the same in every step of a launch.
+struct LmShare {
+  int r0, r1;
+};
+__device__ __forceinline__ LmShare lm_share(int vocab, int n_layers) {
+  const int G = gridDim.x;
+  const StepWorkers w = step_workers(G);
+  const int adv = (2 * w.qkv + 4 * w.vec + w.cross + w.fc1) % G;  // a layer's eight runs
+  const int late0 = ((n_layers * adv) % G - w.vec + G) % G;       // the last fc2's run
+  const int b = blockIdx.x;
+  return {lm_rows_before(b, vocab, G, late0, w.vec), lm_rows_before(b + 1, vocab, G, late0, w.vec)};
+}
+
+// With NV vectors (the prompt pass) the LM head scores the last one, at position pos_raw + NV - 1. The
+// last rows of the share are read from LDS, loaded there at the start of the launch.
 template <int NV = 1>
 __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead& H, const Ll& c, _Float16* h_res,
                                               int& applied, uint64_t* regions, uint64_t* maxima, uint64_t* bcast,
                                               _Float16* y_lds, float* red, LmLds& s, const StepPos& sp,
-                                              int64_t n_tok, int late0, int n_late) {
+                                              int64_t n_tok, const Tl& tl) {
   constexpr int NT = 1024, kWaves = NT / kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = gridDim.x, b = blockIdx.x, vocab = a.vocab;
+  const int G = gridDim.x, b = blockIdx.x;
   const int sub = lane & (kQ8Lpr - 1), rsel = lane / kQ8Lpr;
   const int wv = __builtin_amdgcn_readfirstlane(wave);  // branches on it are wave-uniform
-  // the block's rows: a contiguous share [r0, r1) of the table, in batches of kLmBatchRows; the blocks
-  // that ran the last fc2 start last and take kLmLateWeight / kLmWeight of the others' share
-  const int r0 = lm_rows_before(b, vocab, G, late0, n_late);
-  const int r1 = lm_rows_before(b + 1, vocab, G, late0, n_late);
-  const int nb = (r1 - r0 + kLmBatchRows - 1) / kLmBatchRows;  // <= kLmMaxBatches
+  // the block's rows: a contiguous share [r0, r1) of the table; rows [r0, rb) stream from HBM in batches
+  // of kLmBatchRows, rows [rb, r1) are resident in LDS
+  const LmShare share = lm_share(a.vocab, a.n_layers);  // recomputed: nothing stays live across the layers
+  const LmResView res = lm_res_view(NV == 1 ? a.lm_res_rows : 0);
+  const int r0 = share.r0, r1 = share.r1;
+  const int n_res = min(res.rows, r1 - r0);
+  const int rb = r1 - n_res;
+  const int nb = (rb - r0 + kLmBatchRows - 1) / kLmBatchRows;  // <= kLmMaxBatches
   auto base_of = [&](int k) { return r0 + k * kLmBatchRows; };
   const uint4* wq4 = reinterpret_cast<const uint4*>(H.wq);
   struct Batch {
@@ -1058,8 +1219,8 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     float2 m;
     uint32_t sp;
   };
-  auto load = [&](int k, Batch& bt) {  // rows past r1 load row r1 - 1 and are dropped when scored
-    const size_t row = min(base_of(k) + wave * 4 + rsel, r1 - 1);
+  auto load = [&](int k, Batch& bt) {  // rows past rb load row rb - 1 and are dropped when scored
+    const size_t row = min(base_of(k) + wave * 4 + rsel, rb - 1);
 #pragma unroll
     for (int cc = 0; cc < kQ8C; ++cc) bt.w[cc] = ld_lm_head(wq4 + row * kQ8Chunks + sub + kQ8Lpr * cc);
     bt.m = H.meta[row];
@@ -1069,10 +1230,12 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   // Waves 0-6 request their first batches as soon as the block gets here (its layer work is done, the
   // last fc2 output may be microseconds away); wave 7 alone awaits the missing residual contributions,
   // so its polls do not queue behind the table loads (a wave's loads return in order).
-  Batch bt[kLmBufs];
+  constexpr int kBufs = kLmBufs;
+  Batch bt[kBufs];
+  tl.mark(kTlLm + kTlArrive);
   if (wv < kLmRowWaves) {
 #pragma unroll
-    for (int k = 0; k < kLmBufs; ++k)
+    for (int k = 0; k < kBufs; ++k)
       if (k < nb) load(k, bt[k]);
   } else {
     resid_catch_up<kWave, NV, NV - 1>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp, lane);
@@ -1081,6 +1244,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   __syncthreads();
   ln_final(h_res + (NV - 1) * kHidden, s.gamma, s.beta, H.eps, y_lds, red);
   __syncthreads();
+  tl.mark(kTlLm + kTlY);
   if (H.y_out && b == 0)
     for (int i = tid; i < kHidden / 2; i += kStepThreads)
       reinterpret_cast<unsigned*>(H.y_out)[i] = reinterpret_cast<const unsigned*>(y_lds)[i];
@@ -1128,20 +1292,26 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     }
   }
   __syncthreads();
+  tl.mark(kTlLm + kTlDigits);
   const double ny = static_cast<double>(sqrtf(ysq)) * (1.0 + 0x1p-9);
   const double neta = amax > 0.f ? 0.51 * static_cast<double>(t) * sqrt(static_cast<double>(kHidden)) : 0.0;
   const double nE_per_s = 127.0 * sqrt(static_cast<double>(kHidden)) * (1.0 + 0x1p-30);
   float lb_max = -INFINITY;
-  auto score = [&](int k, const Batch& bt) {
-    const int slot_row = wave * 4 + rsel;
-    const int row = base_of(k) + slot_row;
+  // this lane's chunks of the y digits, read from LDS once for every row it scores (re-reading them per
+  // row made the scan bound by LDS bandwidth: 10 of a row's 15 reads)
+  uint4 ydh[kQ8C], ydl[kQ8C];
+#pragma unroll
+  for (int cc = 0; cc < kQ8C; ++cc) {
+    ydh[cc] = reinterpret_cast<const uint4*>(s.yhi)[sub + kQ8Lpr * cc];
+    ydl[cc] = reinterpret_cast<const uint4*>(s.ylo)[sub + kQ8Lpr * cc];
+  }
+  // row's bounds into slot row - r0 (rows not in range are scored but neither count nor stored)
+  auto score = [&](int row, bool in_range, const Batch& bt) {
     int ah = 0, al = 0;
 #pragma unroll
     for (int cc = 0; cc < kQ8C; ++cc) {
-      const uint4 dh = reinterpret_cast<const uint4*>(s.yhi)[sub + kQ8Lpr * cc];
-      const uint4 dl = reinterpret_cast<const uint4*>(s.ylo)[sub + kQ8Lpr * cc];
-      ah = dot16_i8(bt.w[cc], dh, ah);
-      al = dot16_i8(bt.w[cc], dl, al);
+      ah = dot16_i8(bt.w[cc], ydh[cc], ah);
+      al = dot16_i8(bt.w[cc], ydl[cc], al);
     }
     ah = xor_add_i16(ah);
     al = xor_add_i16(al);
@@ -1149,21 +1319,42 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     const double nE = static_cast<double>(bt.m.x) * nE_per_s + static_cast<double>(bt.m.y);
     const double rv = (ny * static_cast<double>(bt.m.y) + (neta + static_cast<double>(kQ8Gamma) * ny) * nE) *
                       (1.0 + 0x1p-20);
-    const bool live = row < r1 && !bt.sp;
+    const bool live = in_range && !bt.sp;
     const float ub = live ? __double2float_ru(av + rv) : -INFINITY;
     const float lb = live ? __double2float_rd(av - rv) : -INFINITY;
     lb_max = fmaxf(lb_max, lb);
-    if (sub == 0) s.ub[k * kLmBatchRows + slot_row] = ub;
+    if (sub == 0 && in_range) s.ub[row - r0] = ub;
+  };
+  // HBM batch k (in buffer k % kBufs, refilled once scored)
+  auto score_batch = [&](int k, Batch& bt) {
+    const int row = base_of(k) + wave * 4 + rsel;
+    score(row, row < rb, bt);
+    if (k + kBufs < nb) load(k + kBufs, bt);
   };
   if (wv < kLmRowWaves) {
 #pragma unroll
-    for (int k = 0; k < kLmMaxBatches; ++k) {  // batch k in buffer k % kLmBufs, refilled once scored
-      if (k < nb) {
-        score(k, bt[k % kLmBufs]);
-        if (k + kLmBufs < nb) load(k + kLmBufs, bt[k % kLmBufs]);
-      }
-    }
+    for (int k = 0; k < kBufs; ++k)
+      if (k < nb) score_batch(k, bt[k]);
   }
+  tl.mark(kTlLm + kTlRegScored);
+  // the resident rows, 4 per wave at a time, by all 8 waves while the next HBM batches are in flight
+  // (scoring them first, before the batches already in registers, measured 1.4 us a step slower)
+  for (int g = wv; 4 * g < n_res; g += kStepWaves) {  // wave-uniform
+    const int j = 4 * g + rsel, jc = min(j, n_res - 1);
+    Batch rt;
+#pragma unroll
+    for (int cc = 0; cc < kQ8C; ++cc) rt.w[cc] = res.q[jc * kQ8Chunks + sub + kQ8Lpr * cc];
+    rt.m = res.meta[jc];
+    rt.sp = res.sup[jc];
+    score(rb + j, j < n_res, rt);
+  }
+  tl.mark(kTlLm + kTlResScored);
+  if (wv < kLmRowWaves) {
+#pragma unroll
+    for (int k = kBufs; k < kLmMaxBatches; ++k)
+      if (k < nb) score_batch(k, bt[k % kBufs]);
+  }
+  tl.mark(kTlLm + kTlScored);
   lb_max = group_max<64>(lb_max);
   if (lane == 0) red[wave] = lb_max;
   __syncthreads();  // also publishes s.ub
@@ -1171,12 +1362,12 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
 #pragma unroll
   for (int i = 0; i < kStepWaves; ++i) tb = fmaxf(tb, red[i]);
   const float thr = q8_threshold(tb);
-  for (int i = tid; i < nb * kLmBatchRows; i += kStepThreads) {
-    const int row = base_of(i / kLmBatchRows) + i % kLmBatchRows;
+  for (int i = tid; i < r1 - r0; i += kStepThreads) {  // every slot of the share was stored above
     const float ub = s.ub[i];
-    if (row < r1 && ub != -INFINITY && !(ub < thr)) s.cand[atomicAdd(&s.ncand, 1)] = row;
+    if (ub != -INFINITY && !(ub < thr)) s.cand[atomicAdd(&s.ncand, 1)] = r0 + i;
   }
   __syncthreads();
+  tl.mark(kTlLm + kTlCand);
   // exact logits of the candidates: the lane split and order of lm_head_kernel
   using RS = RowSplit<kHidden>;
   const int sub32 = lane & 31, rsel32 = lane >> 5;
@@ -1209,10 +1400,11 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     ll_store(maxima + 2 * b, c.tag, static_cast<unsigned>(m));
     ll_store(maxima + 2 * b + 1, c.tag, static_cast<unsigned>(m >> 32));
   }
+  tl.mark(kTlLm + kTlMaxStored);
   if (b != fin_block()) return;  // block-uniform
   // the maximum over the blocks (thread i takes block i's two words), then the finalize of
   // argmax_finalize_kernel with the step's state words (only this block writes them), broadcast to
-  // every block for the next step as three tagged words: token, position, tokens so far
+  // every block for the next step as tagged words: token, position, tokens so far, end of the launch
   unsigned long long m = 0;
   for (int i = tid; i < G; i += kStepThreads) {
     const int idx[2] = {2 * i, 2 * i + 1};
@@ -1229,6 +1421,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   }
   if (lane == 0) s.fin[wave] = m;
   __syncthreads();
+  tl.mark(kTlLm + kTlFinGathered);
   if (tid == 0) {
 #pragma unroll
     for (int i = 0; i < kStepWaves; ++i) m = s.fin[i] > m ? s.fin[i] : m;
@@ -1240,6 +1433,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     ll_store(bcast + 1, c.tag, static_cast<unsigned>(o.pos));
     ll_store(bcast + 2, c.tag, static_cast<unsigned>(o.n));
     ll_store(bcast + 3, c.tag, stop ? 1u : 0u);
+    tl.mark(kTlLm + kTlFinStored);
     // the token to the host as well (the host polls for it; the token is the whole message, so no
     // ordering with other stores is needed)
     if (H.host_tokens && n_tok < a.max_pos)
@@ -1292,6 +1486,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   // The launch's tags: the epoch every block reads before it arrives; step st of the launch tags its
   // words epoch + 1 + st. The last block to arrive moves the epoch on by the launch's steps, when no
   // block of this one can still be reading it.
+  Tl::clear();
   if (tid == 0) epoch_lds = __hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   const unsigned epoch = epoch_lds;
@@ -1309,22 +1504,31 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   int64_t n_tok = a.has_head && blockIdx.x == fin_block() ? a.state[1] : 0;  // for the finalize
   const int ns_cross = (a.enc_len + kCrossSplitKeys - 1) / kCrossSplitKeys;
 
-  // worker counts: the phases with many rows use every block the previous phase did not
-  // Runs of blocks per phase, taken in turn around the grid: consecutive phases use disjoint blocks and
-  // the LN3 + fc1 phase also avoids the cross-attention blocks (which finish late). At 256 CUs: LN1+q/k/v
-  // 176 blocks, self attention 20 (of a run of 176), out 80, LN2+cross-q 80, cross attention 60,
-  // cross-out 80, LN3+fc1 116, fc2 80. Every step starts the runs at block 0, so a layer's phase
+  // Runs of blocks per phase (step_workers), taken in turn around the grid: consecutive phases use
+  // disjoint blocks and the LN3 + fc1 phase also avoids the cross-attention blocks (which finish late).
+  // Every step starts the runs at block 0, so a layer's phase
   // runs on the same blocks in every step: the self-attention block of a head reads back the cache
   // rows it wrote itself (through its own CU's caches) in the steps before.
-  const int w_vec = min(kVecWorkers, max(1, G * 5 / 16));
-  const int w_cross = min(kCrossWorkers, max(1, G * 15 / 64));
-  const int w_qkv = max(1, G - w_vec);
-  const int w_fc1 = max(1, G - w_vec - w_cross);
+  const StepWorkers wk = step_workers(G);
+  const int w_vec = wk.vec, w_cross = wk.cross, w_qkv = wk.qkv, w_fc1 = wk.fc1;
+  // the resident LM-head rows (the decode steps only: the prompt pass's vectors fill that LDS)
+  if (NV == 1 && a.has_head && a.lm_res_rows > 0) {  // the share's last rows, once for every step of the launch
+    const LmResView res = lm_res_view(a.lm_res_rows);
+    const LmShare share = lm_share(a.vocab, a.n_layers);
+    const int n_res = min(res.rows, share.r1 - share.r0), rb = share.r1 - n_res;
+    const uint4* src = reinterpret_cast<const uint4*>(a.head.wq) + static_cast<size_t>(rb) * kQ8Chunks;
+    for (int i = tid; i < n_res * kQ8Chunks; i += kStepThreads) lm_res_lds[i] = ld_lm_head(src + i);
+    for (int i = tid; i < n_res; i += kStepThreads) {
+      const_cast<float2*>(res.meta)[i] = a.head.meta[rb + i];
+      const_cast<uint8_t*>(res.sup)[i] = a.head.suppress[rb + i];
+    }  // read after the barriers of the first step's phases
+  }
 
   const int n_steps = NV > 1 ? 1 : args.n_steps;
   for (int st = 0; st < n_steps; ++st) {
     const StepArgs& a = step_args();
     const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit};
+    const Tl tl = Tl::at(st);
     if (st > 0) {  // the previous step's token, position, token count and stop flag
       __syncthreads();
       if (tid < 4) {
@@ -1340,6 +1544,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       n_tok = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[2]));
       if (__builtin_amdgcn_readfirstlane(bcast_lds[3])) break;  // an end-of-text token: every block stops
     }
+    tl.mark(0);
     const int pos = static_cast<int>(sp.pos_raw < 0 ? 0 : (sp.pos_raw >= a.max_pos ? a.max_pos - 1 : sp.pos_raw));
     const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
     Sched sc{0, G};
@@ -1362,9 +1567,12 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln1_g, L.ln1_b);
+          tl.phase(l, 1, 0);
           resid_catch_up<kStepThreads, NV>(h_res, applied, 1 + 3 * l, regions, a, c, sp);
+          tl.phase(l, 1, 3);
           resid_layernorm_nv<NV>(lnr, h_res, L.eps1, x_lds, red);
           __syncthreads();
+          tl.phase(l, 1, 1);
           for (;;) {
             gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffQkv, c.tag, base, qs, npairs);
             base += U * qs;
@@ -1372,6 +1580,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             __syncthreads();
             gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
           }
+          tl.phase(l, 1, 2);
         }
         sc.next(W);
       }
@@ -1381,10 +1590,12 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
         const int rank = sc.rank(), W = kStepHeads * NV;  // (head, vector) pairs
         if (rank < W) {
           const int z = rank / kStepHeads;
+          tl.phase(l, 2, 0);
           self_attn_head<NV>(c, rank % kStepHeads, z,
                              NV > 1 ? (min(pos + z, a.max_pos - 1) + kSelfSplitKeys) / kSelfSplitKeys : ns_self,
                              L.self_k, L.self_v, a.max_pos, pos, R + NV * kOffQkv, R + NV * kOffSelfVec, a.scale, att,
-                             part_lds, wgt, den, kvf);
+                             part_lds, wgt, den, kvf, tl, l < kTlLayers ? tl_phase(l, 2) : kTlSlots - 4);
+          tl.phase(l, 2, 2);
         }
         sc.next(w_qkv);
       }
@@ -1399,8 +1610,11 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
           gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
+          tl.phase(l, 3, 0);
+          if (FW_EAGER_CATCH_UP) resid_catch_up<kStepThreads, NV>(h_res, applied, 1 + 3 * l, regions, a, c, sp);
           fetch_attn_vectors<NV>(R + NV * kOffSelfVec, x_lds, c);
           __syncthreads();
+          tl.phase(l, 3, 1);
           for (;;) {
             gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffAttnOut, c.tag, base, qs, npairs);
             base += U * qs;
@@ -1408,6 +1622,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             __syncthreads();
             gv_load(g, L.out_w, L.out_b, npairs, base + wave, qs);
           }
+          tl.phase(l, 3, 2);
         }
         sc.next(W);
       }
@@ -1424,9 +1639,12 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln2_g, L.ln2_b);
+          tl.phase(l, 4, 0);
           resid_catch_up<kStepThreads, NV>(h_res, applied, 2 + 3 * l, regions, a, c, sp);
+          tl.phase(l, 4, 3);
           resid_layernorm_nv<NV>(lnr, h_res, L.eps2, x_lds, red);
           __syncthreads();
+          tl.phase(l, 4, 1);
           for (;;) {
             gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffCrossQ, c.tag, base, qs, npairs);
             base += U * qs;
@@ -1434,6 +1652,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             __syncthreads();
             gv_load(g, L.cq_w, L.cq_b, npairs, base + wave, qs);
           }
+          tl.phase(l, 4, 2);
         }
         sc.next(W);
       }
@@ -1444,9 +1663,11 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
         const int W = min(w_cross, (nitems + 1) / 2);
         const int rank = sc.rank();
         if (rank < W) {
+          tl.phase(l, 5, 0);
           if constexpr (NV == 1)
             cross_attn_items<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
-                                 R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den);
+                                 R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den, tl,
+                                 l < kTlLayers ? tl_phase(l, 5) : kTlSlots - 4);
           else
             cross_attn_items_nv<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + NV * kOffCrossQ,
                                     R + NV * kOffCrossPart, R + NV * kOffCrossVec, a.scale, attv, part_lds, wgt, den);
@@ -1464,8 +1685,11 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
           gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
+          tl.phase(l, 6, 0);
+          if (FW_EAGER_CATCH_UP) resid_catch_up<kStepThreads, NV>(h_res, applied, 2 + 3 * l, regions, a, c, sp);
           fetch_attn_vectors<NV>(R + NV * kOffCrossVec, x_lds, c);
           __syncthreads();
+          tl.phase(l, 6, 1);
           for (;;) {
             gv_finish_nv<kHidden, U, FW_ACT_NONE, NV>(g, x_lds, stage, R + NV * kOffCrossOut, c.tag, base, qs, npairs);
             base += U * qs;
@@ -1473,6 +1697,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             __syncthreads();
             gv_load(g, L.co_w, L.co_b, npairs, base + wave, qs);
           }
+          tl.phase(l, 6, 2);
         }
         sc.next(W);
       }
@@ -1489,9 +1714,12 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln3_g, L.ln3_b);
+          tl.phase(l, 7, 0);
           resid_catch_up<kStepThreads, NV>(h_res, applied, 3 + 3 * l, regions, a, c, sp);
+          tl.phase(l, 7, 3);
           resid_layernorm_nv<NV>(lnr, h_res, L.eps3, x_lds, red);
           __syncthreads();
+          tl.phase(l, 7, 1);
           for (;;) {
             gv_finish_nv<kHidden, U, FW_ACT_GELU, NV>(g, x_lds, stage, R + NV * kOffFfn, c.tag, base, qs, npairs);
             base += U * qs;
@@ -1499,6 +1727,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             __syncthreads();
             gv_load(g, L.fc1_w, L.fc1_b, npairs, base + wave, qs);
           }
+          tl.phase(l, 7, 2);
         }
         sc.next(W);
       }
@@ -1514,6 +1743,8 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
           gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
+          tl.phase(l, 8, 0);
+          if (FW_EAGER_CATCH_UP) resid_catch_up<kStepThreads, NV>(h_res, applied, 3 + 3 * l, regions, a, c, sp);
           // the fc1 output, 2560 words per vector, into LDS
           constexpr int kPer = kFfnWords / kStepThreads;
           static_assert(kFfnWords % kStepThreads == 0, "whole words per thread");
@@ -1527,6 +1758,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             for (int k = 0; k < kPer; ++k) reinterpret_cast<unsigned*>(x_lds + vec * kStepFfn)[idx[k]] = v[k];
           }
           __syncthreads();
+          tl.phase(l, 8, 1);
           for (;;) {
             if constexpr (NV == 1)
               gv_finish<kStepFfn, U, FW_ACT_NONE>(g, x_lds, stage, R + kOffMlpOut, c.tag, last ? a.x_out : nullptr, base,
@@ -1538,6 +1770,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
             __syncthreads();
             gv_load(g, L.fc2_w, L.fc2_b, npairs, base + wave, qs);
           }
+          tl.phase(l, 8, 2);
         }
         sc.next(W);
       }
@@ -1545,9 +1778,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
 
     if (a.has_head) {
       __syncthreads();
-      // the last fc2's run: the w_vec blocks before the schedule's current start
-      lm_head_phase<NV>(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok,
-                        (sc.start - w_vec + G) % G, w_vec);
+      lm_head_phase<NV>(a, a.head, c, h_res, applied, regions, maxima, bcast, x_lds, red, lm, sp, n_tok, tl);
     } else if (NV == 1 && blockIdx.x == 0) {
       // the residual the LM head adds the last fc2 output to: everything up to the last cross-out
       __syncthreads();
@@ -1555,6 +1786,10 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       __syncthreads();
       for (int i = tid; i < kHidden / 2; i += kStepThreads)
         reinterpret_cast<unsigned*>(a.h_out)[i] = reinterpret_cast<const unsigned*>(h_res)[i];
+    }
+    if (FW_STEP_TIMELINE) {
+      __syncthreads();
+      tl.flush();
     }
   }
   if (tid == 0 && arrived == static_cast<unsigned>(G) - 1u) {
@@ -1590,6 +1825,60 @@ extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
 }
 
 extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }
+
+// LM-head rows per block that fit in the step kernel's dynamic LDS on the current device (cached per
+// device): the device's LDS per block less the kernel's static LDS, at most kLmResRows.
+static int step_resident_rows(int dev) {
+  constexpr int kDevs = 64;
+  static int cached[kDevs];  // rows + 1, 0 = not yet computed (a race computes the same value twice)
+  if (dev >= 0 && dev < kDevs && cached[dev] > 0) return cached[dev] - 1;
+  int max_lds = 0;
+  hipFuncAttributes fa{};
+  int rows = 0;
+  if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+      hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(decoder_step_kernel<1>)) == hipSuccess &&
+      static_cast<size_t>(max_lds) > fa.sharedSizeBytes) {
+    const size_t avail = static_cast<size_t>(max_lds) - fa.sharedSizeBytes;
+    rows = kLmResRows;
+    while (rows > 0 && lm_res_bytes(rows) > avail) rows -= 4;
+    if (rows > 0 && hipFuncSetAttribute(reinterpret_cast<const void*>(decoder_step_kernel<1>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(lm_res_bytes(rows))) != hipSuccess)
+      rows = 0;
+  }
+  (void)hipGetLastError();  // a failed query leaves no error for the launch check: the rows are then 0
+  if (dev >= 0 && dev < kDevs) cached[dev] = rows + 1;
+  return rows;
+}
+
+extern "C" int fw_decoder_step_timeline_slots(void) { return FW_STEP_TIMELINE ? kTlSlots : 0; }
+
+extern "C" int fw_decoder_step_timeline(void* buf, int64_t bytes, int steps) {
+#if FW_STEP_TIMELINE
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return fw_fail(FW_EHIP, "decoder_step_timeline: cannot read the device's CU count");
+  const int grid = cus < kMaxGrid ? cus : kMaxGrid;
+  if (buf && (steps < 1 || bytes < static_cast<int64_t>(steps) * grid * kTlSlots * 8))
+    return fw_fail(FW_EINVAL, "decoder_step_timeline: %lld bytes do not hold %d steps of %d blocks x %d slots",
+                   static_cast<long long>(bytes), steps, grid, kTlSlots);
+  long long* p = static_cast<long long*>(buf);
+  const int n = buf ? steps : 0;
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_step_tl), &p, sizeof(p)) != hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_step_tl_steps), &n, sizeof(n)) != hipSuccess)
+    return fw_fail(FW_EHIP, "decoder_step_timeline: hipMemcpyToSymbol failed");
+  return FW_OK;
+#else
+  (void)buf, (void)bytes, (void)steps;
+  return fw_fail(FW_EINVAL, "decoder_step_timeline: this library was built without FW_STEP_TIMELINE");
+#endif
+}
+
+extern "C" int fw_decoder_step_resident_rows(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fw_fail(FW_EHIP, "decoder_step_resident_rows: no device");
+  return step_resident_rows(dev);
+}
 
 static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int n_layers, const fw_dec_head* head,
                                const int64_t* prompt, int n_steps, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
@@ -1687,10 +1976,11 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
   a.x_out = static_cast<_Float16*>(x_out);
   a.ws = static_cast<unsigned char*>(workspace);
   a.spin_limit = spin_limit;
+  a.lm_res_rows = head && !prompt ? step_resident_rows(dev) : 0;
   if (prompt)
     hipLaunchKernelGGL(decoder_step_kernel<kPromptLen>, dim3(grid), dim3(kStepThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(decoder_step_kernel<1>, dim3(grid), dim3(kStepThreads), 0, stream, a);
+    hipLaunchKernelGGL(decoder_step_kernel<1>, dim3(grid), dim3(kStepThreads), lm_res_bytes(a.lm_res_rows), stream, a);
   return fw_check_launch(name);
 }
 

@@ -1,0 +1,205 @@
+"""Phase timeline of the persistent decoder step (``decoder_step_kernel``), from the profiling build.
+
+    FW_LIBRARY=flash_whisper_amd/libflash_whisper_timeline.so python -m flash_whisper_amd.step_timeline
+
+The profiling build (``libflash_whisper_timeline.so``, linked by ``python -m flash_whisper_amd.build``)
+is the product library with the decoder step compiled with FW_STEP_TIMELINE=1: thread 0 of every block
+stores the 100 MHz wall clock at fixed points of each step (fw_decoder_step_timeline in
+include/flash_whisper.h lists them); nothing else changes. This module builds the seeded model,
+transcribes the benchmark clip once (warm-up), runs the log-mel, encoder and prompt pass of a second
+transcribe, then records the decode launch that follows (every token after the first, one launch, as
+``transcribe`` runs it) and prints, per layer and phase, the median over the decode's steps of:
+
+- ``in``: when the phase's input was in its blocks (first / median / last block, after the wait and
+  the phase's prologue: residual catch-up and LayerNorm, or the attention vector's words);
+- ``out``: when the last of its blocks had stored its output (for the cross attention, the heads'
+  combined outputs);
+- ``dur``: ``out`` less the previous phase's ``out``: the phase's share of the step;
+- ``wait``: the median block's ``in`` less the previous phase's ``out``: hand-off and prologue;
+
+all in us from the step's start (the first block to read the previous step's token). With
+``--from-pos P --steps N`` it also records N steps from position P of a cache filled by the warm-up
+(self attention over up to 448 keys), and prints the self-attention phase at every step.
+"""
+
+import argparse
+import os
+import statistics
+import sys
+
+import numpy as np
+
+TICK_US = 0.01  # the 100 MHz wall clock
+PHASES = ('LN1 + q/k/v', 'self attention', 'out', 'LN2 + cross q', 'cross attention', 'cross-out',
+          'LN3 + fc1 + GELU', 'fc2')
+TL_LAYERS, TL_LM, TL_SA = 4, 129, 141
+LM_POINTS = ('arrived', 'final LN done', 'y digits ready', 'first HBM batches scored', 'resident rows scored',
+             'all rows scored', 'candidates listed', 'block maximum stored', 'every block maximum gathered',
+             'token and state stored (last block)')
+
+
+def tl_phase(layer, phase):
+    return 1 + (layer * 8 + phase - 1) * 4
+
+
+def record(model, n_steps, setup):
+    """Runs setup() (enqueues whatever precedes the recorded launch), then records the timeline of the
+    next n_steps decoder steps (one launch); returns int64 [steps, grid, slots] ticks (0: not reached)."""
+    import torch
+
+    lib = model.ext.lib
+    slots = lib.fw_decoder_step_timeline_slots()
+    if slots <= 0:
+        raise RuntimeError('this library records no timeline: set FW_LIBRARY to libflash_whisper_timeline.so')
+    grid = min(torch.cuda.get_device_properties(0).multi_processor_count, 1024)
+    buf = torch.zeros(n_steps, grid, slots, dtype=torch.int64, device='cuda')
+    setup()
+    torch.cuda.synchronize()
+    model.ext._call('fw_decoder_step_timeline', buf.data_ptr(), buf.numel() * 8, n_steps)
+    model._steps(n_steps)
+    torch.cuda.synchronize()
+    model.ext._call('fw_decoder_step_timeline', None, 0, 0)
+    model._check_step_error()
+    return buf.cpu().numpy()
+
+
+def step_stats(tl, n_layers):
+    """Per step: the statistics above in us from the step's start."""
+    out = []
+    for st in range(tl.shape[0]):
+        s = tl[st]
+        if not (s[:, 0] > 0).any():
+            break  # the launch stopped early
+        t0 = s[s[:, 0] > 0, 0].min()
+        us = lambda v: (float(v) - float(t0)) * TICK_US
+        row, prev_out = {}, 0.0
+        for layer in range(min(n_layers, TL_LAYERS)):
+            for p in range(1, 9):
+                base = tl_phase(layer, p)
+                act = s[:, base + 2] > 0
+                ins = np.sort(s[act, base + 1])
+                outs = s[act, base + 3 if p == 5 else base + 2]
+                outs = outs[outs > 0]
+                if not len(ins) or not len(outs):
+                    continue
+                per = (s[act, base + 2] - s[act, base + 1]) * TICK_US  # each block's input -> its stores
+                r = dict(blocks=int(act.sum()), in_first=us(ins[0]), in_med=us(np.median(ins)), in_last=us(ins[-1]),
+                         out=us(outs.max()), enter=us(np.median(s[act, base])), enter_last=us(s[act, base].max()),
+                         work=float(np.median(per)), work_max=float(per.max()))
+                if p == 5:
+                    r['part'] = us(s[act, base + 2].max())  # the split partials stored
+                if p in (1, 4, 7):  # thread 0's residual contributions added, before the LayerNorm
+                    r['resid'] = us(np.median(s[act, base + 3]))
+                r['dur'], r['wait'] = r['out'] - prev_out, r['in_med'] - prev_out
+                prev_out = r['out']
+                row[(layer, p)] = r
+        lm = s[:, TL_LM:TL_LM + len(LM_POINTS)]
+        for k, name in enumerate(LM_POINTS):
+            v = lm[:, k][lm[:, k] > 0]
+            if len(v):
+                row[('lm', k)] = dict(med=us(np.median(v)), last=us(v.max()), blocks=len(v))
+        base = tl_phase(0, 2)
+        act = s[:, base + 2] > 0
+        if act.any():  # layer 0's self attention inside: each block's times after its input was in
+            t_in = s[act, base + 1].astype(np.float64)
+            for k, name in enumerate(('fresh row written', 'first round: wave 0 partial', 'first round merged')):
+                row[('sa', k)] = float(np.median(s[act, TL_SA + k] - t_in)) * TICK_US
+            row[('sa', 3)] = float(np.median(s[act, base + 3] - t_in)) * TICK_US
+            row[('sa', 4)] = float(np.median(s[act, base + 2] - t_in)) * TICK_US
+        nxt = tl[st + 1][:, 0] if st + 1 < tl.shape[0] else None
+        if nxt is not None and (nxt > 0).any():
+            row['period'] = (float(nxt[nxt > 0].min()) - float(t0)) * TICK_US
+        out.append(row)
+    return out
+
+
+def median_over(rows, key, field):
+    vals = [r[key][field] for r in rows if key in r]
+    return statistics.median(vals) if vals else float('nan')
+
+
+def report(rows, n_layers, title):
+    lines = [f'### {title}', '',
+             f'Steps: {len(rows)} (medians over them); step period (start to the next step\'s start): '
+             f'{statistics.median(r["period"] for r in rows if "period" in r):.2f} us', '',
+             '| Layer | Phase | Blocks | entered (median / last) | in first | in median | in last | out | dur | wait | '
+             'block work (median / max) |',
+             '|---:|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|']
+    for layer in range(min(n_layers, TL_LAYERS)):
+        for p in range(1, 9):
+            key = (layer, p)
+            if not any(key in r for r in rows):
+                continue
+            m = lambda f: median_over(rows, key, f)
+            name = PHASES[p - 1] + (f' (partials stored {m("part"):.2f})' if p == 5 else '') + \
+                (f' (residual in {m("resid"):.2f})' if p in (1, 4, 7) else '')
+            lines.append(f'| {layer} | {name} | {int(m("blocks"))} | {m("enter"):.2f} / {m("enter_last"):.2f} | '
+                         f'{m("in_first"):.2f} | {m("in_med"):.2f} | {m("in_last"):.2f} | {m("out"):.2f} | '
+                         f'{m("dur"):.2f} | {m("wait"):.2f} | {m("work"):.2f} / {m("work_max"):.2f} |')
+    lines += ['', '| Layer 0 self attention, after its input (median block) | us |', '|---|---:|']
+    for k, name in enumerate(('fresh row written', 'first round: wave 0 partial', 'first round merged',
+                              'every round merged', 'output stored')):
+        if any(('sa', k) in r for r in rows):
+            lines.append(f'| {name} | {statistics.median(r[("sa", k)] for r in rows if ("sa", k) in r):.2f} |')
+    lines += ['', '| LM head point | median block | last block |', '|---|---:|---:|']
+    for k, name in enumerate(LM_POINTS):
+        key = ('lm', k)
+        if any(key in r for r in rows):
+            lines.append(f'| {name} | {median_over(rows, key, "med"):.2f} | {median_over(rows, key, "last"):.2f} |')
+    return '\n'.join(lines)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    ap.add_argument('--tokens', type=int, default=224)
+    ap.add_argument('--from-pos', type=int, default=440, help='start of the extra run (self attention over long caches)')
+    ap.add_argument('--steps', type=int, default=8, help='steps of the extra run (0: none)')
+    args = ap.parse_args()
+    if not os.environ.get('FW_LIBRARY'):
+        print('set FW_LIBRARY=flash_whisper_amd/libflash_whisper_timeline.so (the profiling build)', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from flash_whisper_amd.audio import synthetic_clip
+    from flash_whisper_amd.model import CustomModel
+
+    torch.set_grad_enabled(False)
+    model = CustomModel(seed=0, selftest=False)
+    clip = synthetic_clip(0)
+    model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)  # warm-up
+    n_layers = model.dims.dec_layers
+    n = args.tokens - 1
+    model.ext.set_eos(model.step_head, ())
+    tl = record(model, n, lambda: model.transcribe(clip, max_new_tokens=1, stop_at_eos=False))
+    rows = step_stats(tl, n_layers)
+    print(f'# device: {torch.cuda.get_device_name(0)}, grid {tl.shape[1]} blocks, '
+          f'{model.ext.lib.fw_decoder_step_resident_rows()} resident LM-head rows per block')
+    print()
+    print(report(rows[1:], n_layers, f'Decode launch of a {args.tokens}-token transcribe: steps 1..{len(rows) - 1} '
+                                     f'(positions 5..{4 + len(rows) - 1}; step 0 also loads the resident rows)'))
+    print()
+    pos0 = 4  # the decode starts after the 4-token prompt
+    sa = [(pos0 + i + 1, r[(0, 2)]['dur'], r[(0, 2)]['in_med'] - r[(0, 1)]['out']) for i, r in enumerate(rows)
+          if (0, 2) in r and (0, 1) in r]
+    pick = [x for x in sa if x[0] in (64, 128, 224)]
+    if args.steps > 0:
+        def setup():
+            with torch.inference_mode():
+                model.state.copy_(torch.tensor([args.from_pos, 0], device='cuda'))
+                model.cur.fill_(int(model.tokens[0]))
+        tl2 = record(model, args.steps, setup)
+        rows2 = step_stats(tl2, n_layers)
+        print(report(rows2, n_layers, f'{args.steps} steps from position {args.from_pos} (cache rows from the '
+                                      f'warm-up transcribe and earlier steps)'))
+        print()
+        pick += [(args.from_pos + i + 1, r[(0, 2)]['dur'], r[(0, 2)]['in_med'] - r[(0, 1)]['out'])
+                 for i, r in enumerate(rows2) if (0, 2) in r and (0, 1) in r]
+    print('### Self attention (layer 0) by cache length L = position + 1', '')
+    print('| L | dur (us) | wait (us) |', '|---:|---:|---:|', sep='\n')
+    for L, dur, wait in pick:
+        print(f'| {L} | {dur:.2f} | {wait:.2f} |')
+
+
+if __name__ == '__main__':
+    main()

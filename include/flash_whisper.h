@@ -258,6 +258,30 @@ int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head*
                     int64_t* state, const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len,
                     float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream);
 
+/* Rows of the int8 LM-head table each block of fw_decoder_step keeps in LDS for the whole launch on the
+ * current device (read from HBM once per launch; the rest of its share streams every step), or a
+ * negative status. No counterpart in the reference (its LM head, whisper_kernels.cu:28-86, streams the
+ * whole fp16 table every step). */
+int fw_decoder_step_resident_rows(void);
+
+/* Phase timeline of fw_decoder_step / fw_decoder_prompt, for a profiling build of the library only
+ * (decode_step.hip compiled with FW_STEP_TIMELINE=1; the product build returns FW_EINVAL and 0 slots).
+ * buf (device memory, NULL to stop recording) receives, for each of the first `steps` steps of every
+ * later launch, each block's 100 MHz wall-clock ticks at fixed points: int64 at
+ * [(step * grid + block) * slots + s], grid = min(CU count, 1024), slots from
+ * fw_decoder_step_timeline_slots(). s = 0: the step starts; 1 + (l * 8 + p - 1) * 4 + k for layer
+ * l < 4, phase p = 1..8 (LN1+q/k/v, self attention, out, LN2+cross q, cross attention, cross-out,
+ * LN3+fc1, fc2) and k = 0 entered with its loads issued, 1 input in, 2 output stored, 3 the cross
+ * attention's head combine stored / the self attention's split rounds done / a LayerNorm phase's
+ * residual contributions added; 129 + k for the LM head: k = 0 arrived, 1 final LayerNorm done, 2 y
+ * digits ready, 3 first two HBM batches scored, 4 resident rows scored, 5 all rows scored, 6 candidates
+ * listed, 7 block maximum stored, 8 (last block) maxima gathered, 9 (last block) token broadcast;
+ * 141 + k inside layer 0's self attention: k = 0 fresh row written, 1 first round's wave-0 partial,
+ * 2 first round merged. Slots a block does not reach in a step read 0. No counterpart in the reference (its
+ * per-kernel times come from nsys, results/run07/report.txt:414-431). Synchronous. */
+int fw_decoder_step_timeline(void* buf, int64_t bytes, int steps);
+int fw_decoder_step_timeline_slots(void);
+
 /* Final residual + LayerNorm + LM head + argmax, then finalize (custom/model.py:121-123):
  * r = fp16(h + x) (x may be NULL); y = LN(r); then exactly fw_lm_head_argmax on y followed by
  * fw_argmax_finalize. best must be zero on entry and is left zero. With tokens, state and cur all
