@@ -80,6 +80,8 @@ def step_stats(tl, n_layers):
                 ins = np.sort(s[act, base + 1])
                 outs = s[act, base + 3 if p == 5 else base + 2]
                 outs = outs[outs > 0]
+                if p == 5 and not len(outs):  # one query: the heads are combined by the cross-out blocks
+                    outs = s[act, base + 2]
                 if not len(ins) or not len(outs):
                     continue
                 per = (s[act, base + 2] - s[act, base + 1]) * TICK_US  # each block's input -> its stores
