@@ -72,6 +72,7 @@ SIGNATURES = {
     'fw_final_layernorm': (c_int, [P, P, P, P, P, c_int, c_float, P]),
     'fw_decoder_step': (c_int, [P, c_int, P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, c_int64, c_int64, P]),
     'fw_decoder_step_resident_rows': (c_int, []),
+    'fw_decoder_step_check': (c_int, [c_int, c_int, c_int, c_int, c_int]),
     'fw_decoder_step_timeline': (c_int, [P, c_int64, c_int]),
     'fw_decoder_step_timeline_slots': (c_int, []),
 }

@@ -1880,21 +1880,61 @@ extern "C" int fw_decoder_step_resident_rows(void) {
   return step_resident_rows(dev);
 }
 
+// The sizes a launch takes, checked against the device: the grid is the CU count (at most kMaxGrid), and
+// every phase must find its blocks in it (the self attention's one block per head and vector within the
+// run after the q/k/v run; the LM head's largest share within the candidate list). Returns FW_OK and the
+// grid, or FW_EINVAL / FW_EHIP with the reason.
+static int step_range_check(const char* name, int n_layers, int vocab, int max_pos, int enc_len) {
+  if (n_layers < 1 || n_layers > kStepMaxLayers)
+    return fw_fail(FW_EINVAL, "%s: n_layers must be in [1, %d]", name, kStepMaxLayers);
+  if (vocab < 1 || max_pos < 1 || max_pos > kMaxCombineSplits * kSelfSplitKeys)
+    return fw_fail(FW_EINVAL, "%s: max_pos must be in [1, %d]", name, kMaxCombineSplits * kSelfSplitKeys);
+  if (enc_len < 1 || enc_len > kMaxCombineSplits * kCrossSplitKeys)
+    return fw_fail(FW_EINVAL, "%s: enc_len must be in [1, %d]", name, kMaxCombineSplits * kCrossSplitKeys);
+  return FW_OK;
+}
+
+static int step_sizes_check(const char* name, int n_layers, int vocab, int max_pos, int enc_len, bool has_head,
+                            int nv, int* grid_out) {
+  if (const int st = step_range_check(name, n_layers, vocab, max_pos, enc_len)) return st;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    return fw_fail(FW_EHIP, "%s: cannot read the device's CU count", name);
+  const int grid = cus < kMaxGrid ? cus : kMaxGrid;
+  const int w_vec = std::min(kVecWorkers, std::max(1, grid * 5 / 16));
+  if (grid - w_vec < kStepHeads * nv)  // the self attention: a block per (head, vector) in the run after q/k/v
+    return fw_fail(FW_EINVAL, "%s: %d CUs run too few blocks (the self attention needs %d beside %d others)", name,
+                   grid, kStepHeads * nv, w_vec);
+  if (has_head) {
+    // the largest share: a block of weight kLmWeight next to the late blocks
+    int most = 0;
+    for (int b = 0; b < grid; ++b)
+      most = std::max(most, lm_rows_before(b + 1, vocab, grid, 0, w_vec) - lm_rows_before(b, vocab, grid, 0, w_vec));
+    if (most + 1 > kLmMaxBatches * kLmBatchRows)  // + 1: the rounding of another placement of the late run
+      return fw_fail(FW_EINVAL, "%s: vocab %d gives a block %d rows of the LM head (at most %d) on %d blocks", name,
+                     vocab, most, kLmMaxBatches * kLmBatchRows, grid);
+  }
+  *grid_out = grid;
+  return FW_OK;
+}
+
+extern "C" int fw_decoder_step_check(int n_layers, int vocab, int max_pos, int enc_len, int prompt) {
+  int grid = 0;
+  return step_sizes_check("decoder_step_check", n_layers, vocab, max_pos, enc_len, true, prompt ? kPromptLen : 1,
+                          &grid);
+}
+
 static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int n_layers, const fw_dec_head* head,
                                const int64_t* prompt, int n_steps, int64_t* cur, int64_t* state, const void* embed, const void* pos_embed, int vocab,
                                int max_pos, int enc_len, float scale, void* h_out, void* x_out, void* workspace,
                                int64_t ws_bytes, int64_t spin_limit, hipStream_t stream) {
   if (!layers || !cur || !state || !embed || !pos_embed || !workspace || (!head && (!h_out || !x_out)))
     return fw_fail(FW_EINVAL, "%s: null pointer", name);
-  if (n_layers < 1 || n_layers > kStepMaxLayers)
-    return fw_fail(FW_EINVAL, "%s: n_layers must be in [1, %d]", name, kStepMaxLayers);
   if (n_steps < 1 || n_steps > kStepMaxSteps || (!head && n_steps != 1))
     return fw_fail(FW_EINVAL, "%s: n_steps must be in [1, %d] (1 without the LM head)", name, kStepMaxSteps);
   if (prompt && (!head || n_steps != 1)) return fw_fail(FW_EINVAL, "%s: the prompt pass is one step with the LM head", name);
-  if (vocab < 1 || max_pos < 1 || max_pos > kMaxCombineSplits * kSelfSplitKeys)
-    return fw_fail(FW_EINVAL, "%s: max_pos must be in [1, %d]", name, kMaxCombineSplits * kSelfSplitKeys);
-  if (enc_len < 1 || enc_len > kMaxCombineSplits * kCrossSplitKeys)
-    return fw_fail(FW_EINVAL, "%s: enc_len must be in [1, %d]", name, kMaxCombineSplits * kCrossSplitKeys);
+  if (const int st = step_range_check(name, n_layers, vocab, max_pos, enc_len)) return st;
   if (ws_bytes < static_cast<int64_t>(fw_decoder_step_workspace_bytes(n_layers)))
     return fw_fail(FW_EINVAL, "%s: workspace too small (%lld < %zu bytes)", name, static_cast<long long>(ws_bytes),
                    fw_decoder_step_workspace_bytes(n_layers));
@@ -1939,21 +1979,14 @@ static int decoder_step_launch(const char* name, const fw_dec_layer* layers, int
     d.self_k = static_cast<_Float16*>(s.self_k); d.self_v = static_cast<_Float16*>(s.self_v);
     d.cross_k = h(s.cross_k); d.cross_v = h(s.cross_v);
   }
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus < 2)
-    return fw_fail(FW_EHIP, "%s: cannot read the device's CU count", name);
-  const int grid = cus < kMaxGrid ? cus : kMaxGrid;
+  // the device-dependent checks last: every argument check above runs without a HIP call
+  int grid = 0, dev = 0;
+  if (const int st = step_sizes_check(name, n_layers, vocab, max_pos, enc_len, head != nullptr, prompt ? kPromptLen : 1,
+                                      &grid))
+    return st;
+  if (hipGetDevice(&dev) != hipSuccess) return fw_fail(FW_EHIP, "%s: no device", name);
   if (head) {
     const fw_dec_head& hd = *head;
-    // the largest share: a block of weight kLmWeight next to min(80, 5 G / 16) late blocks
-    const int n_late = grid * 5 / 16 < kVecWorkers ? (grid * 5 / 16 > 1 ? grid * 5 / 16 : 1) : kVecWorkers;
-    int most = 0;
-    for (int b = 0; b < grid; ++b)
-      most = std::max(most, lm_rows_before(b + 1, vocab, grid, 0, n_late) - lm_rows_before(b, vocab, grid, 0, n_late));
-    if (most + 1 > kLmMaxBatches * kLmBatchRows)  // + 1: the rounding of another placement of the late run
-      return fw_fail(FW_EINVAL, "%s: vocab %d gives a block %d rows of the LM head (at most %d) on %d blocks", name,
-                     vocab, most, kLmMaxBatches * kLmBatchRows, grid);
     a.has_head = 1;
     a.head = StepHead{static_cast<const _Float16*>(hd.ln_gamma), static_cast<const _Float16*>(hd.ln_beta), hd.ln_eps,
                       static_cast<const _Float16*>(hd.w), static_cast<const int8_t*>(hd.wq),

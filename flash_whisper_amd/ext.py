@@ -298,6 +298,12 @@ class WhisperExt:
             self._call('fw_attn_out_gemv_batch', *args, nv, _stream())
 
     # ---- the decoder layers of one token in one launch --------------------------------------
+    def decoder_step_supported(self, n_layers, vocab, max_pos, enc_len, prompt=False):
+        """(True, '') if the one-launch step (or, with `prompt`, the one-launch prompt pass) can run these
+        sizes on the current device, else (False, the reason) (fw_decoder_step_check)."""
+        st = self.lib.fw_decoder_step_check(int(n_layers), int(vocab), int(max_pos), int(enc_len), int(bool(prompt)))
+        return (True, '') if st == _lib.FW_OK else (False, self.lib.fw_last_error().decode(errors='replace'))
+
     def decoder_step_workspace(self, n_layers):
         """Zero-filled workspace of fw_decoder_step_layers for n_layers (one per decoding stream)."""
         nbytes = self.lib.fw_decoder_step_workspace_bytes(int(n_layers))
@@ -333,9 +339,24 @@ class WhisperExt:
                 setattr(table[i], n, t.data_ptr())
             _require(lay['self_k'].shape == lay['self_v'].shape and lay['cross_k'].shape == lay['cross_v'].shape,
                      f'layer {i}: K and V shapes differ')
+            _require(lay['self_k'].shape == layers[0]['self_k'].shape
+                     and lay['cross_k'].shape == layers[0]['cross_k'].shape, f'layer {i}: cache shapes differ')
             for j in (1, 2, 3):
                 setattr(table[i], f'ln{j}_eps', float(lay[f'ln{j}_eps']))
+        # the cache lengths, checked against max_pos / enc_len by every launch that takes the table
+        table.self_len, table.cross_len = layers[0]['self_k'].size(1), layers[0]['cross_k'].size(1)
         return table
+
+    @staticmethod
+    def _check_table(table, max_pos, enc_len):
+        _require(int(max_pos) <= table.self_len, f'max_pos {max_pos} exceeds the self-attention cache ({table.self_len})')
+        _require(int(enc_len) == table.cross_len, f'enc_len {enc_len} differs from the cross K/V length ({table.cross_len})')
+
+    @staticmethod
+    def _check_head(head, vocab, embed, max_pos):
+        _require(int(vocab) == head.vocab, f"vocab {vocab} differs from the LM head's rows ({head.vocab})")
+        _require(embed.size(0) >= int(vocab), f'the embedding has {embed.size(0)} rows for a vocabulary of {vocab}')
+        _require(head.tokens_len >= int(max_pos), f'the token list holds {head.tokens_len} ids, fewer than max_pos')
 
     def decoder_step_layers(self, table, cur, state, embed, pos_embed, max_pos, enc_len, scale, h_out, x_out, ws,
                             spin_limit=2_000_000):
@@ -348,6 +369,7 @@ class WhisperExt:
         _require(embed.dim() == 2 and embed.size(1) == HIDDEN and pos_embed.dim() == 2 and pos_embed.size(1) == HIDDEN
                  and pos_embed.size(0) >= max_pos, 'embed / pos_embed must be [rows, 1280]')
         _require(h_out.numel() == HIDDEN and x_out.numel() == HIDDEN, 'h_out, x_out must be [1280]')
+        self._check_table(table, max_pos, enc_len)
         for t, n in ((cur, 'cur'), (state, 'state')):
             _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
         _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')
@@ -388,6 +410,8 @@ class WhisperExt:
         head = _lib.DecHead(gamma.data_ptr(), beta.data_ptr(), float(eps), w.data_ptr(), wq.data_ptr(), meta.data_ptr(),
                             suppress.data_ptr(), tokens.data_ptr(), _ptr(y_out),
                             host_tokens.address if host_tokens is not None else None)
+        # checked against every launch that takes the head
+        head.vocab, head.tokens_len = w.size(0), tokens.numel()
         self.set_eos(head, eos)
         return head
 
@@ -407,6 +431,9 @@ class WhisperExt:
         (tokens, state and cur advance after every step)."""
         check_half(embed, 'embed')
         check_half(pos_embed, 'pos_embed')
+        _require(pos_embed.size(0) >= int(max_pos), 'pos_embed has fewer rows than max_pos')
+        self._check_table(table, max_pos, enc_len)
+        self._check_head(head, vocab, embed, max_pos)
         for t, n in ((cur, 'cur'), (state, 'state')):
             _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
         _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')
@@ -420,6 +447,9 @@ class WhisperExt:
         token of 4 steps whose first 3 predictions are discarded."""
         check_half(embed, 'embed')
         check_half(pos_embed, 'pos_embed')
+        _require(pos_embed.size(0) >= int(max_pos), 'pos_embed has fewer rows than max_pos')
+        self._check_table(table, max_pos, enc_len)
+        self._check_head(head, vocab, embed, max_pos)
         for t, n in ((prompt, 'prompt'), (cur, 'cur'), (state, 'state')):
             _require(t.dtype == torch.int64 and t.is_cuda and t.is_contiguous(), f'{n} must be contiguous CUDA int64')
         _require(ws.dtype == torch.uint8 and ws.is_cuda and ws.is_contiguous(), 'workspace must be CUDA uint8')

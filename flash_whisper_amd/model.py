@@ -31,6 +31,10 @@ SYNTHETIC = 'synthetic'
 SELF_SPLIT, CROSS_SPLIT = 64, 256  # keys per split block of the decoder's self / cross attention (<= 8 splits)
 
 
+class StepFault(RuntimeError):
+    """A persistent decoder launch ended without a token it owed (a hand-off wait ran out)."""
+
+
 class CustomModel:
     @torch.inference_mode()
     def __init__(self, model_id=SYNTHETIC, cache_dir=None, *, seed=0, dims=TURBO, setup=None, selftest=True,
@@ -74,13 +78,23 @@ class CustomModel:
         self._specs = W.spec_map(dims)
         self._init_encoder()
         self._init_decoder()
+        # the one-launch step and prompt pass need every CU and enough of them; elsewhere the 34-launch
+        # step runs (same tokens)
+        ok, self.persistent_reason = self.ext.decoder_step_supported(d.dec_layers, d.vocab, d.max_pos, d.enc_len)
+        self.persistent_step = self.persistent_step and ok
+        ok_prompt, reason = self.ext.decoder_step_supported(d.dec_layers, d.vocab, d.max_pos, d.enc_len, prompt=True)
+        self.persistent_prompt = self.persistent_prompt and ok_prompt
+        self.persistent_reason = self.persistent_reason or reason
 
         self.mel_filters = torch.from_numpy(mel_filters()).to(dev)
         self._alloc_frontend_buffers()
 
-        self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
-        self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
         self.graph_one = self.graph_chunk = self.graph_prompt = self.graph_enc = None
+        self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
+        if selftest:
+            self.selftest['checks'] += self._selftest_step()
+            self.selftest['ok'] = all(c['ok'] for c in self.selftest['checks'])
+        self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
         self.prompt_graph_one_launch = False
         if capture:
             self.graph_one, self.graph_chunk, self.graph_prompt = self._capture()
@@ -387,11 +401,11 @@ class CustomModel:
         if self.record_events:
             ev[0].record()
         self._steps(n)
+        ev[1].record()
         if self.record_events:
-            ev[1].record()
             self.decode_events.append((ev[0], ev[1], n))
         while len(token_ids) < max_new and not (stop_at_eos and token_ids[-1] in self.eos):
-            token_ids.append(self._poll_host_token(len(token_ids)))
+            token_ids.append(self._poll_host_token(len(token_ids), done=ev[1]))
         return token_ids
 
     def _prompt_one_launch(self):
@@ -402,15 +416,22 @@ class CustomModel:
         """Whether the prompt pass ends in a one-launch step, which stores the first token into host memory."""
         return self._one_launch() and (not self.batch_prompt or self._prompt_one_launch())
 
-    def _poll_host_token(self, i, timeout_s=60.0):
-        """Token i of the one-launch decode, polled from coherent host memory (-1 until it is stored)."""
+    def _poll_host_token(self, i, done=None, timeout_s=60.0):
+        """Token i of the one-launch decode, polled from coherent host memory (-1 until it is stored).
+        ``done`` is an event recorded after the launch: once it has completed and the token is still
+        missing, the launch ended without storing it (a wait of the step ran out and the blocks drained),
+        and StepFault is raised at once instead of waiting for the timeout."""
         host, deadline = self.stream_host.array, time.perf_counter() + timeout_s
+        n = 0
         while True:
             v = int(host[i])
             if v >= 0:
                 return v
+            n += 1
+            if done is not None and n % 256 == 0 and done.query() and int(host[i]) < 0:
+                raise StepFault(f'decoder step: the launch ended without token {i}')
             if time.perf_counter() > deadline:
-                raise RuntimeError(f'decoder step: token {i} did not arrive from the device in {timeout_s:.0f} s')
+                raise StepFault(f'decoder step: token {i} did not arrive from the device in {timeout_s:.0f} s')
 
     def _steps(self, n):
         """n decoder tokens (custom/model.py:107-123, n times): one persistent launch for all of them when
@@ -582,10 +603,104 @@ class CustomModel:
                 self._step(lm_head)
 
     # ---- per-clip ------------------------------------------------------------------------------
+    def _selftest_step(self, seed=7):
+        """Gate checks of the persistent decoder kernels on this model's own weights: three decoder steps
+        as one launch (decoder_step_kernel<1>) against three 34-launch steps, and the 4-token prompt
+        pass as one launch (decoder_step_kernel<4>) against the batched launches, from a seeded cache
+        at a seeded position over a seeded stand-in encoder output: K/V cache, tokens, state and
+        current token bit for bit, and the workspace's error word clear (custom/selftest.py's gate runs
+        the kernels the decode uses; these are the decode's). Afterwards the caches and state are
+        cleared as construction leaves them."""
+        checks = []
+        if not (self.persistent_step and self._one_launch()):
+            return checks
+        g = torch.Generator(device='cuda').manual_seed(seed)
+        self.cross_kv.copy_(torch.randn(self.cross_kv.shape, generator=g, device='cuda'))
+        kv0 = torch.randn(self.self_kv.shape, generator=g, device='cuda').half()
+        pos, cur = 100, 1000 % self.dims.vocab
+
+        def start():
+            self.self_kv.copy_(kv0)
+            self.state.copy_(torch.tensor([pos, 0], device='cuda'))
+            self.cur.fill_(cur)
+            self.tokens.zero_()
+            self.best.zero_()
+
+        def outputs():
+            return [t.clone() for t in (self.self_kv, self.tokens, self.state, self.cur)]
+
+        def same(a, b):
+            return all(torch.equal(x, y) for x, y in zip(a, b))
+
+        try:
+            start()
+            self._steps(3)  # one launch
+            one = outputs()
+            self.persistent_step = False
+            start()
+            for _ in range(3):
+                self._step()
+            chain = outputs()
+            self.persistent_step = True
+            ok = same(one, chain) and self.ext.decoder_step_error(self.step_ws) == 0
+            checks.append({'name': 'decoder_step_one_launch_vs_launches', 'max_err': 0.0 if ok else 1.0, 'ok': ok})
+            if self.batch_prompt and len(self.prompt) == 4:
+                res = []
+                for one_launch in (True, False):
+                    self.persistent_prompt = one_launch
+                    start()
+                    self._enqueue_prompt(reset_state=False)
+                    res.append(outputs())
+                self.persistent_prompt = True
+                ok = same(*res) and self.ext.decoder_step_error(self.step_ws) == 0
+                checks.append({'name': 'decoder_prompt_one_launch_vs_launches', 'max_err': 0.0 if ok else 1.0,
+                               'ok': ok})
+        finally:
+            self.persistent_step = self.persistent_prompt = True
+            for t in (self.self_kv, self.cross_kv, self.state, self.cur, self.tokens, self.best):
+                t.zero_()
+            torch.cuda.synchronize()
+        return checks
+
     def _check_step_error(self):
-        if self.persistent_step and self.ext.decoder_step_error(self.step_ws):
+        if self._step_fault():
             raise RuntimeError('decoder step: a hand-off wait timed out (another kernel on the device, or '
                                'fewer resident blocks than CUs); the tokens of this call are not valid')
+
+    def _step_fault(self):
+        """Whether a persistent launch since the last call flagged a timed-out wait; reading clears the
+        word (synchronises)."""
+        return bool(self.persistent_step and self.ext.decoder_step_error(self.step_ws))
+
+    def _decode_fallback(self, max_new, stop_at_eos, start):
+        """The prompt and every token again on the 34-launch step, eagerly (no graphs), after a persistent
+        launch flagged a timed-out wait: its tokens are never returned. The reference falls back to eager
+        execution when its graph capture fails (custom/model.py:149-171,189-192); the encoder output is
+        still valid, and every cache row is rewritten before it is read. Returns (token_ids, ttft)."""
+        torch.cuda.synchronize()  # a flagged launch drains: every wait stops once the word is set
+        self.ext.decoder_step_error(self.step_ws)  # clears the word
+        saved = (self.persistent_step, self.graph_one, self.graph_chunk, self.graph_prompt)
+        self.persistent_step = False
+        self.graph_one = self.graph_chunk = self.graph_prompt = None
+        try:
+            self.state.zero_()
+            self._enqueue_prompt(reset_state=False)
+            self._publish(0, 1).synchronize()
+            token_ids = [int(self.tokens_host[0])]
+            ttft = time.perf_counter() - start
+            n0 = 1
+            while not ((stop_at_eos and token_ids[-1] in self.eos) or len(token_ids) >= max_new):
+                n = min(CHUNK, max_new - len(token_ids))
+                self._steps(n)
+                self._publish(n0, n).synchronize()
+                for token in self.tokens_host[n0:n0 + n].tolist():
+                    token_ids.append(token)
+                    if (stop_at_eos and token in self.eos) or len(token_ids) >= max_new:
+                        break
+                n0 += n
+        finally:
+            self.persistent_step, self.graph_one, self.graph_chunk, self.graph_prompt = saved
+        return token_ids, ttft
 
     def _check_audio(self, audio, max_new_tokens):
         """custom/model.py:175-178; returns the token budget."""
@@ -680,6 +795,34 @@ class CustomModel:
         self._enqueue_encoder()
         stage[2].record()
 
+        # A persistent launch whose hand-off wait ran out (another kernel on the device, or fewer resident
+        # blocks than CUs) flags it; its tokens are then discarded and the clip is decoded again on the
+        # 34-launch step (_decode_fallback), reported as decode_fallback.
+        self.chunk_events, self.decode_events = [], []
+        try:
+            token_ids, ttft = self._decode(max_new, stop_at_eos, start)
+            ttlt = time.perf_counter() - start
+            fault = self._step_fault()
+        except StepFault:
+            fault = True
+        if fault:
+            token_ids, ttft = self._decode_fallback(max_new, stop_at_eos, start)
+            ttlt = time.perf_counter() - start
+        mel_s = enqueue_s + stage[0].elapsed_time(stage[1]) * 1e-3
+        encoder_s = stage[1].elapsed_time(stage[2]) * 1e-3
+        decode_s = ttlt - mel_s - encoder_s  # from the end of the encoder on the GPU timeline
+        detok_start = time.perf_counter()
+        text = C.detokenize(self.tokenizer, token_ids)
+        return {
+            'text': text, 'token_ids': token_ids, 'ttft_s': ttft, 'ttlt_s': ttlt,
+            'e2e_s': time.perf_counter() - start, 'mel_s': mel_s, 'encoder_s': encoder_s,
+            'decode_s': decode_s, 'detok_s': time.perf_counter() - detok_start, 'n_tokens': len(token_ids),
+            'decode_fallback': fault,
+        }
+
+    def _decode(self, max_new, stop_at_eos, start):
+        """The prompt pass and the decode of transcribe, already enqueued up to the encoder; returns
+        (token_ids, ttft)."""
         # The reference replays a chunk, then reads its tokens before replaying the next
         # (custom/model.py:208-215). With the one-launch step the whole decode is one launch that
         # stops at EOS itself and stores each token into host memory as it goes (_decode_stream).
@@ -691,15 +834,14 @@ class CustomModel:
         if stream and self._prompt_to_host():  # the prompt pass stores the first token into host memory
             self.stream_host.array[:] = -1
             self._enqueue_prompt(reset_state=False)
-            token_ids = [self._poll_host_token(0)]
+            done = torch.cuda.Event()
+            done.record()
+            token_ids = [self._poll_host_token(0, done=done)]
         else:
             self._enqueue_prompt(reset_state=False)
             self._publish(0, 1).synchronize()
             token_ids = [int(self.tokens_host[0])]
         ttft = time.perf_counter() - start
-        mel_s = enqueue_s + stage[0].elapsed_time(stage[1]) * 1e-3
-        encoder_s = stage[1].elapsed_time(stage[2]) * 1e-3
-        self.chunk_events, self.decode_events = [], []
         n_chunks = 0 if stream else -(-(max_new - 1) // CHUNK)
         if stream:
             token_ids = self._decode_stream(token_ids, max_new, stop_at_eos)
@@ -716,13 +858,4 @@ class CustomModel:
                 token_ids.append(token)
                 if (stop_at_eos and token in self.eos) or len(token_ids) >= max_new:
                     break
-        ttlt = time.perf_counter() - start
-        decode_s = ttlt - mel_s - encoder_s  # from the end of the encoder on the GPU timeline
-        self._check_step_error()
-        detok_start = time.perf_counter()
-        text = C.detokenize(self.tokenizer, token_ids)
-        return {
-            'text': text, 'token_ids': token_ids, 'ttft_s': ttft, 'ttlt_s': ttlt,
-            'e2e_s': time.perf_counter() - start, 'mel_s': mel_s, 'encoder_s': encoder_s,
-            'decode_s': decode_s, 'detok_s': time.perf_counter() - detok_start, 'n_tokens': len(token_ids),
-        }
+        return token_ids, ttft

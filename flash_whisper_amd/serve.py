@@ -99,9 +99,17 @@ class Scheduler:
                 run = active[li]
                 if run.event.query() and self._advance(li, run):
                     lane = self.lanes[li]
+                    fallback = False
+                    if lane._step_fault():
+                        # a persistent launch of this lane (the model itself, when it is the only lane)
+                        # flagged a timed-out wait: its ids are not valid; transcribe decodes the clip
+                        # again, falling back to the 34-launch step if it must
+                        with torch.cuda.stream(self.streams[li]):
+                            res = lane.transcribe(clips[run.index], run.max_new, stop_at_eos)
+                        run.token_ids, fallback = res['token_ids'], True
                     results[run.index] = {'token_ids': run.token_ids, 'text': detokenize(lane.tokenizer, run.token_ids),
                                           'ttft_s': run.ttft, 'e2e_s': time.perf_counter() - t0,
-                                          'n_tokens': len(run.token_ids)}
+                                          'n_tokens': len(run.token_ids), 'decode_fallback': fallback}
                     del active[li]
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0

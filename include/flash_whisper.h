@@ -258,6 +258,13 @@ int fw_decoder_step(const fw_dec_layer* layers, int n_layers, const fw_dec_head*
                     int64_t* state, const void* embed, const void* pos_embed, int vocab, int max_pos, int enc_len,
                     float scale, void* workspace, int64_t ws_bytes, int64_t spin_limit, hipStream_t stream);
 
+/* Whether fw_decoder_step (prompt = 0) or fw_decoder_prompt (prompt = 1) can run these sizes on the
+ * current device: FW_OK, or FW_EINVAL with the reason in fw_last_error() (too few CUs for a phase's
+ * blocks, a vocabulary whose per-block LM-head share exceeds the kernel's candidate list, max_pos or
+ * enc_len out of range). The launches run the same checks; a caller probes with it to choose the
+ * 34-launch step instead. No counterpart in the reference (its step is separate launches). */
+int fw_decoder_step_check(int n_layers, int vocab, int max_pos, int enc_len, int prompt);
+
 /* Rows of the int8 LM-head table each block of fw_decoder_step keeps in LDS for the whole launch on the
  * current device (read from HBM once per launch; the rest of its share streams every step), or a
  * negative status. No counterpart in the reference (its LM head, whisper_kernels.cu:28-86, streams the

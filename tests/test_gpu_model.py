@@ -33,6 +33,10 @@ def clip():
 
 def test_selftest_and_encoder_graph(model):
     assert model.selftest['ok'], [c for c in model.selftest['checks'] if not c['ok']]
+    # the gate covers the kernels that decode every token: the one-launch step and prompt pass against
+    # the 34-launch forms on the model's weights
+    names = {c['name'] for c in model.selftest['checks']}
+    assert {'decoder_step_one_launch_vs_launches', 'decoder_prompt_one_launch_vs_launches'} <= names
     assert model.selftest['mel_max_abs_diff'] < 1e-4
     assert model.selftest['encoder_graph'] and model.selftest['encoder_graph_max_abs_diff'] == 0.0
 

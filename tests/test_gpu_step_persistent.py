@@ -179,6 +179,30 @@ def test_flagged_error_ends_waits_and_is_reported(model):
             assert torch.equal(ta, tb)
 
 
+@torch.inference_mode()
+def test_flagged_transcribe_falls_back_to_launch_chain(model):
+    """transcribe with the error word set before it starts: the persistent prompt pass and decode stop
+    waiting at once and their tokens are discarded; the clip is decoded again on the 34-launch step in
+    the same call, which gives the oracle fixture's 224 ids and reports decode_fallback; the word is
+    clear afterwards and the next call runs the persistent step again (custom/model.py:149-171,189-192
+    falls back to eager execution the same way when its graph capture fails)."""
+    import json
+
+    from conftest import GOLDEN
+    from flash_whisper_amd.audio import synthetic_clip
+
+    fx = json.loads((GOLDEN / 'e2e_turbo_seed0.json').read_text())
+    clip = synthetic_clip(0)
+    word = model.step_ws[8:12].view(torch.int32)
+    word.fill_(1)
+    res = model.transcribe(clip, max_new_tokens=fx['n_tokens'], stop_at_eos=False)
+    assert res['decode_fallback'] is True
+    assert res['token_ids'] == fx['ids']
+    assert int(word.item()) == 0 and model.persistent_step
+    res = model.transcribe(clip, max_new_tokens=fx['n_tokens'], stop_at_eos=False)
+    assert res['decode_fallback'] is False and res['token_ids'] == fx['ids']
+
+
 
 @torch.inference_mode()
 def test_streamed_decode_matches_chunked_decode(model):
