@@ -4,6 +4,7 @@
   python tests/golden/make_golden.py hf16    # transformers fp16 encoder, op by op
   python tests/golden/make_golden.py greedy  # transformers greedy loop with prompt / suppress / EOS
   python tests/golden/make_golden.py e2e     # oracle greedy ids on the full synthetic model
+  python tests/golden/make_golden.py varied  # the same with the decoder scaled (ids that vary)
 
 ``hf`` imports the installed third-party ``transformers`` (5.15.0 here; the reference pins 5.20.2 in
 requirements.lock:681) on the CPU, with random init and no download, to record:
@@ -28,6 +29,8 @@ the result.
 ``e2e`` runs the oracle (fp16 rounding points) on the seeded whisper-large-v3-turbo-shaped weights and
 the seeded 30 s clip and records the 224 greedy ids with their top-2 margins, plus checksums and row
 samples of the intermediate tensors (e2e_turbo_seed0.json / .npz).
+``varied`` does the same on those weights with the decoder scaled as tests/weights_varied.py defines
+(e2e_turbo_seed0_varied.json): the seed-0 ids repeat three ids, these vary from step to step.
 """
 
 import json
@@ -298,6 +301,32 @@ def make_e2e(seed=0, n_tokens=224):
     print('ids', res['ids'][:32], '... min margin', m.min(), 'n<2e-3', int((m < 2e-3).sum()))
 
 
+def make_varied(seed=0, n_tokens=224):
+    from flash_whisper_amd import audio as fw_audio
+    from flash_whisper_amd import weights
+    from flash_whisper_amd.config import DecodeSetup, TURBO
+    from oracle.pipeline import transcribe_ids
+
+    sys.path.insert(0, str(OUT.parent))
+    import weights_varied as V
+
+    t0 = time.time()
+    params = V.scaled_decoder(weights.host_params(TURBO, seed))
+    clip = fw_audio.synthetic_clip(seed)
+    setup = DecodeSetup()
+    res = transcribe_ids(params, TURBO, clip, setup.prompt, n_tokens, setup.suppress, setup.begin_suppress)
+    print(f'oracle e2e {time.time() - t0:.1f}s', flush=True)
+    ids = [int(i) for i in res['ids']]
+    meta = dict(seed=seed, n_tokens=n_tokens, ids=ids, margins=[float(m) for m in res['margins']],
+                distinct=len(set(ids)), embed_scale=V.EMBED_SCALE, proj_scale=V.PROJ_SCALE,
+                clip_sha256=fw_audio.sha256(clip), prompt=list(setup.prompt), suppress=list(setup.suppress),
+                begin_suppress=list(setup.begin_suppress),
+                note='oracle fp16 rounding points; seed-0 weights with the decoder scaled (tests/weights_varied.py)')
+    (OUT / V.FIXTURE_NAME).write_text(json.dumps(meta, indent=1) + '\n')
+    m = np.array(res['margins'])
+    print('distinct', len(set(ids)), 'min margin', m.min(), 'n<2e-3', int((m < 2e-3).sum()))
+
+
 if __name__ == '__main__':
     what = sys.argv[1] if len(sys.argv) > 1 else 'all'
     if what in ('hf', 'all'):
@@ -308,3 +337,5 @@ if __name__ == '__main__':
         make_greedy()
     if what in ('e2e', 'all'):
         make_e2e()
+    if what in ('varied', 'all'):
+        make_varied()
