@@ -1,32 +1,37 @@
 """Benchmark of the batch-1 Whisper-large-v3-turbo hot path on one MI355X.
 
 Workload (one "step"): a full ``CustomModel.transcribe`` of a seeded 30 s synthetic clip — HIP log-mel,
-32-layer MFMA encoder + cross K/V in a hipGraph, 4-token prompt, then 224 greedy tokens with the 8-step
-decoder hipGraph (fixed length, no EOS stop), with seeded random-init weights of the
+32-layer MFMA encoder + cross K/V in a hipGraph, then the 4-token prompt pass and the first token in one
+persistent launch, then the other 223 greedy tokens in one more (``decoder_step_kernel``, which streams
+each token to host memory; fixed length, no EOS stop) — with seeded random-init weights of the
 whisper-large-v3-turbo architecture. The reference's timing boundary is kept: the clock starts at an
-in-memory waveform and stops at the token-id list (reference custom/model.py:179-225).
+in-memory waveform and stops at the token-id list (reference custom/model.py:179-225). Each timed
+transcribe runs inside a roctx range (``bench:30s:rep<i>``; flash_whisper_amd.trace).
 
 Reported metric: decode-step us (median GPU time per decoder step: HIP events around the one launch
-that decodes every token after the first, divided by its steps, inside the timed transcribes), the rate of the step's algorithmic bytes (the per-step bytes of
-the path, fp16 LM head included: the decoder weights, cross K/V, self K/V rows and the tied embedding),
-the 30 s-clip E2E ms and TTFT.
+that decodes every token after the first, divided by its steps, inside the timed transcribes), the rate
+of the step's algorithmic bytes (the per-step bytes of the path, fp16 LM head included: the decoder
+weights, cross K/V, self K/V rows and the tied embedding), the 30 s-clip E2E ms and TTFT (median and p90).
 
-``roofline`` covers the dominant kernel, the persistent decoder step (``decoder_step_kernel``: per
-step the 4 decoder layers, final LN, int8 pre-pass LM head, argmax and finalize; one launch decodes
-every token after the first and streams them to host memory): ``achieved`` is the step's algorithmic
-bytes (fp16 LM head, as the unit is defined) over its time, HIP events around that launch on the
-stream it runs on, divided by its steps (``us_per_launch`` / ``steps_per_launch``); ``achieved_read`` counts the bytes the step must read with the int8 table
-instead. ``traffic`` is the kernel's calibrated PMC fetch + write bytes per launch from
-profiles/decoder_step_kernel_traffic.md. ``lm_head`` times the LM-head kernel alone (final LN +
-int8 pre-pass + exact fp16 candidates + argmax, h ~ N(0, 1)) over rotating copies of its table (more
-than the 256 MB MALL) in a hipGraph between HIP events on the graph's stream; with
-``--fp16-lm-head`` the step is not one launch and ``roofline`` is that LM-head kernel's.
+``roofline`` covers the dominant kernel, the persistent decoder step (per step the 4 decoder layers,
+final LN, int8 pre-pass LM head, argmax and finalize): ``achieved`` is the step's algorithmic bytes
+(fp16 LM head, as the unit is defined) over its time, HIP events around that launch on the stream it
+runs on, divided by its steps (``us_per_launch`` / ``steps_per_launch``); ``achieved_read`` counts the
+bytes the step must read with the int8 table instead. ``traffic`` is the kernel's calibrated PMC fetch +
+write bytes per step from profiles/decoder_step_kernel_traffic.md. ``lm_head`` times the 34-launch
+step's LM-head kernel alone (final LN + int8 pre-pass + exact fp16 candidates + argmax, h ~ N(0, 1))
+over rotating copies of its table (more than the 256 MB MALL) in a hipGraph between HIP events on the
+graph's stream; with ``--fp16-lm-head`` the step is not one launch and ``roofline`` is that kernel's.
 
-``configs`` times the path's per-config units standalone, each over rotating buffers of more than
-300 MB so every call streams from HBM: the log-mel front end, split-K self attention at L in
-{1, 64, 224, 448}, and cross attention over 1500 frames + LN/GELU MLP. ``cpu_baseline`` runs the CPU
-oracle end to end on this host (log-mel, encoder, cross K/V, 227 decoder steps) and reports its
-decoder step, TTFT and E2E.
+``clips`` holds the reference's clip-length rows: 5 s and 15 s seeded clips, 20 transcribes each with
+the token budget scaled to the clip (37 and 112), and the 30 s timed transcribes; E2E and TTFT median
+and p90. ``configs`` times the path's per-config units: standalone (each over rotating buffers of more
+than 300 MB so every call streams from HBM: the log-mel front end, the 34-launch step's split-K self
+attention at L in {1, 64, 224, 448}, and its cross attention over 1500 frames + LN/GELU MLP), and
+``in_kernel``: the same units as phases of the persistent step, from its profiling build. Every row
+names its code path. ``cpu_baseline`` times the reference's PyTorch path in fp32 on this host's cores
+(oracle.torch_cpu; 5 end-to-end transcribes and 50 reps per config unit) and runs the numpy oracle once
+end to end as the id check.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -188,6 +193,49 @@ def launch_floor_us(model, reps=200):
     return graph_time_us(lambda i: ext.add_layernorm(h, x, g, b, y, 1e-5), reps)
 
 
+def log(msg):
+    """A progress line on stderr (stdout carries only the JSON line)."""
+    print(f'bench: {msg}', file=sys.stderr, flush=True)
+
+
+def percentile(values, p):
+    """Linear interpolation between the order statistics, as the reference's report (reporting.py:31-38)."""
+    v = sorted(values)
+    pos = (len(v) - 1) * p
+    lo, hi = int(pos), min(int(pos) + 1, len(v) - 1)
+    return v[lo] + (v[hi] - v[lo]) * (pos - lo)
+
+
+def latency_row(results, seconds):
+    """E2E / TTFT median and p90 (ms) over `results` (transcribe dicts), audio seconds per second."""
+    e2e, ttft = [r['e2e_s'] * 1e3 for r in results], [r['ttft_s'] * 1e3 for r in results]
+    med = statistics.median(e2e)
+    return {'e2e_ms': round(med, 3), 'e2e_p90_ms': round(percentile(e2e, 0.9), 3),
+            'ttft_ms': round(statistics.median(ttft), 3), 'ttft_p90_ms': round(percentile(ttft, 0.9), 3),
+            'audio_s_per_s': round(seconds / (med * 1e-3), 1), 'reps': len(results),
+            'tokens': results[0]['n_tokens']}
+
+
+def clip_rows(model, reps, tokens_30s):
+    """The reference's 5 s and 15 s clip rows (runner.py:185-194: 20 reps per length, distinct audio per
+    rep): seeded synthetic clips of that length (the encoder still runs the zero-padded 30 s window), with
+    the 30 s token budget scaled to the clip (37 and 112 of 224: random-init weights never emit EOS)."""
+    from flash_whisper_amd.audio import synthetic_clip
+    from flash_whisper_amd.trace import trace_range
+
+    rows = {}
+    for seconds in (5, 15):
+        tokens = round(tokens_30s * seconds / 30)
+        clips = [synthetic_clip(200 + i, n_samples=seconds * 16000) for i in range(reps)]
+        model.transcribe(clips[0], max_new_tokens=tokens, stop_at_eos=False)  # warm-up at this length
+        res = []
+        for i, clip in enumerate(clips):
+            with trace_range(f'bench:{seconds}s:rep{i}'):
+                res.append(model.transcribe(clip, max_new_tokens=tokens, stop_at_eos=False))
+        rows[f'{seconds}s'] = latency_row(res, seconds)
+    return rows
+
+
 def _row(us, nbytes, launches, sample):
     gbps = nbytes / (us * 1e-6) / 1e9
     return {'us': round(us, 2), 'bytes': int(nbytes), 'gbps': round(gbps, 1), 'frac': round(gbps / HBM_PEAK_GBPS, 4),
@@ -222,6 +270,7 @@ def config_rows(model, reps):
                                                  ws), reps)
     rows['log_mel'] = _row(us, LOG_MEL_BYTES, 2, f'{n} distinct 30 s clips, {reps} calls per graph (per-clip '
                            'frames + finalize launches; the filterbank prepared once)')
+    rows['log_mel']['code_path'] = 'logmel_frames_kernel + logmel_finalize_kernel, as transcribe runs them'
     del waves, outs, ws
 
     # config 2: split-K self attention (split + combine, the reference op) over an fp16 K/V cache
@@ -239,6 +288,9 @@ def config_rows(model, reps):
                                                           pm, pl, pa, hd ** -0.5), reps)
         self_rows[f'L{length}'] = _row(us, 5120 * length + 15360, 2,
                                        f'{n} distinct [20, 448, 64] K/V caches, {reps} calls per graph')
+    self_rows['code_path'] = ('attn_split_kernel + attn_combine_kernel (decode_attention: the 34-launch step\'s '
+                              'kernels, the reference op\'s granularity); the product\'s in-kernel phase is '
+                              'in_kernel.self_attention')
     rows['self_attention'] = self_rows
     del caches
 
@@ -263,8 +315,54 @@ def config_rows(model, reps):
     us = graph_time_us(cross_mlp, reps)
     rows['cross_attention_mlp'] = _row(us, CROSS_MLP_BYTES, 4, f'{n} distinct K/V + MLP weight sets, {reps} calls '
                                        'per graph; the MLP residual is added by the next LayerNorm, as in the step')
+    rows['cross_attention_mlp']['code_path'] = ('decode_attention + ln_gemv(GELU) + gemv: the 34-launch step\'s '
+                                                'kernels; the product\'s phases are in_kernel.cross_attention_mlp')
     del sets
     torch.cuda.empty_cache()
+    return rows
+
+
+def in_kernel_rows(tokens, dims, timeout_s=600):
+    """Configs 2-4 as the product runs them: phases of the persistent decoder step, timed by its
+    profiling build (flash_whisper_amd.step_timeline: the 100 MHz wall clock stored by every block at
+    fixed points of each step; a child process on this GPU while this one is idle). Each row is the
+    phases' share of the step (from the previous phase's last output to this phase's last output,
+    hand-off included), median over the steps and the 4 layers, on the config's algorithmic bytes."""
+    import tempfile
+
+    root = os.path.dirname(os.path.abspath(__file__))
+    lib = os.path.join(root, 'flash_whisper_amd', 'libflash_whisper_timeline.so')
+    if not os.path.exists(lib):
+        return {'skipped': f'{lib} not built'}
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, 'phases.json')
+        env = dict(os.environ, FW_LIBRARY=lib)
+        proc = subprocess.run([sys.executable, '-m', 'flash_whisper_amd.step_timeline', '--tokens', str(tokens),
+                               '--json', path], cwd=root, env=env, capture_output=True, text=True, timeout=timeout_s)
+        if proc.returncode != 0:
+            return {'skipped': f'step_timeline exited with {proc.returncode}: {proc.stderr[-400:]}'}
+        with open(path) as f:
+            tl = json.load(f)
+    ph = tl['phases']
+    rows = {'code_path': 'decoder_step_kernel<1> phases (the product\'s decode), from its profiling build '
+                         '(libflash_whisper_timeline.so); medians over a 224-token decode and 8 steps from '
+                         'position 440, all 4 layers',
+            'step_period_us': tl['step_period_us']}
+    rows['self_attention'] = {
+        k: dict(_row(v['dur_us'], 5120 * int(k[1:]) + 15360, 0, f'{v["samples"]} layer-steps with L in '
+                     f'[{int(k[1:]) - 4}, {int(k[1:])}]'), block_work_us=v['work_us'])
+        for k, v in tl['self_attention_by_length'].items()}
+    cross = ph['cross attention']['dur_us'] + ph['LN3 + fc1 + GELU']['dur_us'] + ph['fc2']['dur_us']
+    rows['cross_attention_mlp'] = dict(
+        _row(cross, CROSS_MLP_BYTES, 0, 'cross attention + LN3/fc1/GELU + fc2 phases per layer (the cross-out '
+             'projection between them is its own phase, cross_out_us)'),
+        cross_attention_us=ph['cross attention']['dur_us'], cross_out_us=ph['cross-out']['dur_us'],
+        fc1_us=ph['LN3 + fc1 + GELU']['dur_us'], fc2_us=ph['fc2']['dur_us'])
+    rows['lm_head'] = _row(tl['lm_head_us'], lm_head_unit_bytes(dims), 0, 'final LN + int8 pre-pass + exact fp16 '
+                           'candidates + argmax + finalize, from the last fc2 output to the token stored')
+    read = lm_head_bytes(dims, True)  # what the phase reads: the int8 table, its scales and bounds
+    rows['lm_head'].update(bytes_read=read, frac_read=round(read / (tl['lm_head_us'] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4))
+    rows['phases'] = ph
     return rows
 
 
@@ -308,11 +406,15 @@ def _blas_threads():
     return 'unknown', os.cpu_count()
 
 
-def cpu_baseline(model, tokens, gpu_ids):
-    """The CPU oracle end to end on this host, on the benchmark clip and the same seeded weights: log-mel,
-    fp16-rounded encoder, cross K/V, the 4 prompt steps (TTFT at the first token), then the remaining
-    decoder steps (fp32 numpy with the reference's fp16 rounding points). `value` is the median decoder
-    step; the ids are compared with the GPU's."""
+def cpu_baseline(model, tokens, gpu_ids, reps, config_reps):
+    """Two CPU legs on this host, on the benchmark clip and the same seeded weights.
+
+    - The reference's PyTorch path in fp32 (oracle.torch_cpu: transformers Whisper, torch.stft log-mel,
+      greedy loop over the HF KV cache; custom/pytorch_model.py:29-89): `reps` end-to-end transcribes of
+      `tokens` tokens and the per-config units over `config_reps` each. `value` is its median decoder step
+      (each token's forward + argmax, pooled over the reps).
+    - The numpy oracle once end to end (log-mel, fp16-rounded encoder, cross K/V, every decoder step in
+      fp32 with the reference's fp16 rounding points): its ids are checked against the GPU's bit for bit."""
     from concurrent.futures import ThreadPoolExecutor
 
     import numpy as np
@@ -323,6 +425,7 @@ def cpu_baseline(model, tokens, gpu_ids):
     from oracle.encoder import cross_kv, encoder_forward
     from oracle.logmel import log_mel
     from oracle.pipeline import pad_wave
+    from oracle.torch_cpu import baseline
 
     d, setup = model.dims, model.setup
     specs = weights.param_specs(d)
@@ -330,6 +433,7 @@ def cpu_baseline(model, tokens, gpu_ids):
         arrays = list(pool.map(lambda s: weights.host_param(*s, seed=model.seed), specs))
     params = {s[0]: a for s, a in zip(specs, arrays)}
     del arrays
+    log('cpu baseline: host parameters generated')
     clip = synthetic_clip(0)
     base, first = suppress_masks(d.vocab, setup.suppress, setup.begin_suppress)
     step_s = []
@@ -357,15 +461,32 @@ def cpu_baseline(model, tokens, gpu_ids):
         pos += 1
         ids.append(masked_argmax(logits, base))
     t_end = time.perf_counter()
+    del dec, enc, ckv
     lib, threads = _blas_threads()
     ms = lambda a, b: round((b - a) * 1e3, 1)
-    return dict(value=round(statistics.median(step_s) * 1e6, 1), unit='us/decode-step', cores=threads, kind='port',
-                sample=f'one end-to-end run of the numpy oracle on the benchmark clip: log-mel, 32 fp16-rounded '
-                       f'encoder layers, cross K/V, {len(step_s)} decoder steps (fp32 math with the reference\'s '
-                       f'fp16 rounding points); value = median decoder step',
-                e2e_ms=ms(t0, t_end), ttft_ms=ms(t0, t_first), mel_ms=ms(t0, t_mel), encoder_ms=ms(t_mel, t_enc),
-                decode_ms=ms(t_enc, t_end), ids_match_gpu=ids == list(gpu_ids), blas=lib, blas_threads=threads,
-                nproc=os.cpu_count(), host=_host_description())
+    oracle = dict(kind='numpy oracle, fp32 math with the reference\'s fp16 rounding points', runs=1,
+                  step_us=round(statistics.median(step_s) * 1e6, 1), e2e_ms=ms(t0, t_end), ttft_ms=ms(t0, t_first),
+                  mel_ms=ms(t0, t_mel), encoder_ms=ms(t_mel, t_enc), decode_ms=ms(t_enc, t_end),
+                  ids_match_gpu=ids == list(gpu_ids), blas=lib, blas_threads=threads)
+
+    log(f'cpu baseline: numpy oracle done ({oracle["e2e_ms"] / 1e3:.1f} s end to end)')
+    torch_cpu = baseline(params, d, setup, clip, tokens, reps=reps, config_reps=config_reps,
+                         progress=lambda m: log(f'cpu baseline: {m}'))
+    log('cpu baseline: fp32 PyTorch path done')
+    cpu_ids = torch_cpu.pop('token_ids')
+    first_diff = next((i for i, (a, b) in enumerate(zip(cpu_ids, gpu_ids)) if a != b), None)
+    import torch
+
+    return dict(value=torch_cpu['step_us'], unit='us/decode-step', cores=torch_cpu['threads'], kind='port',
+                sample=f'the reference\'s PyTorch path (transformers Whisper + greedy loop over the HF KV cache) '
+                       f'in fp32 on {torch_cpu["threads"]} host threads: {reps} end-to-end transcribes of the '
+                       f'benchmark clip ({tokens} tokens each, after an 8-token warm-up), value = median decoder '
+                       f'step pooled over them; configs = the per-config units, median of {config_reps} each',
+                precision='fp32', e2e_ms=torch_cpu['e2e_ms'], e2e_p90_ms=torch_cpu['e2e_p90_ms'],
+                ttft_ms=torch_cpu['ttft_ms'], mel_ms=torch_cpu['mel_ms'], encoder_ms=torch_cpu['encoder_ms'],
+                decode_ms=torch_cpu['decode_ms'], reps=reps, configs=torch_cpu['configs'],
+                fp32_ids_first_difference_from_gpu=first_diff, torch_threads=torch_cpu['threads'],
+                torch=torch.__version__, nproc=os.cpu_count(), host=_host_description(), oracle=oracle)
 
 
 def main():
@@ -375,7 +496,10 @@ def main():
     ap.add_argument('--warmup', type=int, default=2)
     ap.add_argument('--tokens', type=int, default=224)
     ap.add_argument('--kernel-reps', type=int, default=100)
+    ap.add_argument('--clip-reps', type=int, default=20, help='transcribes per 5 s and 15 s clip row (0: skip)')
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--cpu-reps', type=int, default=5, help='end-to-end transcribes of the fp32 PyTorch CPU baseline')
+    ap.add_argument('--cpu-config-reps', type=int, default=50, help='reps per config unit of the CPU baseline')
     ap.add_argument('--no-configs', action='store_true', help='skip the per-config rows')
     ap.add_argument('--lanes', type=int, default=4, help='clips in flight for the serving-throughput extra (0: skip)')
     ap.add_argument('--fp16-lm-head', action='store_true',
@@ -396,6 +520,7 @@ def main():
     from flash_whisper_amd.audio import synthetic_clip
     from flash_whisper_amd.config import CHUNK
     from flash_whisper_amd.model import CustomModel
+    from flash_whisper_amd.trace import trace_range
 
     model = CustomModel(seed=0, lm_q8=not args.fp16_lm_head)
     reason = selftest_gate(model.selftest)
@@ -415,16 +540,18 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({'decode_replays': args.decode_replays, 'steps_per_replay': CHUNK}), flush=True)
         return
-    for _ in range(args.warmup):
-        model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)
+    for i in range(args.warmup):
+        with trace_range(f'bench:warmup:rep{i}'):
+            model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)
 
     model.record_events = True
     rows, step_us = [], []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     launch_us, launch_steps = [], 0
-    for _ in range(args.steps):
-        res = model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)
+    for i in range(args.steps):
+        with trace_range(f'bench:30s:rep{i}'):
+            res = model.transcribe(clip, max_new_tokens=args.tokens, stop_at_eos=False)
         rows.append(res)
         if model.decode_events:  # the whole decode as one launch
             (a, b, n), = model.decode_events
@@ -438,12 +565,25 @@ def main():
     elapsed = time.perf_counter() - t0
     model.record_events = False
 
+    log(f'{args.steps} timed 30 s transcribes done')
     q8 = model.use_lm_q8
-    lm_us = time_lm_head(model, args.kernel_reps, q8)
-    lm16_us = time_lm_head(model, args.kernel_reps, False) if q8 else lm_us
-    floor_us = launch_floor_us(model)
-    configs = None if args.no_configs else config_rows(model, args.kernel_reps)
-    serve = serving_throughput(model, args.lanes, 2 * args.lanes, args.tokens) if args.lanes > 1 else None
+    clips = clip_rows(model, args.clip_reps, args.tokens) if args.clip_reps > 0 else {}
+    clips['30s'] = latency_row(rows, 30)
+    log('5 s and 15 s clip rows done')
+    with trace_range('bench:lm_head'):
+        lm_us = time_lm_head(model, args.kernel_reps, q8)
+        lm16_us = time_lm_head(model, args.kernel_reps, False) if q8 else lm_us
+    with trace_range('bench:launch_floor'):
+        floor_us = launch_floor_us(model)
+    with trace_range('bench:configs'):
+        configs = None if args.no_configs else config_rows(model, args.kernel_reps)
+    if configs is not None:
+        log('standalone config rows done')
+        configs['in_kernel'] = in_kernel_rows(args.tokens, model.dims)
+        log('in-kernel phase rows done')
+    log('LM-head, launch-floor and config rows done')
+    with trace_range('bench:serving'):
+        serve = serving_throughput(model, args.lanes, 2 * args.lanes, args.tokens) if args.lanes > 1 else None
     if args.copy_calibration:
         src = torch.empty(128 << 20, dtype=torch.float16, device='cuda')
         dst = torch.empty_like(src)
@@ -480,7 +620,9 @@ def main():
         'decode_step_roofline_frac': round(step_gbps / HBM_PEAK_GBPS, 4),
         'decode_step_bytes_read': int(read_bytes),
         'decode_launch_floor_us': round(floor_us, 2),
-        'e2e_ms': round(med('e2e_s'), 3), 'ttft_ms': round(med('ttft_s'), 3), 'mel_ms': round(med('mel_s'), 3),
+        'e2e_ms': round(med('e2e_s'), 3), 'ttft_ms': round(med('ttft_s'), 3),
+        'e2e_p90_ms': clips['30s']['e2e_p90_ms'], 'ttft_p90_ms': clips['30s']['ttft_p90_ms'],
+        'mel_ms': round(med('mel_s'), 3),
         'encoder_ms': round(med('encoder_s'), 3), 'decode_ms': round(med('decode_s'), 3),
         'encoder_tflops': round(enc_tflops, 1), 'encoder_mfma_frac': round(enc_tflops / MFMA_FP16_PEAK_TFLOPS, 4),
         'n_tokens': rows[-1]['n_tokens'],
@@ -512,12 +654,15 @@ def main():
         out['lm_head'] = lm_head
     else:
         out['roofline'] = lm_head
+    out['clips'] = clips
     if configs is not None:
         out['configs'] = configs
     if serve is not None:
         out['serving'] = serve
     if not args.no_cpu_baseline:
-        out['cpu_baseline'] = cpu_baseline(model, args.tokens, rows[-1]['token_ids'])
+        with trace_range('bench:cpu_baseline'):
+            out['cpu_baseline'] = cpu_baseline(model, args.tokens, rows[-1]['token_ids'], args.cpu_reps,
+                                               args.cpu_config_reps)
     print(json.dumps(out), flush=True)
 
 

@@ -26,6 +26,7 @@ from .audio import mel_filters
 from .config import CHUNK, N_SAMPLES, SAMPLE_RATE, SPLIT_KEYS, TURBO, DecodeSetup
 from .ext import MAX_BATCH, load_ext
 from .selftest import run_selftest, workspace
+from .trace import trace_range
 
 SYNTHETIC = 'synthetic'
 SELF_SPLIT, CROSS_SPLIT = 64, 256  # keys per split block of the decoder's self / cross attention (<= 8 splits)
@@ -90,11 +91,12 @@ class CustomModel:
         self._alloc_frontend_buffers()
 
         self.graph_one = self.graph_chunk = self.graph_prompt = self.graph_enc = None
-        self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
-        if selftest:
-            self.selftest['checks'] += self._selftest_step()
-            self.selftest['ok'] = all(c['ok'] for c in self.selftest['checks'])
-        self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
+        with trace_range('selftest'):
+            self.selftest = run_selftest(self.ext) if selftest else {'ok': None, 'checks': []}
+            if selftest:
+                self.selftest['checks'] += self._selftest_step()
+                self.selftest['ok'] = all(c['ok'] for c in self.selftest['checks'])
+            self.selftest['mel_max_abs_diff'] = self._mel_diff() if selftest else None
         self.prompt_graph_one_launch = False
         if capture:
             self.graph_one, self.graph_chunk, self.graph_prompt = self._capture()
@@ -780,6 +782,10 @@ class CustomModel:
         for the synthetic benchmark (224 tokens, no EOS stop); the defaults are the reference's."""
         max_new = self._check_audio(audio, max_new_tokens)
         torch.cuda.synchronize()
+        with trace_range('transcribe'):  # every kernel of this clip, and no other, runs inside the range
+            return self._transcribe(audio, max_new, stop_at_eos)
+
+    def _transcribe(self, audio, max_new, stop_at_eos):
         start = time.perf_counter()
 
         # The stages are enqueued back to back and timed with HIP events: the reference synchronises

@@ -151,11 +151,36 @@ def report(rows, n_layers, title):
     return '\n'.join(lines)
 
 
+def summary(rows, rows2, n_layers, pos0, from_pos):
+    """Machine-readable medians: per phase over the decode's steps and layers (``dur``: its share of the
+    step, ``work``: the median block's input-to-stores time), layer-by-layer self attention at cache
+    lengths L in {64, 224, 448} (the 5 steps ending at L, all layers), the LM head (from the last fc2's
+    output to the token stored) and the step period."""
+    layers = range(min(n_layers, TL_LAYERS))
+    med = lambda v: round(statistics.median(v), 3) if v else None
+    phases = {}
+    for p in range(1, 9):
+        hits = [r[(l, p)] for r in rows for l in layers if (l, p) in r]
+        phases[PHASES[p - 1]] = {'dur_us': med([h['dur'] for h in hits]), 'work_us': med([h['work'] for h in hits])}
+    steps = [(pos0 + i + 1, r) for i, r in enumerate(rows)] + [(from_pos + i + 1, r) for i, r in enumerate(rows2)]
+    by_len = {}
+    for length in (64, 224, 448):
+        hits = [r[(l, 2)] for L, r in steps if length - 4 <= L <= length for l in layers if (l, 2) in r]
+        by_len[f'L{length}'] = {'dur_us': med([h['dur'] for h in hits]), 'work_us': med([h['work'] for h in hits]),
+                                'samples': len(hits)}
+    last = (len(layers) - 1, 8)
+    stored = len(LM_POINTS) - 1
+    lm = [r[('lm', stored)]['last'] - r[last]['out'] for r in rows if ('lm', stored) in r and last in r]
+    return {'phases': phases, 'self_attention_by_length': by_len, 'lm_head_us': med(lm),
+            'step_period_us': med([r['period'] for r in rows if 'period' in r]), 'steps': len(rows)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--tokens', type=int, default=224)
     ap.add_argument('--from-pos', type=int, default=440, help='start of the extra run (self attention over long caches)')
     ap.add_argument('--steps', type=int, default=8, help='steps of the extra run (0: none)')
+    ap.add_argument('--json', help='also write the medians of summary() to this file')
     args = ap.parse_args()
     if not os.environ.get('FW_LIBRARY'):
         print('set FW_LIBRARY=flash_whisper_amd/libflash_whisper_timeline.so (the profiling build)', file=sys.stderr)
@@ -185,6 +210,7 @@ def main():
     sa = [(pos0 + i + 1, r[(0, 2)]['dur'], r[(0, 2)]['in_med'] - r[(0, 1)]['out']) for i, r in enumerate(rows)
           if (0, 2) in r and (0, 1) in r]
     pick = [x for x in sa if x[0] in (64, 128, 224)]
+    rows2 = []
     if args.steps > 0:
         def setup():
             with torch.inference_mode():
@@ -201,6 +227,14 @@ def main():
     print('| L | dur (us) | wait (us) |', '|---:|---:|---:|', sep='\n')
     for L, dur, wait in pick:
         print(f'| {L} | {dur:.2f} | {wait:.2f} |')
+    if args.json:
+        import json
+
+        out = summary(rows[1:], rows2, n_layers, pos0 + 1, args.from_pos)
+        out.update(device=torch.cuda.get_device_name(0), grid=int(tl.shape[1]),
+                   resident_rows=int(model.ext.lib.fw_decoder_step_resident_rows()), tokens=args.tokens)
+        with open(args.json, 'w') as f:
+            json.dump(out, f)
 
 
 if __name__ == '__main__':

@@ -16,6 +16,10 @@ Modules and what pins each function (checks live in tests/test_oracle_*.py):
 - ``encoder``: HF WhisperEncoder in fp16 semantics (transformers modeling_whisper.py:379-414, 592-648)
   and the cross K/V projection (custom/model.py:143-147). Pinned by the same transformers tiny-config
   golden vectors (fp32) and by conv1d/attention closed forms.
+- ``torch_cpu``: the reference's PyTorch path (custom/pytorch_model.py:29-89: transformers Whisper, the
+  feature extractor's torch log-mel, greedy loop over the HF KV cache) in fp32 on the host CPU, the
+  timed CPU baseline of bench.py. Its loop is pinned by transformers' own greedy ids on a tiny model
+  (tests/test_torch_cpu_baseline.py); it is a timing baseline, not the id check.
 - ``pipeline``: waveform -> log-mel -> encoder -> cross K/V -> greedy ids (custom/model.py:173-225).
   Its parts are pinned as above; the fp16 rounding points themselves (which only matter at the ulp
   level) are the reference's, checked by construction against whisper_kernels.cu and HF's fp16 casts.

@@ -33,3 +33,23 @@ def test_selftest_gate():
                                    {'name': 'kv_write_1', 'max_err': 0.0, 'ok': True}]}
     assert bench.selftest_gate(bad) == "selftest failed: ['add_layernorm']"
     assert bench.selftest_gate({'ok': None, 'checks': []}) == 'selftest did not run'
+
+
+def test_percentile_is_linear_interpolation():
+    import numpy as np
+
+    rng = np.random.default_rng(3)
+    for n in (1, 2, 5, 20, 21):
+        v = list(rng.standard_normal(n))
+        for p in (0.0, 0.5, 0.9, 1.0):
+            assert bench.percentile(v, p) == pytest.approx(float(np.percentile(v, 100 * p)), abs=1e-12)
+    # the reference's report: 20 reps 1..20 give p90 = 18.1
+    assert bench.percentile(list(range(20, 0, -1)), 0.9) == pytest.approx(18.1)
+
+
+def test_latency_row():
+    rows = [{'e2e_s': (10 + i) * 1e-3, 'ttft_s': 4e-3 + i * 1e-4, 'n_tokens': 37} for i in range(11)]
+    r = bench.latency_row(rows, 5)
+    assert r['e2e_ms'] == 15.0 and r['e2e_p90_ms'] == 19.0 and r['reps'] == 11 and r['tokens'] == 37
+    assert r['ttft_ms'] == pytest.approx(4.5) and r['ttft_p90_ms'] == pytest.approx(4.9)
+    assert r['audio_s_per_s'] == round(5 / 15e-3, 1)
