@@ -88,16 +88,75 @@ def build(verbose=False, jobs=None):
     return LIB
 
 
-def resource_usage():
-    """Per-kernel VGPR/SGPR/LDS/spill report from the compiler, for every source."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    lines = []
+RESOURCE_FIELDS = (('VGPRs', 'VGPRs'), ('AGPRs', 'AGPRs'), ('TotalSGPRs', 'SGPRs'),
+                   ('ScratchSize [bytes/lane]', 'scratch B/lane'), ('Occupancy [waves/SIMD]', 'waves/SIMD'),
+                   ('LDS Size [bytes/block]', 'static LDS B/block'), ('VGPRs Spill', 'VGPR spill'),
+                   ('SGPRs Spill', 'SGPR spill'))
+
+
+def _plain_name(sym):
+    """name<int args> of an Itanium-mangled nested name that c++filt left as it was (it does not know
+    the _Float16 parameter code DF16_)."""
+    import re
+
+    if not sym.startswith('_ZN'):
+        return sym
+    i, parts = 3, []
+    while i < len(sym) and sym[i].isdigit():
+        j = i
+        while sym[j].isdigit():
+            j += 1
+        n = int(sym[i:j])
+        parts.append(sym[j:j + n])
+        i = j + n
+    if not parts:
+        return sym
+    name = parts[-1]
+    if sym[i:i + 1] == 'I':
+        args = re.findall(r'L([ib])(\d+)E', sym[i:sym.find('EE', i) + 2])
+        name += '<' + ', '.join(('true' if v == '1' else 'false') if k == 'b' else v for k, v in args) + '>'
+    return name
+
+
+def _demangle(names):
+    tool = shutil.which('c++filt')
+    if not tool or not names:
+        return names
+    out = subprocess.run([tool], input='\n'.join(names), capture_output=True, text=True).stdout.splitlines()
+    return out if len(out) == len(names) else names
+
+
+def resource_usage(variants=(('', ()), (' (profiling build)', ('-DFW_STEP_TIMELINE=1',)))):
+    """Per-kernel VGPR/AGPR/SGPR/scratch/occupancy/LDS/spill report from the compiler
+    (-Rpass-analysis=kernel-resource-usage) for every source as the library builds it, as markdown.
+    The decoder step's dynamic LDS (the resident LM-head rows) is sized at launch and not counted."""
+    rows = []
     for src in sources():
-        cmd = [HIPCC, *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), '--cuda-device-only',
-               '-Rpass-analysis=kernel-resource-usage', '-c', str(src), '-o', os.devnull]
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        lines += [line for line in proc.stderr.splitlines() if 'remark' in line]
-    return lines
+        for tag, extra in variants:
+            if extra and src.stem != 'decode_step':
+                continue
+            cmd = [HIPCC, *COMMON_FLAGS, *PER_FILE_FLAGS.get(src.name, []), *extra, '--cuda-device-only',
+                   '-Rpass-analysis=kernel-resource-usage', '-c', str(src), '-o', os.devnull]
+            proc = subprocess.run(cmd, capture_output=True, text=True)
+            cur = None
+            for line in proc.stderr.splitlines():
+                if 'remark:' not in line:
+                    continue
+                body = line.split('remark:', 1)[1].split('[-Rpass', 1)[0].strip()
+                key, _, val = body.partition(':')
+                if key == 'Function Name':
+                    cur = {'file': src.name + tag, 'name': val.strip()}
+                    rows.append(cur)
+                elif cur is not None:
+                    cur[key.strip()] = val.strip()
+    names = _demangle([r['name'] for r in rows])
+    out = ['| Source | Kernel | ' + ' | '.join(h for _, h in RESOURCE_FIELDS) + ' |',
+           '|---|---|' + '---:|' * len(RESOURCE_FIELDS)]
+    for r, name in zip(rows, names):
+        short = _plain_name(name) if name.startswith('_Z') else \
+            name.replace('fw::(anonymous namespace)::', '').split('(')[0].removeprefix('void ')
+        out.append(f'| {r["file"]} | `{short}` | ' + ' | '.join(r.get(k, '') for k, _ in RESOURCE_FIELDS) + ' |')
+    return out
 
 
 def main():
