@@ -126,11 +126,16 @@ __device__ __forceinline__ void ll_store(uint64_t* p, unsigned tag, unsigned v) 
 }
 
 // Payloads of the words buf[idx[k]] (idx[k] < 0: not wanted) once each carries the launch's tag. All
-// words are requested at once and only the missing ones again. With kPlain the first read goes through
-// the L2 (blocks of one XCD that read the same words then share one fetch); a word that comes back
-// stale (an old tag: the L2 may hold a line from before its last write) is polled again with
-// agent-scope loads, which always reach the coherent copy. Bounded: a wait that outlives the time
-// limit, or that sees another block's error flag, stops and returns what it read.
+// words are requested at once and only the missing ones again, FW_LL_SLEEP x 64 clocks after the last
+// poll came back (a longer sleep, and two polls of a word in flight at once, each measured slower). With
+// kPlain the first read goes through the L2 (blocks of one XCD that read the same words then share one
+// fetch); a word that comes back stale (an old tag: the L2 may hold a line from before its last write)
+// is polled again with agent-scope loads, which always reach the coherent copy. Bounded: a wait that
+// outlives the time limit, or that sees another block's error flag, stops and returns what it read.
+#ifndef FW_LL_SLEEP
+#define FW_LL_SLEEP 1
+#endif
+static_assert(FW_LL_SLEEP >= 0 && FW_LL_SLEEP <= 127, "s_sleep takes 0..127");
 template <int N, bool kPlain = false>
 __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N], unsigned (&val)[N], const Ll& c) {
   uint64_t w[N];
@@ -145,7 +150,7 @@ __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N]
   if (pending) {
     const long long t0 = wall_clock64();
     for (int it = 1; pending; ++it) {
-      if (!kPlain || it > 1) __builtin_amdgcn_s_sleep(1);
+      if (!kPlain || it > 1) __builtin_amdgcn_s_sleep(FW_LL_SLEEP);
 #pragma unroll
       for (int k = 0; k < N; ++k)
         if (pending >> k & 1ull) w[k] = ll_load(buf + idx[k]);
@@ -527,46 +532,50 @@ struct AttnLds {
   uint4 q[2][3][8];  // q, fresh k, fresh v of the item's head (8 chunks of 8 fp16 each)
 };
 
-// One head's attention output from its split partials (LDS: part[s * kPartWords + d], d < 64 the value
-// sums, then m and l), with combine_finish's arithmetic over kMaxCombineSplits slots (splits past ns
-// empty): thread 0 the split weights, then thread d < 64 element d. The 64 fp16 results go to the
-// head's 32 words of `out` as one coalesced store. All threads of the block call it (barriers).
-__device__ __forceinline__ void head_combine(const float* part, int ns, int head, float* wgt, float* den_lds,
-                                             uint64_t* out, unsigned tag) {
+// Thread d < 64's element of one head's attention output from its split partials: get(s, m, l, a)
+// gives split s's max, exp-sum and value sum for element d (s < ns; splits past ns are empty). The
+// arithmetic is combine_finish's over kMaxCombineSplits slots: the maximum first, then per split in
+// order the weight, the denominator's and the numerator's fused adds (the two sums independent, so one
+// pass keeps each in split order). Every thread works out the weights itself, so no thread waits for
+// another. The 64 fp16 results go to the head's 32 words of `out`: lanes d and d ^ 1 of one wave
+// share a word.
+template <typename Get>
+__device__ __forceinline__ void combine_store(int ns, int d, uint64_t* out, unsigned tag, Get get) {
   constexpr int S = kMaxCombineSplits;
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (s < ns) {
+      float pm, pl, pa;
+      get(s, pm, pl, pa);
+      m = fmaxf(m, pm);
+    }
+  float den = 0.f, num = 0.f;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    float pm = -INFINITY, pl = 0.f, pa = 0.f;
+    if (s < ns) get(s, pm, pl, pa);
+    const float w = pl > 0.f ? __expf(pm - m) : 0.f;
+    den = fmaf(pl, w, den);
+    if (w != 0.f) num = fmaf(pa, w, num);
+  }
+  const unsigned lo = half_bits(f2h(num / den));
+  const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_ds_swizzle(static_cast<int>(lo), 0x041F));  // lane ^ 1
+  if ((d & 1) == 0) ll_store(out + d / 2, tag, lo | (hi << 16));
+}
+
+// One head's attention output from its split partials in LDS (part[s * kPartWords + d], d < 64 the value
+// sums, then m and l), by threads d < 64 (combine_store). All threads of the block call it: its
+// barrier frees part for the caller.
+__device__ __forceinline__ void head_combine(const float* part, int ns, int head, uint64_t* out, unsigned tag) {
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    float pm[S], pl[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      pm[s] = s < ns ? part[s * kPartWords + kHeadDim] : -INFINITY;
-      pl[s] = s < ns ? part[s * kPartWords + kHeadDim + 1] : 0.f;
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < S; ++s) m = fmaxf(m, pm[s]);
-    float den = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const float w = pl[s] > 0.f ? __expf(pm[s] - m) : 0.f;
-      wgt[s] = w;
-      den = fmaf(pl[s], w, den);
-    }
-    den_lds[0] = den;
-  }
-  __syncthreads();
-  if (tid < kHeadDim) {
-    float num = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const float pa = s < ns ? part[s * kPartWords + tid] : 0.f;
-      if (wgt[s] != 0.f) num = fmaf(pa, wgt[s], num);
-    }
-    const unsigned lo = half_bits(f2h(num / den_lds[0]));
-    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_ds_swizzle(static_cast<int>(lo), 0x041F));  // lane ^ 1
-    if ((tid & 1) == 0) ll_store(out + head * 32 + tid / 2, tag, lo | (hi << 16));
-  }
-  __syncthreads();  // part, wgt and den are free again
+  if (tid < kHeadDim)
+    combine_store(ns, tid, out + head * 32, tag, [&](int s, float& m, float& l, float& a) {
+      m = part[s * kPartWords + kHeadDim];
+      l = part[s * kPartWords + kHeadDim + 1];
+      a = part[s * kPartWords + tid];
+    });
+  __syncthreads();  // part is free again
 }
 
 // head_combine for NV vectors at once (the prompt pass): vector v's partials at part[v S kPartWords ..],
@@ -636,11 +645,15 @@ __device__ __forceinline__ void fetch_head_vectors(const uint64_t* qsrc, int hea
 template <int NV = 1>
 __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int ns, _Float16* kc, _Float16* vc,
                                                int max_len, int pos0, const uint64_t* qkv, uint64_t* out, float scale,
-                                               AttnLds& s, float* part, float* wgt, float* den, uint4 (*kvf)[2][8],
+                                               AttnLds& s, float* part, uint4 (*kvf)[2][8],
                                                const Tl& tl, int tl_slot) {
   constexpr int MAXP = 2, kRounds = kMaxCombineSplits / 2;
   const int pos = NV == 1 ? pos0 : min(pos0 + z, max_len - 1);  // as the batched split kernel clamps it
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
+  // an opaque copy of the thread index: the addresses derived from it are computed here, not hoisted
+  // to the kernel's start and kept (spilled) across the layers
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
   const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
   const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
   uint4 kr[kRounds][MAXP], vr[kRounds][MAXP];
@@ -739,7 +752,7 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
     if (tl0 && r == 0) tl.mark(kTlSa + kTlSaMerged);
   }
   tl.mark(tl_slot + 3);
-  head_combine(part, ns, head, wgt, den, NV == 1 ? out : out + z * kVecWords, c.tag);
+  head_combine(part, ns, head, NV == 1 ? out : out + z * kVecWords, c.tag);
 }
 
 // Cross-attention split items: item i is (head i / nsplit, split i % nsplit); a block runs two at once,
@@ -751,7 +764,7 @@ template <int NV = 1>
 __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int workers, int nitems, int nsplit,
                                                  const _Float16* kc, const _Float16* vc, int max_len,
                                                  const uint64_t* qsrc, uint64_t* part_g, uint64_t* out, float scale,
-                                                 AttnLds& s, float* part, float* wgt, float* den, const Tl& tl,
+                                                 AttnLds& s, float* part, const Tl& tl,
                                                  int tl_slot) {
   constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
@@ -817,7 +830,7 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
       for (int k = 0; k < 2; ++k)
         if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(v[k]);
       __syncthreads();
-      head_combine(part, nsplit, h, wgt, den, out + iv * kVecWords, c.tag);
+      head_combine(part, nsplit, h, out + iv * kVecWords, c.tag);
       tl.mark(tl_slot + 3);
     }
   }
@@ -1594,7 +1607,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           self_attn_head<NV>(c, rank % kStepHeads, z,
                              NV > 1 ? (min(pos + z, a.max_pos - 1) + kSelfSplitKeys) / kSelfSplitKeys : ns_self,
                              L.self_k, L.self_v, a.max_pos, pos, R + NV * kOffQkv, R + NV * kOffSelfVec, a.scale, att,
-                             part_lds, wgt, den, kvf, tl, l < kTlLayers ? tl_phase(l, 2) : kTlSlots - 4);
+                             part_lds, kvf, tl, l < kTlLayers ? tl_phase(l, 2) : kTlSlots - 4);
           tl.phase(l, 2, 2);
         }
         sc.next(w_qkv);
@@ -1666,7 +1679,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           tl.phase(l, 5, 0);
           if constexpr (NV == 1)
             cross_attn_items<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
-                                 R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, wgt, den, tl,
+                                 R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, tl,
                                  l < kTlLayers ? tl_phase(l, 5) : kTlSlots - 4);
           else
             cross_attn_items_nv<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + NV * kOffCrossQ,
