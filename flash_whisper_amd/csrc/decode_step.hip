@@ -1052,6 +1052,9 @@ constexpr int kLmMaxBatches = 8;                              // per block: ceil
 #ifndef FW_LM_BUFS
 #define FW_LM_BUFS 2
 #endif
+#ifndef FW_EMBED_WARM
+#define FW_EMBED_WARM 1
+#endif
 constexpr int kLmBufs = FW_LM_BUFS;
 static_assert(kLmBufs >= 1 && kLmBufs <= kLmMaxBatches, "FW_LM_BUFS");
 constexpr int kMaxGrid = 1024;                                // blocks whose maxima the hand-off region holds
@@ -1092,6 +1095,7 @@ struct alignas(16) LmLds {  // yhi / ylo are read as 16-byte chunks
   int ncand;
   unsigned long long best[kStepWaves * 2];
   unsigned long long fin[kStepWaves];  // the finalizing block's wave maxima
+  int64_t warm[2];                     // the finalizing block's token and next position
 };
 
 // y = LN(h_res) with the reduction order of ln_finish<1024, true> (the LM-head kernel's 1024-thread
@@ -1451,6 +1455,21 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     // ordering with other stores is needed)
     if (H.host_tokens && n_tok < a.max_pos)
       __hip_atomic_store(H.host_tokens + n_tok, o.tok, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    s.warm[0] = o.tok;
+    s.warm[1] = o.pos;
+  }
+  if (FW_EMBED_WARM && NV == 1) {
+    // The next step's embedding and position rows, read here with cached loads once the token is
+    // broadcast: the layer-0 LayerNorm blocks, which read them about a microsecond later, then find
+    // them in the memory-side cache instead of HBM. This block's first phase of the next step comes
+    // later, so the wait for the loads is off the step's path.
+    __syncthreads();
+    const _Float16 *ea, *eb;
+    embed_rows_of(s.warm[0], s.warm[1], a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
+    if (tid < 2 * (kHidden / 8)) {
+      const uint4 v = reinterpret_cast<const uint4*>(tid < kHidden / 8 ? ea : eb)[tid % (kHidden / 8)];
+      asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+    }
   }
 }
 

@@ -17,7 +17,6 @@ import statistics
 import time
 
 
-
 def host_threads():
     """Threads for torch's CPU pool: the host's CPU count, capped by OMP_NUM_THREADS where that is set."""
     n = os.cpu_count() or 1
