@@ -194,6 +194,11 @@ enum TlLm { kTlArrive = 0, kTlY, kTlDigits, kTlRegScored, kTlResScored, kTlScore
 constexpr int kTlSa = kTlLm + 12;
 enum TlSa { kTlSaRow = 0, kTlSaPartial, kTlSaMerged, kTlSaWeights };
 static_assert(kTlSa + kTlSaWeights < kTlSlots, "timeline slots");
+// The shader clock (s_memtime) at the step's start and end and the wall clock at its end: their ratio
+// to the wall clock gives the core clock the step ran at.
+constexpr int kTlClk = kTlSa + 8;
+enum TlClk { kTlClkStart = 0, kTlClkEnd, kTlClkWallEnd };
+static_assert(kTlClk + kTlClkWallEnd < kTlSlots, "timeline slots");
 __host__ __device__ constexpr int tl_phase(int l, int p) { return 1 + (l * 8 + (p - 1)) * 4; }
 #if FW_STEP_TIMELINE
 __device__ long long* g_step_tl;  // [steps][G][kTlSlots], or null
@@ -208,6 +213,9 @@ struct Tl {
   }
   __device__ void phase(int l, int ph, int k) const {
     if (l < kTlLayers) mark(tl_phase(l, ph) + k);
+  }
+  __device__ void mark_shader_clock(int s) const {
+    if (p && threadIdx.x == 0) tl_lds[s] = static_cast<long long>(__builtin_amdgcn_s_memtime());
   }
   // After a barrier that ends the step: waves 1-2 copy the slots out and clear them (wave 0 may be
   // polling the next step's words, and its loads would wait behind these stores).
@@ -229,6 +237,7 @@ struct Tl {
 #else
   __device__ void mark(int) const {}
   __device__ void phase(int, int, int) const {}
+  __device__ void mark_shader_clock(int) const {}
   __device__ void flush() const {}
   __device__ static Tl at(int) { return {}; }
   __device__ static void clear() {}
@@ -1577,6 +1586,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       if (__builtin_amdgcn_readfirstlane(bcast_lds[3])) break;  // an end-of-text token: every block stops
     }
     tl.mark(0);
+    tl.mark_shader_clock(kTlClk + kTlClkStart);
     const int pos = static_cast<int>(sp.pos_raw < 0 ? 0 : (sp.pos_raw >= a.max_pos ? a.max_pos - 1 : sp.pos_raw));
     const int ns_self = (pos + kSelfSplitKeys) / kSelfSplitKeys;
     Sched sc{0, G};
@@ -1820,6 +1830,8 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
         reinterpret_cast<unsigned*>(a.h_out)[i] = reinterpret_cast<const unsigned*>(h_res)[i];
     }
     if (FW_STEP_TIMELINE) {
+      tl.mark_shader_clock(kTlClk + kTlClkEnd);
+      tl.mark(kTlClk + kTlClkWallEnd);
       __syncthreads();
       tl.flush();
     }

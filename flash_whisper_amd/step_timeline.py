@@ -33,6 +33,7 @@ TICK_US = 0.01  # the 100 MHz wall clock
 PHASES = ('LN1 + q/k/v', 'self attention', 'out', 'LN2 + cross q', 'cross attention', 'cross-out',
           'LN3 + fc1 + GELU', 'fc2')
 TL_LAYERS, TL_LM, TL_SA = 4, 129, 141
+TL_CLK = TL_SA + 8  # shader clock at the step's start and end, wall clock at its end
 LM_POINTS = ('arrived', 'final LN done', 'y digits ready', 'first HBM batches scored', 'resident rows scored',
              'all rows scored', 'candidates listed', 'block maximum stored', 'every block maximum gathered',
              'token and state stored (last block)')
@@ -108,6 +109,10 @@ def step_stats(tl, n_layers):
                 row[('sa', k)] = float(np.median(s[act, TL_SA + k] - t_in)) * TICK_US
             row[('sa', 3)] = float(np.median(s[act, base + 3] - t_in)) * TICK_US
             row[('sa', 4)] = float(np.median(s[act, base + 2] - t_in)) * TICK_US
+        ok = (s[:, TL_CLK] > 0) & (s[:, TL_CLK + 2] > s[:, 0]) & (s[:, 0] > 0)
+        if ok.any():  # shader clock ticks over wall-clock ticks (100 MHz), per block: the core clock in MHz
+            mhz = (s[ok, TL_CLK + 1] - s[ok, TL_CLK]) / ((s[ok, TL_CLK + 2] - s[ok, 0]) * TICK_US)
+            row['clock_mhz'] = float(np.median(mhz))
         nxt = tl[st + 1][:, 0] if st + 1 < tl.shape[0] else None
         if nxt is not None and (nxt > 0).any():
             row['period'] = (float(nxt[nxt > 0].min()) - float(t0)) * TICK_US
@@ -123,7 +128,9 @@ def median_over(rows, key, field):
 def report(rows, n_layers, title):
     lines = [f'### {title}', '',
              f'Steps: {len(rows)} (medians over them); step period (start to the next step\'s start): '
-             f'{statistics.median(r["period"] for r in rows if "period" in r):.2f} us', '',
+             f'{statistics.median(r["period"] for r in rows if "period" in r):.2f} us; shader clock (s_memtime '
+             f'ticks over wall-clock time, median block): '
+             f'{statistics.median(r["clock_mhz"] for r in rows if "clock_mhz" in r):.0f} MHz', '',
              '| Layer | Phase | Blocks | entered (median / last) | in first | in median | in last | out | dur | wait | '
              'block work (median / max) |',
              '|---:|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|']
@@ -172,7 +179,8 @@ def summary(rows, rows2, n_layers, pos0, from_pos):
     stored = len(LM_POINTS) - 1
     lm = [r[('lm', stored)]['last'] - r[last]['out'] for r in rows if ('lm', stored) in r and last in r]
     return {'phases': phases, 'self_attention_by_length': by_len, 'lm_head_us': med(lm),
-            'step_period_us': med([r['period'] for r in rows if 'period' in r]), 'steps': len(rows)}
+            'step_period_us': med([r['period'] for r in rows if 'period' in r]), 'steps': len(rows),
+            'shader_clock_mhz': med([r['clock_mhz'] for r in rows if 'clock_mhz' in r])}
 
 
 def main():
