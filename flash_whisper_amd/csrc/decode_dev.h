@@ -459,32 +459,40 @@ __device__ __forceinline__ void split_wave_partial(const uint4 (&kr)[MAXP], cons
 #pragma unroll
   for (int t = 0; t < 8; ++t) acc[t] = 0.f;
   if (mx != -INFINITY) {
+    if (w0 + MAXP * 8 <= w1) {  // wave-uniform: every key is live, so no V needs masking (the same sums)
 #pragma unroll
-    for (int p = 0; p < MAXP; ++p) {
-      const float pj = __expf(sc[p] - mx);
-      psum += pj;
-      const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
-      const bool live = w0 + p * 8 + ks < w1;
+      for (int p = 0; p < MAXP; ++p) {
+        const float pj = __expf(sc[p] - mx);
+        psum += pj;
+        const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        acc[2 * t] = fmaf(pj, live ? h2f(v2[t].x) : 0.f, acc[2 * t]);
-        acc[2 * t + 1] = fmaf(pj, live ? h2f(v2[t].y) : 0.f, acc[2 * t + 1]);
+        for (int t = 0; t < 4; ++t) {  // fma with the fp16 operand widened in the instruction (v_fma_mix_f32)
+          acc[2 * t] = fmaf(pj, h2f(v2[t].x), acc[2 * t]);
+          acc[2 * t + 1] = fmaf(pj, h2f(v2[t].y), acc[2 * t + 1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < MAXP; ++p) {
+        const float pj = __expf(sc[p] - mx);
+        psum += pj;
+        const h2v* v2 = reinterpret_cast<const h2v*>(&vr[p]);
+        const bool live = w0 + p * 8 + ks < w1;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[2 * t] = fmaf(pj, live ? h2f(v2[t].x) : 0.f, acc[2 * t]);
+          acc[2 * t + 1] = fmaf(pj, live ? h2f(v2[t].y) : 0.f, acc[2 * t + 1]);
+        }
       }
     }
   }
   psum = xor_add<32>(xor_add<16>(xor_add<8>(psum)));
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    acc[t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[t])));
-  }
+  const float o = sum8_transposed(acc);  // element c * 8 + sum8_index(lane), summed over the 8 key slots
   if (lane == 0) {
     *wm = mx;
     *wl = psum;
   }
-  if (ks == 0) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) wacc_row[c * 8 + t] = acc[t];
-  }
+  wacc_row[c * 8 + sum8_index(lane)] = o;
 }
 
 // The split's (m, l, acc[d]) from the NW wave partials, merged in wave order (after a block barrier).

@@ -891,11 +891,11 @@ __device__ __forceinline__ void split_wave_partial_nv(const uint4 (&kr)[MAXP], c
       }
     }
   }
+  float o[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
     psum[v] = xor_add<32>(xor_add<16>(xor_add<8>(psum[v])));
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[v][t] = xor_add<32>(xor_add<16>(xor_add<8>(acc[v][t])));
+    o[v] = sum8_transposed(acc[v]);
   }
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
@@ -903,10 +903,7 @@ __device__ __forceinline__ void split_wave_partial_nv(const uint4 (&kr)[MAXP], c
       *wm[v] = mx[v];
       *wl[v] = psum[v];
     }
-    if (ks == 0) {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) wacc_row[v][c * 8 + t] = acc[v][t];
-    }
+    wacc_row[v][c * 8 + sum8_index(lane)] = o[v];
   }
 }
 

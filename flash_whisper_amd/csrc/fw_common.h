@@ -87,6 +87,39 @@ __device__ __forceinline__ float xor_max(float v) {
   }
 }
 
+// Eight values per lane, a[t], each summed over the 8 lanes that share lane & 7 (partners lane ^ 8,
+// then ^ 16, then ^ 32: the pairs and order of xor_add<32>(xor_add<16>(xor_add<8>(a[t])))), handing
+// half of a lane's values to its partner at each step: 4 DPP exchanges, 2 row swaps and 1 half swap
+// instead of 8 x 3 exchanges. Every add takes the same two operands as the butterfly's, so each sum is
+// bit-identical to it. The lane ends with the sum of a[sum8_index(lane)].
+__host__ __device__ constexpr int sum8_index(int lane) {
+  return 4 * ((lane >> 3) & 1) + 2 * ((lane >> 4) & 1) + ((lane >> 5) & 1);
+}
+__device__ __forceinline__ float sum8_transposed(const float (&a)[8]) {
+  const bool b3 = (threadIdx.x & 8) != 0;
+  float r1[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    // lanes with bit 3 clear keep a[k] and take lane + 8's a[k]; the others keep a[k + 4] and take
+    // lane - 8's a[k + 4] (two row shifts writing the banks of each side)
+    int r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a[k]), 0x108, 0xF, 0x3, false);
+    r = __builtin_amdgcn_update_dpp(r, __builtin_bit_cast(int, a[k + 4]), 0x118, 0xF, 0xC, false);
+    r1[k] = (b3 ? a[k + 4] : a[k]) + __builtin_bit_cast(float, r);
+  }
+  // rows 0, 2 keep r1[m], rows 1, 3 r1[m + 2]: one row swap trades them, then one add
+  float r2[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    float x = r1[m], y = r1[m + 2];
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+    r2[m] = x + y;
+  }
+  // lanes 0-31 keep r2[0], lanes 32-63 r2[1]
+  float x = r2[0], y = r2[1];
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  return x + y;
+}
+
 // Butterfly sum / max over `width` consecutive lanes (width a power of two <= 64), partners taken in
 // the order width / 2, ..., 2, 1.
 template <int kWidth>
