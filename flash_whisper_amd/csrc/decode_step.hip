@@ -58,7 +58,7 @@ constexpr int kLayerWords = kOffMlpOut + kVecWords;
 constexpr int kCtlBytes = 256;  // control words ahead of the regions: [0] epoch, [1] arrivals, [2] error
 // Worker counts of the phases that need few blocks (pairs of rows / items are spread over them).
 constexpr int kVecWorkers = 80;    // 640 row pairs: one pair per wave
-constexpr int kCrossWorkers = 60;  // 20 heads x 6 splits of the cross attention, two items per block
+constexpr int kCrossWorkers = 120;  // 20 heads x 6 splits of the cross attention, one item per block
 static_assert(kStepHeads * kHeadDim == kHidden, "20 heads of 64");
 static_assert(kStepThreads == 512, "the LayerNorm reduction order of the 8-wave LN+GEMV launches");
 
@@ -764,82 +764,74 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
   head_combine(part, ns, head, NV == 1 ? out : out + z * kVecWords, c.tag);
 }
 
-// Cross-attention split items: item i is (head i / nsplit, split i % nsplit); a block runs two at once,
-// waves 0-3 and 4-7, each exactly as attn_split_kernel<8, false, 4> runs one block, and stores its
-// partial (66 words, one coalesced store). The block that ran a head's last split then collects the
-// head's partials and combines them. With NV vectors, items run vector-major: item i is vector
-// i / (20 nsplit), and each vector's q, partials and output lie in regions of their own.
-template <int NV = 1>
-__device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int workers, int nitems, int nsplit,
-                                                 const _Float16* kc, const _Float16* vc, int max_len,
-                                                 const uint64_t* qsrc, uint64_t* part_g, uint64_t* out, float scale,
-                                                 AttnLds& s, float* part, const Tl& tl,
-                                                 int tl_slot) {
+// Cross-attention split items for one query, one item per block at a time: waves 0-3 run it exactly as
+// attn_split_kernel<8, false, 4> runs one block (one wave per SIMD; waves 4-7 only keep the barriers) and
+// store its partial (66 words, one coalesced store). Item k of the phase is split k % (nsplit - 1) of head
+// k / (nsplit - 1) for k < 20 (nsplit - 1), then the last split of head k - 20 (nsplit - 1); a block takes
+// items rank, rank + workers, ... The block that ran a head's last split then collects the head's
+// partials and combines them, so the combining blocks end the run and the phase after the cross-out can
+// reuse the run's first blocks. A block reaches its last-split items only after its other items, so no
+// wait depends on a block that is itself waiting.
+__device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int workers, int nsplit, const _Float16* kc,
+                                                 const _Float16* vc, int max_len, const uint64_t* qsrc,
+                                                 uint64_t* part_g, uint64_t* out, float scale, AttnLds& s, float* part,
+                                                 const Tl& tl, int tl_slot) {
   constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = wave >> 2, hw = wave & 3;
-  const int t4 = tid & 255, ks = lane >> 3, cc = lane & 7;
-  for (int base = 2 * rank; base < nitems; base += 2 * workers) {  // block-uniform
-    const int item = base + half;
-    const bool act = item < nitems;
-    const int per_v = kStepHeads * nsplit;
-    const int vec = NV > 1 && act ? item / per_v : 0, hitem = act ? item - vec * per_v : 0;
-    const int head = hitem / nsplit, split = hitem % nsplit;
+  const int tid = threadIdx.x, lane = tid & 63, ks = lane >> 3, cc = lane & 7;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, no lane masks
+  const int nitems = kStepHeads * nsplit, n_first = kStepHeads * (nsplit - 1);
+  for (int k = rank; k < nitems; k += workers) {  // block-uniform
+    const bool last = k >= n_first;
+    const int head = last ? k - n_first : k / (nsplit - 1), split = last ? nsplit - 1 : k % (nsplit - 1);
     const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
     const int begin = split * kKeys;
-    const int w0 = begin + hw * MAXP * 8;
-    const int wend = min(min(w0 + MAXP * 8, begin + kKeys), max_len);
     const int n = min(kKeys, max_len - begin);
+    const int w0 = begin + (wave & 3) * MAXP * 8;
+    const int wend = min(min(w0 + MAXP * 8, begin + kKeys), max_len);
     uint4 kr[MAXP], vr[MAXP];
+    if (wave < 4) {
 #pragma unroll
-    for (int p = 0; p < MAXP; ++p) {
-      // keys past wend (and an idle half's) load row wend - 1 and are masked: no load under a lane mask
-      const int j = max(0, min(w0 + p * 8 + ks, wend - 1));
-      kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
-      vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      for (int p = 0; p < MAXP; ++p) {
+        // keys past wend load row wend - 1 and are masked: no load under a lane mask
+        const int j = max(0, min(w0 + p * 8 + ks, wend - 1));
+        kr[p] = reinterpret_cast<const uint4*>(kc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+        vr[p] = reinterpret_cast<const uint4*>(vc + hoff + static_cast<size_t>(j) * kHeadDim)[cc];
+      }
     }
-    {  // the head's query: 32 words per half
-      const int word = t4;
-      int idx[1] = {act && word < 32 ? vec * kVecWords + head * 32 + word : -1};
+    {  // the head's query: 32 words
+      int idx[1] = {tid < 32 ? head * 32 + tid : -1};
       unsigned v[1];
       ll_wait<1>(qsrc, idx, v, c);
-      if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[half][0][0])[word] = v[0];
+      if (idx[0] >= 0) reinterpret_cast<unsigned*>(&s.q[0][0][0])[tid] = v[0];
     }
     __syncthreads();
-    if (base == 2 * rank) tl.mark(tl_slot + 1);
-    if (act && n > 0)
-      split_wave_partial<MAXP>(kr, vr, s.q[half][0][cc], w0, min(wend, begin + n), scale, &s.wm[half][hw],
-                               &s.wl[half][hw], s.wacc[half][hw]);
+    if (k == rank) tl.mark(tl_slot + 1);
+    if (wave < 4 && n > 0)
+      split_wave_partial<MAXP>(kr, vr, s.q[0][0][cc], w0, min(wend, begin + n), scale, &s.wm[0][wave],
+                               &s.wl[0][wave], s.wacc[0][wave]);
     __syncthreads();
-    if (act && t4 < kPartWords) {
+    if (tid < kPartWords) {
       float m = -INFINITY, l = 0.f, o = 0.f;
-      if (n > 0) split_merge<4>(s.wm[half], s.wl[half], s.wacc[half], t4 < kHeadDim ? t4 : 0, m, l, o);
-      const float val = t4 < kHeadDim ? o : (t4 == kHeadDim ? m : l);
-      ll_store(part_g + static_cast<size_t>(vec) * kPartRegion + static_cast<size_t>(split * kStepHeads + head) * kPartWords +
-                   t4,
-               c.tag, __float_as_uint(val));
+      if (n > 0) split_merge<4>(s.wm[0], s.wl[0], s.wacc[0], tid < kHeadDim ? tid : 0, m, l, o);
+      const float val = tid < kHeadDim ? o : (tid == kHeadDim ? m : l);
+      ll_store(part_g + static_cast<size_t>(split * kStepHeads + head) * kPartWords + tid, c.tag, __float_as_uint(val));
     }
     __syncthreads();  // s is reused below
     tl.mark(tl_slot + 2);
-    // heads whose last split this block ran: collect their partials and combine
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const int it = base + hf;
-      if (it >= nitems || it % nsplit != nsplit - 1) continue;  // block-uniform
-      const int iv = NV > 1 ? it / per_v : 0, h = (it - iv * per_v) / nsplit;
-      const uint64_t* vpart = part_g + static_cast<size_t>(iv) * kPartRegion;
+    if (last) {  // block-uniform: collect the head's partials and combine
       int idx[2];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int t = tid + k * kStepThreads;
-        idx[k] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + h) * kPartWords + t % kPartWords : -1;
+      for (int q = 0; q < 2; ++q) {
+        const int t = tid + q * kStepThreads;
+        idx[q] = t < nsplit * kPartWords ? ((t / kPartWords) * kStepHeads + head) * kPartWords + t % kPartWords : -1;
       }
       unsigned v[2];
-      ll_wait<2>(vpart, idx, v, c);
+      ll_wait<2>(part_g, idx, v, c);
 #pragma unroll
-      for (int k = 0; k < 2; ++k)
-        if (idx[k] >= 0) part[tid + k * kStepThreads] = __uint_as_float(v[k]);
+      for (int q = 0; q < 2; ++q)
+        if (idx[q] >= 0) part[tid + q * kStepThreads] = __uint_as_float(v[q]);
       __syncthreads();
-      head_combine(part, nsplit, h, out + iv * kVecWords, c.tag);
+      head_combine(part, nsplit, head, out, c.tag);
       tl.mark(tl_slot + 3);
     }
   }
@@ -1188,16 +1180,17 @@ __host__ __device__ inline int lm_rows_before(int b, int vocab, int G, int late0
   return static_cast<int>(static_cast<int64_t>(vocab) * weight / total);
 }
 
-// Blocks per phase run: the phases with many rows use every block the previous phase did not. At 256
-// CUs: LN1+q/k/v 176 blocks, self attention 20 (of a run of 176), out 80, LN2+cross-q 80, cross
-// attention 60, cross-out 80, LN3+fc1 116, fc2 80.
+// Blocks per phase run: the phases with many rows use every block the previous phase did not, except
+// LN3+fc1, which also takes the first half of the cross-attention run (those blocks end their items
+// early; the combining blocks are the run's last). At 256 CUs: LN1+q/k/v 176 blocks, self attention 20
+// (of a run of 176), out 80, LN2+cross-q 80, cross attention 120, cross-out 80, LN3+fc1 116, fc2 80.
 struct StepWorkers {
   int qkv, vec, cross, fc1;
 };
 __device__ __forceinline__ StepWorkers step_workers(int G) {
   const int vec = min(kVecWorkers, max(1, G * 5 / 16));
-  const int cross = min(kCrossWorkers, max(1, G * 15 / 64));
-  return {max(1, G - vec), vec, cross, max(1, G - vec - cross)};
+  const int cross = min(kCrossWorkers, max(1, G * 15 / 32));
+  return {max(1, G - vec), vec, cross, max(1, G - vec - cross / 2)};
 }
 
 // The block's share [r0, r1) of the LM-head table: the blocks that ran the last fc2 start last and take
@@ -1543,7 +1536,8 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const int ns_cross = (a.enc_len + kCrossSplitKeys - 1) / kCrossSplitKeys;
 
   // Runs of blocks per phase (step_workers), taken in turn around the grid: consecutive phases use
-  // disjoint blocks and the LN3 + fc1 phase also avoids the cross-attention blocks (which finish late).
+  // disjoint blocks, and the LN3 + fc1 phase reuses only the first half of the cross-attention run
+  // (its blocks finish their items early; the blocks that combine a head's splits are the run's last).
   // Every step starts the runs at block 0, so a layer's phase
   // runs on the same blocks in every step: the self-attention block of a head reads back the cache
   // rows it wrote itself (through its own CU's caches) in the steps before.
@@ -1699,17 +1693,20 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       {
         __syncthreads();
         const int nitems = kStepHeads * ns_cross;  // (head, split) items; each runs the NV queries
-        const int W = min(w_cross, (nitems + 1) / 2);
         const int rank = sc.rank();
-        if (rank < W) {
-          tl.phase(l, 5, 0);
-          if constexpr (NV == 1)
-            cross_attn_items<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ,
-                                 R + kOffCrossPart, R + kOffCrossVec, a.scale, att, part_lds, tl,
-                                 l < kTlLayers ? tl_phase(l, 5) : kTlSlots - 4);
-          else
-            cross_attn_items_nv<NV>(c, rank, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + NV * kOffCrossQ,
-                                    R + NV * kOffCrossPart, R + NV * kOffCrossVec, a.scale, attv, part_lds, wgt, den);
+        if constexpr (NV == 1) {
+          const int W = min(w_cross, nitems);
+          if (rank < W) {
+            tl.phase(l, 5, 0);
+            cross_attn_items(c, rank, W, ns_cross, L.cross_k, L.cross_v, a.enc_len, R + kOffCrossQ, R + kOffCrossPart,
+                             R + kOffCrossVec, a.scale, att, part_lds, tl, l < kTlLayers ? tl_phase(l, 5) : kTlSlots - 4);
+          }
+        } else {  // two items per block on the second half of the run (LN3 + fc1 reuses the first half)
+          const int lo = w_cross / 2, W = min(w_cross - lo, (nitems + 1) / 2);
+          if (rank >= lo && rank - lo < W)
+            cross_attn_items_nv<NV>(c, rank - lo, W, nitems, ns_cross, L.cross_k, L.cross_v, a.enc_len,
+                                    R + NV * kOffCrossQ, R + NV * kOffCrossPart, R + NV * kOffCrossVec, a.scale, attv,
+                                    part_lds, wgt, den);
         }
         sc.next(w_cross);
       }
