@@ -294,6 +294,31 @@ __device__ __forceinline__ void gv_finish(const Gv<K, U>& g, const _Float16* x_l
   uint4 xr[RS::kC];
 #pragma unroll
   for (int c = 0; c < RS::kC; ++c) xr[c] = reinterpret_cast<const uint4*>(x_lds)[sub + RS::kLPR * c];
+  if constexpr (ACT == FW_ACT_GELU && K == kHidden && U > 1) {
+    // The U row pairs' GELUs in one evaluation: after the row sums every lane of a 32-lane half holds its
+    // row's value, so lanes 8u .. 8u + 7 of each half take pass u's and one erf covers all passes (the same
+    // function of the same fp32 values as one evaluation per pass; erf is most of a pass's instructions).
+    static_assert(U <= 4, "8 lanes per pass in each half");
+    float z = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {  // passes past the rows (q < 0) score a clamped row; their values are dropped
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < RS::kC; ++c) acc = dot8(g.w[u][0][c], xr[c], acc);
+      acc = group_sum<RS::kLPR>(acc);
+      const float y = acc + h2f(g.b[u][0]);
+      z = ((lane & 31) >> 3) == u ? y : z;
+    }
+    float gz = gelu_erf(round_h(z));
+    asm volatile("" : "+v"(gz));  // rounded to fp32 first, as gemv_kernel does (see below)
+    const int gb = static_cast<int>(half_bits(f2h(gz)));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(gb, 8 * u));
+      const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(gb, 32 + 8 * u));
+      if (g.q[u] >= 0 && lane == 0) stage[u * kStepWaves + wave] = lo | (hi << 16);
+    }
+  } else {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (g.q[u] < 0) continue;  // wave-uniform
@@ -321,6 +346,7 @@ __device__ __forceinline__ void gv_finish(const Gv<K, U>& g, const _Float16* x_l
       hi = bits[1];
     }
     if (lane == 0) stage[u * kStepWaves + wave] = lo | (hi << 16);
+  }
   }
   __syncthreads();
   if (threadIdx.x < U * kStepWaves) {
