@@ -680,7 +680,7 @@ __device__ __forceinline__ void fetch_head_vectors(const uint64_t* qsrc, int hea
 template <int NV = 1>
 __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int ns, _Float16* kc, _Float16* vc,
                                                int max_len, int pos0, const uint64_t* qkv, uint64_t* out, float scale,
-                                               AttnLds& s, float* part, uint4 (*kvf)[2][8],
+                                               AttnLds& s, float* part, float* wave_slots, uint4 (*kvf)[2][8],
                                                const Tl& tl, int tl_slot) {
   constexpr int MAXP = 2, kRounds = kMaxCombineSplits / 2;
   const int pos = NV == 1 ? pos0 : min(pos0 + z, max_len - 1);  // as the batched split kernel clamps it
@@ -744,6 +744,66 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
   const uint4 qc = s.q[0][0][cc];
   const bool tl0 = tl_slot == tl_phase(0, 2);
   if (tl0) tl.mark(kTlSa + kTlSaRow);
+  if constexpr (NV == 1) {
+    // Every round's wave partials into slots of their own (split s, wave hw), so the rounds run back to
+    // back without a barrier; then one merge step. Each split's (m, l, acc) is split_merge<4> of its four
+    // wave partials and the head's output combine_store over the splits, as in the rounds below.
+    float* wm = wave_slots;                                 // [kMaxCombineSplits][4]
+    float* wl = wave_slots + kMaxCombineSplits * 4;         // [kMaxCombineSplits][4]
+    float* wacc = wave_slots + 2 * kMaxCombineSplits * 4;   // [kMaxCombineSplits][4][64]
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+      if (2 * r >= ns) break;  // block-uniform
+      const int split = half + 2 * r, begin = split * kSelfSplitKeys;
+      const int w0 = begin + hw * MAXP * 8;
+      const int wend = min(min(w0 + MAXP * 8, begin + kSelfSplitKeys), max_len);
+      const int n = min(kSelfSplitKeys, pos + 1 - begin);
+      if (split < ns) {
+#pragma unroll
+        for (int p = 0; p < MAXP; ++p)
+          if (w0 + p * 8 + ks == pos) {  // the new row replaces the (stale) cached one
+            kr[r][p] = s.q[0][1][cc];
+            vr[r][p] = s.q[0][2][cc];
+          }
+        split_wave_partial<MAXP>(kr[r], vr[r], qc, w0, min(wend, begin + n), scale, &wm[split * 4 + hw],
+                                 &wl[split * 4 + hw], wacc + (split * 4 + hw) * kHeadDim);
+      }
+    }
+    if (tl0) tl.mark(kTlSa + kTlSaPartial);
+    __syncthreads();
+    using WaccRow = const float (*)[kHeadDim];
+    if (ns <= 2) {  // block-uniform: thread d merges both splits itself and combines them, no second barrier
+      if (tid < kHeadDim) {
+        float m0, l0, o0, m1 = -INFINITY, l1 = 0.f, o1 = 0.f;
+        split_merge<4>(wm, wl, reinterpret_cast<WaccRow>(wacc), tid, m0, l0, o0);
+        if (ns > 1) split_merge<4>(wm + 4, wl + 4, reinterpret_cast<WaccRow>(wacc + 4 * kHeadDim), tid, m1, l1, o1);
+        if (tl0) tl.mark(kTlSa + kTlSaMerged);
+        combine_store(ns, tid, out + head * 32, c.tag, [&](int sp, float& m, float& l, float& a) {
+          m = sp == 0 ? m0 : m1;
+          l = sp == 0 ? l0 : l1;
+          a = sp == 0 ? o0 : o1;
+        });
+      }
+      tl.mark(tl_slot + 3);
+      __syncthreads();  // the slots and part are free again
+    } else {  // thread (split, d) merges, then the combine
+      const int sp = tid >> 6, d = tid & 63;
+      if (sp < ns) {
+        float m, l, o;
+        split_merge<4>(wm + sp * 4, wl + sp * 4, reinterpret_cast<WaccRow>(wacc + sp * 4 * kHeadDim), d, m, l, o);
+        part[sp * kPartWords + d] = o;
+        if (d == 0) {
+          part[sp * kPartWords + kHeadDim] = m;
+          part[sp * kPartWords + kHeadDim + 1] = l;
+        }
+      }
+      __syncthreads();
+      if (tl0) tl.mark(kTlSa + kTlSaMerged);
+      tl.mark(tl_slot + 3);
+      head_combine(part, ns, head, out, c.tag);
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < kRounds; ++r) {
     if (2 * r >= ns) break;  // block-uniform
@@ -1523,7 +1583,8 @@ template <int NV>
 __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs args) {
   const StepArgs& a = args;
   __shared__ __align__(16) _Float16 h_res[NV * kHidden];
-  __shared__ __align__(16) _Float16 x_lds[NV * kStepFfn];
+  __shared__ __align__(16) _Float16 x_lds[NV * kStepFfn];  // also the self attention's wave partials
+  static_assert(sizeof(x_lds) >= (2 + kHeadDim) * kMaxCombineSplits * 4 * sizeof(float), "self-attention slots");
   __shared__ __align__(16) uint4 kvf[NV > 1 ? NV : 1][2][8];  // the prompt pass: fresh k / v rows of a head
   __shared__ float red[8 * kStepWaves];  // LayerNorm sums (16 slots each for the LM head's 1024-thread order)
   __shared__ __align__(16) LmLds lm;
@@ -1653,7 +1714,8 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           self_attn_head<NV>(c, rank % kStepHeads, z,
                              NV > 1 ? (min(pos + z, a.max_pos - 1) + kSelfSplitKeys) / kSelfSplitKeys : ns_self,
                              L.self_k, L.self_v, a.max_pos, pos, R + NV * kOffQkv, R + NV * kOffSelfVec, a.scale, att,
-                             part_lds, kvf, tl, l < kTlLayers ? tl_phase(l, 2) : kTlSlots - 4);
+                             part_lds, reinterpret_cast<float*>(x_lds), kvf, tl,
+                             l < kTlLayers ? tl_phase(l, 2) : kTlSlots - 4);
           tl.phase(l, 2, 2);
         }
         sc.next(w_qkv);
