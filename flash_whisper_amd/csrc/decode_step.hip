@@ -1284,6 +1284,7 @@ __device__ __forceinline__ StepWorkers step_workers(int G) {
 // advance by the same worker counts in every layer, so the share is the same in every step of a launch.
 struct LmShare {
   int r0, r1;
+  bool late;  // the block ran the last fc2
 };
 __device__ __forceinline__ LmShare lm_share(int vocab, int n_layers) {
   const int G = gridDim.x;
@@ -1291,7 +1292,8 @@ __device__ __forceinline__ LmShare lm_share(int vocab, int n_layers) {
   const int adv = (2 * w.qkv + 4 * w.vec + w.cross + w.fc1) % G;  // a layer's eight runs
   const int late0 = ((n_layers * adv) % G - w.vec + G) % G;       // the last fc2's run
   const int b = blockIdx.x;
-  return {lm_rows_before(b, vocab, G, late0, w.vec), lm_rows_before(b + 1, vocab, G, late0, w.vec)};
+  return {lm_rows_before(b, vocab, G, late0, w.vec), lm_rows_before(b + 1, vocab, G, late0, w.vec),
+          (b - late0 + G) % G < w.vec};
 }
 
 // With NV vectors (the prompt pass) the LM head scores the last one, at position pos_raw + NV - 1. The
@@ -1335,7 +1337,16 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   constexpr int kBufs = kLmBufs;
   Batch bt[kBufs];
   tl.mark(kTlLm + kTlArrive);
-  if (wv < kLmRowWaves) {
+  if (share.late) {  // block-uniform
+    // The blocks that ran the last fc2 arrive last, when its output is already stored: every thread adds
+    // it first (one poll round, not queued behind this block's table loads), then the table is requested.
+    resid_catch_up<kStepThreads, NV, NV - 1>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp);
+    if (wv < kLmRowWaves) {
+#pragma unroll
+      for (int k = 0; k < kBufs; ++k)
+        if (k < nb) load(k, bt[k]);
+    }
+  } else if (wv < kLmRowWaves) {
 #pragma unroll
     for (int k = 0; k < kBufs; ++k)
       if (k < nb) load(k, bt[k]);
