@@ -488,12 +488,7 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_q8_kernel(const _Float16* 
     ylo[2 * tid + 1] = static_cast<int8_t>(n1 - 128 * h1);
   }
   __syncthreads();  // publishes the digits and y_lds
-  // Upper bounds. |y|: an fp32 sum of <= 1280 non-negative terms is within 1280 * 2^-24 < 2^-10
-  // relative. |eta|: with t and 1 / t each rounded once and y / t = y * tinv to within 3 * 2^-24 of
-  // |y / t| <= kQ8YMax (< 0.003), every |y_i - t y_int_i| <= 0.503 t (one more rounding included).
-  const double ny = static_cast<double>(sqrtf(ysq)) * (1.0 + 0x1p-9);
-  const double neta = amax > 0.f ? 0.51 * static_cast<double>(t) * sqrt(static_cast<double>(kHidden)) : 0.0;
-  const double nE_per_s = 127.0 * sqrt(static_cast<double>(kHidden)) * (1.0 + 0x1p-30);
+  const Q8Step q8 = q8_step(amax, ysq);  // the same t as above
   uint4 dh[kQ8C], dl[kQ8C];
 #pragma unroll
   for (int c = 0; c < kQ8C; ++c) {
@@ -513,14 +508,11 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_q8_kernel(const _Float16* 
     }
     ah = xor_add_i16(ah);
     al = xor_add_i16(al);
-    const double a = static_cast<double>(b.m.x) * static_cast<double>(t) *
-                     static_cast<double>(128ll * ah + al);
-    const double nE = static_cast<double>(b.m.x) * nE_per_s + static_cast<double>(b.m.y);
-    const double r = (ny * static_cast<double>(b.m.y) + (neta + static_cast<double>(kQ8Gamma) * ny) * nE) *
-                     (1.0 + 0x1p-20);
+    float ub, lb;
+    q8_bounds(ah, al, b.m, q8, ub, lb);
     const bool live = row < vocab && !b.sp;
-    const float ub = live ? __double2float_ru(a + r) : -INFINITY;
-    const float lb = live ? __double2float_rd(a - r) : -INFINITY;
+    ub = live ? ub : -INFINITY;
+    lb = live ? lb : -INFINITY;
     lb_max = fmaxf(lb_max, lb);
     if (sub == 0) ub_lds[k * kLmRowsIter + slot_row] = ub;
   };

@@ -557,6 +557,39 @@ __device__ __forceinline__ int dot16_i8(const uint4& a, const uint4& b, int acc)
   return acc;
 }
 
+// The bound of the int8 pre-pass in fp32. With y's scale t, ||y|| <= ny and ||eta|| <= neta (eta = y - t
+// y_int), a row with scale s, error bound e and exact digit dots ah, al (y_int = 128 hi + lo) has its fp32
+// logit X within r = ny e + (neta + gamma ny)(127 s sqrt(1280) + e) of A = s t (128 ah + al). Written
+// r = e a_e + s b_s with a_e = ny + k, b_s = k 127 sqrt(1280), k = neta + gamma ny (per step). In fp32:
+// n = 128 ah + al is within 2^-24 (128 |ah| + |n|) (ah rounded once, al exact, one fma), so s t n within
+// 3 2^-24 |s t| (128 |ah| + |n|); that term is covered 8 times over, r's six roundings of positive terms by
+// the factor 1 + 2^-18, and the last add's rounding by what is left of both. So ub >= A + r and
+// lb <= A - r: the interval holds the interval of the exact bound, and every argument made for that one
+// (the candidate rule) holds for it.
+struct Q8Step {
+  float t, a_e, b_s;
+};
+__device__ __forceinline__ Q8Step q8_step(float amax, float ysq) {
+  // |y|: an fp32 sum of <= 1280 non-negative terms is within 1280 * 2^-24 < 2^-10 relative. |eta|: with
+  // t and 1 / t each rounded once and y / t = y * tinv to within 3 * 2^-24 of |y / t| <= kQ8YMax
+  // (< 0.003), every |y_i - t y_int_i| <= 0.503 t (one more rounding included).
+  const float t = amax > 0.f ? amax / static_cast<float>(kQ8YMax) : 1.0f;
+  const float ny = sqrtf(ysq) * (1.0f + 0x1p-9f);
+  const float neta = amax > 0.f ? 0.51f * t * 35.77708764f : 0.f;  // sqrt(1280)
+  const float k = fmaf(kQ8Gamma, ny, neta);
+  return {t, ny + k, k * 4543.6901f};                               // 127 sqrt(1280)
+}
+__device__ __forceinline__ void q8_bounds(int ah, int al, float2 m, const Q8Step& q, float& ub, float& lb) {
+  const float st = m.x * q.t;
+  const float fh = static_cast<float>(ah);
+  const float n = fmaf(128.0f, fh, static_cast<float>(al));
+  const float av = st * n;
+  const float err = (st * 0x1p-21f) * fmaf(128.0f, fabsf(fh), fabsf(n));
+  const float r = fmaf(fmaf(m.y, q.a_e, m.x * q.b_s), 1.0f + 0x1p-18f, err + 1e-30f);
+  ub = av + r;
+  lb = av - r;
+}
+
 // Smallest X that can still tie or beat a row whose fp32 logit is at least T once both are rounded to
 // fp16 (round to nearest even; logits at or beyond 65520 round to +-inf and tie there).
 __device__ __forceinline__ float q8_threshold(float t) {

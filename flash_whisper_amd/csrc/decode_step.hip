@@ -1406,9 +1406,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   }
   __syncthreads();
   tl.mark(kTlLm + kTlDigits);
-  const double ny = static_cast<double>(sqrtf(ysq)) * (1.0 + 0x1p-9);
-  const double neta = amax > 0.f ? 0.51 * static_cast<double>(t) * sqrt(static_cast<double>(kHidden)) : 0.0;
-  const double nE_per_s = 127.0 * sqrt(static_cast<double>(kHidden)) * (1.0 + 0x1p-30);
+  const Q8Step q8 = q8_step(amax, ysq);  // the same t as above
   float lb_max = -INFINITY;
   // this lane's chunks of the y digits, read from LDS once for every row it scores (re-reading them per
   // row made the scan bound by LDS bandwidth: 10 of a row's 15 reads)
@@ -1428,13 +1426,11 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     }
     ah = xor_add_i16(ah);
     al = xor_add_i16(al);
-    const double av = static_cast<double>(bt.m.x) * static_cast<double>(t) * static_cast<double>(128ll * ah + al);
-    const double nE = static_cast<double>(bt.m.x) * nE_per_s + static_cast<double>(bt.m.y);
-    const double rv = (ny * static_cast<double>(bt.m.y) + (neta + static_cast<double>(kQ8Gamma) * ny) * nE) *
-                      (1.0 + 0x1p-20);
+    float ub, lb;
+    q8_bounds(ah, al, bt.m, q8, ub, lb);
     const bool live = in_range && !bt.sp;
-    const float ub = live ? __double2float_ru(av + rv) : -INFINITY;
-    const float lb = live ? __double2float_rd(av - rv) : -INFINITY;
+    ub = live ? ub : -INFINITY;
+    lb = live ? lb : -INFINITY;
     lb_max = fmaxf(lb_max, lb);
     if (sub == 0 && in_range) s.ub[row - r0] = ub;
   };

@@ -34,19 +34,52 @@ def threshold(t):
     return min(t - (abs(t) * 2.0 ** -9 + 2.0 ** -23), 65504.0)
 
 
+F32 = np.float32
+
+
+def fma32(a, b, c):
+    """fp32 fused multiply-add (the fp64 product of two fp32 values is exact; the sum is rounded to fp64,
+    then to fp32: a double rounding that differs from one rounding only in rare ties)."""
+    f64 = lambda x: np.asarray(x, F32).astype(np.float64)
+    return (f64(a) * f64(b) + f64(c)).astype(F32)
+
+
+def q8_step(amax, ysq):
+    """The kernel's per-step constants (q8_step in flash_whisper_amd/csrc/decode_dev.h), in fp32."""
+    t = F32(F32(amax) / F32(YMAX)) if amax > 0 else F32(1)
+    ny = F32(F32(np.sqrt(F32(ysq))) * F32(1 + 2.0 ** -9))
+    neta = F32(F32(F32(0.51) * t) * F32(35.77708764)) if amax > 0 else F32(0)
+    k = fma32(GAMMA, ny, neta)
+    return t, F32(ny + k), F32(k * F32(4543.6901))
+
+
+def q8_bounds(ah, al, s, e, step, radius_scale=1.0, err_term=True):
+    """The kernel's fp32 interval for a row's logit (q8_bounds in decode_dev.h), element-wise over rows;
+    radius_scale = 0 plants the mistake of ranking by the estimate alone, err_term = False the mistake of
+    leaving out the term that covers the fp32 rounding of the estimate."""
+    t, a_e, b_s = step
+    st = (np.asarray(s, F32) * t).astype(F32)
+    fh = np.asarray(ah, np.float64).astype(F32)
+    n = fma32(F32(128), fh, np.asarray(al, np.float64).astype(F32))
+    av = (st * n).astype(F32)
+    err = ((st * F32(2.0 ** -21)).astype(F32) * fma32(F32(128), np.abs(fh), np.abs(n))).astype(F32) * F32(err_term)
+    inner = fma32(np.asarray(e, F32), a_e, (np.asarray(s, F32) * b_s).astype(F32))
+    r = fma32(inner, F32(1 + 2.0 ** -18), (err + F32(1e-30)).astype(F32)) * F32(radius_scale)
+    return (av + r).astype(F32), (av - r).astype(F32)
+
+
 def candidates(q, s, e, y, live, radius_scale=1.0):
     y = np.asarray(y, np.float32)
     amax = np.abs(y).max()
-    t = np.float32(amax / YMAX) if amax > 0 else np.float32(1)
     tinv = np.float32(YMAX / amax) if amax > 0 else np.float32(0)
     yi = np.clip(np.rint(y * tinv), -YMAX, YMAX)
-    ny = np.sqrt((y.astype(np.float64) ** 2).sum()) * (1 + 2 ** -9)
-    neta = ETA_PER_T * np.float64(t) * np.sqrt(D) if amax > 0 else 0.0   # closed-form bound on |y - t yi|
-    a = s.astype(np.float64) * np.float64(t) * (q @ yi)            # exact integer dot, then scaled
-    n_e = s.astype(np.float64) * 127 * np.sqrt(D) * (1 + 2 ** -30) + e
-    r = (ny * e + (neta + GAMMA * ny) * n_e) * (1 + 2 ** -20) * radius_scale
-    ub = np.where(live, a + r, -np.inf)
-    lb = np.where(live, a - r, -np.inf)
+    ysq = F32((y.astype(np.float64) ** 2).sum())
+    hi = np.floor((yi + 64) / 128)                                  # the kernel's two digits
+    lo = yi - 128 * hi
+    ah, al = q @ hi, q @ lo                                         # exact integer dots
+    ub, lb = q8_bounds(ah, al, s, e, q8_step(amax, ysq), radius_scale)
+    ub = np.where(live, ub, -np.inf)
+    lb = np.where(live, lb, -np.inf)
     thr = threshold(lb.max())
     return np.nonzero(live & ~(ub < thr))[0]
 
@@ -156,3 +189,42 @@ def test_eta_closed_form_bound_dominates():
         assert per.max() <= 0.503, per.max()
         assert np.sqrt((eta.astype(np.float64) ** 2).sum()) <= ETA_PER_T * np.float64(t) * np.sqrt(D)
     assert worst > 0.49  # the rounding errors do reach t / 2: the check is not vacuous
+
+
+def test_fp32_interval_holds_the_exact_bound():
+    """The kernel's fp32 interval [lb, ub] contains [A - r, A + r] with A = s t (128 ah + al) exact and r
+    the radius of the soundness argument at its tightest: ||y|| <= sqrt(ysq) (1 + 2^-10) and
+    ||eta|| <= 0.503 t sqrt(1280) (the bounds proved above and at q8_step). Random and adversarial values:
+    digit dots at their extremes, 128 ah cancelling al, tiny and large scales, e = 0, y = 0."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(7)
+    n_cases = 4000
+    ah = rng.integers(-20_600_000, 20_600_000, n_cases)
+    al = rng.integers(-10_400_000, 10_400_000, n_cases)
+    ah[:500] = rng.integers(-81_000, 81_000, 500)          # 128 ah + al near 0
+    al[:500] = -128 * ah[:500] + rng.integers(-3, 4, 500)
+    ah[500:600], al[500:600] = 20_600_000, 10_400_000       # the extremes
+    ah[600:700], al[600:700] = -20_600_000, -10_400_000
+    s = F32(10.0 ** rng.uniform(-8, 0, n_cases))
+    e = F32(s * F32(10.0 ** rng.uniform(-3, 1.6, n_cases)))
+    e[700:800] = 0
+    worst, escaped = np.inf, 0
+    for i in range(n_cases):
+        amax = F32(0) if i % 97 == 0 else F32(10.0 ** rng.uniform(-3, 4.5))
+        ysq = F32(0) if amax == 0 else F32(amax * amax * rng.uniform(1, D))
+        step = q8_step(amax, ysq)
+        ub, lb = q8_bounds(np.array([ah[i]]), np.array([al[i]]), s[i:i + 1], e[i:i + 1], step)
+        a_exact = Fraction(float(s[i])) * Fraction(float(step[0])) * (128 * int(ah[i]) + int(al[i]))
+        ny = np.sqrt(np.float64(ysq)) * (1 + 2.0 ** -10)
+        neta = 0.503 * np.float64(step[0]) * np.sqrt(D) if amax > 0 else 0.0
+        r = (ny * np.float64(e[i]) + (neta + GAMMA * ny) * (127 * np.float64(s[i]) * np.sqrt(D) + np.float64(e[i])))
+        r = Fraction(float(r * (1 + 1e-12)))
+        assert Fraction(float(ub[0])) >= a_exact + r, i
+        assert Fraction(float(lb[0])) <= a_exact - r, i
+        if r > 0:
+            worst = min(worst, float((Fraction(float(ub[0])) - a_exact) / r))
+        ub0, lb0 = q8_bounds(np.array([ah[i]]), np.array([al[i]]), s[i:i + 1], e[i:i + 1], step, err_term=False)
+        escaped += Fraction(float(ub0[0])) < a_exact + r or Fraction(float(lb0[0])) > a_exact - r
+    assert escaped > 0  # without the rounding term the interval misses the exact one somewhere
+    assert worst < 1.02  # and it is not wider than it needs to be by more than 2% (0.51 t against 0.503 t)
