@@ -505,6 +505,40 @@ __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, in
   }
 }
 
+// Contribution 0 (the token + position embedding, resid_catch_up's first add) in two steps, so a phase can
+// request the rows before its weight rows: the rows come back first (loads return in order) and the add
+// does not wait for the weights.
+struct EmbRegs {
+  h2v p[2], q[2];
+};
+__device__ __forceinline__ void embed_load(EmbRegs& e, const StepArgs& a, const StepPos& sp) {
+  const _Float16 *ea, *eb;
+  embed_rows_of(sp.tok, sp.pos_raw, a.embed, a.pos_embed, a.vocab, a.max_pos, &ea, &eb);
+  const int t = threadIdx.x;
+  const int i1 = t + kStepThreads < kVecWords ? t + kStepThreads : t;  // threads past the pairs repeat theirs
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = k == 0 ? t : i1;
+    e.p[k] = reinterpret_cast<const h2v*>(ea)[i];
+    e.q[k] = reinterpret_cast<const h2v*>(eb)[i];
+  }
+}
+__device__ __forceinline__ void embed_store(const EmbRegs& e, _Float16* h_res, int& applied) {
+  h2v* h2 = reinterpret_cast<h2v*>(h_res);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = t + k * kStepThreads;
+    if (i < kVecWords) {
+      h2v o;
+      o.x = f2h(h2f(e.p[k].x) + h2f(e.q[k].x));
+      o.y = f2h(h2f(e.p[k].y) + h2f(e.q[k].y));
+      h2[i] = o;
+    }
+  }
+  applied = 1;
+}
+
 // y = LN(h_res) with gamma / beta, the arithmetic of ln_finish<512, true> on the (already rounded)
 // residual: ln_params requests gamma and beta (before the phase's input is awaited), resid_layernorm
 // takes the residual pairs each thread owns (the ones it wrote itself) and finishes the LayerNorm.
@@ -1139,6 +1173,9 @@ constexpr int kLmMaxBatches = 8;                              // per block: ceil
 #ifndef FW_EMBED_WARM
 #define FW_EMBED_WARM 1
 #endif
+#ifndef FW_QKV_WARM
+#define FW_QKV_WARM 1  // layer 0's q/k/v rows read into L2 while the token is awaited
+#endif
 constexpr int kLmBufs = FW_LM_BUFS;
 static_assert(kLmBufs >= 1 && kLmBufs <= kLmMaxBatches, "FW_LM_BUFS");
 constexpr int kMaxGrid = 1024;                                // blocks whose maxima the hand-off region holds
@@ -1655,20 +1692,39 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
     const StepArgs& a = step_args();
     const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit};
     const Tl tl = Tl::at(st);
+    constexpr int kBcastWave = kStepWaves - 1;  // polls the previous step's token
+    // Layer 0's q/k/v rows do not depend on the token: the blocks of that run (it starts at block 0) read
+    // them into their XCD's L2 while they wait for it, so the phase finds them there. The wave that polls
+    // for the token reads none (its poll would return behind them), and the others take the loads' values
+    // only after the token is in (a wait for them before the barrier would hold the poll back).
+    Gv<kHidden, 2> gw;
+    const bool warm = FW_QKV_WARM && NV == 1 && st > 0 && static_cast<int>(blockIdx.x) < w_qkv && wave != kBcastWave;
+    if (warm)
+      gv_load(gw, a.layer[0].qkv_w, a.layer[0].qkv_b, kQkvWords, static_cast<int>(blockIdx.x) * kStepWaves + wave,
+              w_qkv * kStepWaves);
     if (st > 0) {  // the previous step's token, position, token count and stop flag
       __syncthreads();
-      if (tid < 4) {
-        const int idx[1] = {tid};
+      const int bt = tid - kBcastWave * kWave;
+      if (bt >= 0 && bt < 4) {
+        const int idx[1] = {bt};
         unsigned v[1];
         const Ll prev{ctl, c.tag - 1u, a.spin_limit};
         ll_wait<1>(bcast, idx, v, prev);
-        bcast_lds[tid] = v[0];
+        bcast_lds[bt] = v[0];
       }
       __syncthreads();
       sp.tok = __builtin_amdgcn_readfirstlane(bcast_lds[0]);  // uniform: scalar registers
       sp.pos_raw = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[1]));
       n_tok = static_cast<int>(__builtin_amdgcn_readfirstlane(bcast_lds[2]));
       if (__builtin_amdgcn_readfirstlane(bcast_lds[3])) break;  // an end-of-text token: every block stops
+    }
+    if (warm) {
+      unsigned x = 0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int k = 0; k < Gv<kHidden, 2>::RS::kC; ++k) x ^= gw.w[u][0][k].x;
+      asm volatile("" ::"v"(x));  // the loads complete by here, not in the phase
     }
     tl.mark(0);
     tl.mark_shader_clock(kTlClk + kTlClkStart);
@@ -1691,9 +1747,13 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
           Gv<kHidden, U> g;
           int base = rank * kStepWaves;  // the block's first word; a block-uniform loop over passes of U words
           const int qs = W * kStepWaves;
+          EmbRegs emb;
+          const bool emb_first = NV == 1 && applied == 0;  // block-uniform: layer 0 of a step
+          if (emb_first) embed_load(emb, a, sp);
           gv_load(g, L.qkv_w, L.qkv_b, npairs, base + wave, qs);
           LnRegs<kStepThreads> lnr;
           ln_params(lnr, L.ln1_g, L.ln1_b);
+          if (emb_first) embed_store(emb, h_res, applied);
           tl.phase(l, 1, 0);
           resid_catch_up<kStepThreads, NV>(h_res, applied, 1 + 3 * l, regions, a, c, sp);
           tl.phase(l, 1, 3);
