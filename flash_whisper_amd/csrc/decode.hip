@@ -652,13 +652,8 @@ __global__ void __launch_bounds__(NW * 64) attn_split_kernel(AttnArgs a) {
   split_merge_store<NW>(wm, wl, wacc, a, slot);
 }
 
-// Splits of up to 256 keys (the cross attention): FW_ATTN256_P passes of 8 keys per wave, 32 / P
-// waves. 4 waves of 64 keys measured 0.9 us faster per decoder step than 8 waves of 32 on MI355X.
-#ifndef FW_ATTN256_P
-#define FW_ATTN256_P 8
-#endif
-static_assert(FW_ATTN256_P >= 2 && 32 % FW_ATTN256_P == 0,
-              "FW_ATTN256_P: whole waves of P passes over 256 keys, at most 16 waves");
+// Splits of up to 256 keys (the cross attention): FW_ATTN256_P passes of 8 keys per wave, 32 / P waves
+// (decode_dev.h; the one-launch step's cross attention has the same layout).
 int launch_attn_split(const AttnArgs& a, int nsplit, int heads, hipStream_t s, int nq = 1) {
   const dim3 grid(nsplit, heads, nq);
   constexpr int kP256 = FW_ATTN256_P, kW256 = 32 / FW_ATTN256_P;

@@ -435,6 +435,14 @@ __device__ __forceinline__ int attn_pos(const AttnArgs& a) {
   return static_cast<int>(p < 0 ? 0 : (p >= a.max_len ? a.max_len - 1 : p));
 }
 
+// Splits of up to 256 keys (the cross attention): FW_ATTN256_P passes of 8 keys per wave, 32 / P waves.
+// 4 waves of 64 keys measured 0.9 us faster per decoder step than 8 waves of 32 on MI355X (34 launches).
+#ifndef FW_ATTN256_P
+#define FW_ATTN256_P 8
+#endif
+static_assert(FW_ATTN256_P >= 4 && 32 % FW_ATTN256_P == 0,
+              "FW_ATTN256_P: whole waves of P passes over 256 keys, at most 8 waves");
+
 // The scores, softmax and P.V of one wave's keys of a split (MAXP passes of 8 keys, keys at or past w1
 // masked): the wave's (max, exp-sum, value sum) go to wm, wl and wacc_row for split_merge_store. Lane
 // l holds key w0 + 8 p + l / 8 of pass p and chunk l % 8 of its row; fp32 throughout, the scale

@@ -896,9 +896,13 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
                                                  const _Float16* vc, int max_len, const uint64_t* qsrc,
                                                  uint64_t* part_g, uint64_t* out, float scale, AttnLds& s, float* part,
                                                  const Tl& tl, int tl_slot) {
-  constexpr int MAXP = 8, kKeys = kCrossSplitKeys;
+  constexpr int MAXP = FW_ATTN256_P, kNW = kCrossSplitKeys / (8 * MAXP), kKeys = kCrossSplitKeys;
+  static_assert(kNW <= kStepWaves && kNW <= 8, "one item's waves in a block");
   const int tid = threadIdx.x, lane = tid & 63, ks = lane >> 3, cc = lane & 7;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches, no lane masks
+  float* wm = &s.wm[0][0];            // [8] (the two halves' slots, contiguous)
+  float* wl = &s.wl[0][0];
+  float* wacc = &s.wacc[0][0][0];     // [8][64]
   const int nitems = kStepHeads * nsplit, n_first = kStepHeads * (nsplit - 1);
   for (int k = rank; k < nitems; k += workers) {  // block-uniform
     const bool last = k >= n_first;
@@ -906,10 +910,10 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
     const size_t hoff = static_cast<size_t>(head) * max_len * kHeadDim;
     const int begin = split * kKeys;
     const int n = min(kKeys, max_len - begin);
-    const int w0 = begin + (wave & 3) * MAXP * 8;
+    const int w0 = begin + (wave % kNW) * MAXP * 8;
     const int wend = min(min(w0 + MAXP * 8, begin + kKeys), max_len);
     uint4 kr[MAXP], vr[MAXP];
-    if (wave < 4) {
+    if (wave < kNW) {
 #pragma unroll
       for (int p = 0; p < MAXP; ++p) {
         // keys past wend load row wend - 1 and are masked: no load under a lane mask
@@ -926,13 +930,14 @@ __device__ __forceinline__ void cross_attn_items(const Ll& c, int rank, int work
     }
     __syncthreads();
     if (k == rank) tl.mark(tl_slot + 1);
-    if (wave < 4 && n > 0)
-      split_wave_partial<MAXP>(kr, vr, s.q[0][0][cc], w0, min(wend, begin + n), scale, &s.wm[0][wave],
-                               &s.wl[0][wave], s.wacc[0][wave]);
+    if (wave < kNW && n > 0)
+      split_wave_partial<MAXP>(kr, vr, s.q[0][0][cc], w0, min(wend, begin + n), scale, wm + wave, wl + wave,
+                               wacc + wave * kHeadDim);
     __syncthreads();
     if (tid < kPartWords) {
       float m = -INFINITY, l = 0.f, o = 0.f;
-      if (n > 0) split_merge<4>(s.wm[0], s.wl[0], s.wacc[0], tid < kHeadDim ? tid : 0, m, l, o);
+      if (n > 0)
+        split_merge<kNW>(wm, wl, reinterpret_cast<const float(*)[kHeadDim]>(wacc), tid < kHeadDim ? tid : 0, m, l, o);
       const float val = tid < kHeadDim ? o : (tid == kHeadDim ? m : l);
       ll_store(part_g + static_cast<size_t>(split * kStepHeads + head) * kPartWords + tid, c.tag, __float_as_uint(val));
     }
