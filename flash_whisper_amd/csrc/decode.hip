@@ -476,7 +476,6 @@ __global__ void __launch_bounds__(kLmNW * 64) lm_head_q8_kernel(const _Float16* 
     amax = fmaxf(amax, red[2 * kLmNW + i]);
     ysq += red[3 * kLmNW + i];
   }
-  const float t = amax > 0.f ? amax / static_cast<float>(kQ8YMax) : 1.0f;
   const float tinv = amax > 0.f ? static_cast<float>(kQ8YMax) / amax : 0.f;
   if (has_pair) {
     const int n0 = static_cast<int>(fminf(fmaxf(rintf(y0 * tinv), -kQ8YMax), kQ8YMax));

@@ -55,7 +55,16 @@ constexpr int kOffCrossOut = kOffCrossVec + kVecWords;
 constexpr int kOffFfn = kOffCrossOut + kVecWords;
 constexpr int kOffMlpOut = kOffFfn + kFfnWords;
 constexpr int kLayerWords = kOffMlpOut + kVecWords;
-constexpr int kCtlBytes = 256;  // control words ahead of the regions: [0] epoch, [1] arrivals, [2] error
+// Workspace: control words ([0] epoch, [1] arrivals, [2] error), one bit per 8 KB page of the hand-off
+// area (the half of the chip the page is local to), the latencies fw_decoder_step_calibrate measures, and
+// the hand-off area (16 KB aligned). The regions below are laid out in logical words; logical page k
+// (1024 words) has two physical copies, pages 2k and 2k + 1 of the area (see ll_store / ll_wait).
+constexpr int kCtlBytes = 256;
+constexpr int kGroupBytes = 256;
+constexpr int kPageWords = 1024;               // 8 KB pages: memory alternates between the two halves of
+constexpr int kMaxPages = kGroupBytes * 8;     // the chip every 8 KB
+constexpr int kCalibBytes = 2 * kMaxPages * 4;  // fp32 latency per physical page, for two pairs of XCDs
+constexpr size_t kAreaAlign = 16384;
 // Worker counts of the phases that need few blocks (pairs of rows / items are spread over them).
 constexpr int kVecWorkers = 80;    // 640 row pairs: one pair per wave
 constexpr int kCrossWorkers = 120;  // 20 heads x 6 splits of the cross attention, one item per block
@@ -116,13 +125,48 @@ struct Ll {
   unsigned* ctl;
   unsigned tag;
   long long limit;
+  int grp;  // the half of the chip this block runs on (XCDs 0-3: 0, XCDs 4-7: 1)
 };
+
+// The two halves of an MI355X (XCDs 0-3 and 4-7, one I/O die each) reach memory on their own die
+// faster: a tagged word whose 8 KB page is local to both producer and consumer hands off in about
+// 0.4 us, one on the other die's memory in about 0.6 us (one producer and consumer on different dies:
+// 0.5 us either way). Every hand-off word is therefore stored twice, once in a page local to each half
+// (which physical page of the pair 2k, 2k + 1 is local to which half is measured once per workspace,
+// fw_decoder_step_calibrate), and every block polls the copy local to its own half; the consumers of a
+// word also split over two copies.
+__shared__ unsigned hx_groups[kMaxPages / 32];  // bit j: physical page j is local to half 1
+__device__ __forceinline__ int xcc_half() {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return (x & 0xf) >= 4 ? 1 : 0;
+}
+__device__ __forceinline__ uint64_t* hx_area(const unsigned char* ws) {
+  const uintptr_t p = reinterpret_cast<uintptr_t>(ws) + kCtlBytes + kGroupBytes + kCalibBytes;
+  return reinterpret_cast<uint64_t*>((p + kAreaAlign - 1) & ~(kAreaAlign - 1));
+}
+__device__ __forceinline__ const uint64_t* step_area();  // the launch's hand-off area (defined below)
+// Physical word of logical word p (a pointer into the logical layout based at the area) in the copy local
+// to half g.
+__device__ __forceinline__ const uint64_t* hx_copy(const uint64_t* p, int g) {
+  const uint64_t* base = step_area();
+  const size_t w = static_cast<size_t>(p - base);
+  const unsigned pg = static_cast<unsigned>(w / kPageWords) * 2;
+  const unsigned sel = ((hx_groups[pg >> 5] >> (pg & 31)) & 1u) ^ static_cast<unsigned>(g);
+  return base + static_cast<size_t>(pg + sel) * kPageWords + (w % kPageWords);
+}
 
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Stores logical word p in both copies.
 __device__ __forceinline__ void ll_store(uint64_t* p, unsigned tag, unsigned v) {
-  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t* base = const_cast<uint64_t*>(step_area());
+  const size_t w = static_cast<size_t>(p - base);
+  uint64_t* q = base + (w / kPageWords) * 2 * kPageWords + (w % kPageWords);
+  const uint64_t x = (static_cast<uint64_t>(tag) << 32) | v;
+  __hip_atomic_store(q, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + kPageWords, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Payloads of the words buf[idx[k]] (idx[k] < 0: not wanted) once each carries the launch's tag. All
@@ -139,9 +183,12 @@ static_assert(FW_LL_SLEEP >= 0 && FW_LL_SLEEP <= 127, "s_sleep takes 0..127");
 template <int N, bool kPlain = false>
 __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N], unsigned (&val)[N], const Ll& c) {
   uint64_t w[N];
+  const uint64_t* src[N];
   const uint64_t want = static_cast<uint64_t>(c.tag) << 32;
 #pragma unroll
-  for (int k = 0; k < N; ++k) w[k] = idx[k] >= 0 ? (kPlain ? buf[idx[k]] : ll_load(buf + idx[k])) : want;
+  for (int k = 0; k < N; ++k) src[k] = hx_copy(buf + (idx[k] >= 0 ? idx[k] : 0), c.grp);
+#pragma unroll
+  for (int k = 0; k < N; ++k) w[k] = idx[k] >= 0 ? (kPlain ? *src[k] : ll_load(src[k])) : want;
   static_assert(N <= 64, "one pending bit per word");
   unsigned long long pending = 0;
 #pragma unroll
@@ -153,7 +200,7 @@ __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N]
       if (!kPlain || it > 1) __builtin_amdgcn_s_sleep(FW_LL_SLEEP);
 #pragma unroll
       for (int k = 0; k < N; ++k)
-        if (pending >> k & 1ull) w[k] = ll_load(buf + idx[k]);
+        if (pending >> k & 1ull) w[k] = ll_load(src[k]);
       pending = 0;
 #pragma unroll
       for (int k = 0; k < N; ++k)
@@ -1430,7 +1477,6 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     amax = fmaxf(amax, red[2 * kWaves + i]);
     ysq += red[3 * kWaves + i];
   }
-  const float t = amax > 0.f ? amax / static_cast<float>(kQ8YMax) : 1.0f;
   const float tinv = amax > 0.f ? static_cast<float>(kQ8YMax) / amax : 0.f;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -1620,6 +1666,12 @@ struct Sched {
 // The kernel's arguments, re-read from the kernel-argument segment wherever this is called: the
 // pointer is opaque to the compiler, so it cannot hoist argument loads out of the step loop and keep
 // them in registers across a whole step (scalar loads of the segment are cheap; the registers are not).
+// The area from the kernel arguments directly (not through step_args: the compiler may keep the address
+// in two scalar registers across the launch, which every hand-off uses).
+__device__ __forceinline__ const uint64_t* step_area() {
+  return hx_area(((const StepArgs*)__builtin_amdgcn_kernarg_segment_ptr())->ws);  // an address-space cast
+}
+
 __device__ __forceinline__ const StepArgs& step_args() {
   auto p = __builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(p));
@@ -1648,7 +1700,10 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const int tid = threadIdx.x, wave = tid >> 6;
   const int G = gridDim.x;
   unsigned* ctl = reinterpret_cast<unsigned*>(a.ws);
-  uint64_t* regions = reinterpret_cast<uint64_t*>(a.ws + kCtlBytes);
+  uint64_t* regions = const_cast<uint64_t*>(step_area());  // the logical layout's base
+  const int grp = xcc_half();
+  for (int i = tid; i < kMaxPages / 32; i += kStepThreads)
+    hx_groups[i] = reinterpret_cast<const unsigned*>(a.ws + kCtlBytes)[i];  // read after the barrier below
 
   // The launch's tags: the epoch every block reads before it arrives; step st of the launch tags its
   // words epoch + 1 + st. The last block to arrive moves the epoch on by the launch's steps, when no
@@ -1695,7 +1750,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const int n_steps = NV > 1 ? 1 : args.n_steps;
   for (int st = 0; st < n_steps; ++st) {
     const StepArgs& a = step_args();
-    const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit};
+    const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit, grp};
     const Tl tl = Tl::at(st);
     constexpr int kBcastWave = kStepWaves - 1;  // polls the previous step's token
     // Layer 0's q/k/v rows do not depend on the token: the blocks of that run (it starts at block 0) read
@@ -1713,7 +1768,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       if (bt >= 0 && bt < 4) {
         const int idx[1] = {bt};
         unsigned v[1];
-        const Ll prev{ctl, c.tag - 1u, a.spin_limit};
+        const Ll prev{ctl, c.tag - 1u, a.spin_limit, grp};
         ll_wait<1>(bcast, idx, v, prev);
         bcast_lds[bt] = v[0];
       }
@@ -1996,10 +2051,91 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   }
 }
 
+// Which half of the chip each physical page of the hand-off area is local to. The blocks on XCDs 0 and 1
+// (half 0) hand a word of every page back and forth kCalIters times, as do the blocks on XCDs 4 and 5
+// (half 1) on another line of the page; a page is local to the pair that does it faster (about 0.4 against
+// 0.6 us a hand-off). step_calibrate_clear first zeroes the words used (and the latencies), and
+// step_calibrate_finish turns the latencies into the group bits and zeroes the words again. Every wait is
+// bounded: a pair whose partner does not run (another XCD numbering) stops and leaves its latencies 0,
+// and its pages keep bit 0 (each copy of a word then sits on a fixed page of the pair: correct, only not
+// placed by locality).
+constexpr int kCalIters = 16;
+constexpr int kCalWord[2] = {8, 8 + kPageWords / 2};  // one 128-byte line per pair, in the page's halves
+__global__ void __launch_bounds__(256) step_calibrate_clear(unsigned char* ws, int n_pages) {
+  uint64_t* area = hx_area(ws);
+  float* lat = reinterpret_cast<float*>(ws + kCtlBytes + kGroupBytes);
+  for (int j = threadIdx.x; j < n_pages; j += blockDim.x) {
+    area[static_cast<size_t>(j) * kPageWords + kCalWord[0]] = 0;
+    area[static_cast<size_t>(j) * kPageWords + kCalWord[1]] = 0;
+    lat[j] = 0.f;
+    lat[kMaxPages + j] = 0.f;
+  }
+}
+__global__ void __launch_bounds__(64) step_calibrate_kernel(unsigned char* ws, int n_pages) {
+  if (threadIdx.x != 0 || blockIdx.x >= 8) return;
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  xcc &= 0xf;
+  const int pair = (xcc == 0 || xcc == 1) ? 0 : ((xcc == 4 || xcc == 5) ? 1 : -1);
+  if (pair < 0 || blockIdx.x != xcc) return;  // one block per role: block b on XCD b
+  const int me = static_cast<int>(xcc & 1);
+  uint64_t* area = hx_area(ws);
+  float* lat = reinterpret_cast<float*>(ws + kCtlBytes + kGroupBytes) + pair * kMaxPages;
+  constexpr long long kLimit = 200000;  // 2 ms of the 100 MHz clock per wait
+  auto wait_for = [&](const uint64_t* w, uint64_t v) {
+    const long long t0 = wall_clock64();
+    for (int it = 1; __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < v; ++it)
+      if ((it & 15) == 0 && wall_clock64() - t0 > kLimit) return false;
+    return true;
+  };
+  for (int j = 0; j < n_pages; ++j) {
+    uint64_t* w = area + static_cast<size_t>(j) * kPageWords + kCalWord[pair];
+    const long long t0 = wall_clock64();
+    for (int i = 1; i <= kCalIters; ++i) {  // block 0 of the pair stores odd values, block 1 even ones
+      if ((me == 1 || i > 1) && !wait_for(w, 2ull * i - (me == 0 ? 2 : 1))) return;
+      __hip_atomic_store(w, 2ull * i - (me == 0 ? 1 : 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!wait_for(w, 2ull * kCalIters)) return;
+    if (me == 0) lat[j] = static_cast<float>(wall_clock64() - t0);
+  }
+}
+__global__ void __launch_bounds__(256) step_calibrate_finish(unsigned char* ws, int n_pages) {
+  uint64_t* area = hx_area(ws);
+  const float* lat = reinterpret_cast<const float*>(ws + kCtlBytes + kGroupBytes);
+  unsigned* groups = reinterpret_cast<unsigned*>(ws + kCtlBytes);
+  for (int i = threadIdx.x; i < kMaxPages / 32; i += blockDim.x) {
+    unsigned bits = 0;
+    for (int b = 0; b < 32; ++b) {
+      const int j = i * 32 + b;
+      if (j < n_pages && lat[j] > 0.f && lat[kMaxPages + j] > 0.f && lat[kMaxPages + j] < lat[j]) bits |= 1u << b;
+    }
+    groups[i] = bits;
+  }
+  for (int j = threadIdx.x; j < n_pages; j += blockDim.x) {
+    area[static_cast<size_t>(j) * kPageWords + kCalWord[0]] = 0;
+    area[static_cast<size_t>(j) * kPageWords + kCalWord[1]] = 0;
+  }
+}
+
 }  // namespace
 }  // namespace fw
 
 using namespace fw;
+
+static size_t step_logical_pages(int n_layers);
+
+extern "C" int fw_decoder_step_calibrate(void* workspace, int64_t ws_bytes, int n_layers, hipStream_t stream) {
+  const size_t need = fw_decoder_step_workspace_bytes(n_layers);
+  if (!workspace || need == 0 || ws_bytes < static_cast<int64_t>(need))
+    return fw_fail(FW_EINVAL, "decoder_step_calibrate: workspace of %lld bytes, %zu needed for %d layers",
+                   static_cast<long long>(ws_bytes), need, n_layers);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const int n_pages = static_cast<int>(2 * step_logical_pages(n_layers));
+  hipLaunchKernelGGL(step_calibrate_clear, dim3(1), dim3(256), 0, stream, ws, n_pages);
+  hipLaunchKernelGGL(step_calibrate_kernel, dim3(64), dim3(64), 0, stream, ws, n_pages);
+  hipLaunchKernelGGL(step_calibrate_finish, dim3(1), dim3(256), 0, stream, ws, n_pages);
+  return fw_check_launch("decoder_step_calibrate");
+}
 
 extern "C" void* fw_host_alloc_coherent(size_t bytes) {
   void* p = nullptr;
@@ -2014,12 +2150,23 @@ extern "C" void fw_host_free(void* p) {
   if (p) (void)hipHostFree(p);
 }
 
+// Logical pages of the hand-off regions: each layer's regions (for the prompt pass's kPromptLen vectors),
+// the LM head's block maxima and the token broadcast.
+static size_t step_logical_pages(int n_layers) {
+  const size_t words = static_cast<size_t>(n_layers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8;
+  return (words + kPageWords - 1) / kPageWords;
+}
+static_assert(2 * ((static_cast<size_t>(kStepMaxLayers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8 + kPageWords - 1) /
+                   kPageWords) <= kMaxPages,
+              "one group bit per physical page");
+
 extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
   // control words, each layer's hand-off regions (for the prompt pass's kPromptLen vectors), the LM
   // head's per-block maxima, then the words the finalizing block broadcasts to the next step (four, in
   // eight)
-  return kCtlBytes + (static_cast<size_t>(n_layers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8) * sizeof(uint64_t);
+  const size_t pages = step_logical_pages(n_layers);
+  return kCtlBytes + kGroupBytes + kCalibBytes + kAreaAlign + 2 * pages * kPageWords * sizeof(uint64_t);
 }
 
 extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }

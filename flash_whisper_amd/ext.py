@@ -305,10 +305,13 @@ class WhisperExt:
         return (True, '') if st == _lib.FW_OK else (False, self.lib.fw_last_error().decode(errors='replace'))
 
     def decoder_step_workspace(self, n_layers):
-        """Zero-filled workspace of fw_decoder_step_layers for n_layers (one per decoding stream)."""
+        """Zero-filled workspace of fw_decoder_step_layers for n_layers (one per decoding stream), its
+        hand-off pages placed for the device's two halves (fw_decoder_step_calibrate)."""
         nbytes = self.lib.fw_decoder_step_workspace_bytes(int(n_layers))
         _require(nbytes > 0, f'decoder_step: n_layers must be in [1, {self.lib.fw_decoder_step_max_layers()}]')
-        return torch.zeros(nbytes, dtype=torch.uint8, device='cuda')
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device='cuda')
+        self._call('fw_decoder_step_calibrate', ws.data_ptr(), nbytes, int(n_layers), _stream())
+        return ws
 
     def decoder_layer_table(self, layers):
         """The fw_dec_layer array for decoder_step_layers. `layers`: one dict per layer with the tensors

@@ -183,9 +183,19 @@ typedef struct fw_dec_layer {
 /* Bytes of the workspace fw_decoder_step_layers needs for n_layers (0 if n_layers is out of range). The
  * caller allocates it once, zero-filled, 256-byte aligned, and passes the same workspace to every call
  * of one decoding stream; it holds control words (an epoch, an arrival count, an error flag: uint32 at
- * byte offsets 0, 4, 8) and the tagged hand-off vectors. */
+ * byte offsets 0, 4, 8), the placement fw_decoder_step_calibrate records, and the tagged hand-off
+ * vectors. */
 size_t fw_decoder_step_workspace_bytes(int n_layers);
 int fw_decoder_step_max_layers(void);
+
+/* Places the workspace's hand-off words: measures, for each 8 KB page of the workspace's hand-off area,
+ * which half of the device (XCDs 0-3 or 4-7, each with its own I/O die) reaches it faster, and records it
+ * in the workspace. Every hand-off word is kept in two copies, one on a page local to each half, and
+ * each block polls the copy local to it. Call once after allocating the workspace (a few milliseconds of
+ * device time, three launches on `stream`, no host synchronisation); a workspace that is never calibrated
+ * gives the same results, with the copies placed without regard to locality. No counterpart in the
+ * reference: it places the data of the one-launch step. */
+int fw_decoder_step_calibrate(void* workspace, int64_t ws_bytes, int n_layers, hipStream_t stream);
 
 /* The decoder layers of one token in ONE launch: replaces the per-layer op chain of the reference step
  * (custom/model.py:107-121: add_layernorm, the q/k/v, out, cross-q, cross-out, fc1, fc2 F.linear
