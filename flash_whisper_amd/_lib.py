@@ -63,6 +63,7 @@ SIGNATURES = {
     'fw_synth_normal_f16_host': (c_int, [P, c_int64, c_int64, c_uint64, c_uint64, c_float, c_float]),
     'fw_decoder_step_workspace_bytes': (ctypes.c_size_t, [c_int]),
     'fw_decoder_step_calibrate': (c_int, [P, c_int64, c_int, P]),
+    'fw_decoder_step_calibrated': (c_int, [P]),
     'fw_decoder_step_max_layers': (c_int, []),
     'fw_decoder_step_layers': (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_float, P, P, P, c_int64, c_int64,
                                        P]),

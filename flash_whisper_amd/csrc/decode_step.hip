@@ -2061,9 +2061,14 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
 // placed by locality).
 constexpr int kCalIters = 16;
 constexpr int kCalWord[2] = {8, 8 + kPageWords / 2};  // one 128-byte line per pair, in the page's halves
+constexpr int kCalClaim = 16;   // control words 16-23: one claim per XCD (the first block there takes it)
+constexpr int kCalDone = 3;     // control word 3: pages calibrated by both pairs (the last calibration)
 __global__ void __launch_bounds__(256) step_calibrate_clear(unsigned char* ws, int n_pages) {
   uint64_t* area = hx_area(ws);
   float* lat = reinterpret_cast<float*>(ws + kCtlBytes + kGroupBytes);
+  unsigned* ctl = reinterpret_cast<unsigned*>(ws);
+  if (threadIdx.x < 8) ctl[kCalClaim + threadIdx.x] = 0u;
+  if (threadIdx.x == 0) ctl[kCalDone] = 0u;
   for (int j = threadIdx.x; j < n_pages; j += blockDim.x) {
     area[static_cast<size_t>(j) * kPageWords + kCalWord[0]] = 0;
     area[static_cast<size_t>(j) * kPageWords + kCalWord[1]] = 0;
@@ -2072,12 +2077,14 @@ __global__ void __launch_bounds__(256) step_calibrate_clear(unsigned char* ws, i
   }
 }
 __global__ void __launch_bounds__(64) step_calibrate_kernel(unsigned char* ws, int n_pages) {
-  if (threadIdx.x != 0 || blockIdx.x >= 8) return;
+  if (threadIdx.x != 0) return;
   unsigned xcc;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
   xcc &= 0xf;
   const int pair = (xcc == 0 || xcc == 1) ? 0 : ((xcc == 4 || xcc == 5) ? 1 : -1);
-  if (pair < 0 || blockIdx.x != xcc) return;  // one block per role: block b on XCD b
+  unsigned* ctl = reinterpret_cast<unsigned*>(ws);
+  // one block per role: the first of the launch's blocks to land on the XCD (the launch has 8 per XCD)
+  if (pair < 0 || atomicCAS(ctl + kCalClaim + xcc, 0u, 1u) != 0u) return;
   const int me = static_cast<int>(xcc & 1);
   uint64_t* area = hx_area(ws);
   float* lat = reinterpret_cast<float*>(ws + kCtlBytes + kGroupBytes) + pair * kMaxPages;
@@ -2098,6 +2105,7 @@ __global__ void __launch_bounds__(64) step_calibrate_kernel(unsigned char* ws, i
     if (!wait_for(w, 2ull * kCalIters)) return;
     if (me == 0) lat[j] = static_cast<float>(wall_clock64() - t0);
   }
+  if (me == 0) atomicAdd(ctl + kCalDone, 1u);  // 2 once both pairs have measured every page
 }
 __global__ void __launch_bounds__(256) step_calibrate_finish(unsigned char* ws, int n_pages) {
   uint64_t* area = hx_area(ws);
@@ -2135,6 +2143,13 @@ extern "C" int fw_decoder_step_calibrate(void* workspace, int64_t ws_bytes, int 
   hipLaunchKernelGGL(step_calibrate_kernel, dim3(64), dim3(64), 0, stream, ws, n_pages);
   hipLaunchKernelGGL(step_calibrate_finish, dim3(1), dim3(256), 0, stream, ws, n_pages);
   return fw_check_launch("decoder_step_calibrate");
+}
+
+extern "C" int fw_decoder_step_calibrated(const void* workspace) {
+  unsigned v = 0;
+  if (!workspace || hipMemcpy(&v, static_cast<const unsigned*>(workspace) + kCalDone, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess)
+    return fw_fail(FW_EHIP, "decoder_step_calibrated: cannot read the workspace");
+  return v == 2u ? 1 : 0;
 }
 
 extern "C" void* fw_host_alloc_coherent(size_t bytes) {

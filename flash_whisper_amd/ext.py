@@ -313,6 +313,12 @@ class WhisperExt:
         self._call('fw_decoder_step_calibrate', ws.data_ptr(), nbytes, int(n_layers), _stream())
         return ws
 
+    def decoder_step_calibrated(self, ws):
+        """True if the workspace's hand-off pages were placed by a complete calibration (synchronises)."""
+        st = self.lib.fw_decoder_step_calibrated(ws.data_ptr())
+        _require(st >= 0, self.lib.fw_last_error().decode(errors='replace'))
+        return st == 1
+
     def decoder_layer_table(self, layers):
         """The fw_dec_layer array for decoder_step_layers. `layers`: one dict per layer with the tensors
         named in _lib.DEC_LAYER_TENSORS (biases may be None), ln{1,2,3}_eps, and self_k / self_v

@@ -196,6 +196,9 @@ int fw_decoder_step_max_layers(void);
  * gives the same results, with the copies placed without regard to locality. No counterpart in the
  * reference: it places the data of the one-launch step. */
 int fw_decoder_step_calibrate(void* workspace, int64_t ws_bytes, int n_layers, hipStream_t stream);
+/* 1 if the last fw_decoder_step_calibrate of this workspace measured every page (both halves' XCD pairs
+ * ran), 0 if not, FW_EHIP if the workspace cannot be read. Synchronous (a 4-byte device-to-host copy). */
+int fw_decoder_step_calibrated(const void* workspace);
 
 /* The decoder layers of one token in ONE launch: replaces the per-layer op chain of the reference step
  * (custom/model.py:107-121: add_layernorm, the q/k/v, out, cross-q, cross-out, fc1, fc2 F.linear
