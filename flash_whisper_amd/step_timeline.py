@@ -105,7 +105,7 @@ def step_stats(tl, n_layers):
         act = s[:, base + 2] > 0
         if act.any():  # layer 0's self attention inside: each block's times after its input was in
             t_in = s[act, base + 1].astype(np.float64)
-            for k, name in enumerate(('fresh row written', 'first round: wave 0 partial', 'first round merged')):
+            for k, name in enumerate(('fresh row written', 'wave 0 partials (every round)', 'splits merged')):
                 row[('sa', k)] = float(np.median(s[act, TL_SA + k] - t_in)) * TICK_US
             row[('sa', 3)] = float(np.median(s[act, base + 3] - t_in)) * TICK_US
             row[('sa', 4)] = float(np.median(s[act, base + 2] - t_in)) * TICK_US
@@ -146,8 +146,8 @@ def report(rows, n_layers, title):
                          f'{m("in_first"):.2f} | {m("in_med"):.2f} | {m("in_last"):.2f} | {m("out"):.2f} | '
                          f'{m("dur"):.2f} | {m("wait"):.2f} | {m("work"):.2f} / {m("work_max"):.2f} |')
     lines += ['', '| Layer 0 self attention, after its input (median block) | us |', '|---|---:|']
-    for k, name in enumerate(('fresh row written', 'first round: wave 0 partial', 'first round merged',
-                              'every round merged', 'output stored')):
+    for k, name in enumerate(('fresh row written', 'wave 0 partials (every round)', 'splits merged',
+                              'combined (or merged, more than 2 splits)', 'output stored')):
         if any(('sa', k) in r for r in rows):
             lines.append(f'| {name} | {statistics.median(r[("sa", k)] for r in rows if ("sa", k) in r):.2f} |')
     lines += ['', '| LM head point | median block | last block |', '|---|---:|---:|']
