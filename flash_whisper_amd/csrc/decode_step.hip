@@ -237,7 +237,7 @@ __device__ __forceinline__ unsigned half_bits(_Float16 x) { return __builtin_bit
 #endif
 constexpr int kTlLayers = 4, kTlSlots = 160, kTlLm = 1 + kTlLayers * 8 * 4;
 enum TlLm { kTlArrive = 0, kTlY, kTlDigits, kTlRegScored, kTlResScored, kTlScored, kTlCand, kTlMaxStored,
-            kTlFinGathered, kTlFinStored };
+            kTlFinGathered, kTlFinStored, kTlCaught };
 constexpr int kTlSa = kTlLm + 12;
 enum TlSa { kTlSaRow = 0, kTlSaPartial, kTlSaMerged, kTlSaWeights };
 static_assert(kTlSa + kTlSaWeights < kTlSlots, "timeline slots");
@@ -1225,6 +1225,9 @@ constexpr int kLmMaxBatches = 8;                              // per block: ceil
 #ifndef FW_EMBED_WARM
 #define FW_EMBED_WARM 1
 #endif
+#ifndef FW_LM_CATCH_FIRST
+#define FW_LM_CATCH_FIRST 0  // every block adds the last fc2 output before requesting its table rows
+#endif
 #ifndef FW_QKV_WARM
 #define FW_QKV_WARM 1  // layer 0's q/k/v rows read into L2 while the token is awaited
 #endif
@@ -1426,7 +1429,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   constexpr int kBufs = kLmBufs;
   Batch bt[kBufs];
   tl.mark(kTlLm + kTlArrive);
-  if (share.late) {  // block-uniform
+  if (FW_LM_CATCH_FIRST || share.late) {  // block-uniform
     // The blocks that ran the last fc2 arrive last, when its output is already stored: every thread adds
     // it first (one poll round, not queued behind this block's table loads), then the table is requested.
     resid_catch_up<kStepThreads, NV, NV - 1>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp);
@@ -1443,6 +1446,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     resid_catch_up<kWave, NV, NV - 1>(h_res, applied, 3 * a.n_layers + 1, regions, a, c, sp, lane);
   }
   applied = 3 * a.n_layers + 1;
+  tl.mark(kTlLm + kTlCaught);  // thread 0: wave 0's part (every contribution added in its waves)
   __syncthreads();
   ln_final(h_res + (NV - 1) * kHidden, s.gamma, s.beta, H.eps, y_lds, red);
   __syncthreads();
@@ -1528,14 +1532,15 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     score(row, row < rb, bt);
     if (k + kBufs < nb) load(k + kBufs, bt);
   };
-  if (wv < kLmRowWaves) {
+  if (!FW_LM_CATCH_FIRST && wv < kLmRowWaves) {
 #pragma unroll
     for (int k = 0; k < kBufs; ++k)
       if (k < nb) score_batch(k, bt[k]);
   }
   tl.mark(kTlLm + kTlRegScored);
   // the resident rows, 4 per wave at a time, by all 8 waves while the next HBM batches are in flight
-  // (scoring them first, before the batches already in registers, measured 1.4 us a step slower)
+  // (scoring them first, before batches that arrived at the block long before, measured 1.4 us a step
+  // slower; with the batches requested after the catch-up they go first)
   for (int g = wv; 4 * g < n_res; g += kStepWaves) {  // wave-uniform
     const int j = 4 * g + rsel, jc = min(j, n_res - 1);
     Batch rt;
@@ -1548,7 +1553,7 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   tl.mark(kTlLm + kTlResScored);
   if (wv < kLmRowWaves) {
 #pragma unroll
-    for (int k = kBufs; k < kLmMaxBatches; ++k)
+    for (int k = FW_LM_CATCH_FIRST ? 0 : kBufs; k < kLmMaxBatches; ++k)
       if (k < nb) score_batch(k, bt[k % kBufs]);
   }
   tl.mark(kTlLm + kTlScored);

@@ -36,7 +36,7 @@ TL_LAYERS, TL_LM, TL_SA = 4, 129, 141
 TL_CLK = TL_SA + 8  # shader clock at the step's start and end, wall clock at its end
 LM_POINTS = ('arrived', 'final LN done', 'y digits ready', 'first HBM batches scored', 'resident rows scored',
              'all rows scored', 'candidates listed', 'block maximum stored', 'every block maximum gathered',
-             'token and state stored (last block)')
+             'token and state stored (last block)', 'residual caught up (thread 0; before the final LN)')
 
 
 def tl_phase(layer, phase):
