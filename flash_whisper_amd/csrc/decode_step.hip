@@ -62,9 +62,14 @@ constexpr int kLayerWords = kOffMlpOut + kVecWords;
 constexpr int kCtlBytes = 256;
 constexpr int kGroupBytes = 256;
 constexpr int kPageWords = 1024;               // 8 KB pages: memory alternates between the two halves of
-constexpr int kMaxPages = kGroupBytes * 8;     // the chip every 8 KB
-constexpr int kCalibBytes = 2 * kMaxPages * 4;  // fp32 latency per physical page, for two pairs of XCDs
-constexpr size_t kAreaAlign = 16384;
+constexpr int kMaxPages = kGroupBytes * 8;     // the chip every 8 KB (logical pages: one bit each)
+constexpr int kCalibBytes = 2 * kMaxPages * 4;  // fp32 latency per logical page, for two pairs of XCDs
+#ifndef FW_HX_PER_HALF
+#define FW_HX_PER_HALF 1  // copies of every hand-off page on each half (1, 2 or 4; XCDs share them in turn)
+#endif
+static_assert(FW_HX_PER_HALF == 1 || FW_HX_PER_HALF == 2 || FW_HX_PER_HALF == 4, "FW_HX_PER_HALF");
+constexpr int kCopies = 2 * FW_HX_PER_HALF;    // physical pages per logical page, alternating halves
+constexpr size_t kAreaAlign = static_cast<size_t>(kCopies) * kPageWords * 8;  // a group never crosses 2 MB
 // Worker counts of the phases that need few blocks (pairs of rows / items are spread over them).
 constexpr int kVecWorkers = 80;    // 640 row pairs: one pair per wave
 constexpr int kCrossWorkers = 120;  // 20 heads x 6 splits of the cross attention, one item per block
@@ -125,48 +130,52 @@ struct Ll {
   unsigned* ctl;
   unsigned tag;
   long long limit;
-  int grp;  // the half of the chip this block runs on (XCDs 0-3: 0, XCDs 4-7: 1)
+  int xcc;  // the XCD this block runs on (XCDs 0-3: half 0, XCDs 4-7: half 1)
 };
 
 // The two halves of an MI355X (XCDs 0-3 and 4-7, one I/O die each) reach memory on their own die
 // faster: a tagged word whose 8 KB page is local to both producer and consumer hands off in about
 // 0.4 us, one on the other die's memory in about 0.6 us (one producer and consumer on different dies:
-// 0.5 us either way). Every hand-off word is therefore stored twice, once in a page local to each half
-// (which physical page of the pair 2k, 2k + 1 is local to which half is measured once per workspace,
-// fw_decoder_step_calibrate), and every block polls the copy local to its own half; the consumers of a
-// word also split over two copies.
-__shared__ unsigned hx_groups[kMaxPages / 32];  // bit j: physical page j is local to half 1
-__device__ __forceinline__ int xcc_half() {
+// 0.5 us either way). Memory alternates between the dies every 8 KB, so logical page k of the hand-off
+// area is stored in kCopies consecutive physical pages, kCopies k .. kCopies k + kCopies - 1, every
+// other one on each die; which die the first is on is measured once per workspace
+// (fw_decoder_step_calibrate). Every hand-off word is written to all of them, and each block polls
+// one on its own die (the XCDs of a half take its copies in turn): the consumers of a word split over
+// the copies.
+__shared__ unsigned hx_groups[kMaxPages / 32];  // bit k: the first physical page of logical page k is on half 1
+__device__ __forceinline__ int xcc_id() {
   unsigned x;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-  return (x & 0xf) >= 4 ? 1 : 0;
+  return static_cast<int>(x & 7u);
 }
 __device__ __forceinline__ uint64_t* hx_area(const unsigned char* ws) {
   const uintptr_t p = reinterpret_cast<uintptr_t>(ws) + kCtlBytes + kGroupBytes + kCalibBytes;
   return reinterpret_cast<uint64_t*>((p + kAreaAlign - 1) & ~(kAreaAlign - 1));
 }
 __device__ __forceinline__ const uint64_t* step_area();  // the launch's hand-off area (defined below)
-// Physical word of logical word p (a pointer into the logical layout based at the area) in the copy local
-// to half g.
-__device__ __forceinline__ const uint64_t* hx_copy(const uint64_t* p, int g) {
+// Physical word of logical word p (a pointer into the logical layout based at the area) in the copy that
+// XCD x polls: on x's half, the (x mod FW_HX_PER_HALF)-th of that half's pages of the group.
+__device__ __forceinline__ const uint64_t* hx_copy(const uint64_t* p, int x) {
   const uint64_t* base = step_area();
   const size_t w = static_cast<size_t>(p - base);
-  const unsigned pg = static_cast<unsigned>(w / kPageWords) * 2;
-  const unsigned sel = ((hx_groups[pg >> 5] >> (pg & 31)) & 1u) ^ static_cast<unsigned>(g);
-  return base + static_cast<size_t>(pg + sel) * kPageWords + (w % kPageWords);
+  const unsigned k = static_cast<unsigned>(w / kPageWords);
+  const unsigned half = static_cast<unsigned>(x) >> 2, slot = static_cast<unsigned>(x) % FW_HX_PER_HALF;
+  const unsigned sel = ((hx_groups[k >> 5] >> (k & 31)) & 1u) ^ half;
+  return base + (static_cast<size_t>(k) * kCopies + 2 * slot + sel) * kPageWords + (w % kPageWords);
 }
 
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Stores logical word p in both copies.
+// Stores logical word p in every copy.
 __device__ __forceinline__ void ll_store(uint64_t* p, unsigned tag, unsigned v) {
   uint64_t* base = const_cast<uint64_t*>(step_area());
   const size_t w = static_cast<size_t>(p - base);
-  uint64_t* q = base + (w / kPageWords) * 2 * kPageWords + (w % kPageWords);
+  uint64_t* q = base + (w / kPageWords) * kCopies * kPageWords + (w % kPageWords);
   const uint64_t x = (static_cast<uint64_t>(tag) << 32) | v;
-  __hip_atomic_store(q, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + kPageWords, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j)
+    __hip_atomic_store(q + j * kPageWords, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Payloads of the words buf[idx[k]] (idx[k] < 0: not wanted) once each carries the launch's tag. All
@@ -186,7 +195,7 @@ __device__ __forceinline__ void ll_wait(const uint64_t* buf, const int (&idx)[N]
   const uint64_t* src[N];
   const uint64_t want = static_cast<uint64_t>(c.tag) << 32;
 #pragma unroll
-  for (int k = 0; k < N; ++k) src[k] = hx_copy(buf + (idx[k] >= 0 ? idx[k] : 0), c.grp);
+  for (int k = 0; k < N; ++k) src[k] = hx_copy(buf + (idx[k] >= 0 ? idx[k] : 0), c.xcc);
 #pragma unroll
   for (int k = 0; k < N; ++k) w[k] = idx[k] >= 0 ? (kPlain ? *src[k] : ll_load(src[k])) : want;
   static_assert(N <= 64, "one pending bit per word");
@@ -1706,7 +1715,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const int G = gridDim.x;
   unsigned* ctl = reinterpret_cast<unsigned*>(a.ws);
   uint64_t* regions = const_cast<uint64_t*>(step_area());  // the logical layout's base
-  const int grp = xcc_half();
+  const int xcc = xcc_id();
   for (int i = tid; i < kMaxPages / 32; i += kStepThreads)
     hx_groups[i] = reinterpret_cast<const unsigned*>(a.ws + kCtlBytes)[i];  // read after the barrier below
 
@@ -1755,7 +1764,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   const int n_steps = NV > 1 ? 1 : args.n_steps;
   for (int st = 0; st < n_steps; ++st) {
     const StepArgs& a = step_args();
-    const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit, grp};
+    const Ll c{ctl, epoch + 1u + static_cast<unsigned>(st), a.spin_limit, xcc};
     const Tl tl = Tl::at(st);
     constexpr int kBcastWave = kStepWaves - 1;  // polls the previous step's token
     // Layer 0's q/k/v rows do not depend on the token: the blocks of that run (it starts at block 0) read
@@ -1773,7 +1782,7 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
       if (bt >= 0 && bt < 4) {
         const int idx[1] = {bt};
         unsigned v[1];
-        const Ll prev{ctl, c.tag - 1u, a.spin_limit, grp};
+        const Ll prev{ctl, c.tag - 1u, a.spin_limit, xcc};
         ll_wait<1>(bcast, idx, v, prev);
         bcast_lds[bt] = v[0];
       }
@@ -2056,10 +2065,10 @@ __global__ void __launch_bounds__(kStepThreads) decoder_step_kernel(StepArgs arg
   }
 }
 
-// Which half of the chip each physical page of the hand-off area is local to. The blocks on XCDs 0 and 1
-// (half 0) hand a word of every page back and forth kCalIters times, as do the blocks on XCDs 4 and 5
-// (half 1) on another line of the page; a page is local to the pair that does it faster (about 0.4 against
-// 0.6 us a hand-off). step_calibrate_clear first zeroes the words used (and the latencies), and
+// Which half of the chip the first physical page of each logical page of the hand-off area is local to
+// (the group's other pages alternate from it). The blocks on XCDs 0 and 1 (half 0) hand a word of that
+// page back and forth kCalIters times, as do the blocks on XCDs 4 and 5 (half 1) on another line of the
+// page; a page is local to the pair that does it faster (about 0.4 against 0.6 us a hand-off). step_calibrate_clear first zeroes the words used (and the latencies), and
 // step_calibrate_finish turns the latencies into the group bits and zeroes the words again. Every wait is
 // bounded: a pair whose partner does not run (another XCD numbering) stops and leaves its latencies 0,
 // and its pages keep bit 0 (each copy of a word then sits on a fixed page of the pair: correct, only not
@@ -2075,8 +2084,8 @@ __global__ void __launch_bounds__(256) step_calibrate_clear(unsigned char* ws, i
   if (threadIdx.x < 8) ctl[kCalClaim + threadIdx.x] = 0u;
   if (threadIdx.x == 0) ctl[kCalDone] = 0u;
   for (int j = threadIdx.x; j < n_pages; j += blockDim.x) {
-    area[static_cast<size_t>(j) * kPageWords + kCalWord[0]] = 0;
-    area[static_cast<size_t>(j) * kPageWords + kCalWord[1]] = 0;
+    area[static_cast<size_t>(j) * kCopies * kPageWords + kCalWord[0]] = 0;
+    area[static_cast<size_t>(j) * kCopies * kPageWords + kCalWord[1]] = 0;
     lat[j] = 0.f;
     lat[kMaxPages + j] = 0.f;
   }
@@ -2101,7 +2110,7 @@ __global__ void __launch_bounds__(64) step_calibrate_kernel(unsigned char* ws, i
     return true;
   };
   for (int j = 0; j < n_pages; ++j) {
-    uint64_t* w = area + static_cast<size_t>(j) * kPageWords + kCalWord[pair];
+    uint64_t* w = area + static_cast<size_t>(j) * kCopies * kPageWords + kCalWord[pair];
     const long long t0 = wall_clock64();
     for (int i = 1; i <= kCalIters; ++i) {  // block 0 of the pair stores odd values, block 1 even ones
       if ((me == 1 || i > 1) && !wait_for(w, 2ull * i - (me == 0 ? 2 : 1))) return;
@@ -2125,8 +2134,8 @@ __global__ void __launch_bounds__(256) step_calibrate_finish(unsigned char* ws, 
     groups[i] = bits;
   }
   for (int j = threadIdx.x; j < n_pages; j += blockDim.x) {
-    area[static_cast<size_t>(j) * kPageWords + kCalWord[0]] = 0;
-    area[static_cast<size_t>(j) * kPageWords + kCalWord[1]] = 0;
+    area[static_cast<size_t>(j) * kCopies * kPageWords + kCalWord[0]] = 0;
+    area[static_cast<size_t>(j) * kCopies * kPageWords + kCalWord[1]] = 0;
   }
 }
 
@@ -2143,7 +2152,7 @@ extern "C" int fw_decoder_step_calibrate(void* workspace, int64_t ws_bytes, int 
     return fw_fail(FW_EINVAL, "decoder_step_calibrate: workspace of %lld bytes, %zu needed for %d layers",
                    static_cast<long long>(ws_bytes), need, n_layers);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  const int n_pages = static_cast<int>(2 * step_logical_pages(n_layers));
+  const int n_pages = static_cast<int>(step_logical_pages(n_layers));  // the first page of each group
   hipLaunchKernelGGL(step_calibrate_clear, dim3(1), dim3(256), 0, stream, ws, n_pages);
   hipLaunchKernelGGL(step_calibrate_kernel, dim3(64), dim3(64), 0, stream, ws, n_pages);
   hipLaunchKernelGGL(step_calibrate_finish, dim3(1), dim3(256), 0, stream, ws, n_pages);
@@ -2176,9 +2185,9 @@ static size_t step_logical_pages(int n_layers) {
   const size_t words = static_cast<size_t>(n_layers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8;
   return (words + kPageWords - 1) / kPageWords;
 }
-static_assert(2 * ((static_cast<size_t>(kStepMaxLayers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8 + kPageWords - 1) /
-                   kPageWords) <= kMaxPages,
-              "one group bit per physical page");
+static_assert((static_cast<size_t>(kStepMaxLayers) * kPromptLen * kLayerWords + 2 * kMaxGrid + 8 + kPageWords - 1) /
+                  kPageWords <= kMaxPages,
+              "one group bit per logical page");
 
 extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   if (n_layers < 1 || n_layers > kStepMaxLayers) return 0;
@@ -2186,7 +2195,7 @@ extern "C" size_t fw_decoder_step_workspace_bytes(int n_layers) {
   // head's per-block maxima, then the words the finalizing block broadcasts to the next step (four, in
   // eight)
   const size_t pages = step_logical_pages(n_layers);
-  return kCtlBytes + kGroupBytes + kCalibBytes + kAreaAlign + 2 * pages * kPageWords * sizeof(uint64_t);
+  return kCtlBytes + kGroupBytes + kCalibBytes + kAreaAlign + kCopies * pages * kPageWords * sizeof(uint64_t);
 }
 
 extern "C" int fw_decoder_step_max_layers(void) { return kStepMaxLayers; }
