@@ -507,18 +507,26 @@ __device__ __forceinline__ void split_wave_partial(const uint4 (&kr)[MAXP], cons
 template <int NW>
 __device__ __forceinline__ void split_merge(const float* wm, const float* wl, const float (*wacc)[kHeadDim], int d,
                                             float& m, float& l, float& o) {
+  // every wave's values first (one batch of LDS reads), then the merge with selects: a branch per wave
+  // made each read a round trip of its own
+  float pm[NW], pl[NW], pa[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    pm[w] = wm[w];
+    pl[w] = wl[w];
+    pa[w] = wacc[w][d];
+  }
   m = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < NW; ++w) m = fmaxf(m, wm[w]);
+  for (int w = 0; w < NW; ++w) m = fmaxf(m, pm[w]);
   l = 0.f;
   o = 0.f;
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    if (wl[w] > 0.f) {
-      const float wgt = __expf(wm[w] - m);
-      l = fmaf(wl[w], wgt, l);
-      o = fmaf(wacc[w][d], wgt, o);
-    }
+    const float wgt = __expf(pm[w] - m);
+    const bool live = pl[w] > 0.f;
+    l = live ? fmaf(pl[w], wgt, l) : l;
+    o = live ? fmaf(pa[w], wgt, o) : o;
   }
 }
 

@@ -238,7 +238,8 @@ __device__ __forceinline__ unsigned half_bits(_Float16 x) { return __builtin_bit
 // has slots tl_phase(l, p) + {0 entered and its loads issued, 1 input in (after the prologue), 2 output
 // stored, 3 the cross attention's combine stored, the self attention's split rounds done, or a
 // LayerNorm phase's residual contributions added (thread 0's share)}, the LM
-// head the slots from kTlLm on (TlLm), layer 0's self attention a few more from kTlSa on (TlSa). In the
+// head the slots from kTlLm on (TlLm), layer 0's self attention a few more from kTlSa on (TlSa) and
+// each of its waves' partials from kTlWave on. In the
 // product build every mark is empty.
 // ---------------------------------------------------------------------------------------------
 #ifndef FW_STEP_TIMELINE
@@ -248,13 +249,16 @@ constexpr int kTlLayers = 4, kTlSlots = 160, kTlLm = 1 + kTlLayers * 8 * 4;
 enum TlLm { kTlArrive = 0, kTlY, kTlDigits, kTlRegScored, kTlResScored, kTlScored, kTlCand, kTlMaxStored,
             kTlFinGathered, kTlFinStored, kTlCaught };
 constexpr int kTlSa = kTlLm + 12;
-enum TlSa { kTlSaRow = 0, kTlSaPartial, kTlSaMerged, kTlSaWeights };
-static_assert(kTlSa + kTlSaWeights < kTlSlots, "timeline slots");
+enum TlSa { kTlSaRow = 0, kTlSaPartial, kTlSaMerged, kTlSaBarrier };
+static_assert(kTlSa + kTlSaBarrier < kTlSlots, "timeline slots");
 // The shader clock (s_memtime) at the step's start and end and the wall clock at its end: their ratio
 // to the wall clock gives the core clock the step ran at.
 constexpr int kTlClk = kTlSa + 8;
 enum TlClk { kTlClkStart = 0, kTlClkEnd, kTlClkWallEnd };
 static_assert(kTlClk + kTlClkWallEnd < kTlSlots, "timeline slots");
+// Layer 0's self attention: each wave's partials done (lane 0 of wave w marks slot kTlWave + w).
+constexpr int kTlWave = kTlClk + 3;
+static_assert(kTlWave + kStepWaves <= kTlSlots, "timeline slots");
 __host__ __device__ constexpr int tl_phase(int l, int p) { return 1 + (l * 8 + (p - 1)) * 4; }
 #if FW_STEP_TIMELINE
 __device__ long long* g_step_tl;  // [steps][G][kTlSlots], or null
@@ -269,6 +273,9 @@ struct Tl {
   }
   __device__ void phase(int l, int ph, int k) const {
     if (l < kTlLayers) mark(tl_phase(l, ph) + k);
+  }
+  __device__ void mark_wave(int s) const {
+    if (p && (threadIdx.x & (kWave - 1)) == 0) tl_lds[s + threadIdx.x / kWave] = wall_clock64();
   }
   __device__ void mark_shader_clock(int s) const {
     if (p && threadIdx.x == 0) tl_lds[s] = static_cast<long long>(__builtin_amdgcn_s_memtime());
@@ -293,6 +300,7 @@ struct Tl {
 #else
   __device__ void mark(int) const {}
   __device__ void phase(int, int, int) const {}
+  __device__ void mark_wave(int) const {}
   __device__ void mark_shader_clock(int) const {}
   __device__ void flush() const {}
   __device__ static Tl at(int) { return {}; }
@@ -667,22 +675,25 @@ struct AttnLds {
 template <typename Get>
 __device__ __forceinline__ void combine_store(int ns, int d, uint64_t* out, unsigned tag, Get get) {
   constexpr int S = kMaxCombineSplits;
+  // every split's values first (get may read LDS: one batch of reads, not one round trip per split)
+  float pm[S], pl[S], pa[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    get(s, pm[s], pl[s], pa[s]);
+    if (s >= ns) {
+      pm[s] = -INFINITY;
+      pl[s] = pa[s] = 0.f;
+    }
+  }
   float m = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < S; ++s)
-    if (s < ns) {
-      float pm, pl, pa;
-      get(s, pm, pl, pa);
-      m = fmaxf(m, pm);
-    }
+  for (int s = 0; s < S; ++s) m = fmaxf(m, pm[s]);
   float den = 0.f, num = 0.f;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    float pm = -INFINITY, pl = 0.f, pa = 0.f;
-    if (s < ns) get(s, pm, pl, pa);
-    const float w = pl > 0.f ? __expf(pm - m) : 0.f;
-    den = fmaf(pl, w, den);
-    if (w != 0.f) num = fmaf(pa, w, num);
+    const float w = pl[s] > 0.f ? __expf(pm[s] - m) : 0.f;
+    den = fmaf(pl[s], w, den);
+    num = w != 0.f ? fmaf(pa[s], w, num) : num;
   }
   const unsigned lo = half_bits(f2h(num / den));
   const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_ds_swizzle(static_cast<int>(lo), 0x041F));  // lane ^ 1
@@ -859,8 +870,10 @@ __device__ __forceinline__ void self_attn_head(const Ll& c, int head, int z, int
                                  &wl[split * 4 + hw], wacc + (split * 4 + hw) * kHeadDim);
       }
     }
+    if (tl0) tl.mark_wave(kTlWave);
     if (tl0) tl.mark(kTlSa + kTlSaPartial);
     __syncthreads();
+    if (tl0) tl.mark(kTlSa + kTlSaBarrier);
     using WaccRow = const float (*)[kHeadDim];
     if (ns <= 2) {  // block-uniform: thread d merges both splits itself and combines them, no second barrier
       if (tid < kHeadDim) {

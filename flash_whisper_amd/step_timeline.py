@@ -34,6 +34,7 @@ PHASES = ('LN1 + q/k/v', 'self attention', 'out', 'LN2 + cross q', 'cross attent
           'LN3 + fc1 + GELU', 'fc2')
 TL_LAYERS, TL_LM, TL_SA = 4, 129, 141
 TL_CLK = TL_SA + 8  # shader clock at the step's start and end, wall clock at its end
+TL_WAVE = TL_CLK + 3  # layer 0's self attention: each wave's partials done
 LM_POINTS = ('arrived', 'final LN done', 'y digits ready', 'first HBM batches scored', 'resident rows scored',
              'all rows scored', 'candidates listed', 'block maximum stored', 'every block maximum gathered',
              'token and state stored (last block)', 'residual caught up (thread 0; before the final LN)')
@@ -107,7 +108,13 @@ def step_stats(tl, n_layers):
             t_in = s[act, base + 1].astype(np.float64)
             for k, name in enumerate(('fresh row written', 'wave 0 partials (every round)', 'splits merged')):
                 row[('sa', k)] = float(np.median(s[act, TL_SA + k] - t_in)) * TICK_US
+            if (s[act, TL_SA + 3] > 0).all():
+                row[('sa', 5)] = float(np.median(s[act, TL_SA + 3] - t_in)) * TICK_US
             row[('sa', 3)] = float(np.median(s[act, base + 3] - t_in)) * TICK_US
+            for w in range(8):
+                v = s[act, TL_WAVE + w]
+                if (v > 0).all():
+                    row[('wave', w)] = float(np.median(v - t_in)) * TICK_US
             row[('sa', 4)] = float(np.median(s[act, base + 2] - t_in)) * TICK_US
         ok = (s[:, TL_CLK] > 0) & (s[:, TL_CLK + 2] > s[:, 0]) & (s[:, 0] > 0)
         if ok.any():  # shader clock ticks over wall-clock ticks (100 MHz), per block: the core clock in MHz
@@ -147,9 +154,16 @@ def report(rows, n_layers, title):
                          f'{m("dur"):.2f} | {m("wait"):.2f} | {m("work"):.2f} / {m("work_max"):.2f} |')
     lines += ['', '| Layer 0 self attention, after its input (median block) | us |', '|---|---:|']
     for k, name in enumerate(('fresh row written', 'wave 0 partials (every round)', 'splits merged',
-                              'combined (or merged, more than 2 splits)', 'output stored')):
+                              'combined (or merged, more than 2 splits)', 'output stored',
+                              'past the barrier after the partials')):
         if any(('sa', k) in r for r in rows):
             lines.append(f'| {name} | {statistics.median(r[("sa", k)] for r in rows if ("sa", k) in r):.2f} |')
+    waves = [w for w in range(8) if any(('wave', w) in r for r in rows)]
+    if waves:
+        lines += ['', '| Layer 0 self attention: wave w\'s partials done, after the input (median block) | ' +
+                  ' | '.join(f'w{w}' for w in waves) + ' |', '|---|' + '---:|' * len(waves),
+                  '| us | ' + ' | '.join(f'{statistics.median(r[("wave", w)] for r in rows if ("wave", w) in r):.2f}'
+                                         for w in waves) + ' |']
     lines += ['', '| LM head point | median block | last block |', '|---|---:|---:|']
     for k, name in enumerate(LM_POINTS):
         key = ('lm', k)
