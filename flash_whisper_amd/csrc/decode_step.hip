@@ -550,19 +550,30 @@ __device__ __forceinline__ void resid_catch_up(_Float16* h_res, int& applied, in
       }
       unsigned v[kGroup * kPer];
       ll_wait<kGroup * kPer>(regions, idx, v, c);
+      // the thread's pairs read first (one batch of LDS reads: a branch per pair made each read a round
+      // trip of its own), the contributions added in order (every add rounds to fp16), then stored
+      h2v hv[kPer];
 #pragma unroll
-      for (int g = 0; g < kGroup; ++g) {  // in order: every add rounds to fp16
+      for (int k = 0; k < kPer; ++k) {
+        const int w = t + k * kThreads;
+        hv[k] = h2[w < kWords ? w : 0];
+      }
+#pragma unroll
+      for (int g = 0; g < kGroup; ++g) {
+        if (g >= ng) break;  // uniform
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
-          if (idx[g * kPer + k] < 0) continue;
-          const int w = t + k * kThreads;
-          const h2v hp = h2[w];
           const h2v xp = __builtin_bit_cast(h2v, v[g * kPer + k]);
           h2v o;
-          o.x = f2h(h2f(hp.x) + h2f(xp.x));
-          o.y = f2h(h2f(hp.y) + h2f(xp.y));
-          h2[w] = o;
+          o.x = f2h(h2f(hv[k].x) + h2f(xp.x));
+          o.y = f2h(h2f(hv[k].y) + h2f(xp.y));
+          hv[k] = o;
         }
+      }
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int w = t + k * kThreads;
+        if (w < kWords) h2[w] = hv[k];
       }
       applied += ng;
     }
