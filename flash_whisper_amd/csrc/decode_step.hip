@@ -1628,12 +1628,13 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
   }
   if (sub32 == 0) s.best[wave * 2 + rsel32] = mine;
   __syncthreads();
-  if (tid == 0) {
-    unsigned long long m = 0;
-#pragma unroll
-    for (int i = 0; i < kStepWaves * 2; ++i) m = s.best[i] > m ? s.best[i] : m;
-    ll_store(maxima + 2 * b, c.tag, static_cast<unsigned>(m));
-    ll_store(maxima + 2 * b + 1, c.tag, static_cast<unsigned>(m >> 32));
+  if (wv == 0) {  // lanes 0-15 take one slot each, reduced across lanes (no chain of LDS reads)
+    unsigned long long m = lane < kStepWaves * 2 ? s.best[lane] : 0ull;
+    m = u64_group_max<kStepWaves * 2>(m);
+    if (lane == 0) {
+      ll_store(maxima + 2 * b, c.tag, static_cast<unsigned>(m));
+      ll_store(maxima + 2 * b + 1, c.tag, static_cast<unsigned>(m >> 32));
+    }
   }
   tl.mark(kTlLm + kTlMaxStored);
   if (b != fin_block()) return;  // block-uniform
@@ -1648,18 +1649,12 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     const unsigned long long x = (static_cast<unsigned long long>(v[1]) << 32) | v[0];
     m = x > m ? x : m;
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const unsigned lo = __shfl_xor(static_cast<unsigned>(m), o), hi = __shfl_xor(static_cast<unsigned>(m >> 32), o);
-    const unsigned long long x = (static_cast<unsigned long long>(hi) << 32) | lo;
-    m = x > m ? x : m;
-  }
+  m = u64_group_max<kWave>(m);
   if (lane == 0) s.fin[wave] = m;
   __syncthreads();
   tl.mark(kTlLm + kTlFinGathered);
+  if (wv == 0) m = u64_group_max<kStepWaves>(lane < kStepWaves ? s.fin[lane] : 0ull);
   if (tid == 0) {
-#pragma unroll
-    for (int i = 0; i < kStepWaves; ++i) m = s.fin[i] > m ? s.fin[i] : m;
     const FinArgs fin{H.tokens, a.state, a.cur, a.max_pos};
     const FinOut o = finalize_known(m, n_tok, sp.pos_raw + NV - 1, fin);
     bool stop = false;

@@ -36,9 +36,8 @@ __device__ __forceinline__ float round_h(float x) { return static_cast<float>(st
 // the two results hold, lane by lane, the value and its partner. Every step combines the same two
 // operands as a __shfl_xor step would.
 template <int O>
-__device__ __forceinline__ float xor_lane(float v) {
+__device__ __forceinline__ int xor_lane_bits(int x) {
   static_assert(O == 1 || O == 2 || O == 4 || O == 8, "DPP partner for O <= 8");
-  const int x = __builtin_bit_cast(int, v);
   int r;
   if constexpr (O == 1) {
     r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
@@ -51,7 +50,11 @@ __device__ __forceinline__ float xor_lane(float v) {
     r = __builtin_amdgcn_update_dpp(0, x, 0x108, 0xF, 0x3, false);  // banks 0, 1 <- lane + 8 (row_shl:8)
     r = __builtin_amdgcn_update_dpp(r, x, 0x118, 0xF, 0xC, false);  // banks 2, 3 <- lane - 8 (row_shr:8)
   }
-  return __builtin_bit_cast(float, r);
+  return r;
+}
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+  return __builtin_bit_cast(float, xor_lane_bits<O>(__builtin_bit_cast(int, v)));
 }
 // {v, v[l ^ O]} in some order per lane, for O = 16 or 32. Issued as inline assembly: the compiler's
 // builtins for these swaps hand back the first register for both results. The leading s_nop covers
@@ -85,6 +88,37 @@ __device__ __forceinline__ float xor_max(float v) {
   } else {
     return fmaxf(v, xor_lane<O>(v));
   }
+}
+
+// Maximum of a 64-bit key over kWidth consecutive lanes (a power of two <= 64; every lane of the wave
+// active) by the butterflies above, both halves of a key moved by the same exchange: no LDS round trips
+// (a loop over keys in LDS, or ds_bpermute shuffles, costs one per step).
+template <int O>
+__device__ __forceinline__ unsigned long long u64_xor_max(unsigned long long v) {
+  const int lo = static_cast<int>(static_cast<unsigned>(v)), hi = static_cast<int>(static_cast<unsigned>(v >> 32));
+  unsigned long long a, b;
+  if constexpr (O >= 16) {
+    float alo, blo, ahi, bhi;
+    xor_pair<O>(__builtin_bit_cast(float, lo), alo, blo);
+    xor_pair<O>(__builtin_bit_cast(float, hi), ahi, bhi);
+    a = (static_cast<unsigned long long>(__builtin_bit_cast(unsigned, ahi)) << 32) | __builtin_bit_cast(unsigned, alo);
+    b = (static_cast<unsigned long long>(__builtin_bit_cast(unsigned, bhi)) << 32) | __builtin_bit_cast(unsigned, blo);
+  } else {
+    a = v;
+    b = (static_cast<unsigned long long>(static_cast<unsigned>(xor_lane_bits<O>(hi))) << 32) |
+        static_cast<unsigned>(xor_lane_bits<O>(lo));
+  }
+  return a > b ? a : b;
+}
+template <int kWidth>
+__device__ __forceinline__ unsigned long long u64_group_max(unsigned long long v) {
+  if constexpr (kWidth >= 64) v = u64_xor_max<32>(v);
+  if constexpr (kWidth >= 32) v = u64_xor_max<16>(v);
+  if constexpr (kWidth >= 16) v = u64_xor_max<8>(v);
+  if constexpr (kWidth >= 8) v = u64_xor_max<4>(v);
+  if constexpr (kWidth >= 4) v = u64_xor_max<2>(v);
+  if constexpr (kWidth >= 2) v = u64_xor_max<1>(v);
+  return v;
 }
 
 // Eight values per lane, a[t], each summed over the 8 lanes that share lane & 7 (partners lane ^ 8,
