@@ -247,7 +247,7 @@ __device__ __forceinline__ unsigned half_bits(_Float16 x) { return __builtin_bit
 #endif
 constexpr int kTlLayers = 4, kTlSlots = 160, kTlLm = 1 + kTlLayers * 8 * 4;
 enum TlLm { kTlArrive = 0, kTlY, kTlDigits, kTlRegScored, kTlResScored, kTlScored, kTlCand, kTlMaxStored,
-            kTlFinGathered, kTlFinStored, kTlCaught };
+            kTlFinGathered, kTlFinStored, kTlCaught, kTlBatch0 };
 constexpr int kTlSa = kTlLm + 12;
 enum TlSa { kTlSaRow = 0, kTlSaPartial, kTlSaMerged, kTlSaBarrier };
 static_assert(kTlSa + kTlSaBarrier < kTlSlots, "timeline slots");
@@ -1565,6 +1565,10 @@ __device__ __forceinline__ void lm_head_phase(const StepArgs& a, const StepHead&
     score(row, row < rb, bt);
     if (k + kBufs < nb) load(k + kBufs, bt);
   };
+  if (FW_STEP_TIMELINE && !FW_LM_CATCH_FIRST && wv == 0 && nb > 0) {  // profiling: batch 0 of wave 0 in
+    asm volatile("" ::"v"(bt[0].w[kQ8C - 1].x));
+    tl.mark(kTlLm + kTlBatch0);
+  }
   if (!FW_LM_CATCH_FIRST && wv < kLmRowWaves) {
 #pragma unroll
     for (int k = 0; k < kBufs; ++k)

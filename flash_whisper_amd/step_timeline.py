@@ -37,7 +37,8 @@ TL_CLK = TL_SA + 8  # shader clock at the step's start and end, wall clock at it
 TL_WAVE = TL_CLK + 3  # layer 0's self attention: each wave's partials done
 LM_POINTS = ('arrived', 'final LN done', 'y digits ready', 'first HBM batches scored', 'resident rows scored',
              'all rows scored', 'candidates listed', 'block maximum stored', 'every block maximum gathered',
-             'token and state stored (last block)', 'residual caught up (thread 0; before the final LN)')
+             'token and state stored (last block)', 'residual caught up (thread 0; before the final LN)',
+             'first HBM batch of wave 0 in registers (after the y digits)')
 
 
 def tl_phase(layer, phase):
