@@ -1382,7 +1382,11 @@ __device__ __forceinline__ int fin_block() { return gridDim.x - 1; }
 
 // LM-head rows of blocks 0 .. b - 1: the table split in proportion to block weights, kLmWeight for
 // most blocks and kLmLateWeight for the n_late blocks from late0 on (taken round the grid).
-constexpr int kLmWeight = 7, kLmLateWeight = 6;
+#ifndef FW_LM_LATE_WEIGHT
+#define FW_LM_LATE_WEIGHT 6  // sevenths of a share for the blocks that ran the last fc2
+#endif
+constexpr int kLmWeight = 7, kLmLateWeight = FW_LM_LATE_WEIGHT;
+static_assert(kLmLateWeight >= 1 && kLmLateWeight <= 14, "FW_LM_LATE_WEIGHT");
 __host__ __device__ inline int lm_rows_before(int b, int vocab, int G, int late0, int n_late) {
   const int wrap = late0 + n_late - G;  // late blocks past the end of the grid, counted from block 0
   const int late = (wrap > 0 ? min(b, wrap) : 0) + max(0, min(b, min(G, late0 + n_late)) - late0);
@@ -2304,7 +2308,7 @@ static int step_sizes_check(const char* name, int n_layers, int vocab, int max_p
     return fw_fail(FW_EINVAL, "%s: %d CUs run too few blocks (the self attention needs %d beside %d others)", name,
                    grid, kStepHeads * nv, w_vec);
   if (has_head) {
-    // the largest share: a block of weight kLmWeight next to the late blocks
+    // the largest share (any placement of the late run)
     int most = 0;
     for (int b = 0; b < grid; ++b)
       most = std::max(most, lm_rows_before(b + 1, vocab, grid, 0, w_vec) - lm_rows_before(b, vocab, grid, 0, w_vec));
