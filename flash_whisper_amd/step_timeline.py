@@ -191,7 +191,7 @@ def summary(rows, rows2, n_layers, pos0, from_pos):
         by_len[f'L{length}'] = {'dur_us': med([h['dur'] for h in hits]), 'work_us': med([h['work'] for h in hits]),
                                 'samples': len(hits)}
     last = (len(layers) - 1, 8)
-    stored = len(LM_POINTS) - 1
+    stored = LM_POINTS.index('token and state stored (last block)')
     lm = [r[('lm', stored)]['last'] - r[last]['out'] for r in rows if ('lm', stored) in r and last in r]
     return {'phases': phases, 'self_attention_by_length': by_len, 'lm_head_us': med(lm),
             'step_period_us': med([r['period'] for r in rows if 'period' in r]), 'steps': len(rows),
