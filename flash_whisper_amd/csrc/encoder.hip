@@ -11,7 +11,8 @@ namespace {
 // ------------------------------------------------------------------------------------------
 // GEMM: out[m, n] = epi(sum_k A[m, k] * W[n, k]).  Block tile BM x 128 x 64 with BM in
 // {256, 192, 128, 64}; waves in a (BM / 64 or 2) x 2 arrangement, each wave a (64 or 32) x 64 tile of
-// v_mfma_f32_32x32x16_f16 products (192-row tiles: 2 x 4 waves of 96 x 32).
+// v_mfma_f32_32x32x16_f16 products (192-row tiles: 2 x 4 waves of 96 x 32; 64-row tiles: 2 x 4 waves
+// of 32 x 32).
 //  - LDS: one [rows][64] fp16 tile per operand and stage, 8 x 16-byte chunks per row, chunk c of
 //    row r stored in slot swz_slot(r, c) = c ^ ((r >> 1) & 7), so the 16 rows a 16-lane group reads
 //    for one MFMA operand cover all 64 banks (conflict-free ds_read_b128).
@@ -286,9 +287,11 @@ __device__ __forceinline__ void mma_frags(const Frags<kTM, kTN>& f, f16v (&acc)[
 // have ST - 1 stages of MFMA time to land and LDS read latency is hidden behind the MFMAs.
 // The LDS ring depth ST is picked per tile height: 256-row tiles use three 48 KB stages (one 8-wave
 // block per CU); 128-row tiles (8 waves of 32 x 64; the split-k products) four 32 KB stages; 64-row
-// tiles (launched when 128-row tiles would leave CUs idle) four 24 KB stages.
+// tiles (launched when 128-row tiles would leave CUs idle) four 24 KB stages (5 or 6 measured the same).
 // Tuning knobs (defaults measured on MI355X): ring depths per tile height, the minimum number of
-// 256-row tiles for that shape, waves per 256-row block, and the XCD rectangle grouping.
+// 256-row tiles for that shape, waves per 256-row and 64-row block, and the XCD rectangle grouping.
+// 8 waves on the 64-row tiles (two per SIMD) against 4: out projection 14.8 -> 14.35 us, stem conv
+// 36.0 -> 33.0 us (kernel trace, same box).
 #ifndef FW_ST128
 #define FW_ST128 4
 #endif
@@ -323,10 +326,14 @@ static_assert(FW_MIN_TILES256 >= 1, "FW_MIN_TILES256 must be positive");
 #endif
 static_assert(FW_W256 == 2 || FW_W256 == 4 || FW_W256 == 8 || FW_W256 == 16,
               "FW_W256: 2 x (FW_W256 / 2) waves, each a whole number of 32-row MFMA tiles of the 256 rows");
+#ifndef FW_W64
+#define FW_W64 8  // waves per 64-row block: 8 (2 x 4 of 32 x 32) or 4 (2 x 2 of 32 x 64)
+#endif
+static_assert(FW_W64 == 4 || FW_W64 == 8, "FW_W64: 4 or 8 waves per 64-row block");
 template <int BM>
-constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 || BM == 128 ? 8 : 4; }
+constexpr int gemm_waves() { return BM == 256 ? FW_W256 : BM == 192 || BM == 128 ? 8 : FW_W64; }
 template <int BM>
-constexpr int gemm_wave_cols() { return BM == 192 ? 4 : 2; }
+constexpr int gemm_wave_cols() { return BM == 192 || (BM == 64 && FW_W64 == 8) ? 4 : 2; }
 
 // Source of the implicit conv's zero padding rows: a k stage of one A row is 64 halves.
 __device__ __align__(16) _Float16 g_zero_row[kBK];
